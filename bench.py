@@ -1,0 +1,200 @@
+"""Benchmark: prefill->decode KV handoff on one MI355X.
+
+Workload: Qwen2.5-1.5B-shaped BF16 pool (28 layers, 2 KV
+heads x 128, 16-token pages of 448 KiB) in a 2112 MiB arena; a 5040-token
+prefix = 315 pages whose destination runs are uniform in 1..5 pages.
+
+A step is one handoff launch over the device-resident run list (all layers'
+K and V of all 315 pages). Before every step a 1 GiB scrub write evicts the
+source and destination from L2 / MALL (Infinity Cache), so every step reads
+from and writes to HBM; the scrub is outside the per-launch HIP-event timing.
+
+Prints ONE JSON line. value = algorithmic bytes (read + write of every copied
+page) / mean kernel duration, in GB/s. ms_per_step = that mean handoff kernel
+latency. The CPU baseline is the oracle's restatement of the reference's
+per-run memcpy loop (split_pd_engine.cpp:96-108), one thread, on a host copy of
+the same pool and plan.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "paged-batch-engine_amd"))
+sys.path.insert(0, str(ROOT))
+
+PEAK_GBPS = 8000.0
+METRIC = "KV handoff HBM GB/s (% of peak) + latency for 5040-tok Qwen2.5-1.5B prefix"
+PMC_SUMMARY = ROOT / "profiles" / "handoff_copy_c2_pmc.txt"
+
+
+def _traffic_from_profile():
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE
+    + WRITE_SIZE of copy_runs_kernel, scaled by the plain-copy calibration)."""
+    if not PMC_SUMMARY.exists():
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", PMC_SUMMARY.read_text(), re.M)
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(w, host_arena, seconds: float):
+    """Reference-faithful host copy: coalesce + one memcpy per run, 1 thread."""
+    from oracle import oracle as O
+    import numpy as np
+    g = w.geometry
+    reps, t0 = 0, time.perf_counter()
+    O.copy_handoff(host_arena, w.src_ids, w.dst_ids, g.half(), g.layers)  # first touch
+    t0 = time.perf_counter()
+    while True:
+        O.copy_handoff(host_arena, w.src_ids, w.dst_ids, g.half(), g.layers)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    per = el / reps
+    return {"value": round(w.algorithmic_bytes() / per / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": f"{reps} handoffs of the config-2 plan (315 pages, {w.copied_bytes()} B "
+                      f"copied each) in {el:.1f} s; {per * 1e3:.2f} ms per handoff",
+            "ms_per_handoff": round(per * 1e3, 3)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-scrub", action="store_true", help="hot-cache timing (diagnostic)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the handoff is a same-GPU page migration.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+    import pbe_handoff as P
+    import workload as W
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    w = W.config2(0)
+    g = w.geometry
+    kv = P.shape(g.layers, g.kv_heads, g.head_dim, g.page_tokens)
+
+    arena = torch.empty(w.arena_bytes, dtype=torch.uint8, device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2)
+    vals = arena.view(torch.bfloat16)
+    chunk = 1 << 26
+    for i in range(0, vals.numel(), chunk):
+        v = vals[i:i + chunk]
+        v.copy_((torch.randn(v.numel(), generator=gen, device=dev) * w.sigma).to(torch.bfloat16))
+    scrub = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    view = P.view_of(arena.data_ptr(), w.arena_bytes)
+    runs = P.build_runs(w.src_ids, w.dst_ids, kv)
+    rl = P.RunList.bf16(view, view, runs, kv)
+    info = rl.info()
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    # correctness of this exact run: device result vs oracle on the same pool
+    from oracle import oracle as O
+    torch.cuda.synchronize()
+    host_before = arena.cpu().numpy()
+    expected = host_before.copy()
+    O.copy_handoff(expected, w.src_ids, w.dst_ids, g.half(), g.layers)
+    rl.copy(sp)
+    torch.cuda.synchronize()
+    parity = bool(np.array_equal(arena.cpu().numpy(), expected))
+    del expected
+
+    for i in range(args.warmup):
+        if not args.no_scrub:
+            scrub.fill_(i & 0xff)
+        rl.copy(sp)
+    torch.cuda.synchronize()
+
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        if not args.no_scrub:
+            scrub.fill_((i + 1) & 0xff)
+        starts[i].record(stream)
+        rl.copy(sp)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    times_ms = np.array([s.elapsed_time(e) for s, e in zip(starts, ends)])
+    mean_ms = float(times_ms.mean())
+    alg = w.algorithmic_bytes()
+    achieved = alg / (mean_ms * 1e-3) / 1e9
+
+    # end-to-end handoff latency of the one-call form (validate, coalesce,
+    # stage, launch, wait), as copy_shared_kv does before commit_kv
+    lat = []
+    for i in range(20):
+        if not args.no_scrub:
+            scrub.fill_(i & 0xff)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        P.copy_shared_kv(view, w.src_ids, w.dst_ids, kv, 0, sp)
+        torch.cuda.synchronize()
+        lat.append(time.perf_counter() - t)
+    e2e_us = float(np.median(lat) * 1e6)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(w, host_before, args.cpu_seconds)
+        cpu["cores_on_host"] = os.cpu_count()
+
+    traffic = _traffic_from_profile()
+    line = {
+        "metric": METRIC,
+        "value": round(achieved, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(mean_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1.5) BF16 pool, seeded page plan)",
+        "config": {"workload": w.name, "layers": g.layers, "kv_heads": g.kv_heads,
+                   "head_dim": g.head_dim, "page_tokens": g.page_tokens,
+                   "page_bytes": g.page_bytes(), "prefix_tokens": 5040, "pages": w.pages,
+                   "runs": int(info.runs), "arena_mib": w.arena_bytes >> 20,
+                   "cache": "cold (1 GiB scrub before each step)" if not args.no_scrub else "hot"},
+        "latency_us": {"kernel_mean": round(mean_ms * 1e3, 2),
+                       "kernel_p50": round(float(np.median(times_ms)) * 1e3, 2),
+                       "kernel_min": round(float(times_ms.min()) * 1e3, 2),
+                       "handoff_e2e_p50": round(e2e_us, 1)},
+        "pct_of_peak": round(100 * achieved / PEAK_GBPS, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
+                     "traffic": traffic, "algorithmic_bytes": alg},
+        "cpu_baseline": cpu,
+        "parity_vs_oracle": parity,
+        "wall_ms_per_step_incl_scrub": round(wall / args.steps * 1e3, 4),
+    }
+    print(json.dumps(line))
+    rl.close()
+    return 0 if parity else 3
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,205 @@
+/*
+ * pbe_handoff.h -- C ABI of the MI355X prefill->decode KV handoff.
+ *
+ * Plain C: pointers, sizes and status codes; no exceptions cross this
+ * boundary and no framework types appear in the signatures. Every call returns
+ * PBE_OK (0) on success, a positive code for "not yet", or a negative error;
+ * pbe_last_error() gives the calling thread's last message.
+ *
+ * Terms (they follow the reference's shared-KV arena):
+ *   half   one layer's K or V plane of one page: page_tokens*kv_heads*head_dim*elem
+ *          bytes (shared_kv_arena.h:35-36, block_allocator.cpp:369-372).
+ *   page   all layers' K and V of page_tokens tokens, [layer][K|V][tok][head][dim],
+ *          2*layers*half bytes.
+ *   block id  byte offset / half; page ids are multiples of 2*layers
+ *          (split_pd_engine.cpp:76, shared_kv_arena.cpp:128,224-229).
+ *   run    maximal stretch of pages whose source and destination ids both
+ *          advance by one page (split_pd_engine.cpp:96-101).
+ *
+ * Threading: the arena, event and run-list objects may be used from any thread
+ * but not concurrently on the same object; launches go to the caller's stream.
+ * Lifetime: a run list holds resolved device addresses of the arena views it
+ * was built for; destroy it before unmapping those views.
+ */
+#ifndef PBE_HANDOFF_H_
+#define PBE_HANDOFF_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PBE_OK 0
+#define PBE_NOT_READY 1          /* event/copy still in flight */
+#define PBE_ERR_INVALID (-1)     /* rejected before any device work was queued */
+#define PBE_ERR_HIP (-2)         /* a HIP call failed; see pbe_last_error() */
+#define PBE_ERR_UNKNOWN (-3)     /* completion unknown: retain every resource */
+#define PBE_ERR_NOMEM (-4)
+#define PBE_ERR_UNSUPPORTED (-5)
+
+#define PBE_MAX_SEGMENTS 16
+#define PBE_IPC_HANDLE_BYTES 64
+
+/* Last error message of the calling thread ("" if none). */
+const char* pbe_last_error(void);
+/* Library version string, e.g. "pbe-handoff 1.0 gfx950". */
+const char* pbe_version(void);
+
+/* KV page geometry. elem_bytes is 2 for BF16 pools, 1 for FP8 payload pools. */
+typedef struct pbe_kv_shape {
+  int32_t layers;
+  int32_t kv_heads;
+  int32_t head_dim;
+  int32_t page_tokens;
+} pbe_kv_shape;
+
+/* One coalesced run: `pages` whole pages from src_block to dst_block. */
+typedef struct pbe_run {
+  int32_t src_block;
+  int32_t dst_block;
+  int32_t pages;
+} pbe_run;
+
+/* A process-local mapping of a (possibly segmented) arena. Byte offset o lies
+ * in segment o / segment_bytes at base[seg] + o % segment_bytes. A single
+ * allocation is nseg = 1, segment_bytes = bytes. Callers may fill this for
+ * memory they own; pbe_arena_view() fills it for arenas made here. */
+typedef struct pbe_arena_view {
+  uint64_t bytes;
+  uint64_t segment_bytes;
+  uint32_t nseg;
+  uint32_t reserved;
+  void* base[PBE_MAX_SEGMENTS];
+} pbe_arena_view;
+
+/* ---- arena: owner allocation + IPC export/import ------------------------
+ * Replaces run_shared_kv_owner's cudaMalloc/cudaIpcGetMemHandle
+ * (shared_kv_owner.cpp:25,28) and SharedKVArenaClient's cudaIpcOpenMemHandle
+ * (shared_kv_client.cpp:81). The arena is split into segments of at most
+ * segment_bytes (a multiple of the page size chosen by the caller), each its
+ * own hipMalloc, so every exported allocation stays below 2 GiB. */
+typedef struct pbe_arena pbe_arena;
+
+typedef struct pbe_arena_ipc {
+  uint32_t version;
+  uint32_t nseg;
+  uint64_t bytes;
+  uint64_t segment_bytes;
+  uint64_t epoch;
+  uint8_t gpu_uuid[16];
+  uint8_t handles[PBE_MAX_SEGMENTS][PBE_IPC_HANDLE_BYTES];
+} pbe_arena_ipc;
+
+int pbe_arena_create(int device, uint64_t bytes, uint64_t segment_bytes, uint64_t epoch,
+                     pbe_arena** out);
+int pbe_arena_export(const pbe_arena* arena, pbe_arena_ipc* out);
+/* Opens every segment in this process; fails if the exporter's GPU UUID differs
+ * (shared_kv_client.cpp:72-73 checks the same). */
+int pbe_arena_import(const pbe_arena_ipc* ipc, int device, pbe_arena** out);
+int pbe_arena_get_view(const pbe_arena* arena, pbe_arena_view* out);
+uint64_t pbe_arena_epoch(const pbe_arena* arena);
+int pbe_arena_destroy(pbe_arena* arena);
+
+/* ---- IPC completion events -------------------------------------------
+ * hipEventInterprocess|hipEventDisableTiming events whose handle crosses
+ * processes (pattern of demo/cuda_ipc_event_probe.cu:24-27,70-75 and
+ * data/ipc_pool.h:24-26): P records "KV written", D waits on it in its
+ * stream before the copy, D records "copy done", P waits before retiring. */
+typedef struct pbe_event pbe_event;
+int pbe_event_create(int device, int interprocess, pbe_event** out);
+int pbe_event_export(const pbe_event* event, uint8_t out[PBE_IPC_HANDLE_BYTES]);
+int pbe_event_import(const uint8_t handle[PBE_IPC_HANDLE_BYTES], int device, pbe_event** out);
+int pbe_event_record(pbe_event* event, void* stream);
+int pbe_event_wait(pbe_event* event, void* stream); /* stream waits, host does not */
+int pbe_event_query(pbe_event* event);              /* PBE_OK or PBE_NOT_READY */
+int pbe_event_synchronize(pbe_event* event);
+int pbe_event_destroy(pbe_event* event);
+
+/* ---- host-side plan ----------------------------------------------------
+ * Source id checks of copy_shared_kv (split_pd_engine.cpp:70-77): id >= 0,
+ * id % (2*layers) == 0 and (id + 2*layers)*half <= arena bytes. On failure
+ * *bad_index is the first offending position. */
+int pbe_validate_ids(const int32_t* ids, int64_t n, const pbe_kv_shape* shape,
+                     uint32_t elem_bytes, uint64_t arena_bytes, int64_t* bad_index);
+
+/* Coalesce page-major id lists into runs (split_pd_engine.cpp:96-101). A run
+ * additionally breaks where either side would cross a segment boundary
+ * (segment_bytes 0 = unsegmented). `out` holds n entries. */
+int pbe_build_runs(const int32_t* src_ids, const int32_t* dst_ids, int64_t n,
+                   const pbe_kv_shape* shape, uint32_t elem_bytes, uint64_t segment_bytes,
+                   pbe_run* out, int64_t* n_runs);
+
+/* ---- device-resident run lists ----------------------------------------
+ * Validated on the host (every run inside one segment of its view, no source
+ * range overlapping a destination range), resolved to device addresses and
+ * uploaded once; a list is reusable for any number of launches. */
+typedef struct pbe_runlist pbe_runlist;
+
+typedef struct pbe_runlist_info {
+  int64_t runs;
+  int64_t pages;
+  uint64_t src_bytes;    /* bytes read per launch */
+  uint64_t dst_bytes;    /* payload bytes written per launch */
+  uint64_t scale_bytes;  /* scale bytes written per launch (FP8 per-token-head) */
+  uint64_t slices;       /* work units of the launch */
+} pbe_runlist_info;
+
+/* BF16 (or any-dtype) identity copy inside/between arena views. The list
+ * replaces the reference's one cudaMemcpyAsync per run (split_pd_engine.cpp:104). */
+int pbe_runlist_create(const pbe_arena_view* src, const pbe_arena_view* dst,
+                       const pbe_run* runs, int64_t n_runs, const pbe_kv_shape* shape,
+                       uint32_t elem_bytes, int device, pbe_runlist** out);
+
+#define PBE_FP8_SCALE_PER_TOKEN_HEAD 0 /* amax per (token, head) row, scales written */
+#define PBE_FP8_SCALE_TABLE 1          /* static amax per (layer, K|V, head) */
+
+/* Fused BF16 -> FP8 E4M3 handoff. src ids are in BF16 half units, dst ids in
+ * FP8 half units (half/2). In per-token-head mode, dst_scales is the base of a
+ * page-major scale pool of 2*layers*page_tokens*kv_heads fp32 per page, page
+ * index = dst_block / (2*layers); it may be NULL in table mode. */
+int pbe_runlist_create_fp8(const pbe_arena_view* src, const pbe_arena_view* dst,
+                           void* dst_scales, uint64_t dst_scales_bytes, const pbe_run* runs,
+                           int64_t n_runs, const pbe_kv_shape* shape, int device,
+                           pbe_runlist** out);
+int pbe_runlist_get_info(const pbe_runlist* list, pbe_runlist_info* out);
+int pbe_runlist_destroy(pbe_runlist* list);
+
+/* ---- launches (asynchronous on `stream`, a hipStream_t; NULL = default) ----
+ * One kernel for every layer's K and V of every page in the list. */
+int pbe_handoff_copy(const pbe_runlist* list, void* stream);
+/* scale_mode PBE_FP8_SCALE_*; amax_table (device, 2*layers*kv_heads fp32,
+ * index (2*layer+kv)*kv_heads+head) is read only in table mode. */
+int pbe_handoff_copy_fp8(const pbe_runlist* list, int scale_mode, const float* amax_table,
+                         void* stream);
+
+/* ---- one-call form of copy_shared_kv's data path -----------------------
+ * Validates ids against the arena (as split_pd_engine.cpp:70-77), coalesces,
+ * builds and uploads a run list, launches one copy and returns the copied
+ * bytes in *copied (the reference's return value, split_pd_engine.cpp:107,114).
+ * The run list is released after the launch completes on `stream`; the call
+ * does not wait for the copy. */
+int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids,
+                       const int32_t* dst_ids, int64_t n, const pbe_kv_shape* shape,
+                       int device, void* stream, uint64_t* copied);
+
+/* ---- generic component-list copy ---------------------------------------
+ * Executes an arbitrary list of (src, dst, bytes) device copies in one launch:
+ * the device form of ExecuteCpuTransfer (transfer_plan.cpp:392-403) used by
+ * the HIP TransferBackend. Ops must have 16-byte aligned addresses and sizes;
+ * the list is copied to device memory owned by the call. */
+typedef struct pbe_copy_op {
+  uint64_t src;
+  uint64_t dst;
+  uint64_t bytes;
+} pbe_copy_op;
+int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream);
+
+/* GPU UUID of `device` (16 bytes), as compared across processes. */
+int pbe_device_uuid(int device, uint8_t out[16]);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PBE_HANDOFF_H_ */

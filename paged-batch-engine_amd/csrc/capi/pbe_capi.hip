@@ -1,0 +1,809 @@
+// C ABI of the MI355X KV handoff: arena ownership and IPC, IPC events,
+// host-side run planning and validation, device run lists and launches.
+// Every entry point validates its whole input on the host before any device
+// work is queued, so a rejected call never writes a destination byte.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../kernels/handoff_kernels.h"
+#include "pbe_handoff.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(PBE_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define PBE_HIP(call)                                        \
+  do {                                                       \
+    const hipError_t pbe_e_ = (call);                        \
+    if (pbe_e_ != hipSuccess) return hip_fail(pbe_e_, #call); \
+  } while (0)
+
+// Makes `device` current for the scope and restores the caller's device.
+class DeviceScope {
+ public:
+  explicit DeviceScope(int device) {
+    if (hipGetDevice(&old_) != hipSuccess) {
+      err_ = hipErrorNoDevice;
+      return;
+    }
+    err_ = hipSetDevice(device);
+  }
+  ~DeviceScope() {
+    if (err_ == hipSuccess) (void)hipSetDevice(old_);
+  }
+  hipError_t error() const { return err_; }
+
+ private:
+  int old_ = 0;
+  hipError_t err_ = hipSuccess;
+};
+
+#define PBE_DEVICE_SCOPE(dev)                                          \
+  DeviceScope pbe_scope_(dev);                                         \
+  if (pbe_scope_.error() != hipSuccess) return hip_fail(pbe_scope_.error(), "select device")
+
+bool shape_ok(const pbe_kv_shape* s) {
+  return s && s->layers > 0 && s->kv_heads > 0 && s->head_dim > 0 && s->page_tokens > 0;
+}
+
+// half = one layer's K or V plane of one page (block_allocator.cpp:369-372).
+uint64_t half_bytes(const pbe_kv_shape& s, uint32_t elem_bytes) {
+  return (uint64_t)s.page_tokens * (uint64_t)s.kv_heads * (uint64_t)s.head_dim * elem_bytes;
+}
+
+bool view_ok(const pbe_arena_view* v) {
+  if (!v || v->nseg == 0 || v->nseg > PBE_MAX_SEGMENTS || v->bytes == 0 || v->segment_bytes == 0)
+    return false;
+  if ((v->bytes + v->segment_bytes - 1) / v->segment_bytes != v->nseg) return false;
+  for (uint32_t i = 0; i < v->nseg; ++i)
+    if (!v->base[i]) return false;
+  return true;
+}
+
+// Resolves [offset, offset+len) of a view to a device address; the span must
+// lie inside one segment and inside the view.
+bool resolve(const pbe_arena_view& v, uint64_t offset, uint64_t len, uint64_t* addr) {
+  if (offset > v.bytes || len > v.bytes - offset) return false;
+  const uint64_t seg = offset / v.segment_bytes;
+  const uint64_t in_seg = offset % v.segment_bytes;
+  if (seg >= v.nseg || len > v.segment_bytes - in_seg) return false;
+  *addr = reinterpret_cast<uint64_t>(v.base[seg]) + in_seg;
+  return true;
+}
+
+// Rejects any destination span overlapping another destination span or any
+// source span (a copy must never race with itself).
+bool spans_disjoint(std::vector<std::pair<uint64_t, uint64_t>> dst,
+                    std::vector<std::pair<uint64_t, uint64_t>> src) {
+  std::sort(dst.begin(), dst.end());
+  for (size_t i = 1; i < dst.size(); ++i)
+    if (dst[i].first < dst[i - 1].second) return false;
+  std::sort(src.begin(), src.end());
+  size_t j = 0;
+  for (const auto& s : src) {
+    while (j < dst.size() && dst[j].second <= s.first) ++j;
+    if (j < dst.size() && dst[j].first < s.second) return false;
+  }
+  return true;
+}
+
+// Checks on the host that [ptr, ptr+bytes) lies inside one allocation a kernel
+// on `device` may touch (device memory of that GPU, or pinned host memory), so
+// a bad pointer is rejected instead of faulting the GPU. Verified allocation
+// ranges are remembered in `known` for the rest of the call.
+struct Range {
+  uint64_t begin, end;
+};
+bool accessible(const void* ptr, uint64_t bytes, int device, std::vector<Range>* known) {
+  const uint64_t p = reinterpret_cast<uint64_t>(ptr);
+  if (!p || bytes > ~0ull - p) return false;
+  for (const Range& r : *known)
+    if (p >= r.begin && p + bytes <= r.end) return true;
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, const_cast<void*>(ptr)) != hipSuccess || !base) {
+    (void)hipGetLastError();
+    return false;
+  }
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, ptr) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  const bool ok_type = (attr.type == hipMemoryTypeDevice && attr.device == device) ||
+                       attr.type == hipMemoryTypeHost;
+  const Range r{reinterpret_cast<uint64_t>(base), reinterpret_cast<uint64_t>(base) + size};
+  if (!ok_type || p < r.begin || p + bytes > r.end) return false;
+  known->push_back(r);
+  return true;
+}
+
+bool view_accessible(const pbe_arena_view& v, int device, std::vector<Range>* known) {
+  for (uint32_t i = 0; i < v.nseg; ++i) {
+    const uint64_t len = std::min(v.segment_bytes, v.bytes - (uint64_t)i * v.segment_bytes);
+    if (!accessible(v.base[i], len, device, known)) return false;
+  }
+  return true;
+}
+
+int cu_count(int device) {
+  static std::mutex mu;
+  static int cached[64] = {0};
+  std::lock_guard<std::mutex> lock(mu);
+  if (device < 0 || device >= 64) return 256;
+  if (!cached[device]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cached[device] = cus;
+  }
+  return cached[device];
+}
+
+// Waves to keep resident for a streaming copy: enough 16-byte loads in flight
+// to cover HBM latency on every CU. PBE_WAVES_PER_CU / PBE_SLICES_PER_WAVE
+// override the choice (tuning experiments only).
+pbe::LaunchShape launch_shape(uint64_t total_slices, int device) {
+  pbe::LaunchShape shape;
+  if (const char* env = std::getenv("PBE_SLICES_PER_WAVE")) {
+    shape.slices_per_wave = std::max(1, std::atoi(env));
+    return shape;
+  }
+  int per_cu = 16;
+  if (const char* env = std::getenv("PBE_WAVES_PER_CU")) per_cu = std::max(1, std::atoi(env));
+  const uint64_t target = (uint64_t)cu_count(device) * (uint64_t)per_cu;
+  shape.slices_per_wave = (uint32_t)std::max<uint64_t>(1, (total_slices + target - 1) / target);
+  return shape;
+}
+
+}  // namespace
+
+struct pbe_arena {
+  int device = 0;
+  bool owner = false;
+  uint64_t bytes = 0, segment_bytes = 0, epoch = 0;
+  uint32_t nseg = 0;
+  void* base[PBE_MAX_SEGMENTS] = {};
+  uint8_t uuid[16] = {};
+};
+
+struct pbe_event {
+  int device = 0;
+  bool imported = false;
+  hipEvent_t event = nullptr;
+};
+
+struct pbe_runlist {
+  int device = 0;
+  bool fp8 = false;
+  bool has_scales = false;
+  pbe::DevRun* runs = nullptr;  // device memory
+  uint32_t n_runs = 0;
+  uint32_t total_slices = 0;
+  uint64_t page_bytes = 0;      // source bytes per page
+  pbe_runlist_info info{};
+  pbe::LaunchShape shape;
+  pbe_kv_shape kv{};
+};
+
+extern "C" {
+
+const char* pbe_last_error(void) { return g_error.c_str(); }
+
+const char* pbe_version(void) { return "pbe-handoff 1.0 gfx950"; }
+
+int pbe_device_uuid(int device, uint8_t out[16]) {
+  if (!out) return fail(PBE_ERR_INVALID, "null output");
+  hipUUID uuid;
+  PBE_HIP(hipDeviceGetUuid(&uuid, device));
+  std::memcpy(out, uuid.bytes, 16);
+  return PBE_OK;
+}
+
+// ---------------------------------------------------------------- arena
+int pbe_arena_create(int device, uint64_t bytes, uint64_t segment_bytes, uint64_t epoch,
+                     pbe_arena** out) {
+  if (!out) return fail(PBE_ERR_INVALID, "null output");
+  *out = nullptr;
+  if (!bytes || !epoch) return fail(PBE_ERR_INVALID, "arena bytes and epoch must be non-zero");
+  if (!segment_bytes) segment_bytes = bytes;
+  if (segment_bytes % 256) return fail(PBE_ERR_INVALID, "segment size must be 256-byte aligned");
+  const uint64_t nseg = (bytes + segment_bytes - 1) / segment_bytes;
+  if (nseg > PBE_MAX_SEGMENTS) return fail(PBE_ERR_INVALID, "arena needs %llu > %d segments",
+                                           (unsigned long long)nseg, PBE_MAX_SEGMENTS);
+  PBE_DEVICE_SCOPE(device);
+  pbe_arena* a = new (std::nothrow) pbe_arena;
+  if (!a) return fail(PBE_ERR_NOMEM, "arena object");
+  a->device = device;
+  a->owner = true;
+  a->bytes = bytes;
+  a->segment_bytes = segment_bytes;
+  a->epoch = epoch;
+  a->nseg = (uint32_t)nseg;
+  for (uint32_t i = 0; i < a->nseg; ++i) {
+    const uint64_t len = std::min(segment_bytes, bytes - (uint64_t)i * segment_bytes);
+    const hipError_t e = hipMalloc(&a->base[i], len);  // dedicated, never pool-cached
+    if (e != hipSuccess) {
+      for (uint32_t j = 0; j < i; ++j) (void)hipFree(a->base[j]);
+      delete a;
+      return hip_fail(e, "hipMalloc(arena segment)");
+    }
+  }
+  if (pbe_device_uuid(device, a->uuid) != PBE_OK) std::memset(a->uuid, 0, 16);
+  *out = a;
+  return PBE_OK;
+}
+
+int pbe_arena_export(const pbe_arena* a, pbe_arena_ipc* out) {
+  if (!a || !out) return fail(PBE_ERR_INVALID, "null argument");
+  if (!a->owner) return fail(PBE_ERR_INVALID, "only the owner exports an arena");
+  PBE_DEVICE_SCOPE(a->device);
+  pbe_arena_ipc ipc;
+  std::memset(&ipc, 0, sizeof(ipc));
+  ipc.version = 1;
+  ipc.nseg = a->nseg;
+  ipc.bytes = a->bytes;
+  ipc.segment_bytes = a->segment_bytes;
+  ipc.epoch = a->epoch;
+  std::memcpy(ipc.gpu_uuid, a->uuid, 16);
+  static_assert(sizeof(hipIpcMemHandle_t) <= PBE_IPC_HANDLE_BYTES, "IPC handle size");
+  for (uint32_t i = 0; i < a->nseg; ++i) {
+    hipIpcMemHandle_t h;
+    PBE_HIP(hipIpcGetMemHandle(&h, a->base[i]));
+    std::memcpy(ipc.handles[i], &h, sizeof(h));
+  }
+  *out = ipc;
+  return PBE_OK;
+}
+
+int pbe_arena_import(const pbe_arena_ipc* ipc, int device, pbe_arena** out) {
+  if (!ipc || !out) return fail(PBE_ERR_INVALID, "null argument");
+  *out = nullptr;
+  if (ipc->version != 1 || ipc->nseg == 0 || ipc->nseg > PBE_MAX_SEGMENTS || !ipc->bytes ||
+      !ipc->segment_bytes || (ipc->bytes + ipc->segment_bytes - 1) / ipc->segment_bytes != ipc->nseg)
+    return fail(PBE_ERR_INVALID, "malformed arena IPC descriptor");
+  uint8_t uuid[16];
+  int rc = pbe_device_uuid(device, uuid);
+  if (rc != PBE_OK) return rc;
+  if (std::memcmp(uuid, ipc->gpu_uuid, 16) != 0)
+    return fail(PBE_ERR_INVALID, "arena owner and importer GPU UUID differ");
+  PBE_DEVICE_SCOPE(device);
+  pbe_arena* a = new (std::nothrow) pbe_arena;
+  if (!a) return fail(PBE_ERR_NOMEM, "arena object");
+  a->device = device;
+  a->owner = false;
+  a->bytes = ipc->bytes;
+  a->segment_bytes = ipc->segment_bytes;
+  a->epoch = ipc->epoch;
+  a->nseg = ipc->nseg;
+  std::memcpy(a->uuid, uuid, 16);
+  for (uint32_t i = 0; i < a->nseg; ++i) {
+    hipIpcMemHandle_t h;
+    std::memcpy(&h, ipc->handles[i], sizeof(h));
+    const hipError_t e = hipIpcOpenMemHandle(&a->base[i], h, hipIpcMemLazyEnablePeerAccess);
+    if (e != hipSuccess) {
+      for (uint32_t j = 0; j < i; ++j) (void)hipIpcCloseMemHandle(a->base[j]);
+      delete a;
+      return hip_fail(e, "hipIpcOpenMemHandle(arena segment)");
+    }
+  }
+  *out = a;
+  return PBE_OK;
+}
+
+int pbe_arena_get_view(const pbe_arena* a, pbe_arena_view* out) {
+  if (!a || !out) return fail(PBE_ERR_INVALID, "null argument");
+  std::memset(out, 0, sizeof(*out));
+  out->bytes = a->bytes;
+  out->segment_bytes = a->segment_bytes;
+  out->nseg = a->nseg;
+  for (uint32_t i = 0; i < a->nseg; ++i) out->base[i] = a->base[i];
+  return PBE_OK;
+}
+
+uint64_t pbe_arena_epoch(const pbe_arena* a) { return a ? a->epoch : 0; }
+
+int pbe_arena_destroy(pbe_arena* a) {
+  if (!a) return PBE_OK;
+  PBE_DEVICE_SCOPE(a->device);
+  int rc = PBE_OK;
+  for (uint32_t i = 0; i < a->nseg; ++i) {
+    if (!a->base[i]) continue;
+    const hipError_t e = a->owner ? hipFree(a->base[i]) : hipIpcCloseMemHandle(a->base[i]);
+    if (e != hipSuccess) rc = hip_fail(e, a->owner ? "hipFree(arena)" : "hipIpcCloseMemHandle");
+  }
+  delete a;
+  return rc;
+}
+
+// ---------------------------------------------------------------- events
+int pbe_event_create(int device, int interprocess, pbe_event** out) {
+  if (!out) return fail(PBE_ERR_INVALID, "null output");
+  *out = nullptr;
+  PBE_DEVICE_SCOPE(device);
+  pbe_event* ev = new (std::nothrow) pbe_event;
+  if (!ev) return fail(PBE_ERR_NOMEM, "event object");
+  ev->device = device;
+  const unsigned flags =
+      hipEventDisableTiming | (interprocess ? (unsigned)hipEventInterprocess : 0u);
+  const hipError_t e = hipEventCreateWithFlags(&ev->event, flags);
+  if (e != hipSuccess) {
+    delete ev;
+    return hip_fail(e, "hipEventCreateWithFlags");
+  }
+  *out = ev;
+  return PBE_OK;
+}
+
+int pbe_event_export(const pbe_event* ev, uint8_t out[PBE_IPC_HANDLE_BYTES]) {
+  if (!ev || !out) return fail(PBE_ERR_INVALID, "null argument");
+  static_assert(sizeof(hipIpcEventHandle_t) <= PBE_IPC_HANDLE_BYTES, "event handle size");
+  PBE_DEVICE_SCOPE(ev->device);
+  hipIpcEventHandle_t h;
+  PBE_HIP(hipIpcGetEventHandle(&h, ev->event));
+  std::memset(out, 0, PBE_IPC_HANDLE_BYTES);
+  std::memcpy(out, &h, sizeof(h));
+  return PBE_OK;
+}
+
+int pbe_event_import(const uint8_t handle[PBE_IPC_HANDLE_BYTES], int device, pbe_event** out) {
+  if (!handle || !out) return fail(PBE_ERR_INVALID, "null argument");
+  *out = nullptr;
+  PBE_DEVICE_SCOPE(device);
+  pbe_event* ev = new (std::nothrow) pbe_event;
+  if (!ev) return fail(PBE_ERR_NOMEM, "event object");
+  ev->device = device;
+  ev->imported = true;
+  hipIpcEventHandle_t h;
+  std::memcpy(&h, handle, sizeof(h));
+  const hipError_t e = hipIpcOpenEventHandle(&ev->event, h);
+  if (e != hipSuccess) {
+    delete ev;
+    return hip_fail(e, "hipIpcOpenEventHandle");
+  }
+  *out = ev;
+  return PBE_OK;
+}
+
+int pbe_event_record(pbe_event* ev, void* stream) {
+  if (!ev) return fail(PBE_ERR_INVALID, "null event");
+  PBE_DEVICE_SCOPE(ev->device);
+  PBE_HIP(hipEventRecord(ev->event, static_cast<hipStream_t>(stream)));
+  return PBE_OK;
+}
+
+int pbe_event_wait(pbe_event* ev, void* stream) {
+  if (!ev) return fail(PBE_ERR_INVALID, "null event");
+  PBE_DEVICE_SCOPE(ev->device);
+  PBE_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(stream), ev->event, 0));
+  return PBE_OK;
+}
+
+int pbe_event_query(pbe_event* ev) {
+  if (!ev) return fail(PBE_ERR_INVALID, "null event");
+  PBE_DEVICE_SCOPE(ev->device);
+  const hipError_t e = hipEventQuery(ev->event);
+  if (e == hipSuccess) return PBE_OK;
+  if (e == hipErrorNotReady) return PBE_NOT_READY;
+  fail(PBE_ERR_UNKNOWN, "hipEventQuery: %s", hipGetErrorString(e));
+  return PBE_ERR_UNKNOWN;
+}
+
+int pbe_event_synchronize(pbe_event* ev) {
+  if (!ev) return fail(PBE_ERR_INVALID, "null event");
+  PBE_DEVICE_SCOPE(ev->device);
+  const hipError_t e = hipEventSynchronize(ev->event);
+  if (e != hipSuccess) return fail(PBE_ERR_UNKNOWN, "hipEventSynchronize: %s", hipGetErrorString(e));
+  return PBE_OK;
+}
+
+int pbe_event_destroy(pbe_event* ev) {
+  if (!ev) return PBE_OK;
+  PBE_DEVICE_SCOPE(ev->device);
+  const hipError_t e = hipEventDestroy(ev->event);
+  delete ev;
+  if (e != hipSuccess) return hip_fail(e, "hipEventDestroy");
+  return PBE_OK;
+}
+
+// ---------------------------------------------------------------- planning
+int pbe_validate_ids(const int32_t* ids, int64_t n, const pbe_kv_shape* shape,
+                     uint32_t elem_bytes, uint64_t arena_bytes, int64_t* bad_index) {
+  if (bad_index) *bad_index = -1;
+  if ((!ids && n) || n < 0 || !shape_ok(shape) || !elem_bytes)
+    return fail(PBE_ERR_INVALID, "invalid id list or shape");
+  const uint64_t half = half_bytes(*shape, elem_bytes);
+  const int64_t stride = 2 * (int64_t)shape->layers;
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t id = ids[i];
+    if (id < 0 || id % stride != 0 || ((uint64_t)id + (uint64_t)stride) * half > arena_bytes) {
+      if (bad_index) *bad_index = i;
+      return fail(PBE_ERR_INVALID, "block id %lld at %lld outside the shared page layout",
+                  (long long)id, (long long)i);
+    }
+  }
+  return PBE_OK;
+}
+
+int pbe_build_runs(const int32_t* src_ids, const int32_t* dst_ids, int64_t n,
+                   const pbe_kv_shape* shape, uint32_t elem_bytes, uint64_t segment_bytes,
+                   pbe_run* out, int64_t* n_runs) {
+  if (!n_runs || n < 0 || (n && (!src_ids || !dst_ids || !out)) || !shape_ok(shape) || !elem_bytes)
+    return fail(PBE_ERR_INVALID, "invalid run-building arguments");
+  const uint64_t half = half_bytes(*shape, elem_bytes);
+  const int32_t stride = 2 * shape->layers;
+  const uint64_t page_bytes = (uint64_t)stride * half;
+  // A page may extend a run only if it is address-contiguous with the previous
+  // page in the same segment, on both sides.
+  auto same_segment = [&](int32_t prev, int32_t cur) {
+    if (!segment_bytes) return true;
+    return ((uint64_t)prev * half) / segment_bytes ==
+           ((uint64_t)cur * half + page_bytes - 1) / segment_bytes;
+  };
+  int64_t runs = 0;
+  for (int64_t i = 0; i < n;) {
+    int64_t end = i + 1;
+    while (end < n && src_ids[end] == src_ids[end - 1] + stride &&
+           dst_ids[end] == dst_ids[end - 1] + stride && same_segment(src_ids[i], src_ids[end]) &&
+           same_segment(dst_ids[i], dst_ids[end]))
+      ++end;
+    out[runs].src_block = src_ids[i];
+    out[runs].dst_block = dst_ids[i];
+    out[runs].pages = (int32_t)(end - i);
+    ++runs;
+    i = end;
+  }
+  *n_runs = runs;
+  return PBE_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- run lists
+namespace {
+
+struct Resolved {
+  std::vector<pbe::DevRun> runs;
+  pbe_runlist_info info{};
+};
+
+// Builds device run entries for either kernel. src pages are src_page_bytes
+// long in the src view, dst pages dst_page_bytes long in the dst view;
+// scale pages (FP8) scale_page_bytes long at scales.
+int resolve_runs(const pbe_arena_view& src, const pbe_arena_view& dst, uint64_t src_half,
+                 uint64_t dst_half, int32_t stride, const pbe_run* runs, int64_t n_runs,
+                 uint64_t scales, uint64_t scales_bytes, uint64_t scale_page_bytes,
+                 uint32_t slice, Resolved* out) {
+  if (n_runs <= 0 || n_runs > 0x7fffffff) return fail(PBE_ERR_INVALID, "run count out of range");
+  const uint64_t src_page = (uint64_t)stride * src_half;
+  const uint64_t dst_page = (uint64_t)stride * dst_half;
+  std::vector<std::pair<uint64_t, uint64_t>> dst_spans, src_spans;
+  out->runs.resize((size_t)n_runs);
+  uint64_t slices = 0;
+  for (int64_t i = 0; i < n_runs; ++i) {
+    const pbe_run& r = runs[i];
+    if (r.src_block < 0 || r.dst_block < 0 || r.pages <= 0 || r.src_block % stride ||
+        r.dst_block % stride)
+      return fail(PBE_ERR_INVALID, "run %lld: ids must be non-negative page ids, pages > 0",
+                  (long long)i);
+    pbe::DevRun d{};
+    const uint64_t sb = (uint64_t)r.pages * src_page, db = (uint64_t)r.pages * dst_page;
+    if (!resolve(src, (uint64_t)r.src_block * src_half, sb, &d.src))
+      return fail(PBE_ERR_INVALID, "run %lld: source span outside one arena segment", (long long)i);
+    if (!resolve(dst, (uint64_t)r.dst_block * dst_half, db, &d.dst))
+      return fail(PBE_ERR_INVALID, "run %lld: destination span outside one arena segment",
+                  (long long)i);
+    if (scale_page_bytes) {
+      const uint64_t off = (uint64_t)(r.dst_block / stride) * scale_page_bytes;
+      const uint64_t len = (uint64_t)r.pages * scale_page_bytes;
+      if (off > scales_bytes || len > scales_bytes - off)
+        return fail(PBE_ERR_INVALID, "run %lld: scale span outside the scale pool", (long long)i);
+      d.aux = scales + off;
+      dst_spans.emplace_back(d.aux, d.aux + len);
+    }
+    d.pages = (uint32_t)r.pages;
+    d.slice_begin = (uint32_t)slices;
+    slices += (sb + slice - 1) / slice;
+    if (slices > 0xfffffff0ull) return fail(PBE_ERR_INVALID, "run list too large for one launch");
+    src_spans.emplace_back(d.src, d.src + sb);
+    dst_spans.emplace_back(d.dst, d.dst + db);
+    out->info.src_bytes += sb;
+    out->info.dst_bytes += db;
+    out->info.pages += r.pages;
+    if (scale_page_bytes) out->info.scale_bytes += (uint64_t)r.pages * scale_page_bytes;
+    out->runs[(size_t)i] = d;
+  }
+  if (!spans_disjoint(dst_spans, src_spans))
+    return fail(PBE_ERR_INVALID, "run list writes a byte twice or overwrites its own source");
+  out->info.runs = n_runs;
+  out->info.slices = slices;
+  return PBE_OK;
+}
+
+int upload_runlist(Resolved& res, int device, bool fp8, bool has_scales, uint64_t page_bytes,
+                   const pbe_kv_shape& kv, pbe_runlist** out) {
+  PBE_DEVICE_SCOPE(device);
+  pbe_runlist* list = new (std::nothrow) pbe_runlist;
+  if (!list) return fail(PBE_ERR_NOMEM, "run list object");
+  const size_t bytes = res.runs.size() * sizeof(pbe::DevRun);
+  hipError_t e = hipMalloc(&list->runs, bytes);
+  if (e == hipSuccess) e = hipMemcpy(list->runs, res.runs.data(), bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    if (list->runs) (void)hipFree(list->runs);
+    delete list;
+    return hip_fail(e, "upload run list");
+  }
+  list->device = device;
+  list->fp8 = fp8;
+  list->has_scales = has_scales;
+  list->n_runs = (uint32_t)res.runs.size();
+  list->total_slices = (uint32_t)res.info.slices;
+  list->page_bytes = page_bytes;
+  list->info = res.info;
+  list->kv = kv;
+  list->shape = launch_shape(res.info.slices, device);
+  *out = list;
+  return PBE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pbe_runlist_create(const pbe_arena_view* src, const pbe_arena_view* dst, const pbe_run* runs,
+                       int64_t n_runs, const pbe_kv_shape* shape, uint32_t elem_bytes, int device,
+                       pbe_runlist** out) {
+  if (!out) return fail(PBE_ERR_INVALID, "null output");
+  *out = nullptr;
+  if (!view_ok(src) || !view_ok(dst) || !runs || !shape_ok(shape) || !elem_bytes)
+    return fail(PBE_ERR_INVALID, "invalid arena view, run list or shape");
+  const uint64_t half = half_bytes(*shape, elem_bytes);
+  if (half % 16) return fail(PBE_ERR_INVALID, "half-plane bytes must be a multiple of 16");
+  {
+    PBE_DEVICE_SCOPE(device);
+    std::vector<Range> known;
+    if (!view_accessible(*src, device, &known) || !view_accessible(*dst, device, &known))
+      return fail(PBE_ERR_INVALID, "arena view is not device memory of device %d", device);
+  }
+  Resolved res;
+  int rc = resolve_runs(*src, *dst, half, half, 2 * shape->layers, runs, n_runs, 0, 0, 0,
+                        pbe::slice_bytes(pbe::KernelKind::kCopy), &res);
+  if (rc != PBE_OK) return rc;
+  return upload_runlist(res, device, false, false, 2ull * shape->layers * half, *shape, out);
+}
+
+int pbe_runlist_create_fp8(const pbe_arena_view* src, const pbe_arena_view* dst, void* dst_scales,
+                           uint64_t dst_scales_bytes, const pbe_run* runs, int64_t n_runs,
+                           const pbe_kv_shape* shape, int device, pbe_runlist** out) {
+  if (!out) return fail(PBE_ERR_INVALID, "null output");
+  *out = nullptr;
+  if (!view_ok(src) || !view_ok(dst) || !runs || !shape_ok(shape))
+    return fail(PBE_ERR_INVALID, "invalid arena view, run list or shape");
+  const uint32_t lanes = (uint32_t)shape->head_dim / 8u;
+  if (shape->head_dim % 8 || lanes == 0 || lanes > 64 || (lanes & (lanes - 1)))
+    return fail(PBE_ERR_UNSUPPORTED, "FP8 handoff needs head_dim = 8 * 2^k <= 512");
+  const uint64_t half16 = half_bytes(*shape, 2), half8 = half_bytes(*shape, 1);
+  const uint64_t rows = (uint64_t)shape->page_tokens * shape->kv_heads;
+  const uint64_t scale_page = dst_scales ? 2ull * shape->layers * rows * 4u : 0;
+  if (dst_scales && (reinterpret_cast<uint64_t>(dst_scales) % 4))
+    return fail(PBE_ERR_INVALID, "scale pool must be 4-byte aligned");
+  if (half16 % 16) return fail(PBE_ERR_INVALID, "half-plane bytes must be a multiple of 16");
+  {
+    PBE_DEVICE_SCOPE(device);
+    std::vector<Range> known;
+    if (!view_accessible(*src, device, &known) || !view_accessible(*dst, device, &known) ||
+        (dst_scales && !accessible(dst_scales, dst_scales_bytes, device, &known)))
+      return fail(PBE_ERR_INVALID, "arena view or scale pool is not memory of device %d", device);
+  }
+  Resolved res;
+  int rc = resolve_runs(*src, *dst, half16, half8, 2 * shape->layers, runs, n_runs,
+                        reinterpret_cast<uint64_t>(dst_scales), dst_scales_bytes, scale_page,
+                        pbe::slice_bytes(pbe::KernelKind::kFp8), &res);
+  if (rc != PBE_OK) return rc;
+  return upload_runlist(res, device, true, dst_scales != nullptr, 2ull * shape->layers * half16,
+                        *shape, out);
+}
+
+int pbe_runlist_get_info(const pbe_runlist* list, pbe_runlist_info* out) {
+  if (!list || !out) return fail(PBE_ERR_INVALID, "null argument");
+  *out = list->info;
+  return PBE_OK;
+}
+
+int pbe_runlist_destroy(pbe_runlist* list) {
+  if (!list) return PBE_OK;
+  PBE_DEVICE_SCOPE(list->device);
+  const hipError_t e = hipFree(list->runs);
+  delete list;
+  if (e != hipSuccess) return hip_fail(e, "hipFree(run list)");
+  return PBE_OK;
+}
+
+int pbe_handoff_copy(const pbe_runlist* list, void* stream) {
+  if (!list) return fail(PBE_ERR_INVALID, "null run list");
+  if (list->fp8) return fail(PBE_ERR_INVALID, "FP8 run list passed to the BF16 copy");
+  PBE_DEVICE_SCOPE(list->device);
+  PBE_HIP(pbe::launch_copy_runs(list->runs, list->n_runs, list->total_slices, list->page_bytes,
+                                list->shape, static_cast<hipStream_t>(stream)));
+  return PBE_OK;
+}
+
+int pbe_handoff_copy_fp8(const pbe_runlist* list, int scale_mode, const float* amax_table,
+                         void* stream) {
+  if (!list) return fail(PBE_ERR_INVALID, "null run list");
+  if (!list->fp8) return fail(PBE_ERR_INVALID, "BF16 run list passed to the FP8 copy");
+  if (scale_mode == PBE_FP8_SCALE_PER_TOKEN_HEAD && !list->has_scales)
+    return fail(PBE_ERR_INVALID, "per-token-head scales need a scale pool");
+  if (scale_mode == PBE_FP8_SCALE_TABLE && !amax_table)
+    return fail(PBE_ERR_INVALID, "table mode needs an amax table");
+  if (scale_mode != PBE_FP8_SCALE_PER_TOKEN_HEAD && scale_mode != PBE_FP8_SCALE_TABLE)
+    return fail(PBE_ERR_INVALID, "unknown scale mode %d", scale_mode);
+  PBE_DEVICE_SCOPE(list->device);
+  const pbe_kv_shape& kv = list->kv;
+  const uint32_t rows_per_plane = (uint32_t)(kv.page_tokens * kv.kv_heads);
+  PBE_HIP(pbe::launch_copy_runs_fp8(
+      list->runs, list->n_runs, list->total_slices, list->page_bytes, (uint32_t)kv.head_dim / 8u,
+      rows_per_plane, (uint32_t)kv.kv_heads, rows_per_plane * 2u * (uint32_t)kv.layers,
+      scale_mode == PBE_FP8_SCALE_TABLE, amax_table, list->shape,
+      static_cast<hipStream_t>(stream)));
+  return PBE_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- one-call forms
+namespace {
+
+// Per-device pinned staging + device buffer for the one-call entry points.
+// A buffer is reused only after the launch that read it has completed.
+struct Staging {
+  std::mutex mu;
+  void* host = nullptr;
+  void* dev = nullptr;
+  size_t cap = 0;
+  hipEvent_t done = nullptr;
+  bool pending = false;
+};
+
+Staging& staging_for(int device) {
+  static Staging slots[64];
+  return slots[device & 63];
+}
+
+// Copies `bytes` of `data` to a device buffer that stays valid until the next
+// call on this device, ordered on `stream`. Caller holds st.mu.
+int stage(Staging& st, const void* data, size_t bytes, hipStream_t stream, void** dev_out) {
+  if (st.pending) {
+    PBE_HIP(hipEventSynchronize(st.done));
+    st.pending = false;
+  }
+  if (bytes > st.cap) {
+    if (st.host) (void)hipHostFree(st.host);
+    if (st.dev) (void)hipFree(st.dev);
+    st.host = st.dev = nullptr;
+    st.cap = 0;
+    size_t cap = 4096;
+    while (cap < bytes) cap *= 2;
+    PBE_HIP(hipHostMalloc(&st.host, cap, hipHostMallocDefault));
+    PBE_HIP(hipMalloc(&st.dev, cap));
+    st.cap = cap;
+  }
+  if (!st.done) PBE_HIP(hipEventCreateWithFlags(&st.done, hipEventDisableTiming));
+  std::memcpy(st.host, data, bytes);
+  PBE_HIP(hipMemcpyAsync(st.dev, st.host, bytes, hipMemcpyHostToDevice, stream));
+  *dev_out = st.dev;
+  return PBE_OK;
+}
+
+int stage_done(Staging& st, hipStream_t stream) {
+  PBE_HIP(hipEventRecord(st.done, stream));
+  st.pending = true;
+  return PBE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, const int32_t* dst_ids,
+                       int64_t n, const pbe_kv_shape* shape, int device, void* stream,
+                       uint64_t* copied) {
+  if (copied) *copied = 0;
+  if (!view_ok(arena) || !shape_ok(shape) || n <= 0 || !src_ids || !dst_ids)
+    return fail(PBE_ERR_INVALID, "invalid handoff arguments");
+  int64_t bad = -1;
+  int rc = pbe_validate_ids(src_ids, n, shape, 2, arena->bytes, &bad);
+  if (rc != PBE_OK) return rc;
+  rc = pbe_validate_ids(dst_ids, n, shape, 2, arena->bytes, &bad);
+  if (rc != PBE_OK) return rc;
+  std::vector<pbe_run> runs((size_t)n);
+  int64_t n_runs = 0;
+  rc = pbe_build_runs(src_ids, dst_ids, n, shape, 2, arena->nseg > 1 ? arena->segment_bytes : 0,
+                      runs.data(), &n_runs);
+  if (rc != PBE_OK) return rc;
+  const uint64_t half = half_bytes(*shape, 2);
+  if (half % 16) return fail(PBE_ERR_INVALID, "half-plane bytes must be a multiple of 16");
+  {
+    PBE_DEVICE_SCOPE(device);
+    std::vector<Range> known;
+    if (!view_accessible(*arena, device, &known))
+      return fail(PBE_ERR_INVALID, "arena view is not device memory of device %d", device);
+  }
+  Resolved res;
+  rc = resolve_runs(*arena, *arena, half, half, 2 * shape->layers, runs.data(), n_runs, 0, 0, 0,
+                    pbe::slice_bytes(pbe::KernelKind::kCopy), &res);
+  if (rc != PBE_OK) return rc;
+  PBE_DEVICE_SCOPE(device);
+  Staging& st = staging_for(device);
+  std::lock_guard<std::mutex> lock(st.mu);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  void* dev = nullptr;
+  rc = stage(st, res.runs.data(), res.runs.size() * sizeof(pbe::DevRun), s, &dev);
+  if (rc != PBE_OK) return rc;
+  PBE_HIP(pbe::launch_copy_runs(static_cast<const pbe::DevRun*>(dev), (uint32_t)n_runs,
+                                (uint32_t)res.info.slices, 2ull * shape->layers * half,
+                                launch_shape(res.info.slices, device), s));
+  rc = stage_done(st, s);
+  if (rc != PBE_OK) return rc;
+  if (copied) *copied = res.info.src_bytes;
+  return PBE_OK;
+}
+
+int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream) {
+  if (n_ops < 0 || (n_ops && !ops) || n_ops > 0x7fffffff)
+    return fail(PBE_ERR_INVALID, "invalid op list");
+  if (!n_ops) return PBE_OK;
+  std::vector<std::pair<uint64_t, uint64_t>> dst, src;
+  for (int64_t i = 0; i < n_ops; ++i) {
+    if (!ops[i].src || !ops[i].dst || !ops[i].bytes)
+      return fail(PBE_ERR_INVALID, "op %lld: null pointer or zero bytes", (long long)i);
+    dst.emplace_back(ops[i].dst, ops[i].dst + ops[i].bytes);
+    src.emplace_back(ops[i].src, ops[i].src + ops[i].bytes);
+  }
+  if (!spans_disjoint(dst, src))
+    return fail(PBE_ERR_INVALID, "op list writes a byte twice or overwrites its own source");
+  PBE_DEVICE_SCOPE(device);
+  {
+    std::vector<Range> known;
+    for (int64_t i = 0; i < n_ops; ++i)
+      if (!accessible(reinterpret_cast<const void*>(ops[i].src), ops[i].bytes, device, &known) ||
+          !accessible(reinterpret_cast<const void*>(ops[i].dst), ops[i].bytes, device, &known))
+        return fail(PBE_ERR_INVALID, "op %lld: endpoint is not device or pinned memory",
+                    (long long)i);
+  }
+  Staging& st = staging_for(device);
+  std::lock_guard<std::mutex> lock(st.mu);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  void* dev = nullptr;
+  static_assert(sizeof(pbe_copy_op) == sizeof(pbe::DevOp), "op layout");
+  int rc = stage(st, ops, (size_t)n_ops * sizeof(pbe_copy_op), s, &dev);
+  if (rc != PBE_OK) return rc;
+  PBE_HIP(pbe::launch_copy_ops(static_cast<const pbe::DevOp*>(dev), (uint32_t)n_ops, s));
+  return stage_done(st, s);
+}
+
+}  // extern "C"

@@ -1,0 +1,48 @@
+// Internal interface between the C ABI layer and the gfx950 kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pbe {
+
+constexpr int kThreadsPerBlock = 256;
+constexpr int kCopyUnroll = 8;  // 8 KiB per wave slice for the identity copy
+constexpr int kFp8Unroll = 8;   // 8 KiB of BF16 source per wave slice
+
+// Device form of one run: resolved addresses in this process's mapping.
+// slice_begin is the exclusive prefix of slices over the preceding runs.
+struct DevRun {
+  uint64_t src;          // first source byte
+  uint64_t dst;          // first destination payload byte
+  uint64_t aux;          // first destination scale byte (FP8 per-token-head), else 0
+  uint32_t slice_begin;  // first global slice of this run
+  uint32_t pages;        // whole pages in the run
+};
+static_assert(sizeof(DevRun) == 32, "device run entry is 32 bytes");
+
+struct DevOp {
+  uint64_t src;
+  uint64_t dst;
+  uint64_t bytes;
+};
+
+enum class KernelKind { kCopy, kFp8 };
+
+struct LaunchShape {
+  uint32_t slices_per_wave = 1;
+};
+
+uint32_t slice_bytes(KernelKind kind);
+
+hipError_t launch_copy_runs(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
+                            uint64_t page_bytes, const LaunchShape& shape, hipStream_t stream);
+
+hipError_t launch_copy_runs_fp8(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
+                                uint64_t page_bytes, uint32_t lanes_per_row,
+                                uint32_t rows_per_plane, uint32_t kv_heads,
+                                uint32_t rows_per_page, bool table, const float* amax_table,
+                                const LaunchShape& shape, hipStream_t stream);
+
+hipError_t launch_copy_ops(const DevOp* ops, uint32_t n_ops, hipStream_t stream);
+
+}  // namespace pbe

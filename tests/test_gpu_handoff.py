@@ -1,0 +1,204 @@
+"""GPU parity of the BF16 handoff copy against the CPU oracle.
+
+Every case fills a device arena with seeded BF16 values, snapshots it, runs the
+HIP kernel through the C ABI, and compares the WHOLE arena with the oracle
+applied to the snapshot: copied pages must be bit-identical and every byte
+outside the destination pages must be unchanged (canary check).
+"""
+import numpy as np
+import pytest
+
+import pbe_handoff as P
+import workload as W
+from oracle import oracle as O
+from tests.conftest import say
+from tests.gpu_util import device_arena, fill_bf16, first_diff, snapshot, stream_ptr
+
+pytestmark = pytest.mark.gpu
+
+
+def _kv(g: W.Geometry) -> P.KvShape:
+    return P.shape(g.layers, g.kv_heads, g.head_dim, g.page_tokens)
+
+
+def _run_runlist_case(torch, w: W.Workload, seed: int, batched: bool = True):
+    g = w.geometry
+    kv = _kv(g)
+    bufs, view = device_arena(torch, w.arena_bytes, w.segment_bytes)
+    for i, b in enumerate(bufs):
+        fill_bf16(torch, b, w.sigma, seed + i)
+    torch.cuda.synchronize()
+    before = snapshot(bufs)
+    expected = before.copy()
+    O.copy_handoff(expected, w.src_ids, w.dst_ids, g.half(), g.layers)
+    reqs = [w] if batched else [W.Workload(w.name, g, w.arena_bytes, w.segment_bytes, [r])
+                                for r in w.requests]
+    for part in reqs:
+        runs = P.build_runs(part.src_ids, part.dst_ids, kv, 2, w.segment_bytes)
+        with P.RunList.bf16(view, view, runs, kv) as rl:
+            info = rl.info()
+            assert info.pages == part.pages
+            assert info.src_bytes == part.pages * g.page_bytes()
+            rl.copy(stream_ptr(torch))
+            torch.cuda.synchronize()
+    after = snapshot(bufs)
+    assert np.array_equal(after, expected), first_diff(after, expected)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_small_random_plans(torch_cuda, seed):
+    shapes = [(3, 2, 64), (1, 1, 8), (5, 4, 128), (2, 2, 16), (7, 1, 32), (4, 8, 64)]
+    L, H, D = shapes[seed]
+    w = W.small(seed=seed, layers=L, kv_heads=H, head_dim=D, n_pages=96, handoff_pages=13 + seed,
+                max_run=1 + seed)
+    say(f"small seed={seed} L={L} H={H} D={D} pages={w.pages}")
+    _run_runlist_case(torch_cuda, w, seed)
+
+
+def test_small_segmented_arena(torch_cuda):
+    w = W.small(seed=11, layers=2, kv_heads=2, head_dim=64, n_pages=120, handoff_pages=20,
+                max_run=6, segment_pages=40)
+    say(f"segmented small pages={w.pages} segs={w.arena_bytes // w.segment_bytes}")
+    _run_runlist_case(torch_cuda, w, 11)
+
+
+def test_config1_qwen05b(torch_cuda):
+    w = W.config1(0)
+    say("config1")
+    _run_runlist_case(torch_cuda, w, 1)
+
+
+def test_config2_qwen15b_5040(torch_cuda):
+    w = W.config2(0)
+    say("config2")
+    _run_runlist_case(torch_cuda, w, 2)
+
+
+@pytest.mark.parametrize("batched", [True, False])
+def test_config3_multi_request(torch_cuda, batched):
+    w = W.config3(0)
+    say(f"config3 batched={batched}")
+    _run_runlist_case(torch_cuda, w, 3, batched=batched)
+
+
+def test_config5_segmented_7b(torch_cuda):
+    w = W.config5(0)
+    say("config5 in-process, 3 segments")
+    _run_runlist_case(torch_cuda, w, 5)
+
+
+def test_copy_shared_kv_one_call(torch_cuda):
+    torch = torch_cuda
+    w = W.config2(1)
+    g = w.geometry
+    kv = _kv(g)
+    say("pbe_copy_shared_kv config2 seed1")
+    bufs, view = device_arena(torch, w.arena_bytes)
+    fill_bf16(torch, bufs[0], w.sigma, 7)
+    torch.cuda.synchronize()
+    before = snapshot(bufs)
+    expected = before.copy()
+    ref_bytes = O.copy_handoff(expected, w.src_ids, w.dst_ids, g.half(), g.layers)
+    copied = P.copy_shared_kv(view, w.src_ids, w.dst_ids, kv, 0, stream_ptr(torch))
+    torch.cuda.synchronize()
+    assert copied == ref_bytes == w.copied_bytes()
+    after = snapshot(bufs)
+    assert np.array_equal(after, expected), first_diff(after, expected)
+    # a second call reuses the staging buffer
+    w2 = W.config2(2)
+    expected2 = after.copy()
+    O.copy_handoff(expected2, w2.src_ids, w2.dst_ids, g.half(), g.layers)
+    P.copy_shared_kv(view, w2.src_ids, w2.dst_ids, kv, 0, stream_ptr(torch))
+    torch.cuda.synchronize()
+    after2 = snapshot(bufs)
+    assert np.array_equal(after2, expected2), first_diff(after2, expected2)
+
+
+def test_copy_shared_kv_rejects_bad_ids_before_any_write(torch_cuda):
+    torch = torch_cuda
+    w = W.small(seed=3, n_pages=32, handoff_pages=5)
+    g = w.geometry
+    kv = _kv(g)
+    bufs, view = device_arena(torch, w.arena_bytes)
+    fill_bf16(torch, bufs[0], 1.0, 3)
+    torch.cuda.synchronize()
+    before = snapshot(bufs)
+    bad = [
+        (w.src_ids + 1, w.dst_ids),                                   # not a page id
+        (w.src_ids, np.where(np.arange(w.pages) == 2, -g.stride, w.dst_ids)),  # negative
+        (w.src_ids, np.full(w.pages, 32 * g.stride)),                 # past the arena
+        (w.src_ids, w.src_ids),                                       # overwrite own source
+        (w.src_ids, np.full(w.pages, w.dst_ids[0])),                  # dst written twice
+    ]
+    for i, (s, d) in enumerate(bad):
+        say(f"bad ids case {i}")
+        with pytest.raises(P.PbeError) as e:
+            P.copy_shared_kv(view, s, d, kv, 0, stream_ptr(torch))
+        assert e.value.code == P.PBE_ERR_INVALID
+    torch.cuda.synchronize()
+    assert np.array_equal(snapshot(bufs), before)
+
+
+def test_runlist_rejects_foreign_memory(torch_cuda):
+    torch = torch_cuda
+    kv = P.shape(2, 2, 64)
+    host = np.zeros(8 * kv.page_bytes(), np.uint8)
+    view = P.view_of(host.ctypes.data, host.nbytes)
+    with pytest.raises(P.PbeError) as e:
+        P.RunList.bf16(view, view, [(0, 4 * kv.layers * 2, 1)], kv)
+    assert e.value.code == P.PBE_ERR_INVALID
+
+
+def test_component_ops_match_generic_plan(torch_cuda):
+    """The generic plan form (2*layers component copies per page,
+    pd_handoff.cpp:192-213) through pbe_copy_ops equals the run copy."""
+    torch = torch_cuda
+    w = W.small(seed=5, layers=3, kv_heads=2, head_dim=64, n_pages=64, handoff_pages=11)
+    g = w.geometry
+    say("copy_ops component form")
+    bufs, view = device_arena(torch, w.arena_bytes)
+    fill_bf16(torch, bufs[0], 1.0, 5)
+    torch.cuda.synchronize()
+    before = snapshot(bufs)
+    expected = before.copy()
+    O.copy_components(expected, w.src_ids, w.dst_ids, g.half(), g.layers)
+    base = bufs[0].data_ptr()
+    half = g.half()
+    ops = []
+    for s, d in zip(w.src_ids.tolist(), w.dst_ids.tolist()):
+        for plane in range(2 * g.layers):
+            ops.append((base + (s + plane) * half, base + (d + plane) * half, half))
+    P.copy_ops(ops, 0, stream_ptr(torch))
+    torch.cuda.synchronize()
+    after = snapshot(bufs)
+    assert np.array_equal(after, expected), first_diff(after, expected)
+    # unaligned byte ops take the byte path
+    torch.cuda.synchronize()
+    src_off, dst_off = 3, 5 * half + 7
+    P.copy_ops([(base + src_off, base + dst_off, 37)], 0, stream_ptr(torch))
+    torch.cuda.synchronize()
+    after2 = snapshot(bufs)
+    exp2 = after.copy()
+    exp2[dst_off:dst_off + 37] = after[src_off:src_off + 37]
+    assert np.array_equal(after2, exp2), first_diff(after2, exp2)
+
+
+def test_repeated_launches_are_idempotent(torch_cuda):
+    torch = torch_cuda
+    w = W.config2(3)
+    g = w.geometry
+    kv = _kv(g)
+    say("repeat launches config2 seed3")
+    bufs, view = device_arena(torch, w.arena_bytes)
+    fill_bf16(torch, bufs[0], w.sigma, 9)
+    torch.cuda.synchronize()
+    before = snapshot(bufs)
+    expected = before.copy()
+    O.copy_handoff(expected, w.src_ids, w.dst_ids, g.half(), g.layers)
+    runs = P.build_runs(w.src_ids, w.dst_ids, kv)
+    with P.RunList.bf16(view, view, runs, kv) as rl:
+        for _ in range(5):
+            rl.copy(stream_ptr(torch))
+        torch.cuda.synchronize()
+    after = snapshot(bufs)
+    assert np.array_equal(after, expected), first_diff(after, expected)
