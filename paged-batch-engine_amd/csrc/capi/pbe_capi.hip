@@ -149,34 +149,30 @@ bool view_accessible(const pbe_arena_view& v, int device, std::vector<Range>* kn
   return true;
 }
 
-int cu_count(int device) {
-  static std::mutex mu;
-  static int cached[64] = {0};
-  std::lock_guard<std::mutex> lock(mu);
-  if (device < 0 || device >= 64) return 256;
-  if (!cached[device]) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
-        cus <= 0)
-      cus = 256;
-    cached[device] = cus;
-  }
-  return cached[device];
+// Identity-copy kernel variant. The defaults are the measured best on MI355X;
+// PBE_UNROLL / PBE_POLICY / PBE_BLOCK / PBE_LDS override them for tuning
+// experiments only.
+pbe::CopyConfig copy_config() {
+  pbe::CopyConfig c;
+  if (const char* e = std::getenv("PBE_UNROLL")) c.unroll = std::atoi(e);
+  if (c.unroll != 2 && c.unroll != 4 && c.unroll != 8) c.unroll = pbe::kCopyUnroll;
+  if (const char* e = std::getenv("PBE_POLICY")) c.policy = std::atoi(e);
+  if (const char* e = std::getenv("PBE_BLOCK")) c.block = std::atoi(e);
+  if (c.block != 64 && c.block != 256 && c.block != 1024) c.block = 256;
+  if (const char* e = std::getenv("PBE_LDS")) c.lds_bytes = (uint32_t)std::atoi(e);
+  return c;
 }
 
-// Waves to keep resident for a streaming copy: enough 16-byte loads in flight
-// to cover HBM latency on every CU. PBE_WAVES_PER_CU / PBE_SLICES_PER_WAVE
-// override the choice (tuning experiments only).
-pbe::LaunchShape launch_shape(uint64_t total_slices, int device) {
+pbe::LaunchShape launch_shape(uint64_t total_slices, int device, const pbe::CopyConfig& cfg) {
+  (void)total_slices;
+  (void)device;
   pbe::LaunchShape shape;
-  if (const char* env = std::getenv("PBE_SLICES_PER_WAVE")) {
+  shape.copy = cfg;
+  // One slice per wave measured best on MI355X: the dispatcher keeps every CU
+  // full and each wave has all of its loads in flight at once.
+  shape.slices_per_wave = 1;
+  if (const char* env = std::getenv("PBE_SLICES_PER_WAVE"))
     shape.slices_per_wave = std::max(1, std::atoi(env));
-    return shape;
-  }
-  int per_cu = 16;
-  if (const char* env = std::getenv("PBE_WAVES_PER_CU")) per_cu = std::max(1, std::atoi(env));
-  const uint64_t target = (uint64_t)cu_count(device) * (uint64_t)per_cu;
-  shape.slices_per_wave = (uint32_t)std::max<uint64_t>(1, (total_slices + target - 1) / target);
   return shape;
 }
 
@@ -545,7 +541,7 @@ int resolve_runs(const pbe_arena_view& src, const pbe_arena_view& dst, uint64_t 
 }
 
 int upload_runlist(Resolved& res, int device, bool fp8, bool has_scales, uint64_t page_bytes,
-                   const pbe_kv_shape& kv, pbe_runlist** out) {
+                   const pbe_kv_shape& kv, const pbe::CopyConfig& cfg, pbe_runlist** out) {
   PBE_DEVICE_SCOPE(device);
   pbe_runlist* list = new (std::nothrow) pbe_runlist;
   if (!list) return fail(PBE_ERR_NOMEM, "run list object");
@@ -565,7 +561,7 @@ int upload_runlist(Resolved& res, int device, bool fp8, bool has_scales, uint64_
   list->page_bytes = page_bytes;
   list->info = res.info;
   list->kv = kv;
-  list->shape = launch_shape(res.info.slices, device);
+  list->shape = launch_shape(res.info.slices, device, cfg);
   *out = list;
   return PBE_OK;
 }
@@ -590,10 +586,11 @@ int pbe_runlist_create(const pbe_arena_view* src, const pbe_arena_view* dst, con
       return fail(PBE_ERR_INVALID, "arena view is not device memory of device %d", device);
   }
   Resolved res;
+  const pbe::CopyConfig cfg = copy_config();
   int rc = resolve_runs(*src, *dst, half, half, 2 * shape->layers, runs, n_runs, 0, 0, 0,
-                        pbe::slice_bytes(pbe::KernelKind::kCopy), &res);
+                        pbe::slice_bytes(pbe::KernelKind::kCopy, cfg), &res);
   if (rc != PBE_OK) return rc;
-  return upload_runlist(res, device, false, false, 2ull * shape->layers * half, *shape, out);
+  return upload_runlist(res, device, false, false, 2ull * shape->layers * half, *shape, cfg, out);
 }
 
 int pbe_runlist_create_fp8(const pbe_arena_view* src, const pbe_arena_view* dst, void* dst_scales,
@@ -622,10 +619,10 @@ int pbe_runlist_create_fp8(const pbe_arena_view* src, const pbe_arena_view* dst,
   Resolved res;
   int rc = resolve_runs(*src, *dst, half16, half8, 2 * shape->layers, runs, n_runs,
                         reinterpret_cast<uint64_t>(dst_scales), dst_scales_bytes, scale_page,
-                        pbe::slice_bytes(pbe::KernelKind::kFp8), &res);
+                        pbe::slice_bytes(pbe::KernelKind::kFp8, pbe::CopyConfig{}), &res);
   if (rc != PBE_OK) return rc;
   return upload_runlist(res, device, true, dst_scales != nullptr, 2ull * shape->layers * half16,
-                        *shape, out);
+                        *shape, pbe::CopyConfig{}, out);
 }
 
 int pbe_runlist_get_info(const pbe_runlist* list, pbe_runlist_info* out) {
@@ -754,8 +751,9 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
       return fail(PBE_ERR_INVALID, "arena view is not device memory of device %d", device);
   }
   Resolved res;
+  const pbe::CopyConfig cfg = copy_config();
   rc = resolve_runs(*arena, *arena, half, half, 2 * shape->layers, runs.data(), n_runs, 0, 0, 0,
-                    pbe::slice_bytes(pbe::KernelKind::kCopy), &res);
+                    pbe::slice_bytes(pbe::KernelKind::kCopy, cfg), &res);
   if (rc != PBE_OK) return rc;
   PBE_DEVICE_SCOPE(device);
   Staging& st = staging_for(device);
@@ -766,7 +764,7 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
   if (rc != PBE_OK) return rc;
   PBE_HIP(pbe::launch_copy_runs(static_cast<const pbe::DevRun*>(dev), (uint32_t)n_runs,
                                 (uint32_t)res.info.slices, 2ull * shape->layers * half,
-                                launch_shape(res.info.slices, device), s));
+                                launch_shape(res.info.slices, device, cfg), s));
   rc = stage_done(st, s);
   if (rc != PBE_OK) return rc;
   if (copied) *copied = res.info.src_bytes;

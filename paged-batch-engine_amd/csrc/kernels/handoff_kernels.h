@@ -6,7 +6,7 @@
 namespace pbe {
 
 constexpr int kThreadsPerBlock = 256;
-constexpr int kCopyUnroll = 8;  // 8 KiB per wave slice for the identity copy
+constexpr int kCopyUnroll = 4;  // 4 KiB per wave slice for the identity copy
 constexpr int kFp8Unroll = 8;   // 8 KiB of BF16 source per wave slice
 
 // Device form of one run: resolved addresses in this process's mapping.
@@ -28,11 +28,22 @@ struct DevOp {
 
 enum class KernelKind { kCopy, kFp8 };
 
-struct LaunchShape {
-  uint32_t slices_per_wave = 1;
+// Identity-copy variant: 16-byte vectors per lane per slice (unroll), cache
+// policy of loads/stores (index into the kernel's policy table), workgroup
+// size, and dynamic LDS per workgroup (caps workgroups per CU).
+struct CopyConfig {
+  int unroll = kCopyUnroll;
+  int policy = 0;
+  int block = 256;
+  uint32_t lds_bytes = 0;
 };
 
-uint32_t slice_bytes(KernelKind kind);
+struct LaunchShape {
+  uint32_t slices_per_wave = 1;
+  CopyConfig copy;
+};
+
+uint32_t slice_bytes(KernelKind kind, const CopyConfig& cfg);
 
 hipError_t launch_copy_runs(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
                             uint64_t page_bytes, const LaunchShape& shape, hipStream_t stream);

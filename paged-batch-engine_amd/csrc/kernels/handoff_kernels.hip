@@ -29,6 +29,9 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef PBE_GLOBAL const uint8_t* gsrc_t;
 typedef PBE_GLOBAL uint8_t* gdst_t;
 
+constexpr int kWave = 64;
+constexpr int kWavesPerBlock = kThreadsPerBlock / kWave;
+
 __device__ __forceinline__ u32x4 ld16(gsrc_t p, uint32_t off) {
   return __builtin_nontemporal_load(reinterpret_cast<PBE_GLOBAL const u32x4*>(p + off));
 }
@@ -38,16 +41,12 @@ __device__ __forceinline__ void st16(gdst_t p, uint32_t off, u32x4 v) {
 __device__ __forceinline__ void st8(gdst_t p, uint32_t off, u32x2 v) {
   __builtin_nontemporal_store(v, reinterpret_cast<PBE_GLOBAL u32x2*>(p + off));
 }
-
-constexpr int kWave = 64;
-constexpr int kWavesPerBlock = kThreadsPerBlock / kWave;
-
-// Largest index r in [0, n) with runs[r].slice_begin <= s (runs[0] starts at 0).
-// Each level lets the 64 lanes probe 64 evenly spaced candidates at once, so
-// n runs take ceil(log64(n)) dependent loads instead of log2(n).
-__device__ __forceinline__ uint32_t find_run(const DevRun* __restrict__ runs, uint32_t n,
-                                             uint32_t s, uint32_t lane) {
-  uint32_t lo = 0, count = n;
+// Largest index r in [lo, n) with runs[r].slice_begin <= s, given
+// runs[lo].slice_begin <= s. Each level lets the 64 lanes probe 64 evenly
+// spaced candidates at once, so n runs take ceil(log64(n)) dependent loads.
+__device__ __forceinline__ uint32_t find_run(const DevRun* __restrict__ runs, uint32_t lo,
+                                             uint32_t n, uint32_t s, uint32_t lane) {
+  uint32_t count = n - lo;
   for (;;) {
     const uint32_t stride = (count + kWave - 1) / kWave;
     const uint32_t probe = lane * stride;
@@ -60,46 +59,83 @@ __device__ __forceinline__ uint32_t find_run(const DevRun* __restrict__ runs, ui
   }
 }
 
-template <int kUnroll>
-__device__ __forceinline__ void copy_slice(gsrc_t src, gdst_t dst, uint64_t nbytes,
+// Cache policy of a copy variant. kGlobalNt uses global_load/store with the
+// non-temporal bit; the others use buffer instructions with explicit gfx950
+// cache-policy bits (bit0 sc0, bit1 nt, bit4 sc1) on loads / stores.
+struct PolicyBits {
+  bool buffer;
+  int load_aux;
+  int store_aux;
+};
+constexpr PolicyBits kPolicies[] = {
+    {false, 0, 0},        // 0: global_* nt / nt
+    {true, 0x02, 0x02},   // 1: buffer nt / nt
+    {true, 0x03, 0x03},   // 2: buffer sc0 nt
+    {true, 0x12, 0x12},   // 3: buffer sc1 nt
+    {true, 0x13, 0x13},   // 4: buffer sc0 sc1 nt
+    {true, 0x11, 0x11},   // 5: buffer sc0 sc1
+    {true, 0x02, 0x13},   // 6: load nt, store sc0 sc1 nt
+    {true, 0x13, 0x02},   // 7: load sc0 sc1 nt, store nt
+    {true, 0x00, 0x00},   // 8: buffer default policy
+};
+constexpr int kNumPolicies = sizeof(kPolicies) / sizeof(kPolicies[0]);
+
+template <int kUnroll, int kPolicy>
+__device__ __forceinline__ void copy_slice(uint64_t src, uint64_t dst, uint64_t nbytes,
                                            uint32_t lane) {
   constexpr uint32_t kSlice = kWave * 16u * kUnroll;
-  u32x4 v[kUnroll];
-  if (nbytes >= kSlice) {
+  constexpr PolicyBits pol = kPolicies[kPolicy];
+  if constexpr (!pol.buffer) {
+    gsrc_t s = reinterpret_cast<gsrc_t>(src);
+    gdst_t d = reinterpret_cast<gdst_t>(dst);
+    if (nbytes >= kSlice) {
+      u32x4 v[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) v[u] = ld16(src, (u * kWave + lane) * 16u);
+      for (int u = 0; u < kUnroll; ++u) v[u] = ld16(s, (u * kWave + lane) * 16u);
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) st16(dst, (u * kWave + lane) * 16u, v[u]);
+      for (int u = 0; u < kUnroll; ++u) st16(d, (u * kWave + lane) * 16u, v[u]);
+    } else {
+      // Last, partial slice of a run: rare, so keep it small rather than wide.
+      for (uint32_t off = lane * 16u; off < nbytes; off += kWave * 16u) st16(d, off, ld16(s, off));
+    }
   } else {
-    // Last, partial slice of a run: rare, so keep it small rather than wide.
-    for (uint32_t off = lane * 16u; off < nbytes; off += kWave * 16u) st16(dst, off, ld16(src, off));
+    // Buffer resources clamp to the slice: out-of-range lanes read 0 and
+    // their stores are dropped by the hardware, so no per-lane bound test.
+    const uint32_t n = nbytes >= kSlice ? kSlice : (uint32_t)nbytes;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(src), (short)0, n, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rd =
+        __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(dst), (short)0, n, 0x00020000);
+    u32x4 v[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, (u * kWave + lane) * 16u, 0, pol.load_aux);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      __builtin_amdgcn_raw_buffer_store_b128(v[u], rd, (u * kWave + lane) * 16u, 0, pol.store_aux);
   }
 }
 
 // Identity copy of every run: the device form of the reference's per-run
-// cudaMemcpyAsync loop (split_pd_engine.cpp:96-108).
-template <int kUnroll>
-__global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_kernel(
+// cudaMemcpyAsync loop (split_pd_engine.cpp:96-108). Wave w copies the
+// contiguous slice range [w*k, (w+1)*k) (k = slices_per_wave).
+template <int kUnroll, int kPolicy, int kBlock>
+__global__ __launch_bounds__(kBlock) void copy_runs_kernel(
     const DevRun* __restrict__ runs, uint32_t n_runs, uint32_t total_slices,
     uint32_t slices_per_wave, uint64_t page_bytes) {
   constexpr uint32_t kSlice = kWave * 16u * kUnroll;
   const uint32_t lane = threadIdx.x % kWave;
-  const uint32_t wave = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
-  const uint32_t s_begin = wave * slices_per_wave;
-  if (s_begin >= total_slices) return;
-  const uint32_t s_end = min(s_begin + slices_per_wave, total_slices);
-  uint32_t r = find_run(runs, n_runs, s_begin, lane);
-  uint32_t next = r + 1 < n_runs ? runs[r + 1].slice_begin : 0xffffffffu;
-  for (uint32_t s = s_begin; s < s_end; ++s) {
-    while (s >= next) {
-      ++r;
-      next = r + 1 < n_runs ? runs[r + 1].slice_begin : 0xffffffffu;
-    }
+  const uint32_t wave = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
+  uint32_t s = wave * slices_per_wave;
+  const uint32_t s_end = min(s + slices_per_wave, total_slices);
+  if (s >= s_end) return;
+  uint32_t r = find_run(runs, 0, n_runs, s, lane);
+  for (; s < s_end; ++s) {
+    if (r + 1 < n_runs && runs[r + 1].slice_begin <= s) r = find_run(runs, r + 1, n_runs, s, lane);
     const DevRun& run = runs[r];
     const uint64_t rel = (uint64_t)(s - run.slice_begin) * kSlice;
     const uint64_t run_bytes = (uint64_t)run.pages * page_bytes;
-    copy_slice<kUnroll>(reinterpret_cast<gsrc_t>(run.src + rel),
-                        reinterpret_cast<gdst_t>(run.dst + rel), run_bytes - rel, lane);
+    copy_slice<kUnroll, kPolicy>(run.src + rel, run.dst + rel, run_bytes - rel, lane);
   }
 }
 
@@ -173,13 +209,9 @@ __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_fp8_kernel(
   const uint32_t s_begin = wave * slices_per_wave;
   if (s_begin >= total_slices) return;
   const uint32_t s_end = min(s_begin + slices_per_wave, total_slices);
-  uint32_t r = find_run(runs, n_runs, s_begin, lane);
-  uint32_t next = r + 1 < n_runs ? runs[r + 1].slice_begin : 0xffffffffu;
+  uint32_t r = find_run(runs, 0, n_runs, s_begin, lane);
   for (uint32_t s = s_begin; s < s_end; ++s) {
-    while (s >= next) {
-      ++r;
-      next = r + 1 < n_runs ? runs[r + 1].slice_begin : 0xffffffffu;
-    }
+    if (r + 1 < n_runs && runs[r + 1].slice_begin <= s) r = find_run(runs, r + 1, n_runs, s, lane);
     const DevRun& run = runs[r];
     const uint64_t rel = (uint64_t)(s - run.slice_begin) * kSlice;
     const uint64_t run_bytes = (uint64_t)run.pages * page_bytes;
@@ -242,16 +274,60 @@ __global__ __launch_bounds__(kThreadsPerBlock) void copy_ops_kernel(
 
 }  // namespace
 
-uint32_t slice_bytes(KernelKind kind) {
-  return kind == KernelKind::kCopy ? kWave * 16u * kCopyUnroll : kWave * 16u * kFp8Unroll;
+uint32_t slice_bytes(KernelKind kind, const CopyConfig& cfg) {
+  return kind == KernelKind::kCopy ? kWave * 16u * (uint32_t)cfg.unroll : kWave * 16u * kFp8Unroll;
 }
+
+namespace {
+struct CopyArgs {
+  uint32_t waves;
+  uint32_t lds_bytes;
+  hipStream_t stream;
+  const DevRun* runs;
+  uint32_t n_runs, total_slices, slices_per_wave;
+  uint64_t page_bytes;
+};
+template <int U, int P, int B>
+void launch_variant(const CopyArgs& a) {
+  const uint32_t blocks = (a.waves + B / kWave - 1) / (B / kWave);
+  hipLaunchKernelGGL((copy_runs_kernel<U, P, B>), dim3(blocks), dim3(B), a.lds_bytes, a.stream,
+                     a.runs, a.n_runs, a.total_slices, a.slices_per_wave, a.page_bytes);
+}
+template <int U, int P>
+bool pick_block(const CopyConfig& c, const CopyArgs& a) {
+  switch (c.block) {
+    case 64: launch_variant<U, P, 64>(a); return true;
+    case 256: launch_variant<U, P, 256>(a); return true;
+    case 1024: launch_variant<U, P, 1024>(a); return true;
+    default: return false;
+  }
+}
+template <int U, int P = 0>
+bool pick_policy(const CopyConfig& c, const CopyArgs& a) {
+  if constexpr (P >= kNumPolicies) {
+    return false;
+  } else {
+    if (c.policy == P) return pick_block<U, P>(c, a);
+    return pick_policy<U, P + 1>(c, a);
+  }
+}
+}  // namespace
 
 hipError_t launch_copy_runs(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
                             uint64_t page_bytes, const LaunchShape& shape, hipStream_t stream) {
-  const uint32_t waves = (total_slices + shape.slices_per_wave - 1) / shape.slices_per_wave;
-  const uint32_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
-  hipLaunchKernelGGL(copy_runs_kernel<kCopyUnroll>, dim3(blocks), dim3(kThreadsPerBlock), 0,
-                     stream, runs, n_runs, total_slices, shape.slices_per_wave, page_bytes);
+  const CopyConfig& c = shape.copy;
+  uint32_t waves = (total_slices + shape.slices_per_wave - 1) / shape.slices_per_wave;
+  if (waves == 0) waves = 1;
+  const CopyArgs a{waves, c.lds_bytes, stream, runs, n_runs, total_slices, shape.slices_per_wave,
+                   page_bytes};
+  bool ok = false;
+  switch (c.unroll) {
+    case 2: ok = pick_policy<2>(c, a); break;
+    case 4: ok = pick_policy<4>(c, a); break;
+    case 8: ok = pick_policy<8>(c, a); break;
+    default: break;
+  }
+  if (!ok) return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
