@@ -73,6 +73,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-scrub", action="store_true", help="hot-cache timing (diagnostic)")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also launch a plain contiguous copy of 256 MiB with the same kernel "
+                         "(rocprofv3 --pmc byte-count calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -155,6 +158,26 @@ def main() -> int:
         lat.append(time.perf_counter() - t)
     e2e_us = float(np.median(lat) * 1e6)
 
+    calib = None
+    if args.calibrate:
+        # one 256 MiB run (1024 pages of 256 KiB) from offset 0 to offset 256 MiB
+        ckv = P.shape(1, 1, 4096, 16)
+        cbuf = torch.empty(2 * (256 << 20), dtype=torch.uint8, device=dev)
+        cview = P.view_of(cbuf.data_ptr(), cbuf.numel())
+        crl = P.RunList.bf16(cview, cview, [(0, (256 << 20) // ckv.half_bytes(), 1024)], ckv)
+        ct = []
+        for i in range(args.steps):
+            scrub.fill_(i & 0xff)
+            a_, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a_.record(stream)
+            crl.copy(sp)
+            b_.record(stream)
+            torch.cuda.synchronize()
+            ct.append(a_.elapsed_time(b_))
+        calib = {"bytes": 256 << 20, "grid_threads": int(crl.info().slices) * 64,
+                 "gbps": round(2 * (256 << 20) / (float(np.mean(ct)) * 1e-3) / 1e9, 1)}
+        crl.close()
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(w, host_before, args.cpu_seconds)
@@ -190,7 +213,10 @@ def main() -> int:
         "cpu_baseline": cpu,
         "parity_vs_oracle": parity,
         "wall_ms_per_step_incl_scrub": round(wall / args.steps * 1e3, 4),
+        "grid_threads": int(info.slices) * 64,
     }
+    if calib:
+        line["calibration_copy"] = calib
     print(json.dumps(line))
     rl.close()
     return 0 if parity else 3

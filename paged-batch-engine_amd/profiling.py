@@ -1,0 +1,135 @@
+"""Summaries of rocprofv3 CSV output for the handoff kernels.
+
+    python paged-batch-engine_amd/profiling.py stats <rocprof_dir> --out FILE --command "..."
+    python paged-batch-engine_amd/profiling.py pmc <fetch_dir> <write_dir> --out FILE --command "..."
+
+`stats` reads the kernel trace of a `rocprofv3 --kernel-trace --stats
+--output-format csv` run and writes per-kernel call counts and durations.
+`pmc` reads two counter runs (`--pmc FETCH_SIZE`, then `--pmc WRITE_SIZE`) of
+`bench.py --calibrate`, which launches the config-2 handoff and a plain
+contiguous copy of known size (CALIB_BYTES) with the same kernel; the plain
+copy's counters give the bytes-per-unit factor used to turn the handoff's
+counters into HBM bytes per launch.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import os
+import statistics
+from collections import defaultdict
+
+CALIB_BYTES = 256 << 20     # the --calibrate plain copy reads and writes this much
+COPY_KERNEL = "copy_runs_kernel"
+
+
+def _csv_rows(root: str, suffix: str):
+    files = sorted(glob.glob(os.path.join(root, "**", f"*{suffix}"), recursive=True))
+    if not files:
+        raise FileNotFoundError(f"no *{suffix} under {root}")
+    rows = []
+    for f in files:
+        with open(f, newline="") as fh:
+            rows.extend(csv.DictReader(fh))
+    return rows
+
+
+def _short(name: str) -> str:
+    name = name.replace("(anonymous namespace)::", "").replace("void ", "")
+    return name.split("(")[0]
+
+
+def kernel_durations(root: str):
+    """{(short kernel name, grid size): [durations ns]} from the kernel trace."""
+    out = defaultdict(list)
+    for r in _csv_rows(root, "kernel_trace.csv"):
+        grid = int(r.get("Grid_Size_X", r.get("Grid_Size", 0)) or 0)
+        dur = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+        out[(_short(r["Kernel_Name"]), grid)].append(dur)
+    return out
+
+
+def stats(root: str, out: str, command: str) -> None:
+    d = kernel_durations(root)
+    lines = [f"# rocprofv3 kernel trace summary", f"command: {command}", "",
+             f"{'kernel':<60} {'grid':>9} {'calls':>6} {'avg_us':>9} {'p50_us':>9} {'min_us':>9}"]
+    for (name, grid), v in sorted(d.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"{name[:60]:<60} {grid:>9} {len(v):>6} {statistics.mean(v) / 1e3:>9.2f} "
+                     f"{statistics.median(v) / 1e3:>9.2f} {min(v) / 1e3:>9.2f}")
+    text = "\n".join(lines) + "\n"
+    with open(out, "w") as fh:
+        fh.write(text)
+    print(text)
+
+
+def _counter_per_dispatch(root: str, counter: str):
+    """{grid size: [counter value per dispatch]} for the copy kernel."""
+    per = defaultdict(lambda: defaultdict(float))
+    grids = {}
+    for r in _csv_rows(root, "counter_collection.csv"):
+        if COPY_KERNEL not in r["Kernel_Name"] or r["Counter_Name"] != counter:
+            continue
+        did = r["Dispatch_Id"]
+        per[did][counter] += float(r["Counter_Value"])
+        grids[did] = int(r.get("Grid_Size", 0) or 0)
+    out = defaultdict(list)
+    for did, v in per.items():
+        out[grids[did]].append(v[counter])
+    return out
+
+
+def pmc(fetch_root: str, write_root: str, out: str, command: str, alg_bytes: int,
+        handoff_grid: int, calib_grid: int) -> None:
+    f = _counter_per_dispatch(fetch_root, "FETCH_SIZE")
+    w = _counter_per_dispatch(write_root, "WRITE_SIZE")
+    f_h, f_c = statistics.median(f[handoff_grid]), statistics.median(f[calib_grid])
+    w_h, w_c = statistics.median(w[handoff_grid]), statistics.median(w[calib_grid])
+    f_scale = CALIB_BYTES / f_c  # bytes per counter unit (KiB nominal)
+    w_scale = CALIB_BYTES / w_c
+    traffic = f_h * f_scale + w_h * w_scale
+    lines = [
+        "# rocprofv3 --pmc summary: HBM traffic of the config-2 handoff copy",
+        f"command: {command}",
+        f"kernel: {COPY_KERNEL} (handoff grid {handoff_grid}, calibration grid {calib_grid})",
+        f"FETCH_SIZE per dispatch: handoff {f_h:.1f}, plain copy of {CALIB_BYTES} B {f_c:.1f}"
+        f" -> {f_scale:.2f} bytes per unit",
+        f"WRITE_SIZE per dispatch: handoff {w_h:.1f}, plain copy of {CALIB_BYTES} B {w_c:.1f}"
+        f" -> {w_scale:.2f} bytes per unit",
+        f"algorithmic_bytes_per_launch: {alg_bytes}",
+        f"fetch_bytes_per_launch: {f_h * f_scale:.0f}",
+        f"write_bytes_per_launch: {w_h * w_scale:.0f}",
+        f"traffic_bytes_per_launch: {traffic:.0f}",
+        f"traffic_over_algorithmic: {traffic / alg_bytes:.4f}",
+    ]
+    text = "\n".join(lines) + "\n"
+    with open(out, "w") as fh:
+        fh.write(text)
+    print(text)
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    s = sub.add_parser("stats")
+    s.add_argument("root")
+    s.add_argument("--out", required=True)
+    s.add_argument("--command", required=True)
+    p = sub.add_parser("pmc")
+    p.add_argument("fetch_root")
+    p.add_argument("write_root")
+    p.add_argument("--out", required=True)
+    p.add_argument("--command", required=True)
+    p.add_argument("--alg-bytes", type=int, required=True)
+    p.add_argument("--handoff-grid", type=int, required=True)
+    p.add_argument("--calib-grid", type=int, required=True)
+    a = ap.parse_args()
+    if a.cmd == "stats":
+        stats(a.root, a.out, a.command)
+    else:
+        pmc(a.fetch_root, a.write_root, a.out, a.command, a.alg_bytes, a.handoff_grid,
+            a.calib_grid)
+
+
+if __name__ == "__main__":
+    main()
