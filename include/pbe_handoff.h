@@ -187,8 +187,11 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids,
 /* ---- generic component-list copy ---------------------------------------
  * Executes an arbitrary list of (src, dst, bytes) device copies in one launch:
  * the device form of ExecuteCpuTransfer (transfer_plan.cpp:392-403) used by
- * the HIP TransferBackend. Ops must have 16-byte aligned addresses and sizes;
- * the list is copied to device memory owned by the call. */
+ * the HIP TransferBackend. Every endpoint must be device memory of `device` or
+ * pinned host memory (checked on the host); ops whose addresses and size are
+ * 16-byte multiples move as 16-byte vectors, others byte by byte. No two ops
+ * may write the same byte or write another op's source. The list is staged
+ * into device memory owned by the library. */
 typedef struct pbe_copy_op {
   uint64_t src;
   uint64_t dst;
@@ -198,6 +201,21 @@ int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream
 
 /* GPU UUID of `device` (16 bytes), as compared across processes. */
 int pbe_device_uuid(int device, uint8_t out[16]);
+
+/* ---- streams and pointer queries for C++ host code ---------------------
+ * Backends above this ABI (the HIP TransferBackend, the shared-arena
+ * connector) own their streams through these calls instead of calling HIP. */
+int pbe_stream_create(int device, void** out);              /* non-blocking, default priority */
+int pbe_stream_destroy(int device, void* stream);
+int pbe_stream_synchronize(int device, void* stream);       /* PBE_OK or PBE_ERR_UNKNOWN */
+/* Makes `stream` wait for a caller-owned hipEvent_t (borrowed, not retained). */
+int pbe_stream_wait_raw_event(int device, void* stream, void* hip_event);
+
+#define PBE_PTR_UNKNOWN 0   /* pageable host or not an allocation: kernels must not touch it */
+#define PBE_PTR_DEVICE 1    /* device memory; *device_out holds its GPU */
+#define PBE_PTR_PINNED_HOST 2
+/* Classifies [ptr, ptr+bytes): the whole span must lie in one allocation. */
+int pbe_pointer_kind(const void* ptr, uint64_t bytes, int* kind, int* device_out);
 
 #ifdef __cplusplus
 }

@@ -17,6 +17,7 @@ enum : int64_t {
   kIdentityMismatch = 11,
   kInvalidArgument = 12,
   kRuntimeError = 13,
+  kNothingLive = 20,
 };
 
 int64_t classify_invalid(const std::invalid_argument& e) {
@@ -36,8 +37,9 @@ extern "C" {
 // op kind 2: release a copy of live[op_index] with field op_align mutated
 //            (0 epoch,1 generation,2 offset,3 bytes,4 model,5 layout,6 id)
 // op kind 3: release(live[op_index]) without dropping it (duplicate release)
-// Then leased_bytes(model m) for every model is appended (n_models int64).
-// Returns 0, or -1 if the scenario itself is malformed.
+// A release op with no live lease is recorded as code 20 and skipped.
+// leased_bytes(model m) of every model is written to model_bytes_out.
+// Returns 0, or -1 if the allocator could not be constructed.
 int ref_alloc_run(uint64_t arena_bytes, uint64_t epoch, int32_t n_models, const uint64_t* limits,
                   int32_t n_ops, const int32_t* op_kind, const int32_t* op_model,
                   const int32_t* op_layout, const uint64_t* op_bytes, const uint64_t* op_align,
@@ -57,8 +59,9 @@ int ref_alloc_run(uint64_t arena_bytes, uint64_t epoch, int32_t n_models, const 
           o[1] = (int64_t)lease.offset;
           o[2] = (int64_t)lease.generation;
           live.push_back(lease);
+        } else if (live.empty()) {
+          o[0] = kNothingLive;
         } else {
-          if (live.empty()) return -1;
           const size_t idx = (size_t)op_index[i] % live.size();
           base::ChunkLease lease = live[idx];
           if (op_kind[i] == 2) {
@@ -94,3 +97,121 @@ int ref_alloc_run(uint64_t arena_bytes, uint64_t epoch, int32_t n_models, const 
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// TransferPlan scenario: builds a source and a destination schema (optionally
+// head-sharded), packs each into a layout whose component order is a seeded
+// permutation, compiles a plan, binds it over two byte buffers and executes it
+// on the CPU. Writes a text log of every plan operation and bound copy
+// (offsets relative to the buffers) followed by an FNV-1a hash of the
+// destination buffer, so two builds can be compared byte for byte.
+//   spec = [version, layers, page, heads, head_size, fp8, placement,
+//           n_src_ranges, (begin, count)..., n_dst_ranges, (begin, count)...,
+//           src_order_seed, dst_order_seed]
+#include <cstdio>
+#include <cstring>
+#include <numeric>
+
+#include "cache/layout_codec.h"
+#include "cache/page_schema.h"
+#include "cache/transfer_plan.h"
+
+namespace {
+std::vector<size_t> seeded_order(size_t n, uint32_t seed) {
+  std::vector<size_t> o(n);
+  std::iota(o.begin(), o.end(), 0);
+  if (!seed) return o;
+  uint32_t x = seed;
+  for (size_t i = n; i > 1; --i) {
+    x = x * 1664525u + 1013904223u;
+    std::swap(o[i - 1], o[x % i]);
+  }
+  return o;
+}
+
+cache::PageSchema sharded(cache::PageSchema s, const std::vector<std::pair<int32_t, int32_t>>& r) {
+  if (r.empty()) return s;
+  std::vector<cache::ComponentDescriptor> parts;
+  for (const auto& c : s.components)
+    for (const auto& p : r) {
+      auto d = c;
+      d.head_begin = p.first;
+      d.head_count = p.second;
+      parts.push_back(d);
+    }
+  s.components = parts;
+  return s;
+}
+
+void emit(std::string* log, const std::string& line) { *log += line + "\n"; }
+}  // namespace
+
+extern "C" int ref_plan_run(const int32_t* spec, int32_t n_spec, char* out, uint64_t cap) {
+  std::string log;
+  try {
+    int32_t i = 0;
+    auto next = [&]() { return i < n_spec ? spec[i++] : 0; };
+    const int32_t version = next(), layers = next(), page = next(), heads = next(), hs = next();
+    const bool fp8 = next() != 0;
+    const auto placement = static_cast<cache::TransferPlacement>(next());
+    std::vector<std::pair<int32_t, int32_t>> sr, dr;
+    for (int32_t k = next(); k > 0; --k) { int32_t b = next(); sr.emplace_back(b, next()); }
+    for (int32_t k = next(); k > 0; --k) { int32_t b = next(); dr.emplace_back(b, next()); }
+    const uint32_t so = (uint32_t)next(), dso = (uint32_t)next();
+    const auto storage = base::MakeKVCacheStorageSpec(
+        base::DataType::kDataTypeBf16,
+        fp8 ? base::BlockStorageMode::kFp8E4M3PerTokenHead : base::BlockStorageMode::kPlain);
+    cache::PageSchema base_schema;
+    auto st = cache::MakeKVPageSchema((uint32_t)version, layers, page, heads, hs, storage, &base_schema);
+    if (!st) { emit(&log, "schema_error"); goto done; }
+    {
+      const auto src = sharded(base_schema, sr), dst = sharded(base_schema, dr);
+      emit(&log, std::string("src_valid ") + (src.validate() ? "1" : "0"));
+      emit(&log, std::string("dst_valid ") + (dst.validate() ? "1" : "0"));
+      emit(&log, "src_fp " + src.fingerprint());
+      cache::TransferPlanner planner;
+      std::shared_ptr<const cache::TransferPlan> plan;
+      st = planner.compile(src, dst, placement, &plan);
+      if (!st) { emit(&log, "compile_error"); goto done; }
+      for (const auto& op : plan->operations)
+        emit(&log, "op " + op.component.semantic_key() + " <- " + op.source_component.semantic_key() +
+                       " -> " + op.destination_component.semantic_key());
+      cache::LayoutDescriptor sl, dl;
+      if (!cache::MakePackedLayout(src, "src", 5, seeded_order(src.components.size(), so), {}, &sl) ||
+          !cache::MakePackedLayout(dst, "dst", 6, seeded_order(dst.components.size(), dso), {}, &dl)) {
+        emit(&log, "layout_error");
+        goto done;
+      }
+      std::vector<uint8_t> sb(sl.total_bytes), db(dl.total_bytes, 0xa5);
+      for (size_t k = 0; k < sb.size(); ++k) sb[k] = (uint8_t)(k * 131u + 7u);
+      cache::BoundTransfer bound;
+      st = cache::BoundTransfer::Bind(*plan, src, dst, {sb.data(), sb.size(), &sl},
+                                      {db.data(), db.size(), &dl}, &bound);
+      if (!st) { emit(&log, "bind_error"); goto done; }
+      for (const auto& op : bound.operations()) {
+        char line[256];
+        std::snprintf(line, sizeof(line), "copy %s src+%zu dst+%zu bytes=%zu vid=%lld/%lld",
+                      op.component.semantic_key().c_str(), (size_t)(op.source - sb.data()),
+                      (size_t)(op.destination - db.data()), op.bytes,
+                      (long long)op.source_virtual_block_id, (long long)op.destination_virtual_block_id);
+        emit(&log, line);
+      }
+      emit(&log, "staging " + std::to_string(bound.staging_bytes()));
+      if (placement == cache::TransferPlacement::kExactDirect) st = cache::ExecuteCpuTransfer(bound);
+      else {
+        std::vector<uint8_t> staging(bound.staging_bytes());
+        st = cache::ExecuteCpuTransferStaged(bound, staging.data(), staging.size());
+      }
+      if (!st) { emit(&log, "execute_error"); goto done; }
+      uint64_t h = 1469598103934665603ull;
+      for (uint8_t b : db) { h ^= b; h *= 1099511628211ull; }
+      emit(&log, "dst_hash " + std::to_string(h));
+    }
+  } catch (const std::exception& e) {
+    emit(&log, std::string("exception ") + e.what());
+  }
+done:
+  if (log.size() + 1 > cap) return -1;
+  std::memcpy(out, log.c_str(), log.size() + 1);
+  return (int)log.size();
+}

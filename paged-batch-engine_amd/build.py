@@ -36,13 +36,27 @@ INCLUDES = [f"-I{ROOT / 'include'}", f"-I{PKG / 'include'}", f"-I{PKG / 'csrc'}"
 
 # Host-only C++ of the drop-in API (no HIP headers): also built with g++ into
 # the CPU unit-test binary.
-HOST_SOURCES: list[str] = []
+HOST_SOURCES = [
+    "csrc/base/base.cpp",
+    "csrc/base/global_chunk_allocator.cpp",
+    "csrc/cache/page_schema.cpp",
+    "csrc/cache/layout_codec.cpp",
+    "csrc/cache/transfer_plan.cpp",
+    "csrc/cache/page_migration.cpp",
+    "csrc/serving/pd_handoff_common.cpp",
+]
+# Host C++ that reaches the GPU only through the C ABI (in the library, not in
+# the CPU-only unit-test binary).
+ABI_HOST_SOURCES = [
+    "csrc/cache/hip_transfer_backend.cpp",
+    "csrc/serving/shared_kv_handoff.cpp",
+]
 # Sources that call HIP (compiled by hipcc).
 HIP_SOURCES = [
     "csrc/kernels/handoff_kernels.hip",
     "csrc/capi/pbe_capi.hip",
 ]
-CPU_TESTS: list[str] = []
+CPU_TESTS = ["tests/cpp/test_drop_in_api.cpp"]
 GPU_TESTS: list[str] = []
 
 
@@ -67,16 +81,18 @@ def build(jobs: int = 8) -> Path:
     steps = []
     for src in HIP_SOURCES:
         steps.append([HIPCC, *HIP_FLAGS, *INCLUDES, "-c", str(PKG / src), "-o", str(_obj(src, "hip"))])
-    for src in HOST_SOURCES:
+    for src in HOST_SOURCES + ABI_HOST_SOURCES:
         steps.append([HIPCC, "-x", "c++", *CXX_FLAGS, *INCLUDES, "-c", str(PKG / src),
                       "-o", str(_obj(src, "host"))])
+    for src in HOST_SOURCES:
         steps.append(["g++", *CXX_FLAGS, *INCLUDES, "-c", str(PKG / src), "-o", str(_obj(src, "gcc"))])
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
         for fut in [pool.submit(_run, s) for s in steps]:
             fut.result()
     so = LIB / "libpbe_handoff.so"
     tmp = LIB / "libpbe_handoff.so.tmp"
-    objs = [str(_obj(s, "hip")) for s in HIP_SOURCES] + [str(_obj(s, "host")) for s in HOST_SOURCES]
+    objs = [str(_obj(s, "hip")) for s in HIP_SOURCES] + \
+        [str(_obj(s, "host")) for s in HOST_SOURCES + ABI_HOST_SOURCES]
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs])
     os.replace(tmp, so)
     # C++ tests: the CPU suite links the g++ objects only (no HIP runtime).
@@ -84,6 +100,10 @@ def build(jobs: int = 8) -> Path:
     for t in CPU_TESTS if cpu_objs else []:
         _run(["g++", *CXX_FLAGS, *INCLUDES, f"-I{ROOT / 'tests' / 'cpp'}", str(ROOT / t), *cpu_objs,
               "-o", str(LIB / "pbe_cpp_tests")])
+    # The scenario driver of oracle/ref_driver.cpp built against this API, so
+    # tests can replay identical scenarios on it and on the reference build.
+    _run(["g++", *CXX_FLAGS, "-shared", *INCLUDES, str(ROOT / "oracle" / "ref_driver.cpp"), *cpu_objs,
+          "-o", str(LIB / "libpbe_api_driver.so")])
     for t in GPU_TESTS:
         _run([HIPCC, *HIP_FLAGS, *INCLUDES, f"-I{ROOT / 'tests' / 'cpp'}", str(ROOT / t),
               f"-L{LIB}", "-lpbe_handoff", "-Wl,-rpath,$ORIGIN",

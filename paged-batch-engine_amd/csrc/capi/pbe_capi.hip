@@ -804,4 +804,63 @@ int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream
   return stage_done(st, s);
 }
 
+// ---------------------------------------------------------------- streams
+int pbe_stream_create(int device, void** out) {
+  if (!out) return fail(PBE_ERR_INVALID, "null output");
+  *out = nullptr;
+  PBE_DEVICE_SCOPE(device);
+  hipStream_t s = nullptr;
+  PBE_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *out = s;
+  return PBE_OK;
+}
+
+int pbe_stream_destroy(int device, void* stream) {
+  if (!stream) return PBE_OK;
+  PBE_DEVICE_SCOPE(device);
+  PBE_HIP(hipStreamDestroy(static_cast<hipStream_t>(stream)));
+  return PBE_OK;
+}
+
+int pbe_stream_synchronize(int device, void* stream) {
+  PBE_DEVICE_SCOPE(device);
+  const hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(PBE_ERR_UNKNOWN, "hipStreamSynchronize: %s", hipGetErrorString(e));
+  return PBE_OK;
+}
+
+int pbe_stream_wait_raw_event(int device, void* stream, void* hip_event) {
+  if (!hip_event) return fail(PBE_ERR_INVALID, "null event");
+  PBE_DEVICE_SCOPE(device);
+  PBE_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(stream), static_cast<hipEvent_t>(hip_event), 0));
+  return PBE_OK;
+}
+
+int pbe_pointer_kind(const void* ptr, uint64_t bytes, int* kind, int* device_out) {
+  if (!kind) return fail(PBE_ERR_INVALID, "null output");
+  *kind = PBE_PTR_UNKNOWN;
+  if (device_out) *device_out = -1;
+  if (!ptr) return PBE_OK;
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  if (hipMemGetAddressRange(&base, &size, const_cast<void*>(ptr)) != hipSuccess || !base) {
+    (void)hipGetLastError();
+    return PBE_OK;
+  }
+  const uint64_t p = reinterpret_cast<uint64_t>(ptr), b = reinterpret_cast<uint64_t>(base);
+  if (bytes > ~0ull - p || p + bytes > b + size) return PBE_OK;
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, ptr) != hipSuccess) {
+    (void)hipGetLastError();
+    return PBE_OK;
+  }
+  if (attr.type == hipMemoryTypeDevice) {
+    *kind = PBE_PTR_DEVICE;
+    if (device_out) *device_out = attr.device;
+  } else if (attr.type == hipMemoryTypeHost) {
+    *kind = PBE_PTR_PINNED_HOST;
+  }
+  return PBE_OK;
+}
+
 }  // extern "C"

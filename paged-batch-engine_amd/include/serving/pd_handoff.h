@@ -1,0 +1,149 @@
+// Prefill->decode handoff descriptors and the connector interface
+// (infMain/include/serving/pd_handoff.h:18-93), plus the MI355X shared-arena
+// connector: the data path of copy_shared_kv (split_pd_engine.cpp:49-115)
+// as one gfx950 run-list kernel per handoff.
+#ifndef PBE_INCLUDE_SERVING_PD_HANDOFF_H_
+#define PBE_INCLUDE_SERVING_PD_HANDOFF_H_
+
+#include <cstdint>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "base/base.h"
+#include "base/kv_cache_format.h"
+#include "pbe_handoff.h"
+
+namespace serving {
+
+struct GlobalRequestId {
+  std::string value;
+  bool empty() const { return value.empty(); }
+};
+
+struct HandoffId {
+  uint64_t value = 0;
+  bool valid() const { return value != 0; }
+};
+
+struct KVPoolDescriptor {
+  int32_t device_id = 0;
+  int32_t layer_num = 0;
+  int32_t block_size = 0;
+  int32_t kv_head_num = 0;
+  int32_t head_size = 0;
+  base::DataType dtype = base::DataType::kDataTypeUnknown;
+  base::BlockStorageMode storage_mode = base::BlockStorageMode::kPlain;
+
+  // K + V payload (+ scales) of one block of one layer; 0 on bad dims.
+  int64_t bytes_per_block_per_layer() const;
+  bool compatible_with(const KVPoolDescriptor& other) const;
+};
+
+struct KVBlockMapping {
+  int32_t layer_idx = 0;
+  std::vector<int32_t> src_block_ids;
+  std::vector<int32_t> dst_block_ids;
+};
+
+struct KVBlockManifest {
+  GlobalRequestId client_request_id;
+  HandoffId handoff_id;
+  int32_t prompt_tokens = 0;
+  int32_t computed_tokens = 0;
+  int32_t first_token = -1;
+  KVPoolDescriptor src_pool;
+  KVPoolDescriptor dst_pool;
+  std::vector<KVBlockMapping> layer_mappings;
+
+  base::Status validate() const;
+};
+
+enum class KVTransferState { kPending, kCompleted, kFailed, kCancelled };
+
+struct KVTransferStatus {
+  KVTransferState state = KVTransferState::kPending;
+  std::string error;
+
+  static KVTransferStatus Pending();
+  static KVTransferStatus Completed();
+  static KVTransferStatus Failed(std::string message);
+  static KVTransferStatus Cancelled(std::string message);
+  bool done() const;
+  bool ok() const;
+};
+
+class KVTransferConnector {
+ public:
+  virtual ~KVTransferConnector() = default;
+  virtual base::Status submit(const KVBlockManifest& manifest, HandoffId* handle) = 0;
+  virtual KVTransferStatus poll(HandoffId handle) = 0;
+  virtual void cancel(HandoffId handle, const std::string& reason) = 0;
+  virtual KVTransferStatus drain(HandoffId handle) { return poll(handle); }
+  virtual void release(HandoffId /*handle*/) {}
+};
+
+// This process's mapping of the shared KV arena and the owner epoch it
+// belongs to (block id = byte offset / half, page-major layout).
+struct SharedArenaBinding {
+  pbe_arena_view view{};
+  uint64_t epoch = 0;
+  int device = 0;
+};
+
+// The data path of copy_shared_kv: checks the source epoch against the
+// binding (split_pd_engine.cpp:54-55), the layer count, that every id is a
+// page id inside the arena (:70-77) and that all layers carry identical
+// page-major id lists (:78-79, :91-93), then coalesces runs and launches one
+// gfx950 copy on `stream` (asynchronous). *copied = bytes copied. Every check
+// happens before any device work, so an error leaves the arena untouched.
+base::Status CopySharedKV(const SharedArenaBinding& arena, uint64_t source_epoch,
+                          const KVBlockManifest& manifest, void* stream, uint64_t* copied);
+
+// KVTransferConnector over CopySharedKV: submit() queues the copy on the
+// connector's stream and records a completion event; poll() queries it,
+// drain() waits, release() forgets finished handoffs. Handoffs that fail
+// validation are recorded as Failed and return the error.
+class SharedArenaKVTransferConnector final : public KVTransferConnector {
+ public:
+  // stream == nullptr: the connector creates (and owns) a non-blocking stream.
+  explicit SharedArenaKVTransferConnector(SharedArenaBinding arena, void* stream = nullptr);
+  ~SharedArenaKVTransferConnector() override;
+  SharedArenaKVTransferConnector(const SharedArenaKVTransferConnector&) = delete;
+  SharedArenaKVTransferConnector& operator=(const SharedArenaKVTransferConnector&) = delete;
+
+  // Source epoch = the binding's epoch (both sides map the same arena).
+  base::Status submit(const KVBlockManifest& manifest, HandoffId* handle) override;
+  // Source epoch as reported by the prefill side.
+  base::Status submit_from(uint64_t source_epoch, const KVBlockManifest& manifest,
+                           HandoffId* handle);
+  KVTransferStatus poll(HandoffId handle) override;
+  void cancel(HandoffId handle, const std::string& reason) override;
+  KVTransferStatus drain(HandoffId handle) override;
+  void release(HandoffId handle) override;
+
+  uint64_t copied_bytes() const { return copied_bytes_; }
+  void* stream() const { return stream_; }
+
+ private:
+  struct Record {
+    HandoffId handle;
+    KVTransferStatus status;
+    pbe_event* done = nullptr;
+    bool cancel_requested = false;
+    std::string cancel_reason;
+  };
+  Record* find(HandoffId handle);
+  KVTransferStatus settle(Record& record, bool wait);
+
+  SharedArenaBinding arena_;
+  void* stream_ = nullptr;
+  bool owns_stream_ = false;
+  uint64_t next_handoff_id_ = 1;
+  uint64_t copied_bytes_ = 0;
+  std::vector<Record> records_;
+};
+
+}  // namespace serving
+
+#endif  // PBE_INCLUDE_SERVING_PD_HANDOFF_H_

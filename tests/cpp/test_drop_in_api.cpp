@@ -1,0 +1,680 @@
+// CPU tests of the C++ drop-in API. The scenarios restate the reference's own
+// tests as behaviour: test/test_global_chunk_allocator.cpp:8-97,
+// test/test_cache_transfer_plan.cpp:130-467, test/test_page_migration.cpp:5-25,
+// test/test_serving/test_pd_handoff.cpp:284-296.
+#include <algorithm>
+#include <cstring>
+#include <memory>
+#include <numeric>
+#include <random>
+#include <stdexcept>
+#include <vector>
+
+#include "base/global_chunk_allocator.h"
+#include "base/kv_cache_format.h"
+#include "cache/layout_codec.h"
+#include "cache/page_migration.h"
+#include "cache/page_schema.h"
+#include "cache/transfer_plan.h"
+#include "minitest.h"
+#include "serving/pd_handoff.h"
+
+using namespace cache;
+
+// ------------------------------------------------------------ chunk allocator
+
+TEST_CASE("chunk allocator: freed bytes are reused across layouts") {
+  base::GlobalChunkAllocator pool(12 << 10, 7);
+  pool.register_model("A", 8 << 10);
+  pool.register_model("B", 8 << 10);
+  const auto a = pool.acquire("A", "24x64", 6 << 10, 512);
+  const auto b = pool.acquire("B", "28x128", 4 << 10, 1024);
+  CHECK_EQ(pool.free_bytes(), 2u << 10);
+  CHECK_THROWS_AS(pool.acquire("B", "28x128", 4 << 10, 1024), std::runtime_error);
+  pool.release(a);
+  const auto again = pool.acquire("B", "28x128", 4 << 10, 1024);
+  CHECK_EQ(again.offset, a.offset);           // best fit reuses the released range
+  CHECK(again.generation != a.generation);
+  CHECK_EQ(pool.leased_bytes("A"), 0u);
+  CHECK_EQ(pool.leased_bytes("B"), 8u << 10);
+  CHECK_THROWS_AS(pool.release(a), std::invalid_argument);
+  pool.release(b);
+  pool.release(again);
+  CHECK_EQ(pool.free_bytes(), pool.bytes());
+  CHECK_EQ(pool.lease_count(), 0u);
+}
+
+TEST_CASE("chunk allocator: every lease field is part of its identity") {
+  base::GlobalChunkAllocator pool(16384, 42);
+  pool.register_model("A", 8192);
+  const auto live = pool.acquire("A", "layout", 4096, 256);
+  for (int field = 0; field < 7; ++field) {
+    auto forged = live;
+    switch (field) {
+      case 0: ++forged.epoch; break;
+      case 1: ++forged.generation; break;
+      case 2: ++forged.offset; break;
+      case 3: ++forged.bytes; break;
+      case 4: forged.model = "B"; break;
+      case 5: forged.layout = "wrong"; break;
+      default: ++forged.id; break;
+    }
+    CHECK_THROWS_AS(pool.release(forged), std::invalid_argument);
+    CHECK_EQ(pool.leased_bytes("A"), 4096u);
+  }
+  pool.release(live);
+  CHECK_THROWS_AS(pool.release(live), std::invalid_argument);
+  CHECK_EQ(pool.free_bytes(), 16384u);
+}
+
+TEST_CASE("chunk allocator: alignment, fragmentation and quota fail atomically") {
+  base::GlobalChunkAllocator pool(8192, 1);
+  pool.register_model("A", 8192);
+  pool.register_model("B", 2048);
+  auto a = pool.acquire("A", "page3", 3072, 1536);
+  auto b = pool.acquire("B", "page2", 2048, 2048);
+  CHECK_EQ(a.offset % 1536, 0u);
+  CHECK_EQ(b.offset % 2048, 0u);
+  const auto free_before = pool.free_bytes();
+  try {
+    pool.acquire("B", "page2", 2048, 2048);
+    CHECK(false);
+  } catch (const base::ChunkAllocationError& e) {
+    CHECK(e.code() == base::ChunkAllocationFailure::kQuota);
+  }
+  CHECK_EQ(pool.free_bytes(), free_before);
+  try {
+    pool.acquire("A", "page4", 4096, 4096);
+    CHECK(false);
+  } catch (const base::ChunkAllocationError& e) {
+    // a at [0, 3072), b at [4096, 6144): only 3072 bytes are free.
+    CHECK(e.code() == base::ChunkAllocationFailure::kExhausted);
+  }
+  CHECK_EQ(pool.free_bytes(), free_before);
+  try {
+    pool.acquire("A", "page2", 2048, 2048);  // 2048 free at 6144: fits
+  } catch (...) {
+    CHECK(false);
+  }
+  try {
+    pool.acquire("A", "page1k", 1024, 1024);  // 1024 free at 3072: fits
+  } catch (...) {
+    CHECK(false);
+  }
+  CHECK_EQ(pool.free_bytes(), 0u);
+  CHECK_THROWS_AS(pool.acquire("A", "bad", 100, 256), std::invalid_argument);
+}
+
+TEST_CASE("chunk allocator: fragmented when enough bytes are free but split") {
+  base::GlobalChunkAllocator pool(8192, 1);
+  pool.register_model("A", 8192);
+  auto a = pool.acquire("A", "p", 2048, 2048);
+  auto b = pool.acquire("A", "p", 2048, 2048);
+  auto c = pool.acquire("A", "p", 2048, 2048);
+  auto d = pool.acquire("A", "p", 2048, 2048);
+  pool.release(a);
+  pool.release(c);
+  try {
+    pool.acquire("A", "p", 4096, 2048);
+    CHECK(false);
+  } catch (const base::ChunkAllocationError& e) {
+    CHECK(e.code() == base::ChunkAllocationFailure::kFragmented);
+  }
+  pool.release(b);  // coalesces [0, 6144)
+  const auto big = pool.acquire("A", "p", 6144, 2048);
+  CHECK_EQ(big.offset, 0u);
+  pool.release(big);
+  pool.release(d);
+  const auto whole = pool.acquire("A", "whole", 8192, 256);
+  CHECK_EQ(whole.offset, 0u);
+}
+
+TEST_CASE("chunk allocator: exhausted vs fragmented and invalid registration") {
+  base::GlobalChunkAllocator pool(4096, 3);
+  CHECK_THROWS_AS(base::GlobalChunkAllocator(0, 1), std::invalid_argument);
+  CHECK_THROWS_AS(base::GlobalChunkAllocator(10, 0), std::invalid_argument);
+  CHECK_THROWS_AS(pool.register_model("", 10), std::invalid_argument);
+  CHECK_THROWS_AS(pool.register_model("A", 0), std::invalid_argument);
+  CHECK_THROWS_AS(pool.register_model("A", 8192), std::invalid_argument);
+  pool.register_model("A", 4096);
+  CHECK_THROWS_AS(pool.register_model("A", 4096), std::invalid_argument);
+  CHECK_THROWS_AS(pool.acquire("nobody", "x", 256, 256), std::invalid_argument);
+  CHECK_THROWS_AS(pool.acquire("A", "", 256, 256), std::invalid_argument);
+  CHECK_THROWS_AS(pool.acquire("A", "x", 0, 256), std::invalid_argument);
+  CHECK_THROWS_AS(pool.acquire("A", "x", 256, 0), std::invalid_argument);
+  auto a = pool.acquire("A", "x", 3072, 1024);
+  try {
+    pool.acquire("A", "x", 2048, 1024);
+    CHECK(false);
+  } catch (const base::ChunkAllocationError& e) {
+    CHECK(e.code() == base::ChunkAllocationFailure::kQuota);
+  }
+  pool.release(a);
+}
+
+TEST_CASE("chunk allocator: randomized leases stay disjoint and accounted") {
+  base::GlobalChunkAllocator pool(12u << 20, 77);
+  pool.register_model("A", pool.bytes());
+  pool.register_model("B", pool.bytes());
+  std::mt19937 rng(42);
+  std::vector<base::ChunkLease> leases;
+  for (int step = 0; step < 4000; ++step) {
+    if (!leases.empty() && rng() % 3 == 0) {
+      const size_t idx = rng() % leases.size();
+      pool.release(leases[idx]);
+      leases.erase(leases.begin() + static_cast<long>(idx));
+    } else {
+      const uint64_t page = (rng() % 2 ? 24 : 28) * 8192ull;
+      const bool model_a = rng() % 2;
+      const uint64_t bytes = page * (1 + rng() % 4);
+      try {
+        leases.push_back(pool.acquire(model_a ? "A" : "B", "gqa", bytes, page));
+      } catch (const std::runtime_error&) {
+      }
+    }
+    std::sort(leases.begin(), leases.end(),
+              [](const base::ChunkLease& x, const base::ChunkLease& y) { return x.offset < y.offset; });
+    uint64_t total = 0, a_bytes = 0, b_bytes = 0;
+    for (size_t i = 0; i < leases.size(); ++i) {
+      CHECK(leases[i].offset + leases[i].bytes <= pool.bytes());
+      if (i) CHECK(leases[i - 1].offset + leases[i - 1].bytes <= leases[i].offset);
+      total += leases[i].bytes;
+      (leases[i].model == "A" ? a_bytes : b_bytes) += leases[i].bytes;
+    }
+    CHECK_EQ(total + pool.free_bytes(), pool.bytes());
+    CHECK_EQ(a_bytes, pool.leased_bytes("A"));
+    CHECK_EQ(b_bytes, pool.leased_bytes("B"));
+  }
+  for (const auto& l : leases) pool.release(l);
+  CHECK_EQ(pool.free_bytes(), pool.bytes());
+}
+
+// ------------------------------------------------------------ schema / plans
+
+namespace {
+
+PageSchema plain_schema() {
+  PageSchema s;
+  CHECK(MakeKVPageSchema(1, 3, 4, 2, 8,
+                         base::MakeKVCacheStorageSpec(base::DataType::kDataTypeBf16,
+                                                      base::BlockStorageMode::kPlain),
+                         &s));
+  return s;
+}
+
+PageSchema fp8_schema() {
+  PageSchema s;
+  CHECK(MakeKVPageSchema(1, 2, 4, 2, 8,
+                         base::MakeKVCacheStorageSpec(base::DataType::kDataTypeBf16,
+                                                      base::BlockStorageMode::kFp8E4M3PerTokenHead),
+                         &s));
+  return s;
+}
+
+PageSchema headed_schema(bool fp8, int32_t heads = 4, uint32_t version = 1) {
+  PageSchema s;
+  CHECK(MakeKVPageSchema(version, 2, 4, heads, 3,
+                         base::MakeKVCacheStorageSpec(base::DataType::kDataTypeBf16,
+                                                      fp8 ? base::BlockStorageMode::kFp8E4M3PerTokenHead
+                                                          : base::BlockStorageMode::kPlain),
+                         &s));
+  return s;
+}
+
+// Splits every component into the given head ranges (tensor-parallel shards).
+PageSchema shard(PageSchema s, const std::vector<std::pair<int32_t, int32_t>>& ranges) {
+  std::vector<ComponentDescriptor> parts;
+  for (const auto& c : s.components)
+    for (const auto& r : ranges) {
+      auto p = c;
+      p.head_begin = r.first;
+      p.head_count = r.second;
+      parts.push_back(p);
+    }
+  s.components = parts;
+  CHECK(s.validate());
+  return s;
+}
+
+std::vector<size_t> iota_order(size_t n) {
+  std::vector<size_t> o(n);
+  std::iota(o.begin(), o.end(), 0);
+  return o;
+}
+
+const ComponentLayout& entry_of(const LayoutDescriptor& l, const ComponentDescriptor& c) {
+  for (const auto& e : l.components)
+    if (e.component.semantic_key() == c.semantic_key()) return e;
+  static ComponentLayout none;
+  CHECK(false);
+  return none;
+}
+
+// One byte value per (layer, kind) component.
+void fill_by_component(const LayoutDescriptor& l, std::vector<uint8_t>* bytes) {
+  for (const auto& e : l.components) {
+    const uint8_t v = static_cast<uint8_t>(1 + e.component.layer * 17 + static_cast<int>(e.component.kind) * 3);
+    std::fill(bytes->begin() + e.offset_bytes, bytes->begin() + e.offset_bytes + e.size_bytes, v);
+  }
+}
+
+// A byte value that depends on (layer, kind, token, absolute head, element, byte),
+// so any slice landing in the wrong place shows up.
+void fill_by_element(const LayoutDescriptor& l, std::vector<uint8_t>* bytes) {
+  for (const auto& e : l.components) {
+    const auto& c = e.component;
+    const size_t width = base::DataTypeSize(c.dtype);
+    size_t at = e.offset_bytes;
+    for (int32_t t = 0; t < c.token_count; ++t)
+      for (int32_t h = 0; h < c.head_count; ++h)
+        for (int32_t x = 0; x < c.elements_per_head; ++x)
+          for (size_t b = 0; b < width; ++b)
+            (*bytes)[at++] = static_cast<uint8_t>(1 + c.layer * 71 + static_cast<int>(c.kind) * 31 +
+                                                  t * 13 + (c.head_begin + h) * 7 + x * 3 +
+                                                  static_cast<int>(b));
+  }
+}
+
+}  // namespace
+
+TEST_CASE("page schema: K, V and scale coverage is required") {
+  auto plain = plain_schema();
+  CHECK(plain.validate());
+  plain.components.pop_back();
+  CHECK(!plain.validate());
+  auto fp8 = fp8_schema();
+  CHECK(fp8.validate());
+  fp8.components.erase(std::find_if(fp8.components.begin(), fp8.components.end(), [](const auto& c) {
+    return c.kind == ComponentKind::kValueScale;
+  }));
+  CHECK(!fp8.validate());
+  auto bad = plain_schema();
+  bad.storage.scale_dtype = base::DataType::kDataTypeFp32;
+  CHECK(!bad.validate());
+  auto overlap = headed_schema(false);
+  overlap.components.push_back(overlap.components.front());
+  overlap.components.back().head_count = 1;
+  CHECK(!overlap.validate());
+}
+
+TEST_CASE("transfer plan: shuffled layouts and virtual block ids round trip") {
+  const auto schema = fp8_schema();
+  const auto src_order = iota_order(schema.components.size());
+  auto host_order = src_order;
+  std::reverse(host_order.begin(), host_order.end());
+  const std::vector<size_t> back_order = {2, 5, 0, 7, 1, 6, 3, 4};
+  LayoutDescriptor src_l, host_l, back_l;
+  REQUIRE(MakePackedLayout(schema, "gpu-layer-first", 11, src_order,
+                           {101, 203, 307, 409, 503, 601, 709, 809}, &src_l));
+  REQUIRE(MakePackedLayout(schema, "host-page-first", 12, host_order,
+                           {9001, 9002, 9003, 9004, 9005, 9006, 9007, 9008}, &host_l));
+  REQUIRE(MakePackedLayout(schema, "gpu-restored", 13, back_order, {41, 37, 31, 29, 23, 19, 17, 13},
+                           &back_l));
+  std::vector<uint8_t> src(src_l.total_bytes), host(host_l.total_bytes, 0), back(back_l.total_bytes, 0);
+  fill_by_component(src_l, &src);
+  TransferPlanner planner;
+  TransferPlan plan;
+  REQUIRE(planner.plan(schema, schema, &plan));
+  BoundTransfer pack;
+  REQUIRE(BoundTransfer::Bind(plan, schema, {src.data(), src.size(), &src_l},
+                              {host.data(), host.size(), &host_l}, &pack));
+  REQUIRE(ExecuteCpuTransfer(pack));
+  CHECK_EQ(pack.source_epoch(), 11u);
+  CHECK_EQ(pack.destination_epoch(), 12u);
+  for (const auto& op : pack.operations()) {
+    CHECK_EQ(op.source_virtual_block_id, entry_of(src_l, op.component).virtual_block_id);
+    CHECK_EQ(op.destination_virtual_block_id, entry_of(host_l, op.component).virtual_block_id);
+  }
+  BoundTransfer unpack;
+  REQUIRE(BoundTransfer::Bind(plan, schema, {host.data(), host.size(), &host_l},
+                              {back.data(), back.size(), &back_l}, &unpack));
+  REQUIRE(ExecuteCpuTransfer(unpack));
+  for (const auto& e : src_l.components) {
+    const auto& o = entry_of(back_l, e.component);
+    CHECK(std::equal(src.begin() + e.offset_bytes, src.begin() + e.offset_bytes + e.size_bytes,
+                     back.begin() + o.offset_bytes));
+  }
+  TransferPlan again;
+  REQUIRE(planner.plan(schema, schema, &again));
+  CHECK_EQ(planner.cache_hits(), 1u);
+  CHECK_EQ(planner.cache_entries(), 1u);
+}
+
+TEST_CASE("transfer plan: a missing or corrupt component fails before any write") {
+  const auto schema = fp8_schema();
+  const auto order = iota_order(schema.components.size());
+  LayoutDescriptor src_l, dst_l;
+  REQUIRE(MakePackedLayout(schema, "source", 1, order, {}, &src_l));
+  REQUIRE(MakePackedLayout(schema, "destination", 2, order, {}, &dst_l));
+  src_l.components.pop_back();
+  std::vector<uint8_t> src(src_l.total_bytes, 0x27), dst(dst_l.total_bytes, 0xa5);
+  const auto original = dst;
+  TransferPlanner planner;
+  TransferPlan plan;
+  REQUIRE(planner.plan(schema, schema, &plan));
+  BoundTransfer bound;
+  CHECK(!BoundTransfer::Bind(plan, schema, {src.data(), src.size(), &src_l},
+                             {dst.data(), dst.size(), &dst_l}, &bound));
+  CHECK(dst == original);
+  src_l.components.push_back(dst_l.components.back());
+  plan.operations.back() = plan.operations.front();
+  CHECK(!BoundTransfer::Bind(plan, schema, {src.data(), src.size(), &src_l},
+                             {dst.data(), dst.size(), &dst_l}, &bound));
+  CHECK(dst == original);
+}
+
+TEST_CASE("transfer plan: shape and dtype mismatches fail before any write") {
+  const auto schema = plain_schema();
+  const auto order = iota_order(schema.components.size());
+  LayoutDescriptor src_l, dst_l;
+  REQUIRE(MakePackedLayout(schema, "source", 1, order, {}, &src_l));
+  REQUIRE(MakePackedLayout(schema, "destination", 2, order, {}, &dst_l));
+  std::vector<uint8_t> src(src_l.total_bytes, 0x33), dst(dst_l.total_bytes, 0x5a);
+  const auto original = dst;
+  dst_l.components.front().component.dtype = base::DataType::kDataTypeFp32;
+  TransferPlanner planner;
+  TransferPlan plan;
+  REQUIRE(planner.plan(schema, schema, &plan));
+  BoundTransfer bound;
+  CHECK(!BoundTransfer::Bind(plan, schema, {src.data(), src.size(), &src_l},
+                             {dst.data(), dst.size(), &dst_l}, &bound));
+  CHECK(dst == original);
+  auto wider = schema;
+  wider.head_size += 1;
+  for (auto& c : wider.components) c.elements_per_head += 1;
+  CHECK(!planner.plan(schema, wider, &plan));
+}
+
+TEST_CASE("transfer plan: independent allocations pack and restore (plain and FP8)") {
+  for (const auto& schema : {plain_schema(), fp8_schema()}) {
+    auto order = iota_order(schema.components.size());
+    LayoutDescriptor gpu_l, host_l, back_l;
+    REQUIRE(MakePackedLayout(schema, "scatter-gpu", 31, order, {}, &gpu_l));
+    std::reverse(order.begin(), order.end());
+    REQUIRE(MakePackedLayout(schema, "packed-host", 32, order, {}, &host_l));
+    REQUIRE(MakePackedLayout(schema, "restored-gpu", 33, order, {}, &back_l));
+    std::vector<std::vector<uint8_t>> originals, restored;
+    for (size_t i = 0; i < schema.components.size(); ++i) {
+      originals.emplace_back(schema.components[i].byte_size(), static_cast<uint8_t>(i + 71));
+      restored.emplace_back(schema.components[i].byte_size(), 0);
+    }
+    std::vector<uint8_t> host(host_l.total_bytes, 0);
+    ConstComponentEndpoint source{{}, &gpu_l}, packed_source{{}, &host_l};
+    MutableComponentEndpoint packed{{}, &host_l}, target{{}, &back_l};
+    for (size_t i = 0; i < schema.components.size(); ++i) {
+      const auto& c = schema.components[i];
+      source.components.push_back({c, originals[i].data(), originals[i].size()});
+      target.components.push_back({c, restored[i].data(), restored[i].size()});
+      const auto& e = entry_of(host_l, c);
+      packed.components.push_back({c, host.data() + e.offset_bytes, e.size_bytes});
+      packed_source.components.push_back({c, host.data() + e.offset_bytes, e.size_bytes});
+    }
+    std::reverse(source.components.begin(), source.components.end());
+    TransferPlanner planner;
+    TransferPlan plan;
+    REQUIRE(planner.plan(schema, schema, &plan));
+    BoundTransfer pack, unpack;
+    REQUIRE(BoundTransfer::BindComponents(plan, schema, source, packed, &pack));
+    REQUIRE(ExecuteCpuTransfer(pack));
+    REQUIRE(BoundTransfer::BindComponents(plan, schema, packed_source, target, &unpack));
+    REQUIRE(ExecuteCpuTransfer(unpack));
+    CHECK(originals == restored);
+    CHECK_EQ(pack.source_epoch(), 31u);
+    CHECK_EQ(unpack.destination_epoch(), 33u);
+
+    // Failed bindings leave the destination bytes and the earlier binding intact.
+    const auto host_before = host;
+    const auto ops_before = pack.operations().size();
+    const auto kept = source;
+    source.components.pop_back();
+    CHECK(!BoundTransfer::BindComponents(plan, schema, source, packed, &pack));
+    source = kept;
+    source.components.back() = source.components.front();
+    CHECK(!BoundTransfer::BindComponents(plan, schema, source, packed, &pack));
+    source = kept;
+    source.components.back().bytes = 1;
+    CHECK(!BoundTransfer::BindComponents(plan, schema, source, packed, &pack));
+    source = kept;
+    source.components.back().component.dtype = base::DataType::kDataTypeFp32;
+    CHECK(!BoundTransfer::BindComponents(plan, schema, source, packed, &pack));
+    source = kept;
+    auto aliased = packed;
+    aliased.components.back().data = aliased.components.front().data;
+    CHECK(!BoundTransfer::BindComponents(plan, schema, source, aliased, &pack));
+    plan.operations.back() = plan.operations.front();
+    CHECK(!BoundTransfer::BindComponents(plan, schema, source, packed, &pack));
+    CHECK(host == host_before);
+    CHECK_EQ(pack.operations().size(), ops_before);
+    CHECK_EQ(pack.source_epoch(), 31u);
+  }
+}
+
+TEST_CASE("transfer plan: head split/merge keeps every element in place") {
+  for (bool fp8 : {false, true}) {
+    const auto src_schema = shard(headed_schema(fp8), {{0, 1}, {1, 3}});
+    const auto dst_schema = shard(headed_schema(fp8), {{0, 2}, {2, 2}});
+    auto src_order = iota_order(src_schema.components.size());
+    auto dst_order = iota_order(dst_schema.components.size());
+    std::reverse(src_order.begin(), src_order.end());
+    std::rotate(dst_order.begin(), dst_order.begin() + 3, dst_order.end());
+    LayoutDescriptor src_l, dst_l;
+    REQUIRE(MakePackedLayout(src_schema, "tp-source", 41, src_order, {}, &src_l));
+    REQUIRE(MakePackedLayout(dst_schema, "tp-destination", 42, dst_order, {}, &dst_l));
+    std::vector<uint8_t> src(src_l.total_bytes), expected(dst_l.total_bytes);
+    fill_by_element(src_l, &src);
+    fill_by_element(dst_l, &expected);
+    for (auto placement : {TransferPlacement::kExactDirect, TransferPlacement::kSenderPack,
+                           TransferPlacement::kReceiverUnpack}) {
+      TransferPlanner planner;
+      std::shared_ptr<const TransferPlan> plan;
+      REQUIRE(planner.compile(src_schema, dst_schema, placement, &plan));
+      std::vector<uint8_t> dst(dst_l.total_bytes, 0xa5);
+      BoundTransfer bound;
+      REQUIRE(BoundTransfer::Bind(*plan, src_schema, dst_schema, {src.data(), src.size(), &src_l},
+                                  {dst.data(), dst.size(), &dst_l}, &bound));
+      if (placement == TransferPlacement::kExactDirect) {
+        REQUIRE(ExecuteCpuTransfer(bound));
+      } else {
+        std::vector<uint8_t> staging(bound.staging_bytes());
+        REQUIRE(ExecuteCpuTransferStaged(bound, staging.data(), staging.size()));
+        CHECK(!ExecuteCpuTransferStaged(bound, staging.data(), staging.size() - 1));
+      }
+      CHECK(dst == expected);
+      CHECK_EQ(bound.source_epoch(), 41u);
+      CHECK_EQ(bound.destination_epoch(), 42u);
+      CHECK(bound.placement() == placement);
+    }
+  }
+}
+
+TEST_CASE("transfer plan: invalid coverage or conversions fail before any write") {
+  auto src_schema = shard(headed_schema(false), {{0, 2}, {2, 2}});
+  auto dst_schema = shard(headed_schema(false), {{0, 1}, {1, 3}});
+  TransferPlanner planner;
+  std::shared_ptr<const TransferPlan> plan;
+  REQUIRE(planner.compile(src_schema, dst_schema, TransferPlacement::kExactDirect, &plan));
+  LayoutDescriptor src_l, dst_l;
+  REQUIRE(MakePackedLayout(src_schema, "source", 1, iota_order(src_schema.components.size()), {}, &src_l));
+  REQUIRE(MakePackedLayout(dst_schema, "destination", 2, iota_order(dst_schema.components.size()), {},
+                           &dst_l));
+  std::vector<uint8_t> src(src_l.total_bytes, 0x37), dst(dst_l.total_bytes, 0xa5);
+  const auto original = dst;
+  auto stale = src_schema;
+  stale.version++;
+  BoundTransfer bound;
+  CHECK(!BoundTransfer::Bind(*plan, stale, dst_schema, {src.data(), src.size(), &src_l},
+                             {dst.data(), dst.size(), &dst_l}, &bound));
+  CHECK(dst == original);
+  auto missing = src_schema;
+  missing.components.pop_back();
+  CHECK(!planner.compile(missing, dst_schema, TransferPlacement::kExactDirect, &plan));
+  auto duplicate = dst_schema;
+  duplicate.components.push_back(duplicate.components.back());
+  CHECK(!planner.compile(src_schema, duplicate, TransferPlacement::kExactDirect, &plan));
+  auto converted = dst_schema;
+  converted.storage = base::MakeKVCacheStorageSpec(base::DataType::kDataTypeBf16,
+                                                   base::BlockStorageMode::kFp8E4M3PerTokenHead);
+  CHECK(!planner.compile(src_schema, converted, TransferPlacement::kExactDirect, &plan));
+  CHECK(dst == original);
+}
+
+TEST_CASE("transfer plan: template cache ignores addresses and stays bounded") {
+  const auto src = shard(headed_schema(false), {{0, 2}, {2, 2}});
+  const auto dst = shard(headed_schema(false), {{0, 1}, {1, 3}});
+  TransferPlanner planner(2, 1u << 20);
+  std::shared_ptr<const TransferPlan> first;
+  REQUIRE(planner.compile(src, dst, TransferPlacement::kSenderPack, &first));
+  for (int i = 0; i < 1000; ++i) {
+    std::shared_ptr<const TransferPlan> again;
+    REQUIRE(planner.compile(src, dst, TransferPlacement::kSenderPack, &again));
+    CHECK(again.get() == first.get());
+  }
+  CHECK_EQ(planner.cache_entries(), 1u);
+  CHECK_EQ(planner.cache_hits(), 1000u);
+  CHECK(planner.cache_bytes() > 0u);
+  std::shared_ptr<const TransferPlan> m2, m3;
+  REQUIRE(planner.compile(src, dst, TransferPlacement::kReceiverUnpack, &m2));
+  REQUIRE(planner.compile(src, dst, TransferPlacement::kExactDirect, &m3));
+  CHECK_EQ(planner.cache_entries(), 2u);
+  CHECK(planner.cache_evictions() >= 1u);
+  CHECK(planner.cache_bytes() <= (1u << 20));
+  CHECK(first.get() != m2.get());
+  CHECK_THROWS_AS(TransferPlanner(0, 1), std::invalid_argument);
+}
+
+TEST_CASE("layout codec: overlapping or non-permutation layouts are rejected") {
+  const auto schema = plain_schema();
+  auto order = iota_order(schema.components.size());
+  order.back() = order.front();
+  LayoutDescriptor l;
+  CHECK(!MakePackedLayout(schema, "duplicate", 1, order, {}, &l));
+  REQUIRE(MakePackedLayout(schema, "overlap", 1, iota_order(schema.components.size()), {}, &l));
+  l.components.back().offset_bytes = l.components.front().offset_bytes;
+  CHECK(!l.validate(schema));
+}
+
+// ------------------------------------------------------------ backends
+
+namespace {
+// A backend that reports Pending until told otherwise and copies on success
+// (test/test_page_migration.cpp:5-25 uses the same fake).
+class DelayedBackend final : public TransferBackend {
+ public:
+  BoundTransfer bound;
+  BackendResult next = BackendResult::kPending;
+  bool copied = false;
+  int submitted = 0, released = 0;
+  bool supports(base::DeviceType d) const override { return d == base::DeviceType::kDeviceCPU; }
+  BackendResult submit(MigrationId, TransferDirection, const BoundTransfer& t) noexcept override {
+    bound = t;
+    ++submitted;
+    copied = false;
+    return next;
+  }
+  BackendResult poll(MigrationId) noexcept override {
+    if (next == BackendResult::kSucceeded && !copied) {
+      if (!ExecuteCpuTransfer(bound)) return BackendResult::kFailedSafe;
+      copied = true;
+    }
+    return next;
+  }
+  BackendResult drain(MigrationId id) noexcept override { return poll(id); }
+  void release(MigrationId) noexcept override {
+    ++released;
+    bound = {};
+  }
+};
+}  // namespace
+
+TEST_CASE("backends: CPU backend copies synchronously; a fake shows pending states") {
+  const auto schema = plain_schema();
+  LayoutDescriptor l;
+  REQUIRE(MakePackedLayout(schema, "p", 1, iota_order(schema.components.size()), {}, &l));
+  std::vector<uint8_t> src(l.total_bytes, 0x38), dst(l.total_bytes, 0);
+  TransferPlanner planner;
+  TransferPlan plan;
+  REQUIRE(planner.plan(schema, schema, &plan));
+  BoundTransfer bound;
+  REQUIRE(BoundTransfer::Bind(plan, schema, {src.data(), src.size(), &l}, {dst.data(), dst.size(), &l},
+                              &bound));
+  auto cpu = MakeCpuTransferBackend();
+  CHECK(cpu->supports(base::DeviceType::kDeviceCPU));
+  CHECK(!cpu->supports(base::DeviceType::kDeviceHIP));
+  CHECK(cpu->submit(1, TransferDirection::kToHost, bound) == BackendResult::kSucceeded);
+  CHECK(dst == src);
+  CHECK(cpu->poll(1) == BackendResult::kSucceeded);
+  CHECK(cpu->submit(2, TransferDirection::kToHost, BoundTransfer{}) == BackendResult::kSucceeded);
+
+  std::fill(dst.begin(), dst.end(), 0);
+  DelayedBackend fake;
+  CHECK(fake.submit(3, TransferDirection::kToGpu, bound) == BackendResult::kPending);
+  CHECK(fake.poll(3) == BackendResult::kPending);
+  CHECK(dst != src);
+  fake.next = BackendResult::kSucceeded;
+  CHECK(fake.drain(3) == BackendResult::kSucceeded);
+  CHECK(dst == src);
+  fake.release(3);
+  CHECK_EQ(fake.released, 1);
+}
+
+// ------------------------------------------------------------ handoff manifest
+
+namespace {
+serving::KVBlockManifest good_manifest() {
+  serving::KVBlockManifest m;
+  m.client_request_id.value = "req-1";
+  m.handoff_id.value = 9;
+  m.prompt_tokens = 41;
+  m.computed_tokens = 41;
+  m.src_pool = {0, 2, 16, 2, 64, base::DataType::kDataTypeBf16, base::BlockStorageMode::kPlain};
+  m.dst_pool = m.src_pool;
+  for (int l = 0; l < 2; ++l) m.layer_mappings.push_back({l, {0, 4, 8}, {12, 16, 20}});
+  return m;
+}
+}  // namespace
+
+TEST_CASE("manifest: validation mirrors the reference") {
+  CHECK(good_manifest().validate());
+  auto m = good_manifest();
+  m.client_request_id.value.clear();
+  CHECK(!m.validate());
+  m = good_manifest();
+  m.handoff_id.value = 0;
+  CHECK(!m.validate());
+  m = good_manifest();
+  m.computed_tokens = 42;
+  CHECK(!m.validate());
+  m = good_manifest();
+  m.dst_pool.head_size = 128;
+  CHECK(!m.validate());
+  m = good_manifest();
+  m.layer_mappings.pop_back();
+  CHECK(!m.validate());
+  m = good_manifest();
+  m.layer_mappings[1].dst_block_ids.pop_back();
+  CHECK(!m.validate());
+  m = good_manifest();
+  m.layer_mappings[0].src_block_ids.clear();
+  m.layer_mappings[0].dst_block_ids.clear();
+  CHECK(!m.validate());
+  serving::KVPoolDescriptor d = good_manifest().src_pool;
+  CHECK_EQ(d.bytes_per_block_per_layer(), 2 * 16 * 2 * 64 * 2);
+  d.storage_mode = base::BlockStorageMode::kFp8E4M3PerTokenHead;
+  CHECK_EQ(d.bytes_per_block_per_layer(), 2 * 16 * 2 * 64 + 2 * 16 * 2 * 4);
+}
+
+TEST_CASE("storage spec: plain and FP8 specs and per-token bytes") {
+  const auto plain = base::MakeKVCacheStorageSpec(base::DataType::kDataTypeBf16, base::BlockStorageMode::kPlain);
+  CHECK(!plain.has_scales());
+  CHECK(base::ValidateKVCacheStorageSpec(plain, base::DeviceType::kDeviceHIP, base::DataType::kDataTypeBf16));
+  // Qwen2.5-1.5B: 28 layers, 2 KV heads x 128, BF16 -> 28 KiB per token.
+  CHECK_EQ(base::KVCacheBytesPerToken(plain, 28, 2, 128), 28u * 1024u);
+  const auto fp8 = base::MakeKVCacheStorageSpec(base::DataType::kDataTypeBf16,
+                                                base::BlockStorageMode::kFp8E4M3PerTokenHead);
+  CHECK(fp8.has_scales());
+  CHECK(base::ValidateKVCacheStorageSpec(fp8, base::DeviceType::kDeviceHIP, base::DataType::kDataTypeBf16));
+  CHECK(!base::ValidateKVCacheStorageSpec(fp8, base::DeviceType::kDeviceCPU, base::DataType::kDataTypeBf16));
+  CHECK_EQ(base::KVCacheBytesPerToken(fp8, 28, 2, 128), 28u * 2 * 2 * 128 + 28u * 2 * 2 * 4);
+}
+
+MINITEST_MAIN()
