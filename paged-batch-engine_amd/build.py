@@ -57,7 +57,7 @@ HIP_SOURCES = [
     "csrc/capi/pbe_capi.hip",
 ]
 CPU_TESTS = ["tests/cpp/test_drop_in_api.cpp"]
-GPU_TESTS: list[str] = []
+GPU_TESTS = ["tests/cpp/test_gpu_backend.cpp"]
 
 
 def _run(cmd: list[str]) -> None:

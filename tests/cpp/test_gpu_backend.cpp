@@ -1,0 +1,217 @@
+// GPU tests of the C++ drop-in API: the HIP TransferBackend (one kernel per
+// BoundTransfer) and the shared-arena handoff connector. Scenarios follow the
+// reference's test/test_page_migration_cuda.cpp:13-108 (byte fills, pending /
+// failed-safe states) and test/test_serving/test_pd_handoff.cpp:429-564
+// (pattern-filled pages compared element-wise after the handoff).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <numeric>
+#include <vector>
+
+#include "cache/page_migration.h"
+#include "cache/transfer_plan.h"
+#include "minitest.h"
+#include "pbe_handoff.h"
+#include "serving/pd_handoff.h"
+
+using namespace cache;
+
+#define HIP_OK(x) REQUIRE((x) == hipSuccess)
+
+namespace {
+
+PageSchema schema_of(bool fp8, int32_t layers = 2) {
+  PageSchema s;
+  MakeKVPageSchema(1, layers, 16, 2, 64,
+                   base::MakeKVCacheStorageSpec(base::DataType::kDataTypeBf16,
+                                                fp8 ? base::BlockStorageMode::kFp8E4M3PerTokenHead
+                                                    : base::BlockStorageMode::kPlain),
+                   &s);
+  return s;
+}
+
+std::vector<size_t> iota_order(size_t n) {
+  std::vector<size_t> o(n);
+  std::iota(o.begin(), o.end(), 0);
+  return o;
+}
+
+BackendResult wait_done(TransferBackend& b, MigrationId id) {
+  BackendResult r = BackendResult::kPending;
+  for (int i = 0; i < 2000000 && r == BackendResult::kPending; ++i) r = b.poll(id);
+  return r;
+}
+
+}  // namespace
+
+TEST_CASE("hip backend: device to device, to host and back to device") {
+  for (bool fp8 : {false, true}) {
+    const auto s = schema_of(fp8);
+    LayoutDescriptor l;
+    REQUIRE(MakePackedLayout(s, "packed", 7, iota_order(s.components.size()), {}, &l));
+    const size_t n = l.total_bytes;
+    uint8_t *d_src = nullptr, *d_dst = nullptr, *d_back = nullptr, *h_pin = nullptr;
+    HIP_OK(hipMalloc(&d_src, n));
+    HIP_OK(hipMalloc(&d_dst, n));
+    HIP_OK(hipMalloc(&d_back, n));
+    HIP_OK(hipHostMalloc(&h_pin, n, hipHostMallocDefault));
+    std::vector<uint8_t> pattern(n);
+    for (size_t i = 0; i < n; ++i) pattern[i] = static_cast<uint8_t>(i * 37u + 11u);
+    HIP_OK(hipMemcpy(d_src, pattern.data(), n, hipMemcpyHostToDevice));
+    HIP_OK(hipMemset(d_dst, 0x21, n));
+    HIP_OK(hipMemset(d_back, 0x21, n));
+    std::memset(h_pin, 0x21, n);
+
+    TransferPlanner planner;
+    TransferPlan plan;
+    REQUIRE(planner.plan(s, s, &plan));
+    auto backend = MakeHipTransferBackend(2, 0);
+    CHECK(backend->supports(base::DeviceType::kDeviceHIP));
+    CHECK(!backend->supports(base::DeviceType::kDeviceCPU));
+
+    BoundTransfer d2d, d2h, h2d;
+    REQUIRE(BoundTransfer::Bind(plan, s, {d_src, n, &l}, {d_dst, n, &l}, &d2d));
+    REQUIRE(BoundTransfer::Bind(plan, s, {d_src, n, &l}, {h_pin, n, &l}, &d2h));
+    REQUIRE(BoundTransfer::Bind(plan, s, {h_pin, n, &l}, {d_back, n, &l}, &h2d));
+
+    CHECK(backend->submit(1, TransferDirection::kGpuToGpu, d2d) == BackendResult::kPending);
+    CHECK(backend->submit(1, TransferDirection::kGpuToGpu, d2d) == BackendResult::kUnknown);  // live id
+    CHECK(backend->submit(2, TransferDirection::kToHost, d2h) == BackendResult::kPending);
+    CHECK(backend->submit(3, TransferDirection::kToHost, d2h) == BackendResult::kFailedSafe);  // no slot
+    CHECK(wait_done(*backend, 1) == BackendResult::kSucceeded);
+    CHECK(backend->drain(2) == BackendResult::kSucceeded);
+    backend->release(1);
+    backend->release(2);
+    CHECK(std::memcmp(h_pin, pattern.data(), n) == 0);
+    std::vector<uint8_t> got(n);
+    HIP_OK(hipMemcpy(got.data(), d_dst, n, hipMemcpyDeviceToHost));
+    CHECK(got == pattern);
+
+    CHECK(backend->submit(4, TransferDirection::kToGpu, h2d) == BackendResult::kPending);
+    CHECK(backend->drain(4) == BackendResult::kSucceeded);
+    backend->release(4);
+    HIP_OK(hipMemcpy(got.data(), d_back, n, hipMemcpyDeviceToHost));
+    CHECK(got == pattern);
+
+    // Wrong-direction or pageable endpoints are refused before any write.
+    std::vector<uint8_t> pageable(n, 0x21);
+    BoundTransfer bad;
+    REQUIRE(BoundTransfer::Bind(plan, s, {d_src, n, &l}, {pageable.data(), n, &l}, &bad));
+    CHECK(backend->submit(5, TransferDirection::kToHost, bad) == BackendResult::kFailedSafe);
+    CHECK(backend->submit(6, TransferDirection::kToGpu, d2d) == BackendResult::kFailedSafe);
+    CHECK(backend->submit(7, TransferDirection::kToHost, d2d) == BackendResult::kFailedSafe);
+    backend->release(5);  // never submitted to a stream: no-op
+    CHECK(std::all_of(pageable.begin(), pageable.end(), [](uint8_t b) { return b == 0x21; }));
+    (void)hipFree(d_src);
+    (void)hipFree(d_dst);
+    (void)hipFree(d_back);
+    (void)hipHostFree(h_pin);
+  }
+}
+
+TEST_CASE("hip backend: a dependency event orders the copy after the producer") {
+  const auto s = schema_of(false);
+  LayoutDescriptor l;
+  REQUIRE(MakePackedLayout(s, "packed", 7, iota_order(s.components.size()), {}, &l));
+  const size_t n = l.total_bytes;
+  uint8_t *d_src = nullptr, *d_dst = nullptr;
+  HIP_OK(hipMalloc(&d_src, n));
+  HIP_OK(hipMalloc(&d_dst, n));
+  hipStream_t producer;
+  hipEvent_t produced;
+  HIP_OK(hipStreamCreateWithFlags(&producer, hipStreamNonBlocking));
+  HIP_OK(hipEventCreateWithFlags(&produced, hipEventDisableTiming));
+  HIP_OK(hipMemsetAsync(d_src, 0x5c, n, producer));  // the "prefill" writes the source
+  HIP_OK(hipEventRecord(produced, producer));
+  TransferPlanner planner;
+  TransferPlan plan;
+  REQUIRE(planner.plan(s, s, &plan));
+  BoundTransfer t;
+  REQUIRE(BoundTransfer::Bind(plan, s, {d_src, n, &l}, {d_dst, n, &l}, &t));
+  {
+    auto backend = MakeHipTransferBackend(1, 0, produced);
+    CHECK(backend->submit(1, TransferDirection::kGpuToGpu, t) == BackendResult::kPending);
+    CHECK(backend->drain(1) == BackendResult::kSucceeded);
+    backend->release(1);
+  }
+  std::vector<uint8_t> got(n);
+  HIP_OK(hipMemcpy(got.data(), d_dst, n, hipMemcpyDeviceToHost));
+  CHECK(std::all_of(got.begin(), got.end(), [](uint8_t b) { return b == 0x5c; }));
+  (void)hipEventDestroy(produced);
+  (void)hipStreamDestroy(producer);
+  (void)hipFree(d_src);
+  (void)hipFree(d_dst);
+}
+
+namespace {
+serving::KVBlockManifest manifest_for(int32_t layers, const std::vector<int32_t>& src,
+                                      const std::vector<int32_t>& dst) {
+  serving::KVBlockManifest m;
+  m.client_request_id.value = "req";
+  m.handoff_id.value = 1;
+  m.prompt_tokens = static_cast<int32_t>(src.size()) * 16;
+  m.computed_tokens = m.prompt_tokens - 3;
+  m.src_pool = {0, layers, 16, 2, 64, base::DataType::kDataTypeBf16, base::BlockStorageMode::kPlain};
+  m.dst_pool = m.src_pool;
+  for (int32_t l = 0; l < layers; ++l) m.layer_mappings.push_back({l, src, dst});
+  return m;
+}
+}  // namespace
+
+TEST_CASE("shared-arena connector: page-major pages arrive intact, errors write nothing") {
+  const int32_t layers = 3;
+  const uint64_t half = 16 * 2 * 64 * 2, page = 2 * layers * half;
+  const uint64_t pages = 40, bytes = pages * page;
+  pbe_arena* arena = nullptr;
+  REQUIRE(pbe_arena_create(0, bytes, 0, 123, &arena) == PBE_OK);
+  serving::SharedArenaBinding bind;
+  REQUIRE(pbe_arena_get_view(arena, &bind.view) == PBE_OK);
+  bind.epoch = 123;
+  bind.device = 0;
+  // Byte (2l+plane)*half of page p holds p*3 + 64*plane + l (the page-major
+  // pattern of demo/shared_kv_reuse_probe.cpp:76-83).
+  std::vector<uint8_t> host(bytes);
+  for (uint64_t p = 0; p < pages; ++p)
+    for (int l = 0; l < layers; ++l)
+      for (int plane = 0; plane < 2; ++plane)
+        std::memset(host.data() + p * page + (2 * l + plane) * half,
+                    static_cast<int>((p * 3 + 64 * plane + l) & 0xff), half);
+  HIP_OK(hipMemcpy(bind.view.base[0], host.data(), bytes, hipMemcpyHostToDevice));
+  const int32_t st = 2 * layers;
+  const std::vector<int32_t> src = {2 * st, 3 * st, 4 * st, 9 * st, 10 * st};
+  const std::vector<int32_t> dst = {20 * st, 21 * st, 30 * st, 31 * st, 5 * st};
+  {
+    serving::SharedArenaKVTransferConnector conn(bind);
+    serving::HandoffId h;
+    REQUIRE(conn.submit(manifest_for(layers, src, dst), &h));
+    CHECK(conn.drain(h).ok());
+    CHECK_EQ(conn.copied_bytes(), src.size() * page);
+    conn.release(h);
+    CHECK(conn.poll(h).state == serving::KVTransferState::kFailed);  // forgotten
+
+    // Errors: stale epoch, non-page-major layers, ids outside the arena.
+    serving::HandoffId bad;
+    CHECK(!conn.submit_from(124, manifest_for(layers, src, dst), &bad));
+    CHECK(conn.poll(bad).state == serving::KVTransferState::kFailed);
+    auto skew = manifest_for(layers, src, dst);
+    skew.layer_mappings[1].src_block_ids[0] += st;
+    CHECK(!conn.submit(skew, &bad));
+    auto out_of_arena = manifest_for(layers, src, {20 * st, 21 * st, 30 * st, 31 * st, 40 * st});
+    CHECK(!conn.submit(out_of_arena, &bad));
+    auto unaligned = manifest_for(layers, src, {20 * st, 21 * st, 30 * st, 31 * st, 5 * st + 1});
+    CHECK(!conn.submit(unaligned, &bad));
+    auto self = manifest_for(layers, src, src);
+    CHECK(!conn.submit(self, &bad));
+  }
+  std::vector<uint8_t> got(bytes);
+  HIP_OK(hipMemcpy(got.data(), bind.view.base[0], bytes, hipMemcpyDeviceToHost));
+  std::vector<uint8_t> want = host;
+  for (size_t i = 0; i < src.size(); ++i)
+    std::memcpy(want.data() + (uint64_t)dst[i] / st * page, host.data() + (uint64_t)src[i] / st * page, page);
+  CHECK(got == want);
+  CHECK(pbe_arena_destroy(arena) == PBE_OK);
+}
+
+MINITEST_MAIN()
