@@ -65,6 +65,89 @@ def cpu_baseline(w, host_arena, seconds: float):
             "ms_per_handoff": round(per * 1e3, 3)}
 
 
+def _timed(torch, stream, scrub, fn, n):
+    """Mean/min event time (ms) of fn() over n cold launches (scrub before each)."""
+    import numpy as np
+    ts = []
+    for i in range(n + 2):
+        scrub.fill_(i & 0xff)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        if i >= 2:
+            ts.append(a.elapsed_time(b))
+    return float(np.mean(ts)), float(np.min(ts))
+
+
+def measure_extra_configs(torch, P, W, scrub, n: int):
+    """Kernel timings of the other handoff configurations (parity-test cases,
+    reported beside the headline line)."""
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    out = []
+
+    def rec(name, alg, ms, extra=None):
+        r = {"workload": name, "algorithmic_bytes": alg, "kernel_us_mean": round(ms[0] * 1e3, 2),
+             "kernel_us_min": round(ms[1] * 1e3, 2),
+             "gbps": round(alg / (ms[0] * 1e-3) / 1e9, 1),
+             "pct_of_peak": round(100 * alg / (ms[0] * 1e-3) / 1e9 / PEAK_GBPS, 1)}
+        r.update(extra or {})
+        out.append(r)
+        print(json.dumps(r), file=sys.stderr, flush=True)
+
+    for cfg in (1, 3, 5):
+        w = W.CONFIGS[cfg](0)
+        g = w.geometry
+        kv = P.shape(g.layers, g.kv_heads, g.head_dim, g.page_tokens)
+        seg = w.segment_bytes or w.arena_bytes
+        bufs = [torch.empty(min(seg, w.arena_bytes - o), dtype=torch.uint8, device=dev)
+                for o in range(0, w.arena_bytes, seg)]
+        view = P.view_of([b.data_ptr() for b in bufs], w.arena_bytes, seg)
+        runs = P.build_runs(w.src_ids, w.dst_ids, kv, 2, w.segment_bytes)
+        rl = P.RunList.bf16(view, view, runs, kv)
+        rec(w.name, w.algorithmic_bytes(), _timed(torch, stream, scrub, lambda: rl.copy(sp), n),
+            {"pages": w.pages, "runs": len(runs), "launches": 1})
+        rl.close()
+        if cfg == 3:  # one launch per request
+            lists = []
+            for r in w.requests:
+                rr = P.build_runs(r.src_ids, r.dst_ids, kv)
+                lists.append(P.RunList.bf16(view, view, rr, kv))
+            rec(w.name + "_per_request", w.algorithmic_bytes(),
+                _timed(torch, stream, scrub, lambda: [x.copy(sp) for x in lists], n),
+                {"pages": w.pages, "launches": len(lists)})
+            for x in lists:
+                x.close()
+        del bufs
+
+    w = W.config4(0)
+    g = w.geometry
+    kv = P.shape(g.layers, g.kv_heads, g.head_dim, g.page_tokens)
+    n_pages = w.meta["n_pages"]
+    src = torch.empty(n_pages * g.page_bytes(2), dtype=torch.uint8, device=dev)
+    src.view(torch.bfloat16).normal_()
+    dst = torch.empty(n_pages * g.page_bytes(1), dtype=torch.uint8, device=dev)
+    scale_page = 2 * g.layers * g.page_tokens * g.kv_heads * 4
+    scales = torch.empty(n_pages * scale_page, dtype=torch.uint8, device=dev)
+    table = torch.tensor(w.amax_table.ravel(), device=dev)
+    runs = P.build_runs(w.src_ids, w.dst_ids, kv)
+    rl = P.RunList.fp8(P.view_of(src.data_ptr(), src.numel()), P.view_of(dst.data_ptr(), dst.numel()),
+                       scales.data_ptr(), scales.numel(), runs, kv)
+    alg = w.algorithmic_bytes()
+    rec(w.name + "_per_token_head", alg + w.pages * scale_page,
+        _timed(torch, stream, scrub, lambda: rl.copy_fp8(P.PBE_FP8_SCALE_PER_TOKEN_HEAD, 0, sp), n),
+        {"pages": w.pages, "scale_bytes": w.pages * scale_page})
+    rec(w.name + "_table", alg + table.numel() * 4,
+        _timed(torch, stream, scrub,
+               lambda: rl.copy_fp8(P.PBE_FP8_SCALE_TABLE, table.data_ptr(), sp), n),
+        {"pages": w.pages})
+    rl.close()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -73,6 +156,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-scrub", action="store_true", help="hot-cache timing (diagnostic)")
+    ap.add_argument("--extra-configs", default="",
+                    help="also time configs 1, 3, 4 and 5 and write them as JSON to this file")
     ap.add_argument("--calibrate", action="store_true",
                     help="also launch a plain contiguous copy of 256 MiB with the same kernel "
                          "(rocprofv3 --pmc byte-count calibration)")
@@ -177,6 +262,10 @@ def main() -> int:
         calib = {"bytes": 256 << 20, "grid_threads": int(crl.info().slices) * 64,
                  "gbps": round(2 * (256 << 20) / (float(np.mean(ct)) * 1e-3) / 1e9, 1)}
         crl.close()
+
+    if args.extra_configs:
+        extra = measure_extra_configs(torch, P, W, scrub, max(10, args.steps // 4))
+        Path(args.extra_configs).write_text(json.dumps(extra, indent=1) + "\n")
 
     cpu = None
     if not args.no_cpu:

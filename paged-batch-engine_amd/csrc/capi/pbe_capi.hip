@@ -163,6 +163,16 @@ pbe::CopyConfig copy_config() {
   return c;
 }
 
+// FP8 kernel variant: the 16-byte vectors per lane per slice (PBE_FP8_UNROLL
+// overrides the default for tuning experiments only).
+pbe::CopyConfig fp8_config() {
+  pbe::CopyConfig c;
+  c.unroll = pbe::kFp8Unroll;
+  if (const char* e = std::getenv("PBE_FP8_UNROLL")) c.unroll = std::atoi(e);
+  if (c.unroll != 2 && c.unroll != 4 && c.unroll != 8) c.unroll = pbe::kFp8Unroll;
+  return c;
+}
+
 pbe::LaunchShape launch_shape(uint64_t total_slices, int device, const pbe::CopyConfig& cfg) {
   (void)total_slices;
   (void)device;
@@ -619,10 +629,10 @@ int pbe_runlist_create_fp8(const pbe_arena_view* src, const pbe_arena_view* dst,
   Resolved res;
   int rc = resolve_runs(*src, *dst, half16, half8, 2 * shape->layers, runs, n_runs,
                         reinterpret_cast<uint64_t>(dst_scales), dst_scales_bytes, scale_page,
-                        pbe::slice_bytes(pbe::KernelKind::kFp8, pbe::CopyConfig{}), &res);
+                        pbe::slice_bytes(pbe::KernelKind::kFp8, fp8_config()), &res);
   if (rc != PBE_OK) return rc;
   return upload_runlist(res, device, true, dst_scales != nullptr, 2ull * shape->layers * half16,
-                        *shape, pbe::CopyConfig{}, out);
+                        *shape, fp8_config(), out);
 }
 
 int pbe_runlist_get_info(const pbe_runlist* list, pbe_runlist_info* out) {

@@ -7,7 +7,7 @@ namespace pbe {
 
 constexpr int kThreadsPerBlock = 256;
 constexpr int kCopyUnroll = 4;  // 4 KiB per wave slice for the identity copy
-constexpr int kFp8Unroll = 8;   // 8 KiB of BF16 source per wave slice
+constexpr int kFp8Unroll = 4;   // 4 KiB of BF16 source per wave slice
 
 // Device form of one run: resolved addresses in this process's mapping.
 // slice_begin is the exclusive prefix of slices over the preceding runs.

@@ -143,13 +143,20 @@ __global__ __launch_bounds__(kBlock) void copy_runs_kernel(
 // Round to nearest even with saturation to +-448, the conversion the reference
 // asks of __nv_cvt_float_to_fp8(v, __NV_SATFINITE, __NV_E4M3)
 // (scatter_kv_kernel.cu:207-210). gfx950's v_cvt_pk_fp8_f32 rounds to nearest
-// even in the OCP format; clamping to +-448 first makes it saturate, and NaN
-// is mapped explicitly because the clamp would otherwise absorb it.
+// even in the OCP format; clamping to +-448 first makes it saturate. A NaN
+// product would be absorbed by the clamp, so lanes that can produce one (a NaN
+// input, or an infinite multiplier meeting a zero) take a path that writes the
+// NaN code explicitly.
 template <bool kHi>
 __device__ __forceinline__ uint32_t cvt_pair_e4m3(float a, float b, uint32_t old) {
   const float ca = fminf(fmaxf(a, -448.f), 448.f);
   const float cb = fminf(fmaxf(b, -448.f), 448.f);
-  uint32_t packed = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ca, cb, (int)old, kHi);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ca, cb, (int)old, kHi);
+}
+
+template <bool kHi>
+__device__ __forceinline__ uint32_t cvt_pair_e4m3_nan(float a, float b, uint32_t old) {
+  uint32_t packed = cvt_pair_e4m3<kHi>(a, b, old);
   const uint32_t sh = kHi ? 16u : 0u;
   if (a != a) packed = (packed & ~(0xffu << sh)) | (0x7fu << sh);
   if (b != b) packed = (packed & ~(0xff00u << sh)) | (0x7f00u << sh);
@@ -159,21 +166,33 @@ __device__ __forceinline__ uint32_t cvt_pair_e4m3(float a, float b, uint32_t old
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// Non-zero iff one of the 8 BF16 values is a NaN ((h & 0x7fff) > 0x7f80 per
+// half-word, evaluated on both halves of each word at once).
+__device__ __forceinline__ uint32_t bf16x8_nan(u32x4 x) {
+  const uint32_t m = 0x7fff7fffu, k = 0x007f007fu;
+  return (((x.x & m) + k) | ((x.y & m) + k) | ((x.z & m) + k) | ((x.w & m) + k)) & 0x80008000u;
+}
+
 // Quantise 8 BF16 values (one 16-byte vector) with multiplier inv into 8 FP8
 // bytes; inv == 0 yields +0 codes as in scatter_kv_kernel.cu:205-206.
 __device__ __forceinline__ u32x2 quantise8(u32x4 x, float inv) {
-  u32x2 out;
-  if (inv > 0.f) {
-    uint32_t w0 = cvt_pair_e4m3<false>(bf16_lo(x.x) * inv, bf16_hi(x.x) * inv, 0u);
-    w0 = cvt_pair_e4m3<true>(bf16_lo(x.y) * inv, bf16_hi(x.y) * inv, w0);
-    uint32_t w1 = cvt_pair_e4m3<false>(bf16_lo(x.z) * inv, bf16_hi(x.z) * inv, 0u);
-    w1 = cvt_pair_e4m3<true>(bf16_lo(x.w) * inv, bf16_hi(x.w) * inv, w1);
+  u32x2 out{0u, 0u};
+  if (!(inv > 0.f)) return out;
+  if (__builtin_expect(bf16x8_nan(x) != 0u || !(inv <= 3.402823466e38f), 0)) {
+    uint32_t w0 = cvt_pair_e4m3_nan<false>(bf16_lo(x.x) * inv, bf16_hi(x.x) * inv, 0u);
+    w0 = cvt_pair_e4m3_nan<true>(bf16_lo(x.y) * inv, bf16_hi(x.y) * inv, w0);
+    uint32_t w1 = cvt_pair_e4m3_nan<false>(bf16_lo(x.z) * inv, bf16_hi(x.z) * inv, 0u);
+    w1 = cvt_pair_e4m3_nan<true>(bf16_lo(x.w) * inv, bf16_hi(x.w) * inv, w1);
     out.x = w0;
     out.y = w1;
-  } else {
-    out.x = 0u;
-    out.y = 0u;
+    return out;
   }
+  uint32_t w0 = cvt_pair_e4m3<false>(bf16_lo(x.x) * inv, bf16_hi(x.x) * inv, 0u);
+  w0 = cvt_pair_e4m3<true>(bf16_lo(x.y) * inv, bf16_hi(x.y) * inv, w0);
+  uint32_t w1 = cvt_pair_e4m3<false>(bf16_lo(x.z) * inv, bf16_hi(x.z) * inv, 0u);
+  w1 = cvt_pair_e4m3<true>(bf16_lo(x.w) * inv, bf16_hi(x.w) * inv, w1);
+  out.x = w0;
+  out.y = w1;
   return out;
 }
 
@@ -189,6 +208,27 @@ __device__ __forceinline__ float amax8(u32x4 x) {
   return m;
 }
 
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, 0xf, 0xf, false));
+}
+
+// Max over aligned groups of kLanes lanes, result in every lane of the group.
+// Groups up to a 16-lane DPP row use DPP lane swaps (quad_perm [1,0,3,2],
+// quad_perm [2,3,0,1], row_half_mirror, row_mirror); wider groups add
+// cross-row shuffles. fmaxf keeps the non-NaN operand, as the reference's
+// warp reduction does.
+template <int kLanes>
+__device__ __forceinline__ float group_max(float m) {
+  if constexpr (kLanes >= 2) m = fmaxf(m, dpp_f<0xb1>(m));
+  if constexpr (kLanes >= 4) m = fmaxf(m, dpp_f<0x4e>(m));
+  if constexpr (kLanes >= 8) m = fmaxf(m, dpp_f<0x141>(m));
+  if constexpr (kLanes >= 16) m = fmaxf(m, dpp_f<0x140>(m));
+  if constexpr (kLanes >= 32) m = fmaxf(m, __shfl_xor(m, 16, kWave));
+  if constexpr (kLanes >= 64) m = fmaxf(m, __shfl_xor(m, 32, kWave));
+  return m;
+}
+
 // Fused BF16 -> FP8 handoff. A row is one (token, kv head) of one K or V
 // plane: head_dim BF16 values = kLanesPerRow lanes x 8 values. Rows are laid
 // out [layer][K|V][token][head] within a page on both sides, so a row's index
@@ -196,6 +236,27 @@ __device__ __forceinline__ float amax8(u32x4 x) {
 //   per-token-head: amax over the row, scale = amax/448 | 1, inv = 448/amax | 0
 //                   (scatter_kv_kernel.cu:166-190), scale written per row;
 //   table:          amax = table[(2*layer+kv)*heads + head], nothing written.
+template <int kUnroll, int kLanesPerRow, bool kTable>
+__device__ __forceinline__ void fp8_step(const u32x4& v, uint32_t row, uint32_t lane,
+                                         gdst_t dst, uint32_t dst_off, uint64_t scales,
+                                         uint32_t rows_per_plane, uint32_t kv_heads,
+                                         uint32_t rows_per_page,
+                                         const float* __restrict__ amax_table) {
+  float inv;
+  if constexpr (kTable) {
+    const uint32_t in_page = row % rows_per_page;
+    const float amax = amax_table[(in_page / rows_per_plane) * kv_heads + in_page % kv_heads];
+    inv = amax > 0.f ? 448.f / amax : 0.f;
+  } else {
+    const float m = group_max<kLanesPerRow>(amax8(v));
+    inv = m > 0.f ? 448.f / m : 0.f;
+    if (lane % kLanesPerRow == 0)
+      __builtin_nontemporal_store(m > 0.f ? m / 448.f : 1.f,
+                                  reinterpret_cast<PBE_GLOBAL float*>(scales) + row);
+  }
+  st8(dst, dst_off, quantise8(v, inv));
+}
+
 template <int kUnroll, int kLanesPerRow, bool kTable>
 __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_fp8_kernel(
     const DevRun* __restrict__ runs, uint32_t n_runs, uint32_t total_slices,
@@ -212,41 +273,34 @@ __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_fp8_kernel(
   uint32_t r = find_run(runs, 0, n_runs, s_begin, lane);
   for (uint32_t s = s_begin; s < s_end; ++s) {
     if (r + 1 < n_runs && runs[r + 1].slice_begin <= s) r = find_run(runs, r + 1, n_runs, s, lane);
+    r = __builtin_amdgcn_readfirstlane(r);
     const DevRun& run = runs[r];
     const uint64_t rel = (uint64_t)(s - run.slice_begin) * kSlice;
-    const uint64_t run_bytes = (uint64_t)run.pages * page_bytes;
-    const uint64_t nbytes = run_bytes - rel;
+    const uint64_t nbytes = (uint64_t)run.pages * page_bytes - rel;
     gsrc_t src = reinterpret_cast<gsrc_t>(run.src + rel);
     gdst_t dst = reinterpret_cast<gdst_t>(run.dst + rel / 2);
-    const uint32_t row0 = (uint32_t)(rel / kRowBytes);  // row index inside the run
-    u32x4 v[kUnroll];
+    const uint64_t scales = run.aux;
+    const uint32_t row0 = (uint32_t)(rel / kRowBytes) + lane / kLanesPerRow;  // row in the run
+    if (nbytes >= kSlice) {
+      u32x4 v[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const uint32_t off = (u * kWave + lane) * 16u;
-      if (off < nbytes) v[u] = ld16(src, off);
-      else v[u] = u32x4{0u, 0u, 0u, 0u};
-    }
+      for (int u = 0; u < kUnroll; ++u) v[u] = ld16(src, (u * kWave + lane) * 16u);
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const uint32_t off = (u * kWave + lane) * 16u;
-      const uint32_t row = row0 + u * kRowsPerStep + lane / kLanesPerRow;
-      float inv;
-      if constexpr (kTable) {
-        const uint32_t in_page = row % rows_per_page;
-        const uint32_t plane = in_page / rows_per_plane;
-        const float amax = amax_table[plane * kv_heads + in_page % kv_heads];
-        inv = amax > 0.f ? 448.f / amax : 0.f;
-      } else {
-        float m = amax8(v[u]);
-#pragma unroll
-        for (int w = kLanesPerRow / 2; w >= 1; w /= 2) m = fmaxf(m, __shfl_xor(m, w, kWave));
-        inv = m > 0.f ? 448.f / m : 0.f;
-        if (lane % kLanesPerRow == 0 && off < nbytes) {
-          const float scale = m > 0.f ? m / 448.f : 1.f;
-          __builtin_nontemporal_store(scale, reinterpret_cast<PBE_GLOBAL float*>(run.aux) + row);
-        }
+      for (int u = 0; u < kUnroll; ++u)
+        fp8_step<kUnroll, kLanesPerRow, kTable>(v[u], row0 + u * kRowsPerStep, lane, dst,
+                                                (u * kWave + lane) * 8u, scales, rows_per_plane,
+                                                kv_heads, rows_per_page, amax_table);
+    } else {
+      // Last, partial slice of a run: whole rows only (slices are multiples
+      // of the row size), one 1 KiB step at a time.
+      for (uint32_t u = 0; u * kWave * 16u < nbytes; ++u) {
+        const uint32_t off = (u * kWave + lane) * 16u;
+        const u32x4 v = off < nbytes ? ld16(src, off) : u32x4{0u, 0u, 0u, 0u};
+        if (off < nbytes)
+          fp8_step<kUnroll, kLanesPerRow, kTable>(v, row0 + u * kRowsPerStep, lane, dst, off / 2,
+                                                  scales, rows_per_plane, kv_heads,
+                                                  rows_per_page, amax_table);
       }
-      if (off < nbytes) st8(dst, off / 2, quantise8(v[u], inv));
     }
   }
 }
@@ -275,7 +329,8 @@ __global__ __launch_bounds__(kThreadsPerBlock) void copy_ops_kernel(
 }  // namespace
 
 uint32_t slice_bytes(KernelKind kind, const CopyConfig& cfg) {
-  return kind == KernelKind::kCopy ? kWave * 16u * (uint32_t)cfg.unroll : kWave * 16u * kFp8Unroll;
+  (void)kind;
+  return kWave * 16u * (uint32_t)cfg.unroll;
 }
 
 namespace {
@@ -331,27 +386,32 @@ hipError_t launch_copy_runs(const DevRun* runs, uint32_t n_runs, uint32_t total_
   return hipGetLastError();
 }
 
-hipError_t launch_copy_runs_fp8(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
-                                uint64_t page_bytes, uint32_t lanes_per_row,
-                                uint32_t rows_per_plane, uint32_t kv_heads,
-                                uint32_t rows_per_page, bool table, const float* amax_table,
-                                const LaunchShape& shape, hipStream_t stream) {
-  const uint32_t waves = (total_slices + shape.slices_per_wave - 1) / shape.slices_per_wave;
-  const uint32_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
-#define PBE_FP8_CASE(L)                                                                     \
-  case L:                                                                                   \
-    if (table)                                                                              \
-      hipLaunchKernelGGL((copy_runs_fp8_kernel<kFp8Unroll, L, true>), dim3(blocks),         \
-                         dim3(kThreadsPerBlock), 0, stream, runs, n_runs, total_slices,     \
-                         shape.slices_per_wave, page_bytes, rows_per_plane, kv_heads,       \
-                         rows_per_page, amax_table);                                        \
-    else                                                                                    \
-      hipLaunchKernelGGL((copy_runs_fp8_kernel<kFp8Unroll, L, false>), dim3(blocks),        \
-                         dim3(kThreadsPerBlock), 0, stream, runs, n_runs, total_slices,     \
-                         shape.slices_per_wave, page_bytes, rows_per_plane, kv_heads,       \
-                         rows_per_page, amax_table);                                        \
-    break;
-  switch (lanes_per_row) {
+namespace {
+template <int U, int L>
+void launch_fp8(bool table, uint32_t blocks, hipStream_t stream, const DevRun* runs,
+                uint32_t n_runs, uint32_t total_slices, uint32_t spw, uint64_t page_bytes,
+                uint32_t rows_per_plane, uint32_t kv_heads, uint32_t rows_per_page,
+                const float* amax_table) {
+  if (table)
+    hipLaunchKernelGGL((copy_runs_fp8_kernel<U, L, true>), dim3(blocks), dim3(kThreadsPerBlock), 0,
+                       stream, runs, n_runs, total_slices, spw, page_bytes, rows_per_plane,
+                       kv_heads, rows_per_page, amax_table);
+  else
+    hipLaunchKernelGGL((copy_runs_fp8_kernel<U, L, false>), dim3(blocks), dim3(kThreadsPerBlock), 0,
+                       stream, runs, n_runs, total_slices, spw, page_bytes, rows_per_plane,
+                       kv_heads, rows_per_page, amax_table);
+}
+template <int U>
+bool launch_fp8_lanes(uint32_t lanes, bool table, uint32_t blocks, hipStream_t stream,
+                      const DevRun* runs, uint32_t n_runs, uint32_t total_slices, uint32_t spw,
+                      uint64_t page_bytes, uint32_t rows_per_plane, uint32_t kv_heads,
+                      uint32_t rows_per_page, const float* amax_table) {
+#define PBE_FP8_CASE(L)                                                                       \
+  case L:                                                                                     \
+    launch_fp8<U, L>(table, blocks, stream, runs, n_runs, total_slices, spw, page_bytes,      \
+                     rows_per_plane, kv_heads, rows_per_page, amax_table);                    \
+    return true;
+  switch (lanes) {
     PBE_FP8_CASE(1)
     PBE_FP8_CASE(2)
     PBE_FP8_CASE(4)
@@ -360,9 +420,40 @@ hipError_t launch_copy_runs_fp8(const DevRun* runs, uint32_t n_runs, uint32_t to
     PBE_FP8_CASE(32)
     PBE_FP8_CASE(64)
     default:
-      return hipErrorInvalidValue;
+      return false;
   }
 #undef PBE_FP8_CASE
+}
+}  // namespace
+
+hipError_t launch_copy_runs_fp8(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
+                                uint64_t page_bytes, uint32_t lanes_per_row,
+                                uint32_t rows_per_plane, uint32_t kv_heads,
+                                uint32_t rows_per_page, bool table, const float* amax_table,
+                                const LaunchShape& shape, hipStream_t stream) {
+  const uint32_t waves = (total_slices + shape.slices_per_wave - 1) / shape.slices_per_wave;
+  const uint32_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
+  bool ok = false;
+  switch (shape.copy.unroll) {
+    case 2:
+      ok = launch_fp8_lanes<2>(lanes_per_row, table, blocks, stream, runs, n_runs, total_slices,
+                               shape.slices_per_wave, page_bytes, rows_per_plane, kv_heads,
+                               rows_per_page, amax_table);
+      break;
+    case 4:
+      ok = launch_fp8_lanes<4>(lanes_per_row, table, blocks, stream, runs, n_runs, total_slices,
+                               shape.slices_per_wave, page_bytes, rows_per_plane, kv_heads,
+                               rows_per_page, amax_table);
+      break;
+    case 8:
+      ok = launch_fp8_lanes<8>(lanes_per_row, table, blocks, stream, runs, n_runs, total_slices,
+                               shape.slices_per_wave, page_bytes, rows_per_plane, kv_heads,
+                               rows_per_page, amax_table);
+      break;
+    default:
+      break;
+  }
+  if (!ok) return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
