@@ -117,11 +117,48 @@ bool spans_disjoint(std::vector<std::pair<uint64_t, uint64_t>> dst,
 struct Range {
   uint64_t begin, end;
 };
+
+// Segments of arenas this library created or imported over IPC, per device.
+// IPC mappings are device memory but need not be visible to the runtime's
+// allocation-range queries, so they are recognised here first.
+struct ArenaRegistry {
+  std::mutex mu;
+  struct Entry {
+    uint64_t begin, end;
+    int device;
+  };
+  std::vector<Entry> entries;
+  void add(const void* p, uint64_t bytes, int device) {
+    std::lock_guard<std::mutex> lock(mu);
+    entries.push_back({reinterpret_cast<uint64_t>(p), reinterpret_cast<uint64_t>(p) + bytes, device});
+  }
+  void remove(const void* p) {
+    std::lock_guard<std::mutex> lock(mu);
+    const uint64_t b = reinterpret_cast<uint64_t>(p);
+    entries.erase(std::remove_if(entries.begin(), entries.end(),
+                                 [b](const Entry& e) { return e.begin == b; }),
+                  entries.end());
+  }
+  bool contains(uint64_t p, uint64_t bytes, int device) { return device_of(p, bytes) == device; }
+  // Device of the registered segment holding [p, p+bytes), or -1.
+  int device_of(uint64_t p, uint64_t bytes) {
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Entry& e : entries)
+      if (p >= e.begin && bytes <= e.end - p && p < e.end) return e.device;
+    return -1;
+  }
+};
+ArenaRegistry& arena_registry() {
+  static ArenaRegistry r;
+  return r;
+}
+
 bool accessible(const void* ptr, uint64_t bytes, int device, std::vector<Range>* known) {
   const uint64_t p = reinterpret_cast<uint64_t>(ptr);
   if (!p || bytes > ~0ull - p) return false;
   for (const Range& r : *known)
     if (p >= r.begin && p + bytes <= r.end) return true;
+  if (arena_registry().contains(p, bytes, device)) return true;
   hipDeviceptr_t base = nullptr;
   size_t size = 0;
   if (hipMemGetAddressRange(&base, &size, const_cast<void*>(ptr)) != hipSuccess || !base) {
@@ -259,6 +296,8 @@ int pbe_arena_create(int device, uint64_t bytes, uint64_t segment_bytes, uint64_
       return hip_fail(e, "hipMalloc(arena segment)");
     }
   }
+  for (uint32_t i = 0; i < a->nseg; ++i)
+    arena_registry().add(a->base[i], std::min(segment_bytes, bytes - (uint64_t)i * segment_bytes), device);
   if (pbe_device_uuid(device, a->uuid) != PBE_OK) std::memset(a->uuid, 0, 16);
   *out = a;
   return PBE_OK;
@@ -317,6 +356,9 @@ int pbe_arena_import(const pbe_arena_ipc* ipc, int device, pbe_arena** out) {
       return hip_fail(e, "hipIpcOpenMemHandle(arena segment)");
     }
   }
+  for (uint32_t i = 0; i < a->nseg; ++i)
+    arena_registry().add(a->base[i],
+                         std::min(a->segment_bytes, a->bytes - (uint64_t)i * a->segment_bytes), device);
   *out = a;
   return PBE_OK;
 }
@@ -339,6 +381,7 @@ int pbe_arena_destroy(pbe_arena* a) {
   int rc = PBE_OK;
   for (uint32_t i = 0; i < a->nseg; ++i) {
     if (!a->base[i]) continue;
+    arena_registry().remove(a->base[i]);
     const hipError_t e = a->owner ? hipFree(a->base[i]) : hipIpcCloseMemHandle(a->base[i]);
     if (e != hipSuccess) rc = hip_fail(e, a->owner ? "hipFree(arena)" : "hipIpcCloseMemHandle");
   }
@@ -803,14 +846,20 @@ int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream
         return fail(PBE_ERR_INVALID, "op %lld: endpoint is not device or pinned memory",
                     (long long)i);
   }
+  // Split large ops so that every wave moves at most kOpPieceBytes.
+  std::vector<pbe::DevOp> pieces;
+  for (int64_t i = 0; i < n_ops; ++i)
+    for (uint64_t off = 0; off < ops[i].bytes; off += pbe::kOpPieceBytes)
+      pieces.push_back({ops[i].src + off, ops[i].dst + off,
+                        std::min<uint64_t>(pbe::kOpPieceBytes, ops[i].bytes - off)});
+  if (pieces.size() > 0xffffffffull) return fail(PBE_ERR_INVALID, "op list too large");
   Staging& st = staging_for(device);
   std::lock_guard<std::mutex> lock(st.mu);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   void* dev = nullptr;
-  static_assert(sizeof(pbe_copy_op) == sizeof(pbe::DevOp), "op layout");
-  int rc = stage(st, ops, (size_t)n_ops * sizeof(pbe_copy_op), s, &dev);
+  int rc = stage(st, pieces.data(), pieces.size() * sizeof(pbe::DevOp), s, &dev);
   if (rc != PBE_OK) return rc;
-  PBE_HIP(pbe::launch_copy_ops(static_cast<const pbe::DevOp*>(dev), (uint32_t)n_ops, s));
+  PBE_HIP(pbe::launch_copy_ops(static_cast<const pbe::DevOp*>(dev), (uint32_t)pieces.size(), s));
   return stage_done(st, s);
 }
 
@@ -851,6 +900,12 @@ int pbe_pointer_kind(const void* ptr, uint64_t bytes, int* kind, int* device_out
   *kind = PBE_PTR_UNKNOWN;
   if (device_out) *device_out = -1;
   if (!ptr) return PBE_OK;
+  const int arena_device = arena_registry().device_of(reinterpret_cast<uint64_t>(ptr), bytes);
+  if (arena_device >= 0) {
+    *kind = PBE_PTR_DEVICE;
+    if (device_out) *device_out = arena_device;
+    return PBE_OK;
+  }
   hipDeviceptr_t base = nullptr;
   size_t size = 0;
   if (hipMemGetAddressRange(&base, &size, const_cast<void*>(ptr)) != hipSuccess || !base) {

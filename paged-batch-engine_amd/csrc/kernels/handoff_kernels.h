@@ -20,6 +20,9 @@ struct DevRun {
 };
 static_assert(sizeof(DevRun) == 32, "device run entry is 32 bytes");
 
+// Ops larger than this are split into pieces before upload.
+constexpr uint64_t kOpPieceBytes = 16384;
+
 struct DevOp {
   uint64_t src;
   uint64_t dst;

@@ -305,22 +305,36 @@ __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_fp8_kernel(
   }
 }
 
-// Generic op-list copy: one wave per op slice. Ops whose addresses and size
-// are 16-byte multiples take the vector path; others fall back to bytes.
+// Generic op-list copy (ops are pre-split on the host into pieces of at most
+// kOpPieceBytes). One wave per piece, grid-stride over pieces. Pieces whose
+// addresses and size are 16-byte multiples move as 16-byte vectors, four in
+// flight per lane; others byte by byte.
 __global__ __launch_bounds__(kThreadsPerBlock) void copy_ops_kernel(
     const DevOp* __restrict__ ops, uint32_t n_ops) {
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t waves = gridDim.x * kWavesPerBlock;
   for (uint32_t i = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave; i < n_ops; i += waves) {
-    const DevOp op = ops[i];
-    const uint8_t* src = reinterpret_cast<const uint8_t*>(op.src);
-    uint8_t* dst = reinterpret_cast<uint8_t*>(op.dst);
+    const DevOp op = ops[__builtin_amdgcn_readfirstlane(i)];
     if (((op.src | op.dst | op.bytes) & 15u) == 0) {
-      for (uint64_t off = (uint64_t)lane * 16u; off < op.bytes; off += kWave * 16u) {
-        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + off));
-        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst + off));
+      gsrc_t src = reinterpret_cast<gsrc_t>(op.src);
+      gdst_t dst = reinterpret_cast<gdst_t>(op.dst);
+      const uint32_t bytes = (uint32_t)op.bytes;
+      for (uint32_t base = 0; base < bytes; base += 4u * kWave * 16u) {
+        u32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t off = base + (u * kWave + lane) * 16u;
+          if (off < bytes) v[u] = ld16(src, off);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t off = base + (u * kWave + lane) * 16u;
+          if (off < bytes) st16(dst, off, v[u]);
+        }
       }
     } else {
+      const uint8_t* src = reinterpret_cast<const uint8_t*>(op.src);
+      uint8_t* dst = reinterpret_cast<uint8_t*>(op.dst);
       for (uint64_t off = lane; off < op.bytes; off += kWave) dst[off] = src[off];
     }
   }
@@ -458,9 +472,8 @@ hipError_t launch_copy_runs_fp8(const DevRun* runs, uint32_t n_runs, uint32_t to
 }
 
 hipError_t launch_copy_ops(const DevOp* ops, uint32_t n_ops, hipStream_t stream) {
-  const uint32_t waves = n_ops;
-  uint32_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
-  if (blocks > 65535u) blocks = 65535u;
+  uint32_t blocks = (n_ops + kWavesPerBlock - 1) / kWavesPerBlock;
+  if (blocks > 16384u) blocks = 16384u;
   hipLaunchKernelGGL(copy_ops_kernel, dim3(blocks), dim3(kThreadsPerBlock), 0, stream, ops,
                      n_ops);
   return hipGetLastError();

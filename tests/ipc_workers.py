@@ -1,0 +1,158 @@
+"""Processes of the cross-process handoff tests (spawned, one GPU).
+
+owner   creates the segmented arena, fills it with a canary byte, exports it
+prefill imports the arena, writes its prefix KV into its source pages, records
+        an interprocess "KV written" event and exports it
+decode  imports the arena and every prefill's event, makes its stream wait on
+        the events (no host sync), copies all requests' runs with one kernel,
+        records an interprocess "copy done" event, then checks the result
+Each role reports {"ok": bool, ...} on its pipe; every wait has a time limit.
+"""
+from __future__ import annotations
+
+import sys
+import time
+import traceback
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent.parent
+CANARY = 0xA5
+TIMEOUT = 90.0
+
+
+def _setup():
+    for p in (str(ROOT), str(ROOT / "paged-batch-engine_amd")):
+        if p not in sys.path:
+            sys.path.insert(0, p)
+    import torch
+    import pbe_handoff as P
+    return torch, P
+
+
+def _recv(conn, what):
+    if not conn.poll(TIMEOUT):
+        raise TimeoutError(f"timed out waiting for {what}")
+    return conn.recv()
+
+
+def _addr(view, offset):
+    seg = offset // view.segment_bytes
+    return view.base[seg] + offset % view.segment_bytes
+
+
+def owner(conn, arena_bytes, segment_bytes, epoch):
+    try:
+        torch, P = _setup()
+        arena = P.Arena.create(arena_bytes, segment_bytes, epoch)
+        view = arena.view()
+        fill = torch.full((segment_bytes,), CANARY, dtype=torch.uint8, device="cuda")
+        ops = []
+        for i in range(view.nseg):
+            n = min(segment_bytes, arena_bytes - i * segment_bytes)
+            ops.append((fill.data_ptr(), view.base[i], n))
+        P.copy_ops(ops, 0, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        conn.send({"ipc": bytes(arena.export())})
+        msg = _recv(conn, "shutdown")
+        assert msg == "shutdown"
+        arena.close()
+        conn.send({"ok": True})
+    except Exception:
+        conn.send({"ok": False, "error": traceback.format_exc()})
+
+
+def prefill(conn, kv_shape, src_ids, seed):
+    """Writes seeded KV into its pages, then hands over an IPC event."""
+    try:
+        torch, P = _setup()
+        ipc_bytes = _recv(conn, "arena")
+        ipc = P.ArenaIpc.from_buffer_copy(ipc_bytes)
+        arena = P.Arena.from_ipc(ipc)
+        view = arena.view()
+        kv = P.KvShape(*kv_shape)
+        half, page = kv.half_bytes(), kv.page_bytes()
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        data = torch.randn(len(src_ids) * page // 2, generator=g, device="cuda").to(torch.bfloat16)
+        base = data.data_ptr()
+        stream = torch.cuda.Stream()
+        ops = [(base + i * page, _addr(view, int(s) * half), page) for i, s in enumerate(src_ids)]
+        written = P.Event.create(0, interprocess=True)
+        with torch.cuda.stream(stream):
+            P.copy_ops(ops, 0, stream.cuda_stream)
+            written.record(stream.cuda_stream)
+        conn.send({"event": written.export()})
+        done_handle = _recv(conn, "copy-done event")
+        done = P.Event.from_ipc(done_handle)
+        done.synchronize()  # the decode side finished reading: pages may retire now
+        done.close()
+        torch.cuda.synchronize()
+        written.close()
+        arena.close()
+        conn.send({"ok": True})
+    except Exception:
+        conn.send({"ok": False, "error": traceback.format_exc()})
+
+
+def decode(conn, kv_shape, requests, n_prefill):
+    """requests: list of (src_ids, dst_ids). Copies every request after its
+    producer's event, in one launch, then verifies the whole arena."""
+    try:
+        import numpy as np
+        torch, P = _setup()
+        ipc = P.ArenaIpc.from_buffer_copy(_recv(conn, "arena"))
+        arena = P.Arena.from_ipc(ipc)
+        view = arena.view()
+        kv = P.KvShape(*kv_shape)
+        half, page = kv.half_bytes(), kv.page_bytes()
+        events = [P.Event.from_ipc(_recv(conn, f"event {i}")) for i in range(n_prefill)]
+        stream = torch.cuda.Stream()
+        sp = stream.cuda_stream
+        src = np.concatenate([np.asarray(r[0], np.int32) for r in requests])
+        dst = np.concatenate([np.asarray(r[1], np.int32) for r in requests])
+        runs = P.build_runs(src, dst, kv, 2, view.segment_bytes if view.nseg > 1 else 0)
+        rl = P.RunList.bf16(view, view, runs, kv)
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        for ev in events:
+            ev.wait(sp)                      # stream waits on the producer, host does not
+        t0.record(stream)
+        rl.copy(sp)
+        t1.record(stream)
+        done = P.Event.create(0, interprocess=True)
+        done.record(sp)
+        conn.send({"done_event": done.export()})
+        stream.synchronize()
+        kernel_ms = t0.elapsed_time(t1)
+        # read the whole arena back and check: dst pages == src pages, all
+        # other pages except sources still hold the canary
+        host = np.empty(ipc.bytes, np.uint8)
+        off = 0
+        for i in range(view.nseg):
+            n = min(view.segment_bytes, ipc.bytes - off)
+            buf = torch.empty(n, dtype=torch.uint8, device="cuda")
+            P.copy_ops([(view.base[i], buf.data_ptr(), n)], 0, sp)
+            stream.synchronize()
+            host[off:off + n] = buf.cpu().numpy()
+            off += n
+        pages = host.reshape(-1, page)
+        sp_idx = src // (2 * kv.layers)
+        dp_idx = dst // (2 * kv.layers)
+        mism = int(np.count_nonzero((pages[dp_idx] != pages[sp_idx]).any(axis=1)))
+        other = np.ones(len(pages), bool)
+        other[sp_idx] = False
+        other[dp_idx] = False
+        canary_bad = int(np.count_nonzero((pages[other] != CANARY).any(axis=1)))
+        src_canary = int(np.count_nonzero((pages[sp_idx] == CANARY).all(axis=1)))
+        rl.close()
+        for ev in events:
+            ev.close()
+        conn.send({"ok": mism == 0 and canary_bad == 0 and src_canary == 0,
+                   "mismatched_pages": mism, "canary_pages_changed": canary_bad,
+                   "source_pages_unwritten": src_canary, "kernel_ms": kernel_ms,
+                   "bytes": int(2 * len(src) * page), "runs": len(runs)})
+        _recv(conn, "exit")
+        done.close()
+        arena.close()
+    except Exception:
+        conn.send({"ok": False, "error": traceback.format_exc()})
