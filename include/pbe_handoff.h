@@ -117,6 +117,27 @@ int pbe_event_query(pbe_event* event);              /* PBE_OK or PBE_NOT_READY *
 int pbe_event_synchronize(pbe_event* event);
 int pbe_event_destroy(pbe_event* event);
 
+/* ---- IPC completion signals ------------------------------------------
+ * Cross-process ordering without host round trips. A signal is a 64-bit
+ * sequence word in its own small device allocation, exported with
+ * hipIpcGetMemHandle. set() is a stream-ordered write (hipStreamWriteValue64)
+ * that follows all earlier work on the stream; wait() makes a stream wait on
+ * the GPU (hipStreamWaitValue64, >=) until the word reaches a value. This is the
+ * completion protocol of the handoff: P sets "KV written" = n after its prefill
+ * kernels, D's stream waits for n before the copy and then sets "copy done" = n,
+ * which P waits for before retiring its pages (pattern of
+ * demo/cuda_ipc_event_probe.cu:24-27,70-75 and data/ipc_pool.h:24-26). On
+ * ROCm 7.2 hipEventRecord rejects hipEventInterprocess events, so interprocess
+ * pbe_event objects cannot be recorded there; signals are the portable form. */
+typedef struct pbe_signal pbe_signal;
+int pbe_signal_create(int device, pbe_signal** out); /* starts at 0 */
+int pbe_signal_export(const pbe_signal* signal, uint8_t out[PBE_IPC_HANDLE_BYTES]);
+int pbe_signal_import(const uint8_t handle[PBE_IPC_HANDLE_BYTES], int device, pbe_signal** out);
+int pbe_signal_set(pbe_signal* signal, uint64_t value, void* stream);
+int pbe_signal_wait(pbe_signal* signal, uint64_t value, void* stream);
+int pbe_signal_read(pbe_signal* signal, uint64_t* value); /* current value, host side */
+int pbe_signal_destroy(pbe_signal* signal);
+
 /* ---- host-side plan ----------------------------------------------------
  * Source id checks of copy_shared_kv (split_pd_engine.cpp:70-77): id >= 0,
  * id % (2*layers) == 0 and (id + 2*layers)*half <= arena bytes. On failure

@@ -240,6 +240,12 @@ struct pbe_event {
   hipEvent_t event = nullptr;
 };
 
+struct pbe_signal {
+  int device = 0;
+  bool imported = false;
+  void* word = nullptr;  // 8-byte sequence value at the start of a 4 KiB allocation
+};
+
 struct pbe_runlist {
   int device = 0;
   bool fp8 = false;
@@ -476,6 +482,86 @@ int pbe_event_destroy(pbe_event* ev) {
   const hipError_t e = hipEventDestroy(ev->event);
   delete ev;
   if (e != hipSuccess) return hip_fail(e, "hipEventDestroy");
+  return PBE_OK;
+}
+
+// ---------------------------------------------------------------- signals
+int pbe_signal_create(int device, pbe_signal** out) {
+  if (!out) return fail(PBE_ERR_INVALID, "null output");
+  *out = nullptr;
+  PBE_DEVICE_SCOPE(device);
+  pbe_signal* sg = new (std::nothrow) pbe_signal;
+  if (!sg) return fail(PBE_ERR_NOMEM, "signal object");
+  sg->device = device;
+  hipError_t e = hipMalloc(&sg->word, 4096);
+  if (e == hipSuccess) e = hipMemset(sg->word, 0, 4096);
+  if (e != hipSuccess) {
+    if (sg->word) (void)hipFree(sg->word);
+    delete sg;
+    return hip_fail(e, "signal allocation");
+  }
+  *out = sg;
+  return PBE_OK;
+}
+
+int pbe_signal_export(const pbe_signal* sg, uint8_t out[PBE_IPC_HANDLE_BYTES]) {
+  if (!sg || !out) return fail(PBE_ERR_INVALID, "null argument");
+  if (sg->imported) return fail(PBE_ERR_INVALID, "only the creator exports a signal");
+  PBE_DEVICE_SCOPE(sg->device);
+  hipIpcMemHandle_t h;
+  PBE_HIP(hipIpcGetMemHandle(&h, sg->word));
+  std::memset(out, 0, PBE_IPC_HANDLE_BYTES);
+  std::memcpy(out, &h, sizeof(h));
+  return PBE_OK;
+}
+
+int pbe_signal_import(const uint8_t handle[PBE_IPC_HANDLE_BYTES], int device, pbe_signal** out) {
+  if (!handle || !out) return fail(PBE_ERR_INVALID, "null argument");
+  *out = nullptr;
+  PBE_DEVICE_SCOPE(device);
+  pbe_signal* sg = new (std::nothrow) pbe_signal;
+  if (!sg) return fail(PBE_ERR_NOMEM, "signal object");
+  sg->device = device;
+  sg->imported = true;
+  hipIpcMemHandle_t h;
+  std::memcpy(&h, handle, sizeof(h));
+  const hipError_t e = hipIpcOpenMemHandle(&sg->word, h, hipIpcMemLazyEnablePeerAccess);
+  if (e != hipSuccess) {
+    delete sg;
+    return hip_fail(e, "hipIpcOpenMemHandle(signal)");
+  }
+  *out = sg;
+  return PBE_OK;
+}
+
+int pbe_signal_set(pbe_signal* sg, uint64_t value, void* stream) {
+  if (!sg) return fail(PBE_ERR_INVALID, "null signal");
+  PBE_DEVICE_SCOPE(sg->device);
+  PBE_HIP(hipStreamWriteValue64(static_cast<hipStream_t>(stream), sg->word, value, 0));
+  return PBE_OK;
+}
+
+int pbe_signal_wait(pbe_signal* sg, uint64_t value, void* stream) {
+  if (!sg) return fail(PBE_ERR_INVALID, "null signal");
+  PBE_DEVICE_SCOPE(sg->device);
+  PBE_HIP(hipStreamWaitValue64(static_cast<hipStream_t>(stream), sg->word, value,
+                               hipStreamWaitValueGte, ~0ull));
+  return PBE_OK;
+}
+
+int pbe_signal_read(pbe_signal* sg, uint64_t* value) {
+  if (!sg || !value) return fail(PBE_ERR_INVALID, "null argument");
+  PBE_DEVICE_SCOPE(sg->device);
+  PBE_HIP(hipMemcpy(value, sg->word, sizeof(uint64_t), hipMemcpyDeviceToHost));
+  return PBE_OK;
+}
+
+int pbe_signal_destroy(pbe_signal* sg) {
+  if (!sg) return PBE_OK;
+  PBE_DEVICE_SCOPE(sg->device);
+  const hipError_t e = sg->imported ? hipIpcCloseMemHandle(sg->word) : hipFree(sg->word);
+  delete sg;
+  if (e != hipSuccess) return hip_fail(e, "signal release");
   return PBE_OK;
 }
 

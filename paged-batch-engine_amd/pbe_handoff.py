@@ -81,6 +81,13 @@ _SIGNATURES = [
     ("pbe_event_query", C.c_int, [_P]),
     ("pbe_event_synchronize", C.c_int, [_P]),
     ("pbe_event_destroy", C.c_int, [_P]),
+    ("pbe_signal_create", C.c_int, [C.c_int, C.POINTER(_P)]),
+    ("pbe_signal_export", C.c_int, [_P, C.POINTER(C.c_uint8)]),
+    ("pbe_signal_import", C.c_int, [C.POINTER(C.c_uint8), C.c_int, C.POINTER(_P)]),
+    ("pbe_signal_set", C.c_int, [_P, C.c_uint64, _P]),
+    ("pbe_signal_wait", C.c_int, [_P, C.c_uint64, _P]),
+    ("pbe_signal_read", C.c_int, [_P, C.POINTER(C.c_uint64)]),
+    ("pbe_signal_destroy", C.c_int, [_P]),
     ("pbe_validate_ids", C.c_int, [_P, C.c_int64, C.POINTER(KvShape), C.c_uint32, C.c_uint64,
                                    C.POINTER(C.c_int64)]),
     ("pbe_build_runs", C.c_int, [_P, _P, C.c_int64, C.POINTER(KvShape), C.c_uint32, C.c_uint64,
@@ -334,6 +341,47 @@ class Event:
     def close(self) -> None:
         if self.handle:
             check(lib().pbe_event_destroy(self.handle))
+            self.handle = 0
+
+
+class Signal:
+    """64-bit sequence word shared across processes (pbe_signal_*)."""
+
+    def __init__(self, handle: int):
+        self.handle = handle
+
+    @classmethod
+    def create(cls, device: int = 0):
+        h = C.c_void_p()
+        check(lib().pbe_signal_create(device, C.byref(h)))
+        return cls(h.value)
+
+    @classmethod
+    def from_ipc(cls, handle_bytes: bytes, device: int = 0):
+        buf = (C.c_uint8 * PBE_IPC_HANDLE_BYTES).from_buffer_copy(handle_bytes)
+        h = C.c_void_p()
+        check(lib().pbe_signal_import(buf, device, C.byref(h)))
+        return cls(h.value)
+
+    def export(self) -> bytes:
+        buf = (C.c_uint8 * PBE_IPC_HANDLE_BYTES)()
+        check(lib().pbe_signal_export(self.handle, buf))
+        return bytes(buf)
+
+    def set(self, value: int, stream: int = 0) -> None:
+        check(lib().pbe_signal_set(self.handle, value, stream or None))
+
+    def wait(self, value: int, stream: int = 0) -> None:
+        check(lib().pbe_signal_wait(self.handle, value, stream or None))
+
+    def read(self) -> int:
+        v = C.c_uint64()
+        check(lib().pbe_signal_read(self.handle, C.byref(v)))
+        return v.value
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib().pbe_signal_destroy(self.handle))
             self.handle = 0
 
 

@@ -1,9 +1,9 @@
 """Cross-process handoff on one GPU: an owner process exports a segmented
 arena (hipIpcGetMemHandle per segment), prefill processes write their KV and
-export interprocess "KV written" events, and the decode process waits on those
-events in its stream, copies every request with one run-list kernel and
-exports a "copy done" event that the prefill processes wait on before
-retiring their pages. The decode side then checks the whole arena."""
+set IPC "KV written" signals, and the decode process's stream waits on those
+signals on the GPU, copies every request with one run-list kernel and sets a
+"copy done" signal that the prefill processes' streams wait on before retiring
+their pages. The decode side then checks the whole arena."""
 import multiprocessing as mp
 
 import pytest
@@ -85,6 +85,7 @@ def test_ipc_handoff_config5_two_prefills():
     say("ipc config5: owner + 2 prefills (32768 + 512 tokens) + decode, 3 segments")
     r = _run((g.layers, g.kv_heads, g.head_dim, g.page_tokens), w.arena_bytes, w.segment_bytes,
              [(q.src_ids, q.dst_ids) for q in w.requests])
-    print(f"[c5 cross-process] kernel {r['kernel_ms'] * 1e3:.1f} us, "
-          f"{r['bytes'] / (r['kernel_ms'] * 1e-3) / 1e9:.1f} GB/s, runs {r['runs']}", flush=True)
+    print(f"[c5 cross-process] first copy {r['kernel_ms'] * 1e3:.1f} us, repeat "
+          f"{r['repeat_ms'] * 1e3:.1f} us = {r['bytes'] / (r['repeat_ms'] * 1e-3) / 1e9:.1f} GB/s, "
+          f"runs {r['runs']}", flush=True)
     assert r["ok"], r
