@@ -48,8 +48,10 @@ HOST_SOURCES = [
 # Host C++ that reaches the GPU only through the C ABI (in the library, not in
 # the CPU-only unit-test binary).
 ABI_HOST_SOURCES = [
+    "csrc/base/shared_kv_arena.cpp",
     "csrc/cache/hip_transfer_backend.cpp",
     "csrc/serving/shared_kv_handoff.cpp",
+    "csrc/serving/decode_kv_reservation.cpp",
 ]
 # Sources that call HIP (compiled by hipcc).
 HIP_SOURCES = [
@@ -95,11 +97,12 @@ def build(jobs: int = 8) -> Path:
         [str(_obj(s, "host")) for s in HOST_SOURCES + ABI_HOST_SOURCES]
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs])
     os.replace(tmp, so)
-    # C++ tests: the CPU suite links the g++ objects only (no HIP runtime).
+    # C++ CPU tests link the library (its HIP runtime dependency loads without
+    # a GPU; the tests only use host paths and metadata-only page groups).
     cpu_objs = [str(_obj(s, "gcc")) for s in HOST_SOURCES]
-    for t in CPU_TESTS if cpu_objs else []:
-        _run(["g++", *CXX_FLAGS, *INCLUDES, f"-I{ROOT / 'tests' / 'cpp'}", str(ROOT / t), *cpu_objs,
-              "-o", str(LIB / "pbe_cpp_tests")])
+    for t in CPU_TESTS:
+        _run(["g++", *CXX_FLAGS, *INCLUDES, f"-I{ROOT / 'tests' / 'cpp'}", str(ROOT / t),
+              f"-L{LIB}", "-lpbe_handoff", "-Wl,-rpath,$ORIGIN", "-o", str(LIB / "pbe_cpp_tests")])
     # The scenario driver of oracle/ref_driver.cpp built against this API, so
     # tests can replay identical scenarios on it and on the reference build.
     _run(["g++", *CXX_FLAGS, "-shared", *INCLUDES, str(ROOT / "oracle" / "ref_driver.cpp"), *cpu_objs,

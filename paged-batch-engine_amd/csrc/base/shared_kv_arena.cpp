@@ -1,0 +1,343 @@
+// Page group over leased Chunks. Allocation, reservation, retire and collect
+// rules follow infMain/source/base/shared_kv_arena.cpp:53-229; completion
+// fences are C-ABI events recorded on the group's stream.
+#include "base/shared_kv_arena.h"
+
+#include <algorithm>
+#include <deque>
+#include <limits>
+#include <set>
+#include <stdexcept>
+#include <unordered_map>
+#include <vector>
+
+namespace base {
+
+// ------------------------------------------------------------ LocalChunkOwner
+
+void LocalChunkOwner::register_model(const std::string& model, uint64_t hard_limit) {
+  std::lock_guard<std::mutex> lock(mu_);
+  allocator_.register_model(model, hard_limit);
+}
+
+ChunkLease LocalChunkOwner::acquire(const std::string& model, const std::string& layout,
+                                    uint64_t bytes, uint64_t alignment) {
+  std::lock_guard<std::mutex> lock(mu_);
+  return allocator_.acquire(model, layout, bytes, alignment);
+}
+
+void LocalChunkOwner::release(const ChunkLease& lease) {
+  std::lock_guard<std::mutex> lock(mu_);
+  allocator_.release(lease);
+}
+
+uint64_t LocalChunkOwner::free_bytes() const {
+  std::lock_guard<std::mutex> lock(mu_);
+  return allocator_.free_bytes();
+}
+
+size_t LocalChunkOwner::lease_count() const {
+  std::lock_guard<std::mutex> lock(mu_);
+  return allocator_.lease_count();
+}
+
+// ------------------------------------------------------------ SharedKVArenaClient
+
+SharedKVArenaClient::SharedKVArenaClient(std::shared_ptr<ChunkOwner> owner,
+                                         const pbe_arena_view& view, std::string model,
+                                         uint64_t hard_limit_bytes, int device)
+    : owner_(std::move(owner)), view_(view), model_(std::move(model)),
+      hard_limit_(hard_limit_bytes), device_(device) {
+  if (!owner_ || model_.empty() || !hard_limit_ || view_.nseg == 0 || view_.nseg > PBE_MAX_SEGMENTS)
+    throw std::invalid_argument("invalid shared KV arena client");
+  if (view_.bytes != owner_->bytes())
+    throw std::runtime_error("shared KV mapping and owner arena sizes differ");
+}
+
+void* SharedKVArenaClient::data() const { return view_.nseg == 1 ? view_.base[0] : nullptr; }
+
+ChunkLease SharedKVArenaClient::acquire(const std::string& layout, uint64_t bytes,
+                                        uint64_t alignment) {
+  ChunkLease lease = owner_->acquire(model_, layout, bytes, alignment);
+  if (lease.epoch != owner_->epoch() || !lease.id || !lease.generation || lease.model != model_ ||
+      lease.layout != layout || lease.bytes != bytes || lease.offset % alignment ||
+      lease.offset > view_.bytes || lease.bytes > view_.bytes - lease.offset)
+    throw std::runtime_error("invalid owner chunk descriptor");
+  return lease;
+}
+
+void SharedKVArenaClient::release(const ChunkLease& lease) { owner_->release(lease); }
+
+// ------------------------------------------------------------ SharedKVPageGroup
+
+struct SharedKVPageGroup::Impl {
+  struct Chunk;
+  struct Page {
+    uint64_t offset = 0;
+    std::vector<char> active, reserved;  // per layer
+    int active_layers = 0;
+    bool retiring = false;
+    pbe_event* fence = nullptr;
+    Chunk* chunk = nullptr;
+  };
+  struct Chunk {
+    ChunkLease lease;
+    std::vector<Page> pages;  // fixed size: Page* stay valid
+    size_t free_pages = 0;
+  };
+
+  std::shared_ptr<SharedKVArenaClient> arena;
+  int layers = 0;
+  uint64_t half = 0, page = 0, chunk_bytes = 0;
+  void* stream = nullptr;
+  std::string layout;
+  std::unordered_map<uint64_t, std::unique_ptr<Chunk>> chunks;  // by lease id
+  std::unordered_map<int, Page*> pages;                         // by page id
+  std::set<int> free_ids;
+  std::deque<Page*> retiring;
+  std::vector<pbe_event*> spare_fences;
+  std::vector<std::deque<int>> pending;  // per layer: ids reserved by layer 0
+  uint64_t leased = 0;
+  bool failed = false;  // an unacknowledged release can never become reusable
+  mutable std::mutex mu;
+
+  int id_of(const Page& p) const { return static_cast<int>(p.offset / half); }
+
+  // True once the fence recorded at the page's last retire has passed.
+  bool fence_done(Page& p) {
+    if (!p.fence) return true;
+    const int rc = pbe_event_query(p.fence);
+    if (rc == PBE_NOT_READY) return false;
+    if (rc != PBE_OK) {
+      failed = true;
+      throw std::runtime_error(std::string("shared KV page fence failed: ") + pbe_last_error());
+    }
+    spare_fences.push_back(p.fence);
+    p.fence = nullptr;
+    return true;
+  }
+
+  void collect_locked() {
+    if (failed) throw std::runtime_error("shared KV page group failed; stop GPU domain");
+    // Fences are recorded on one stream in retire order: stop at the first
+    // that has not passed.
+    while (!retiring.empty()) {
+      Page* p = retiring.front();
+      if (!fence_done(*p)) break;
+      retiring.pop_front();
+      p->retiring = false;
+      free_ids.insert(id_of(*p));
+      Chunk* c = p->chunk;
+      if (++c->free_pages < c->pages.size()) continue;
+      try {
+        arena->release(c->lease);
+      } catch (...) {
+        failed = true;
+        throw;
+      }
+      for (const Page& q : c->pages) {
+        free_ids.erase(id_of(q));
+        pages.erase(id_of(q));
+      }
+      leased -= c->lease.bytes;
+      chunks.erase(c->lease.id);
+    }
+  }
+
+  int reserve(Page& p) {
+    const int id = id_of(p);
+    std::fill(p.active.begin(), p.active.end(), 1);
+    p.active_layers = layers;
+    --p.chunk->free_pages;
+    free_ids.erase(id);
+    for (int l = 1; l < layers; ++l) {
+      p.reserved[l] = 1;
+      pending[l].push_back(id);
+    }
+    return id;
+  }
+
+  void record_fence(Page& p) {
+    if (arena->device() < 0) return;  // metadata-only group: nothing runs on a GPU
+    pbe_event* ev = nullptr;
+    if (!spare_fences.empty()) {
+      ev = spare_fences.back();
+      spare_fences.pop_back();
+    } else if (pbe_event_create(arena->device(), 0, &ev) != PBE_OK) {
+      throw std::runtime_error(std::string("shared KV fence creation failed: ") + pbe_last_error());
+    }
+    if (pbe_event_record(ev, stream) != PBE_OK) {
+      pbe_event_destroy(ev);
+      throw std::runtime_error(std::string("shared KV fence record failed: ") + pbe_last_error());
+    }
+    p.fence = ev;
+  }
+};
+
+namespace {
+uint64_t round_up(uint64_t bytes, uint64_t alignment) {
+  if (bytes > std::numeric_limits<uint64_t>::max() - alignment)
+    throw std::invalid_argument("KV size overflow");
+  return (bytes + alignment - 1) / alignment * alignment;
+}
+}  // namespace
+
+SharedKVPageGroup::SharedKVPageGroup(std::shared_ptr<SharedKVArenaClient> arena, int layers,
+                                     uint64_t half_bytes, uint64_t target, void* stream)
+    : impl_(new Impl) {
+  if (!arena || layers <= 0 || !half_bytes || half_bytes % 256 || !target ||
+      half_bytes > std::numeric_limits<uint64_t>::max() / (2ull * layers))
+    throw std::invalid_argument("unsupported shared KV geometry/alignment");
+  impl_->arena = std::move(arena);
+  impl_->layers = layers;
+  impl_->pending.resize(layers);
+  impl_->half = half_bytes;
+  impl_->page = half_bytes * 2 * layers;
+  impl_->chunk_bytes = round_up(std::max(target, impl_->page), impl_->page);
+  impl_->stream = stream;
+  impl_->layout = "page-major-gqa-v1:" + std::to_string(layers) + ":" + std::to_string(half_bytes);
+  if (capacity() <= 0 || impl_->arena->bytes() / half_bytes > static_cast<uint64_t>(INT32_MAX))
+    throw std::invalid_argument("shared KV capacity exceeds block ID range or is zero");
+  if (impl_->arena->view().nseg > 1 && impl_->arena->view().segment_bytes % impl_->page)
+    throw std::invalid_argument("arena segments must hold whole pages");
+}
+
+SharedKVPageGroup::~SharedKVPageGroup() {
+  // A failed stream sync must quarantine the leases: never return their bytes.
+  if (impl_->arena->device() >= 0 &&
+      pbe_stream_synchronize(impl_->arena->device(), impl_->stream) != PBE_OK)
+    return;
+  for (auto& entry : impl_->chunks) {
+    for (auto& p : entry.second->pages)
+      if (p.fence) pbe_event_destroy(p.fence);
+    try {
+      impl_->arena->release(entry.second->lease);
+    } catch (...) {  // domain shutdown
+    }
+  }
+  for (pbe_event* ev : impl_->spare_fences) pbe_event_destroy(ev);
+}
+
+void SharedKVPageGroup::collect() {
+  std::lock_guard<std::mutex> lock(impl_->mu);
+  impl_->collect_locked();
+}
+
+int SharedKVPageGroup::allocate(int layer) {
+  std::lock_guard<std::mutex> lock(impl_->mu);
+  Impl& m = *impl_;
+  if (m.failed) throw std::runtime_error("shared KV page group failed; stop GPU domain");
+  if (layer < 0 || layer >= m.layers) throw std::invalid_argument("invalid layer");
+  if (layer > 0) {
+    auto& q = m.pending[layer];
+    if (q.empty()) throw std::logic_error("Allocate shared pages in layer order");
+    const int id = q.front();
+    q.pop_front();
+    m.pages.at(id)->reserved[layer] = 0;
+    return id;
+  }
+  m.collect_locked();
+  if (!m.free_ids.empty()) return m.reserve(*m.pages.at(*m.free_ids.begin()));
+  const uint64_t room = m.arena->hard_limit() - m.leased;
+  if (room < m.page) return -1;
+  const uint64_t want = room >= m.chunk_bytes ? m.chunk_bytes : m.page;
+  ChunkLease lease;
+  // Quota / fragmentation may still fit one page; other owner errors propagate.
+  try {
+    lease = m.arena->acquire(m.layout, want, m.page);
+  } catch (const ChunkAllocationError&) {
+    if (want == m.page) return -1;
+    try {
+      lease = m.arena->acquire(m.layout, m.page, m.page);
+    } catch (const ChunkAllocationError&) {
+      return -1;
+    }
+  }
+  auto chunk = std::make_unique<Impl::Chunk>();
+  chunk->lease = lease;
+  chunk->pages.resize(lease.bytes / m.page);
+  for (size_t i = 0; i < chunk->pages.size(); ++i) {
+    Impl::Page& p = chunk->pages[i];
+    p.offset = lease.offset + i * m.page;
+    p.active.assign(m.layers, 0);
+    p.reserved.assign(m.layers, 0);
+    p.chunk = chunk.get();
+    m.pages.emplace(m.id_of(p), &p);
+    m.free_ids.insert(m.id_of(p));
+  }
+  chunk->free_pages = chunk->pages.size();
+  const int id = m.reserve(chunk->pages.front());
+  m.leased += lease.bytes;
+  m.chunks.emplace(lease.id, std::move(chunk));
+  return id;
+}
+
+void SharedKVPageGroup::retire(int layer, int id) {
+  std::lock_guard<std::mutex> lock(impl_->mu);
+  Impl& m = *impl_;
+  if (m.failed) throw std::runtime_error("shared KV page group failed; stop GPU domain");
+  auto found = m.pages.find(id);
+  if (found == m.pages.end()) throw std::logic_error("page does not belong to current chunk generation");
+  Impl::Page& p = *found->second;
+  if (layer < 0 || layer >= m.layers) throw std::out_of_range("invalid layer");
+  if (!p.active[layer] || p.retiring || p.reserved[layer]) throw std::logic_error("double/stale page retire");
+  if (layer == 0) {
+    // Roll back reservations the later layers never consumed.
+    for (int l = 1; l < m.layers; ++l) {
+      if (!p.reserved[l]) continue;
+      auto& q = m.pending[l];
+      q.erase(std::remove(q.begin(), q.end(), id), q.end());
+      p.reserved[l] = 0;
+      p.active[l] = 0;
+      --p.active_layers;
+    }
+  }
+  p.active[layer] = 0;
+  if (--p.active_layers == 0) {
+    // A page is indivisible across layers: one fence after every layer's use.
+    m.record_fence(p);
+    p.retiring = true;
+    m.retiring.push_back(&p);
+    m.collect_locked();
+  }
+}
+
+int SharedKVPageGroup::free_blocks(int layer) const {
+  std::lock_guard<std::mutex> lock(impl_->mu);
+  uint64_t n = (impl_->arena->hard_limit() - impl_->leased) / impl_->page;
+  n += impl_->free_ids.size();
+  n += impl_->pending.at(layer).size();
+  return static_cast<int>(std::min<uint64_t>(INT32_MAX, n));
+}
+
+uint64_t SharedKVPageGroup::leased_bytes() const {
+  std::lock_guard<std::mutex> lock(impl_->mu);
+  return impl_->leased;
+}
+
+uint64_t SharedKVPageGroup::arena_bytes() const { return impl_->arena->bytes(); }
+uint64_t SharedKVPageGroup::arena_epoch() const { return impl_->arena->epoch(); }
+uint64_t SharedKVPageGroup::half_bytes() const { return impl_->half; }
+uint64_t SharedKVPageGroup::page_bytes() const { return impl_->page; }
+int SharedKVPageGroup::layers() const { return impl_->layers; }
+
+int SharedKVPageGroup::capacity() const {
+  return static_cast<int>(std::min<uint64_t>(INT32_MAX, impl_->arena->hard_limit() / impl_->page));
+}
+
+int SharedKVPageGroup::addressable_blocks() const {
+  // Each layer has its own base; the last V plane must stay inside the mapping.
+  return static_cast<int>(impl_->arena->bytes() / impl_->half - 2 * impl_->layers + 1);
+}
+
+void* SharedKVPageGroup::key_base(int layer) const {
+  void* base = impl_->arena->data();
+  return base ? static_cast<char*>(base) + 2ull * layer * impl_->half : nullptr;
+}
+
+void* SharedKVPageGroup::value_base(int layer) const {
+  void* base = impl_->arena->data();
+  return base ? static_cast<char*>(base) + (2ull * layer + 1) * impl_->half : nullptr;
+}
+
+}  // namespace base

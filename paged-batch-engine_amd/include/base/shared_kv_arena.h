@@ -1,0 +1,132 @@
+// Shared KV arena client and page group: drop-in for the reference's
+// base::SharedKVArenaClient / base::SharedKVPageGroup
+// (infMain/include/base/shared_kv_arena.h:14-58).
+//
+// Layout: a page is [layer0 K][layer0 V] ... [layerN K][layerN V], each plane
+// `half` bytes; block ids are byte offsets / half, and page ids are multiples
+// of 2*layers. The page group leases Chunks from the arena owner, carves them
+// into pages, hands the same page id to every layer, and returns a page only
+// after a completion fence recorded at its last retire has passed.
+//
+// The owner is reached through ChunkOwner. The reference talks to an owner
+// process over ZMQ (shared_kv_client.cpp); that control plane is not part of
+// this build, so LocalChunkOwner serves leases in-process (the owner process
+// of a deployment would wrap it behind its RPC).
+#ifndef PBE_INCLUDE_BASE_SHARED_KV_ARENA_H_
+#define PBE_INCLUDE_BASE_SHARED_KV_ARENA_H_
+
+#include <cstdint>
+#include <memory>
+#include <mutex>
+#include <string>
+
+#include "base/global_chunk_allocator.h"
+#include "pbe_handoff.h"
+
+namespace base {
+
+class ChunkOwner {
+ public:
+  virtual ~ChunkOwner() = default;
+  // Throws ChunkAllocationError (quota / fragmented / exhausted) or
+  // std::runtime_error, like the owner RPC (shared_kv_owner.cpp:71-79).
+  virtual ChunkLease acquire(const std::string& model, const std::string& layout, uint64_t bytes,
+                             uint64_t alignment) = 0;
+  // The caller guarantees every GPU access to the Chunk has completed.
+  virtual void release(const ChunkLease& lease) = 0;
+  virtual uint64_t bytes() const = 0;
+  virtual uint64_t epoch() const = 0;
+};
+
+// In-process owner: a mutex-serialized GlobalChunkAllocator.
+class LocalChunkOwner final : public ChunkOwner {
+ public:
+  LocalChunkOwner(uint64_t bytes, uint64_t epoch) : allocator_(bytes, epoch) {}
+  void register_model(const std::string& model, uint64_t hard_limit);
+  ChunkLease acquire(const std::string& model, const std::string& layout, uint64_t bytes,
+                     uint64_t alignment) override;
+  void release(const ChunkLease& lease) override;
+  uint64_t bytes() const override { return allocator_.bytes(); }
+  uint64_t epoch() const override { return allocator_.epoch(); }
+  uint64_t free_bytes() const;
+  size_t lease_count() const;
+
+ private:
+  mutable std::mutex mu_;
+  GlobalChunkAllocator allocator_;
+};
+
+// One process's mapping of the arena plus its model identity and hard limit.
+class SharedKVArenaClient {
+ public:
+  // `view` is this process's mapping (pbe_arena_get_view of a created or
+  // imported arena); its size must equal the owner's arena. device < 0 makes
+  // a metadata-only client (no completion fences; for planning and tests).
+  SharedKVArenaClient(std::shared_ptr<ChunkOwner> owner, const pbe_arena_view& view,
+                      std::string model, uint64_t hard_limit_bytes, int device);
+  SharedKVArenaClient(const SharedKVArenaClient&) = delete;
+  SharedKVArenaClient& operator=(const SharedKVArenaClient&) = delete;
+  // Leases a Chunk and checks the owner's answer (shared_kv_client.cpp:102-111).
+  ChunkLease acquire(const std::string& layout, uint64_t bytes, uint64_t alignment);
+  void release(const ChunkLease& lease);  // caller has completed every GPU access
+  // Base of a single-segment arena (nullptr when segmented: use view()).
+  void* data() const;
+  const pbe_arena_view& view() const { return view_; }
+  uint64_t bytes() const { return view_.bytes; }
+  uint64_t epoch() const { return owner_->epoch(); }
+  uint64_t hard_limit() const { return hard_limit_; }
+  int device() const { return device_; }
+  const std::string& model() const { return model_; }
+
+ private:
+  std::shared_ptr<ChunkOwner> owner_;
+  pbe_arena_view view_;
+  std::string model_;
+  uint64_t hard_limit_;
+  int device_;
+};
+
+class SharedKVPageGroup {
+ public:
+  // half_layer_bytes must be a positive multiple of 256; Chunks are
+  // max(target, page) rounded up to whole pages (shared_kv_arena.cpp:53-69).
+  // `stream` is the stream every user of the pages runs on: retire() records
+  // the completion fence there.
+  SharedKVPageGroup(std::shared_ptr<SharedKVArenaClient> arena, int layers,
+                    uint64_t half_layer_bytes, uint64_t chunk_target_bytes, void* stream);
+  ~SharedKVPageGroup();
+  SharedKVPageGroup(const SharedKVPageGroup&) = delete;
+  SharedKVPageGroup& operator=(const SharedKVPageGroup&) = delete;
+
+  // Layer 0 takes the lowest free page id (leasing a new Chunk if none is
+  // free, falling back to a single-page Chunk on quota/fragmentation) and
+  // reserves the same id for layers 1..L-1, which must allocate in order.
+  // Returns -1 when the model's limit or the arena is exhausted.
+  int allocate(int layer);
+  // Releases one layer of a page. Retiring layer 0 first rolls back the
+  // unconsumed layer reservations. When the last layer retires, a fence is
+  // recorded on the stream; the page is reused only after it completes.
+  void retire(int layer, int block_id);
+  int free_blocks(int layer) const;
+  int capacity() const;
+  uint64_t leased_bytes() const;
+  uint64_t arena_bytes() const;
+  uint64_t arena_epoch() const;
+  int addressable_blocks() const;
+  // K / V plane bases of a single-segment arena (shared_kv_arena.cpp:224-229).
+  void* key_base(int layer) const;
+  void* value_base(int layer) const;
+  // Returns completed pages, and Chunks whose pages are all free, to the owner.
+  void collect();
+  uint64_t half_bytes() const;
+  uint64_t page_bytes() const;
+  int layers() const;
+
+ private:
+  struct Impl;
+  std::unique_ptr<Impl> impl_;
+};
+
+}  // namespace base
+
+#endif  // PBE_INCLUDE_BASE_SHARED_KV_ARENA_H_

@@ -17,6 +17,8 @@
 #include "cache/page_schema.h"
 #include "cache/transfer_plan.h"
 #include "minitest.h"
+#include "base/shared_kv_arena.h"
+#include "serving/decode_kv_reservation.h"
 #include "serving/pd_handoff.h"
 
 using namespace cache;
@@ -675,6 +677,200 @@ TEST_CASE("storage spec: plain and FP8 specs and per-token bytes") {
   CHECK(base::ValidateKVCacheStorageSpec(fp8, base::DeviceType::kDeviceHIP, base::DataType::kDataTypeBf16));
   CHECK(!base::ValidateKVCacheStorageSpec(fp8, base::DeviceType::kDeviceCPU, base::DataType::kDataTypeBf16));
   CHECK_EQ(base::KVCacheBytesPerToken(fp8, 28, 2, 128), 28u * 2 * 2 * 128 + 28u * 2 * 2 * 4);
+}
+
+// ------------------------------------------------------------ page group
+
+namespace {
+// Metadata-only arena mapping (device -1: nothing is ever launched on it).
+pbe_arena_view fake_view(uint64_t bytes, uint64_t segment = 0) {
+  pbe_arena_view v{};
+  v.bytes = bytes;
+  v.segment_bytes = segment ? segment : bytes;
+  v.nseg = static_cast<uint32_t>((bytes + v.segment_bytes - 1) / v.segment_bytes);
+  for (uint32_t i = 0; i < v.nseg; ++i) v.base[i] = reinterpret_cast<void*>(0x100000ull * (i + 1));
+  return v;
+}
+
+struct Group {
+  // 3 layers, half 4 KiB -> page 24 KiB; Chunk target 3 pages.
+  static constexpr uint64_t kHalf = 4096, kPage = 6 * 4096;
+  std::shared_ptr<base::LocalChunkOwner> owner;
+  std::shared_ptr<base::SharedKVArenaClient> client;
+  std::unique_ptr<base::SharedKVPageGroup> group;
+  Group(uint64_t arena_pages, uint64_t limit_bytes, uint64_t target = 3 * kPage) {
+    owner = std::make_shared<base::LocalChunkOwner>(arena_pages * kPage, 9);
+    owner->register_model("d", limit_bytes);
+    client = std::make_shared<base::SharedKVArenaClient>(owner, fake_view(arena_pages * kPage), "d",
+                                                         limit_bytes, -1);
+    group = std::make_unique<base::SharedKVPageGroup>(client, 3, kHalf, target, nullptr);
+  }
+  int page_id(int n) const { return n * 6; }  // block id of the n-th page
+};
+}  // namespace
+
+TEST_CASE("page group: layer 0 picks pages, later layers take the same ids in order") {
+  Group g(12, 12 * Group::kPage);
+  CHECK_EQ(g.group->capacity(), 12);
+  CHECK_EQ(g.group->addressable_blocks(), static_cast<int>(12 * 6 - 6 + 1));
+  const int a = g.group->allocate(0);
+  CHECK_EQ(a, g.page_id(0));
+  CHECK_EQ(g.group->leased_bytes(), 3 * Group::kPage);  // one Chunk of 3 pages
+  const int b = g.group->allocate(0);
+  CHECK_EQ(b, g.page_id(1));
+  CHECK_EQ(g.group->allocate(1), a);
+  CHECK_EQ(g.group->allocate(1), b);
+  CHECK_EQ(g.group->allocate(2), a);
+  CHECK_EQ(g.group->allocate(2), b);
+  CHECK_THROWS_AS(g.group->allocate(1), std::logic_error);
+  CHECK_THROWS_AS(g.group->allocate(3), std::invalid_argument);
+  // 9 unleased pages + 1 free page in the Chunk
+  CHECK_EQ(g.group->free_blocks(0), 10);
+  CHECK(g.group->key_base(1) == reinterpret_cast<char*>(0x100000) + 2 * Group::kHalf);
+  CHECK(g.group->value_base(1) == reinterpret_cast<char*>(0x100000) + 3 * Group::kHalf);
+}
+
+TEST_CASE("page group: retire returns pages, Chunks go back to the owner when empty") {
+  Group g(12, 12 * Group::kPage);
+  std::vector<int> ids;
+  for (int i = 0; i < 4; ++i) ids.push_back(g.group->allocate(0));  // spans two Chunks
+  for (int l = 1; l < 3; ++l)
+    for (int i = 0; i < 4; ++i) CHECK_EQ(g.group->allocate(l), ids[i]);
+  CHECK_EQ(g.group->leased_bytes(), 6 * Group::kPage);
+  CHECK_EQ(g.owner->lease_count(), 2u);
+  for (int l = 0; l < 3; ++l) g.group->retire(l, ids[3]);
+  CHECK_THROWS_AS(g.group->retire(0, ids[3]), std::logic_error);  // double retire
+  CHECK_THROWS_AS(g.group->retire(0, 999), std::logic_error);     // not a page of this group
+  // the second Chunk held only page 3: it is empty now and was released
+  CHECK_EQ(g.owner->lease_count(), 1u);
+  CHECK_EQ(g.group->leased_bytes(), 3 * Group::kPage);
+  for (int i = 0; i < 3; ++i)
+    for (int l = 0; l < 3; ++l) g.group->retire(l, ids[i]);
+  CHECK_EQ(g.owner->lease_count(), 0u);
+  CHECK_EQ(g.owner->free_bytes(), 12 * Group::kPage);
+  // the lowest free id is reused first
+  CHECK_EQ(g.group->allocate(0), g.page_id(0));
+}
+
+TEST_CASE("page group: retiring layer 0 first rolls back unconsumed reservations") {
+  Group g(6, 6 * Group::kPage);
+  const int id = g.group->allocate(0);
+  CHECK_EQ(g.group->allocate(1), id);  // layer 2 never allocated
+  g.group->retire(1, id);
+  g.group->retire(0, id);               // drops the layer-2 reservation, page retires
+  CHECK_THROWS_AS(g.group->allocate(2), std::logic_error);
+  CHECK_EQ(g.owner->lease_count(), 0u);
+}
+
+TEST_CASE("page group: quota, single-page fallback and exhaustion") {
+  // limit = one Chunk + one page: the second lease falls back to one page
+  Group g(12, 4 * Group::kPage);
+  for (int i = 0; i < 3; ++i) g.group->allocate(0);
+  const int fourth = g.group->allocate(0);
+  CHECK_EQ(fourth, g.page_id(3));
+  CHECK_EQ(g.group->leased_bytes(), 4 * Group::kPage);
+  CHECK_EQ(g.group->allocate(0), -1);  // hard limit reached
+  // fragmented arena: no 3-page range left, one page still fits
+  Group f(5, 5 * Group::kPage);
+  auto blocker = f.owner->acquire("d", "other", Group::kPage, Group::kPage);  // page 0
+  (void)blocker;
+  const int x = f.group->allocate(0);  // Chunk at pages 1..3
+  CHECK_EQ(x, f.page_id(1));
+  f.group->allocate(0);
+  f.group->allocate(0);
+  const int y = f.group->allocate(0);  // only page 4 remains: single-page lease
+  CHECK_EQ(y, f.page_id(4));
+  CHECK_EQ(f.group->allocate(0), -1);
+  CHECK_THROWS_AS(base::SharedKVPageGroup(f.client, 3, 100, 1, nullptr), std::invalid_argument);
+  CHECK_THROWS_AS(base::SharedKVPageGroup(f.client, 0, 4096, 1, nullptr), std::invalid_argument);
+}
+
+TEST_CASE("page group: segmented mappings have no flat plane bases") {
+  auto owner = std::make_shared<base::LocalChunkOwner>(12 * Group::kPage, 3);
+  owner->register_model("d", 12 * Group::kPage);
+  auto client = std::make_shared<base::SharedKVArenaClient>(
+      owner, fake_view(12 * Group::kPage, 4 * Group::kPage), "d", 12 * Group::kPage, -1);
+  base::SharedKVPageGroup group(client, 3, Group::kHalf, Group::kPage, nullptr);
+  CHECK(group.key_base(0) == nullptr);
+  CHECK(client->data() == nullptr);
+  CHECK_THROWS_AS(base::SharedKVPageGroup(client, 3, 12288, 1, nullptr), std::invalid_argument);
+  CHECK_THROWS_AS(base::SharedKVArenaClient(owner, fake_view(8 * Group::kPage), "d", 1, -1),
+                  std::runtime_error);
+}
+
+// ------------------------------------------------------------ decode reservation
+
+namespace {
+serving::KVPoolDescriptor pool3() {
+  // 3 layers, 16 tokens x 2 heads x 64 dims BF16: half = 4 KiB
+  return {0, 3, 16, 2, 64, base::DataType::kDataTypeBf16, base::BlockStorageMode::kPlain};
+}
+
+serving::DecodeKVReservationRequest request_for(int32_t computed, int32_t prompt, int32_t pages) {
+  serving::DecodeKVReservationRequest r;
+  r.client_request_id.value = "r";
+  r.handoff_id.value = 5;
+  r.prompt_tokens = prompt;
+  r.computed_tokens = computed;
+  r.first_token = 17;
+  r.src_pool = pool3();
+  std::vector<int32_t> ids;
+  for (int32_t i = 0; i < pages; ++i) ids.push_back(600 + 6 * i);
+  r.src_block_ids_per_layer.assign(3, ids);
+  return r;
+}
+}  // namespace
+
+TEST_CASE("decode reservation: ceil(tokens/16) page-major pages and a valid manifest") {
+  Group g(24, 24 * Group::kPage);
+  serving::DecodeKVReservationManager mgr(g.group.get(), pool3());
+  serving::DecodeKVReservation res;
+  serving::KVBlockManifest man;
+  REQUIRE(mgr.reserve(request_for(41, 50, 4), &res, &man));
+  CHECK(res.valid());
+  CHECK_EQ(res.reserved_tokens, 41);
+  CHECK_EQ(res.first_token, 17);
+  REQUIRE(man.layer_mappings.size() == 3u);
+  for (int l = 0; l < 3; ++l) {
+    CHECK_EQ(man.layer_mappings[l].layer_idx, l);
+    CHECK_EQ(man.layer_mappings[l].src_block_ids.size(), 3u);  // truncated to 3 pages
+    CHECK(man.layer_mappings[l].dst_block_ids == man.layer_mappings[0].dst_block_ids);
+  }
+  CHECK(man.layer_mappings[0].dst_block_ids == (std::vector<int32_t>{0, 6, 12}));
+  CHECK(man.validate());
+  const auto leased = g.group->leased_bytes();
+  mgr.release(&res);
+  CHECK(!res.valid());
+  CHECK_EQ(g.owner->lease_count(), 0u);
+  (void)leased;
+}
+
+TEST_CASE("decode reservation: invalid requests and exhaustion reserve nothing") {
+  Group g(6, 3 * Group::kPage);
+  serving::DecodeKVReservationManager mgr(g.group.get(), pool3());
+  serving::DecodeKVReservation res;
+  serving::KVBlockManifest man;
+  auto r = request_for(41, 50, 4);
+  r.client_request_id.value.clear();
+  CHECK(!mgr.reserve(r, &res, &man));
+  r = request_for(41, 40, 4);
+  CHECK(!mgr.reserve(r, &res, &man));  // computed > prompt
+  r = request_for(41, 50, 2);
+  CHECK(!mgr.reserve(r, &res, &man));  // too few source pages
+  r = request_for(41, 50, 4);
+  r.src_pool.head_size = 128;
+  CHECK(!mgr.reserve(r, &res, &man));  // incompatible pools
+  r = request_for(41, 50, 4);
+  r.src_block_ids_per_layer.pop_back();
+  CHECK(!mgr.reserve(r, &res, &man));
+  CHECK(!res.valid());
+  // 4 pages needed, the limit allows 3: fails and rolls back
+  r = request_for(64, 64, 4);
+  CHECK(!mgr.reserve(r, &res, &man));
+  CHECK_EQ(g.owner->lease_count(), 0u);
+  CHECK(man.layer_mappings.empty());
+  CHECK(mgr.reserve(request_for(48, 48, 3), &res, &man));
+  mgr.release(&res);
 }
 
 MINITEST_MAIN()
