@@ -14,6 +14,8 @@
 #include "cache/transfer_plan.h"
 #include "minitest.h"
 #include "pbe_handoff.h"
+#include "base/shared_kv_arena.h"
+#include "serving/decode_kv_reservation.h"
 #include "serving/pd_handoff.h"
 
 using namespace cache;
@@ -211,6 +213,94 @@ TEST_CASE("shared-arena connector: page-major pages arrive intact, errors write 
   for (size_t i = 0; i < src.size(); ++i)
     std::memcpy(want.data() + (uint64_t)dst[i] / st * page, host.data() + (uint64_t)src[i] / st * page, page);
   CHECK(got == want);
+  CHECK(pbe_arena_destroy(arena) == PBE_OK);
+}
+
+TEST_CASE("end to end: prefill pages -> decode reservation -> connector copy -> fenced retire") {
+  // Qwen2.5-0.5B geometry: 24 layers, 2 KV heads x 64, 16-token pages (192 KiB).
+  const int layers = 24;
+  const uint64_t half = 16 * 2 * 64 * 2, page = 2 * layers * half;
+  const uint64_t arena_bytes = 64 * page;
+  pbe_arena* arena = nullptr;
+  REQUIRE(pbe_arena_create(0, arena_bytes, 16 * page, 4242, &arena) == PBE_OK);  // 4 segments
+  pbe_arena_view view{};
+  REQUIRE(pbe_arena_get_view(arena, &view) == PBE_OK);
+  auto owner = std::make_shared<base::LocalChunkOwner>(arena_bytes, 4242);
+  owner->register_model("prefill", 24 * page);
+  owner->register_model("decode", 40 * page);
+  void* p_stream = nullptr;
+  void* d_stream = nullptr;
+  REQUIRE(pbe_stream_create(0, &p_stream) == PBE_OK);
+  REQUIRE(pbe_stream_create(0, &d_stream) == PBE_OK);
+  {
+    auto p_client = std::make_shared<base::SharedKVArenaClient>(owner, view, "prefill", 24 * page, 0);
+    auto d_client = std::make_shared<base::SharedKVArenaClient>(owner, view, "decode", 40 * page, 0);
+    base::SharedKVPageGroup p_pages(p_client, layers, half, 2 * 1024 * 1024, p_stream);  // 11-page Chunks
+    base::SharedKVPageGroup d_pages(d_client, layers, half, 2 * 1024 * 1024, d_stream);
+    // prefill: a 41-token prompt = 3 pages, every layer
+    std::vector<int32_t> src;
+    for (int i = 0; i < 3; ++i) src.push_back(p_pages.allocate(0));
+    for (int l = 1; l < layers; ++l)
+      for (int i = 0; i < 3; ++i) CHECK_EQ(p_pages.allocate(l), src[i]);
+    // write the prefill KV: byte = page index * 3 + 64 * plane + layer
+    std::vector<uint8_t> host(page);
+    for (size_t i = 0; i < src.size(); ++i) {
+      for (int l = 0; l < layers; ++l)
+        for (int plane = 0; plane < 2; ++plane)
+          std::memset(host.data() + (2 * l + plane) * half, static_cast<int>((i * 3 + 64 * plane + l) & 0xff), half);
+      const uint64_t off = static_cast<uint64_t>(src[i]) * half;
+      uint8_t* dst = static_cast<uint8_t*>(view.base[off / view.segment_bytes]) + off % view.segment_bytes;
+      HIP_OK(hipMemcpy(dst, host.data(), page, hipMemcpyHostToDevice));
+    }
+    // decode: reserve destination pages and build the manifest
+    serving::KVPoolDescriptor pool{0, layers, 16, 2, 64, base::DataType::kDataTypeBf16,
+                                   base::BlockStorageMode::kPlain};
+    serving::DecodeKVReservationManager reservations(&d_pages, pool);
+    serving::DecodeKVReservationRequest req;
+    req.client_request_id.value = "req-41";
+    req.handoff_id.value = 1;
+    req.prompt_tokens = 41;
+    req.computed_tokens = 41;
+    req.src_pool = pool;
+    req.src_block_ids_per_layer.assign(layers, src);
+    serving::DecodeKVReservation res;
+    serving::KVBlockManifest manifest;
+    REQUIRE(reservations.reserve(req, &res, &manifest));
+    serving::SharedArenaBinding binding{view, 4242, 0};
+    serving::SharedArenaKVTransferConnector conn(binding, d_stream);
+    serving::HandoffId h;
+    REQUIRE(conn.submit_from(p_client->epoch(), manifest, &h));
+    CHECK(conn.drain(h).ok());
+    CHECK_EQ(conn.copied_bytes(), 3 * page);
+    // verify destination pages
+    const auto& dst_ids = manifest.layer_mappings[0].dst_block_ids;
+    for (size_t i = 0; i < dst_ids.size(); ++i) {
+      const uint64_t off = static_cast<uint64_t>(dst_ids[i]) * half;
+      const uint8_t* d = static_cast<uint8_t*>(view.base[off / view.segment_bytes]) + off % view.segment_bytes;
+      HIP_OK(hipMemcpy(host.data(), d, page, hipMemcpyDeviceToHost));
+      bool ok = true;
+      for (int l = 0; l < layers && ok; ++l)
+        for (int plane = 0; plane < 2 && ok; ++plane)
+          ok = std::all_of(host.begin() + (2 * l + plane) * half, host.begin() + (2 * l + plane + 1) * half,
+                           [&](uint8_t b) { return b == static_cast<uint8_t>((i * 3 + 64 * plane + l) & 0xff); });
+      CHECK(ok);
+    }
+    // prefill releases its pages after the copy: fences on its stream
+    for (int l = 0; l < layers; ++l)
+      for (int id : src) p_pages.retire(l, id);
+    REQUIRE(pbe_stream_synchronize(0, p_stream) == PBE_OK);
+    p_pages.collect();
+    CHECK_EQ(p_pages.leased_bytes(), 0u);
+    reservations.release(&res);
+    REQUIRE(pbe_stream_synchronize(0, d_stream) == PBE_OK);
+    d_pages.collect();
+    CHECK_EQ(d_pages.leased_bytes(), 0u);
+    conn.release(h);
+  }
+  CHECK_EQ(owner->lease_count(), 0u);
+  CHECK_EQ(owner->free_bytes(), arena_bytes);
+  pbe_stream_destroy(0, p_stream);
+  pbe_stream_destroy(0, d_stream);
   CHECK(pbe_arena_destroy(arena) == PBE_OK);
 }
 
