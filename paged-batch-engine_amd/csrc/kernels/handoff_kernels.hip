@@ -281,15 +281,52 @@ __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_fp8_kernel(
     gdst_t dst = reinterpret_cast<gdst_t>(run.dst + rel / 2);
     const uint64_t scales = run.aux;
     const uint32_t row0 = (uint32_t)(rel / kRowBytes) + lane / kLanesPerRow;  // row in the run
+    constexpr uint32_t kRowsPerSlice = kUnroll * kRowsPerStep;
     if (nbytes >= kSlice) {
       u32x4 v[kUnroll];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) v[u] = ld16(src, (u * kWave + lane) * 16u);
+      if constexpr (kRowsPerSlice <= kWave) {
+        // Batched per slice: lane j owns row j of the slice. It obtains the
+        // row's amax (per-token-head: the row maximum gathered from the
+        // row's lanes; table: the (layer, K|V, head) entry of the row),
+        // computes 448/amax (and the scale) once, and every lane then
+        // fetches its row's multiplier. Divisions and index arithmetic run
+        // once per slice instead of once per 1 KiB step.
+        const uint32_t slice_row0 = row0 - lane / kLanesPerRow;  // first row of the slice
+        float row_amax;
+        if constexpr (kTable) {
+          const uint32_t in_page = (slice_row0 + lane) % rows_per_page;
+          row_amax = amax_table[(in_page / rows_per_plane) * kv_heads + in_page % kv_heads];
+        } else {
+          float m[kUnroll];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u)
-        fp8_step<kUnroll, kLanesPerRow, kTable>(v[u], row0 + u * kRowsPerStep, lane, dst,
-                                                (u * kWave + lane) * 8u, scales, rows_per_plane,
-                                                kv_heads, rows_per_page, amax_table);
+          for (int u = 0; u < kUnroll; ++u) m[u] = group_max<kLanesPerRow>(amax8(v[u]));
+          const uint32_t j_step = lane / kRowsPerStep, j_row = lane % kRowsPerStep;
+          row_amax = 0.f;
+#pragma unroll
+          for (int u = 0; u < kUnroll; ++u) {
+            const float t = __shfl(m[u], (int)(j_row * kLanesPerRow), kWave);
+            if (j_step == (uint32_t)u) row_amax = t;
+          }
+          if (lane < kRowsPerSlice)
+            __builtin_nontemporal_store(row_amax > 0.f ? row_amax / 448.f : 1.f,
+                                        reinterpret_cast<PBE_GLOBAL float*>(scales) + slice_row0 +
+                                            lane);
+        }
+        const float row_inv = row_amax > 0.f ? 448.f / row_amax : 0.f;
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+          const float inv = __shfl(row_inv, (int)(u * kRowsPerStep + lane / kLanesPerRow), kWave);
+          st8(dst, (u * kWave + lane) * 8u, quantise8(v[u], inv));
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u)
+          fp8_step<kUnroll, kLanesPerRow, kTable>(v[u], row0 + u * kRowsPerStep, lane, dst,
+                                                  (u * kWave + lane) * 8u, scales, rows_per_plane,
+                                                  kv_heads, rows_per_page, amax_table);
+      }
     } else {
       // Last, partial slice of a run: whole rows only (slices are multiples
       // of the row size), one 1 KiB step at a time.
