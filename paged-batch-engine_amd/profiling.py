@@ -50,13 +50,21 @@ def kernel_durations(root: str):
     return out
 
 
-def stats(root: str, out: str, command: str) -> None:
+def stats(root: str, out: str, command: str, labels=None) -> None:
+    """labels: {grid size: (workload label, algorithmic bytes per launch)}."""
+    labels = labels or {}
     d = kernel_durations(root)
     lines = [f"# rocprofv3 kernel trace summary", f"command: {command}", "",
-             f"{'kernel':<60} {'grid':>9} {'calls':>6} {'avg_us':>9} {'p50_us':>9} {'min_us':>9}"]
+             f"{'kernel':<48} {'grid':>9} {'calls':>6} {'avg_us':>9} {'p50_us':>9} {'min_us':>9}"
+             f"  {'workload':<28} {'GB/s':>8}"]
     for (name, grid), v in sorted(d.items(), key=lambda kv: -sum(kv[1])):
-        lines.append(f"{name[:60]:<60} {grid:>9} {len(v):>6} {statistics.mean(v) / 1e3:>9.2f} "
-                     f"{statistics.median(v) / 1e3:>9.2f} {min(v) / 1e3:>9.2f}")
+        label, alg = "", None
+        for key, (lab, b) in labels.items():
+            if key == (name, grid) or (isinstance(key, int) and key == grid and "pbe::" in name):
+                label, alg = lab, b
+        gbps = f"{alg / (statistics.mean(v) * 1e-9) / 1e9:8.1f}" if alg else ""
+        lines.append(f"{name[:48]:<48} {grid:>9} {len(v):>6} {statistics.mean(v) / 1e3:>9.2f} "
+                     f"{statistics.median(v) / 1e3:>9.2f} {min(v) / 1e3:>9.2f}  {label:<28} {gbps}")
     text = "\n".join(lines) + "\n"
     with open(out, "w") as fh:
         fh.write(text)
@@ -115,6 +123,8 @@ def main() -> None:
     s.add_argument("root")
     s.add_argument("--out", required=True)
     s.add_argument("--command", required=True)
+    s.add_argument("--label", action="append", default=[],
+                   help="KERNEL_SUBSTRING:GRID=WORKLOAD:ALG_BYTES (repeatable)")
     p = sub.add_parser("pmc")
     p.add_argument("fetch_root")
     p.add_argument("write_root")
@@ -125,7 +135,17 @@ def main() -> None:
     p.add_argument("--calib-grid", type=int, required=True)
     a = ap.parse_args()
     if a.cmd == "stats":
-        stats(a.root, a.out, a.command)
+        labels = {}
+        if a.label:
+            names = {k[0] for k in kernel_durations(a.root)}
+            for spec in a.label:
+                key, val = spec.split("=", 1)
+                sub_name, grid = key.rsplit(":", 1)
+                lab, alg = val.rsplit(":", 1)
+                for n in names:
+                    if sub_name in n:
+                        labels[(n, int(grid))] = (lab, int(alg))
+        stats(a.root, a.out, a.command, labels)
     else:
         pmc(a.fetch_root, a.write_root, a.out, a.command, a.alg_bytes, a.handoff_grid,
             a.calib_grid)
