@@ -58,11 +58,26 @@ def cpu_baseline(w, host_arena, seconds: float):
         if el >= seconds:
             break
     per = el / reps
+    # generic plan form: 2*layers component memcpys of `half` bytes per page
+    # (ExecuteCpuTransfer over the bound manifest, transfer_plan.cpp:392-403)
+    creps, t0 = 0, time.perf_counter()
+    while True:
+        O.copy_components(host_arena, w.src_ids, w.dst_ids, g.half(), g.layers)
+        creps += 1
+        cel = time.perf_counter() - t0
+        if cel >= seconds / 2:
+            break
+    cper = cel / creps
     return {"value": round(w.algorithmic_bytes() / per / 1e9, 3), "unit": "GB/s", "cores": 1,
             "kind": "port",
             "sample": f"{reps} handoffs of the config-2 plan (315 pages, {w.copied_bytes()} B "
-                      f"copied each) in {el:.1f} s; {per * 1e3:.2f} ms per handoff",
-            "ms_per_handoff": round(per * 1e3, 3)}
+                      f"copied each, one memcpy per coalesced run) in {el:.1f} s; "
+                      f"{per * 1e3:.2f} ms per handoff",
+            "ms_per_handoff": round(per * 1e3, 3),
+            "generic_plan_form": {"value": round(w.algorithmic_bytes() / cper / 1e9, 3),
+                                  "unit": "GB/s", "ms_per_handoff": round(cper * 1e3, 3),
+                                  "memcpys_per_handoff": w.pages * 2 * g.layers,
+                                  "sample": f"{creps} handoffs in {cel:.1f} s"}}
 
 
 def _timed(torch, stream, scrub, fn, n):
