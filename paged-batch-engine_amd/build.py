@@ -52,6 +52,7 @@ ABI_HOST_SOURCES = [
     "csrc/cache/hip_transfer_backend.cpp",
     "csrc/serving/shared_kv_handoff.cpp",
     "csrc/serving/decode_kv_reservation.cpp",
+    "csrc/serving/plan_kv_connector.cpp",
 ]
 # Sources that call HIP (compiled by hipcc).
 HIP_SOURCES = [

@@ -12,6 +12,7 @@
 
 #include "base/base.h"
 #include "base/kv_cache_format.h"
+#include "cache/transfer_plan.h"
 #include "pbe_handoff.h"
 
 namespace serving {
@@ -99,6 +100,69 @@ struct SharedArenaBinding {
 // happens before any device work, so an error leaves the arena untouched.
 base::Status CopySharedKV(const SharedArenaBinding& arena, uint64_t source_epoch,
                           const KVBlockManifest& manifest, void* stream, uint64_t* copied);
+
+// A KV pool laid out page-major in an arena mapping (the shared-arena layout):
+// the K plane of layer l of block id b is at byte (2l + b)*half, the V plane
+// at (2l + 1 + b)*half. FP8 pools add a page-major scale pool of
+// 2*layers*block_size*kv_heads fp32 per page ([layer][K|V][token][head]).
+struct ArenaKVPool {
+  pbe_arena_view view{};
+  KVPoolDescriptor pool;
+  void* scales = nullptr;  // FP8 only
+  uint64_t scale_bytes = 0;
+};
+
+// Generic plan form of a handoff (pd_handoff_common.cpp:64-153): builds the
+// source and destination page schemas from the pool descriptors, compiles a
+// plan (cached by `planner`), packs both layouts and binds one BoundTransfer
+// per page over the component addresses of the manifest's block ids. Fails
+// before producing anything on incompatible pools, incomplete or duplicate
+// layer mappings, or ids outside either arena.
+base::Status BindManifestTransfers(const KVBlockManifest& manifest, const ArenaKVPool& source,
+                                   const ArenaKVPool& destination, cache::TransferPlanner* planner,
+                                   std::vector<cache::BoundTransfer>* transfers);
+
+// InProcKVBlockCopyConnector (pd_handoff.cpp:80-213) over arena pools: each
+// handoff is bound through the TransferPlan and all of its component copies
+// (2*layers per page, plus scales for FP8 pools) run as one op-list kernel on
+// the connector's stream, followed by a completion event.
+class InProcKVBlockCopyConnector final : public KVTransferConnector {
+ public:
+  InProcKVBlockCopyConnector(ArenaKVPool source, ArenaKVPool destination, int device,
+                             void* stream = nullptr);
+  ~InProcKVBlockCopyConnector() override;
+  InProcKVBlockCopyConnector(const InProcKVBlockCopyConnector&) = delete;
+  InProcKVBlockCopyConnector& operator=(const InProcKVBlockCopyConnector&) = delete;
+
+  base::Status submit(const KVBlockManifest& manifest, HandoffId* handle) override;
+  KVTransferStatus poll(HandoffId handle) override;
+  void cancel(HandoffId handle, const std::string& reason) override;
+  KVTransferStatus drain(HandoffId handle) override;
+  void release(HandoffId handle) override;
+  uint64_t copied_bytes() const { return copied_bytes_; }
+  size_t last_op_count() const { return last_ops_; }
+
+ private:
+  struct Record {
+    HandoffId handle;
+    KVTransferStatus status;
+    pbe_event* done = nullptr;
+    bool cancel_requested = false;
+    std::string cancel_reason;
+  };
+  Record* find(HandoffId handle);
+  KVTransferStatus settle(Record& record, bool wait);
+
+  ArenaKVPool source_, destination_;
+  int device_;
+  void* stream_ = nullptr;
+  bool owns_stream_ = false;
+  cache::TransferPlanner planner_;
+  uint64_t next_handoff_id_ = 1;
+  uint64_t copied_bytes_ = 0;
+  size_t last_ops_ = 0;
+  std::vector<Record> records_;
+};
 
 // KVTransferConnector over CopySharedKV: submit() queues the copy on the
 // connector's stream and records a completion event; poll() queries it,

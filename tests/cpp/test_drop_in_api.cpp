@@ -873,4 +873,83 @@ TEST_CASE("decode reservation: invalid requests and exhaustion reserve nothing")
   mgr.release(&res);
 }
 
+// ------------------------------------------------------------ generic plan form
+
+TEST_CASE("bind manifest transfers: 2L component ops per page at page-major addresses") {
+  serving::ArenaKVPool pool;
+  pool.pool = pool3();  // 3 layers, half 4 KiB
+  pool.view = fake_view(40 * Group::kPage);
+  auto m = good_manifest();
+  m.src_pool = m.dst_pool = pool3();
+  m.layer_mappings.clear();
+  for (int l = 0; l < 3; ++l) m.layer_mappings.push_back({l, {0, 6, 30}, {60, 66, 120}});
+  cache::TransferPlanner planner;
+  std::vector<cache::BoundTransfer> t;
+  REQUIRE(serving::BindManifestTransfers(m, pool, pool, &planner, &t));
+  REQUIRE(t.size() == 3u);
+  const uint64_t half = Group::kHalf;
+  const uint8_t* base = static_cast<const uint8_t*>(pool.view.base[0]);
+  for (size_t page = 0; page < 3; ++page) {
+    CHECK_EQ(t[page].operations().size(), 6u);
+    for (const auto& op : t[page].operations()) {
+      const uint64_t plane = 2 * op.component.layer + (op.component.kind == cache::ComponentKind::kValue);
+      const uint64_t s_id = m.layer_mappings[0].src_block_ids[page];
+      const uint64_t d_id = m.layer_mappings[0].dst_block_ids[page];
+      CHECK(op.source == base + (s_id + plane) * half);
+      CHECK(op.destination == base + (d_id + plane) * half);
+      CHECK_EQ(op.bytes, half);
+    }
+  }
+  // the plan template was compiled once
+  std::vector<cache::BoundTransfer> again;
+  REQUIRE(serving::BindManifestTransfers(m, pool, pool, &planner, &again));
+  CHECK_EQ(planner.cache_hits(), 1u);
+  // errors bind nothing
+  auto bad = m;
+  bad.layer_mappings[1].dst_block_ids[0] = 40 * 6;  // past the arena
+  std::vector<cache::BoundTransfer> none;
+  CHECK(!serving::BindManifestTransfers(bad, pool, pool, &planner, &none));
+  CHECK(none.empty());
+  bad = m;
+  bad.layer_mappings[2].layer_idx = 1;  // duplicate layer
+  CHECK(!serving::BindManifestTransfers(bad, pool, pool, &planner, &none));
+  bad = m;
+  bad.layer_mappings[0].src_block_ids[1] = 7;  // not a page id
+  CHECK(!serving::BindManifestTransfers(bad, pool, pool, &planner, &none));
+  auto fp8 = pool;
+  fp8.pool.storage_mode = base::BlockStorageMode::kFp8E4M3PerTokenHead;
+  CHECK(!serving::BindManifestTransfers(m, pool, fp8, &planner, &none));  // conversion: no plan
+}
+
+TEST_CASE("bind manifest transfers: FP8 pools add scale components") {
+  serving::ArenaKVPool pool;
+  pool.pool = pool3();
+  pool.pool.storage_mode = base::BlockStorageMode::kFp8E4M3PerTokenHead;
+  pool.view = fake_view(20 * Group::kPage / 2);  // FP8 half = 2 KiB
+  std::vector<uint8_t> scales(20 * 2 * 3 * 16 * 2 * 4);
+  pool.scales = scales.data();
+  pool.scale_bytes = scales.size();
+  auto m = good_manifest();
+  m.src_pool = m.dst_pool = pool.pool;
+  m.layer_mappings.clear();
+  for (int l = 0; l < 3; ++l) m.layer_mappings.push_back({l, {0, 6}, {12, 18}});
+  cache::TransferPlanner planner;
+  std::vector<cache::BoundTransfer> t;
+  REQUIRE(serving::BindManifestTransfers(m, pool, pool, &planner, &t));
+  REQUIRE(t.size() == 2u);
+  CHECK_EQ(t[0].operations().size(), 12u);  // K, V, K-scale, V-scale per layer
+  size_t scale_ops = 0;
+  for (const auto& op : t[1].operations())
+    if (op.component.kind == cache::ComponentKind::kKeyScale) {
+      ++scale_ops;
+      // page 3 (id 18) -> scale page 3, plane 2*layer
+      CHECK(op.destination == scales.data() + (3 * 6 + 2 * op.component.layer) * 32 * 4);
+      CHECK_EQ(op.bytes, 32u * 4u);
+    }
+  CHECK_EQ(scale_ops, 3u);
+  pool.scales = nullptr;
+  std::vector<cache::BoundTransfer> none;
+  CHECK(!serving::BindManifestTransfers(m, pool, pool, &planner, &none));
+}
+
 MINITEST_MAIN()

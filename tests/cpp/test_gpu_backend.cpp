@@ -216,6 +216,66 @@ TEST_CASE("shared-arena connector: page-major pages arrive intact, errors write 
   CHECK(pbe_arena_destroy(arena) == PBE_OK);
 }
 
+TEST_CASE("generic plan form: InProcKVBlockCopyConnector equals the run copy, BF16 and FP8 pools") {
+  for (bool fp8 : {false, true}) {
+    const int layers = 4;
+    const uint64_t elem = fp8 ? 1 : 2;
+    const uint64_t half = 16 * 2 * 64 * elem, page = 2 * layers * half, pages = 24;
+    const uint64_t bytes = pages * page;
+    const uint64_t scale_page = 2 * layers * 16 * 2 * 4;
+    uint8_t *arena = nullptr, *scales = nullptr;
+    HIP_OK(hipMalloc(&arena, bytes));
+    HIP_OK(hipMalloc(&scales, pages * scale_page));
+    std::vector<uint8_t> host(bytes), host_sc(pages * scale_page);
+    for (size_t i = 0; i < host.size(); ++i) host[i] = static_cast<uint8_t>(i * 131u + 17u);
+    for (size_t i = 0; i < host_sc.size(); ++i) host_sc[i] = static_cast<uint8_t>(i * 7u + 3u);
+    HIP_OK(hipMemcpy(arena, host.data(), bytes, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(scales, host_sc.data(), host_sc.size(), hipMemcpyHostToDevice));
+    serving::ArenaKVPool pool;
+    pool.view.bytes = bytes;
+    pool.view.segment_bytes = bytes;
+    pool.view.nseg = 1;
+    pool.view.base[0] = arena;
+    pool.pool = {0, layers, 16, 2, 64, base::DataType::kDataTypeBf16,
+                 fp8 ? base::BlockStorageMode::kFp8E4M3PerTokenHead : base::BlockStorageMode::kPlain};
+    if (fp8) {
+      pool.scales = scales;
+      pool.scale_bytes = pages * scale_page;
+    }
+    const int st = 2 * layers;
+    const std::vector<int32_t> src = {1 * st, 2 * st, 3 * st, 7 * st, 9 * st};
+    const std::vector<int32_t> dst = {10 * st, 11 * st, 20 * st, 21 * st, 22 * st};
+    serving::KVBlockManifest m;
+    m.client_request_id.value = "g";
+    m.handoff_id.value = 3;
+    m.prompt_tokens = m.computed_tokens = 80;
+    m.src_pool = m.dst_pool = pool.pool;
+    for (int l = 0; l < layers; ++l) m.layer_mappings.push_back({l, src, dst});
+    {
+      serving::InProcKVBlockCopyConnector conn(pool, pool, 0);
+      serving::HandoffId h;
+      REQUIRE(conn.submit(m, &h));
+      CHECK(conn.drain(h).ok());
+      CHECK_EQ(conn.last_op_count(), src.size() * 2 * layers * (fp8 ? 2 : 1));
+      conn.release(h);
+    }
+    std::vector<uint8_t> got(bytes), got_sc(host_sc.size());
+    HIP_OK(hipMemcpy(got.data(), arena, bytes, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(got_sc.data(), scales, got_sc.size(), hipMemcpyDeviceToHost));
+    std::vector<uint8_t> want = host, want_sc = host_sc;
+    for (size_t i = 0; i < src.size(); ++i) {
+      std::memcpy(want.data() + dst[i] / st * page, host.data() + src[i] / st * page, page);
+      if (fp8)
+        std::memcpy(want_sc.data() + dst[i] / st * scale_page, host_sc.data() + src[i] / st * scale_page,
+                    scale_page);
+    }
+    CHECK(got == want);
+    CHECK(got_sc == want_sc);
+    (void)hipFree(arena);
+    (void)hipFree(scales);
+  }
+}
+
 TEST_CASE("end to end: prefill pages -> decode reservation -> connector copy -> fenced retire") {
   // Qwen2.5-0.5B geometry: 24 layers, 2 KV heads x 64, 16-token pages (192 KiB).
   const int layers = 24;
