@@ -126,6 +126,18 @@ def measure_extra_configs(torch, P, W, scrub, n: int):
         rec(w.name, w.algorithmic_bytes(), _timed(torch, stream, scrub, lambda: rl.copy(sp), n),
             {"pages": w.pages, "runs": len(runs), "launches": 1})
         rl.close()
+        if cfg == 3:
+            # generic plan form: 2*layers component copies of `half` bytes per
+            # page in one op-list launch (op list staged per call, included)
+            half = g.half()
+            ops = P.op_array([(view.base[0] + (s + plane) * half,
+                               view.base[0] + (d + plane) * half, half)
+                              for s, d in zip(w.src_ids.tolist(), w.dst_ids.tolist())
+                              for plane in range(2 * g.layers)])
+            rec(w.name + "_component_ops", w.algorithmic_bytes(),
+                _timed(torch, stream, scrub, lambda: P.copy_ops(ops, 0, sp), n),
+                {"pages": w.pages, "ops": ops[1], "launches": 1,
+                 "note": "includes host validation and op-list staging per call"})
         if cfg == 3:  # one launch per request
             lists = []
             for r in w.requests:

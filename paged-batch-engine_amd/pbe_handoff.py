@@ -259,11 +259,19 @@ def copy_shared_kv(view: ArenaView, src_ids, dst_ids, kv: KvShape, device: int =
     return copied.value
 
 
+def op_array(ops):
+    """Packs (src, dst, bytes) tuples into a reusable CopyOp array."""
+    import numpy as np
+    a = np.ascontiguousarray(np.asarray(ops, dtype=np.uint64).reshape(-1, 3))
+    arr = (CopyOp * max(1, len(a))).from_buffer_copy(a.tobytes() or bytes(24))
+    return arr, len(a)
+
+
 def copy_ops(ops, device: int = 0, stream: int = 0) -> None:
-    arr = (CopyOp * max(1, len(ops)))()
-    for i, (s, d, b) in enumerate(ops):
-        arr[i] = CopyOp(s, d, b)
-    check(lib().pbe_copy_ops(arr, len(ops), device, stream or None))
+    """ops: list of (src, dst, bytes) or the (array, n) pair from op_array()."""
+    arr, n = ops if isinstance(ops, tuple) and len(ops) == 2 and not isinstance(ops[0], int) \
+        else op_array(ops)
+    check(lib().pbe_copy_ops(arr, n, device, stream or None))
 
 
 class Arena:

@@ -202,3 +202,45 @@ def test_repeated_launches_are_idempotent(torch_cuda):
         torch.cuda.synchronize()
     after = snapshot(bufs)
     assert np.array_equal(after, expected), first_diff(after, expected)
+
+
+def test_more_than_4096_runs_three_level_search(torch_cuda):
+    """6000 single-page runs: the wave-parallel run search needs three levels
+    (64 x 64 < 6000), on a geometry whose page is not a slice multiple."""
+    torch = torch_cuda
+    g = W.Geometry(1, 1, 24)                 # half 768 B, page 1536 B
+    n_pages = 13000
+    rng = np.random.default_rng(6)
+    pages = rng.permutation(n_pages)[:12000]
+    src = (pages[:6000] * g.stride).astype(np.int32)
+    dst = (pages[6000:] * g.stride).astype(np.int32)
+    kv = _kv(g)
+    runs = P.build_runs(src, dst, kv)
+    assert len(runs) > 4096
+    say(f"three-level search: {len(runs)} runs")
+    bufs, view = device_arena(torch, n_pages * g.page_bytes())
+    fill_bf16(torch, bufs[0], 1.0, 66)
+    torch.cuda.synchronize()
+    expected = snapshot(bufs).copy()
+    O.copy_handoff(expected, src, dst, g.half(), g.layers)
+    with P.RunList.bf16(view, view, runs, kv) as rl:
+        rl.copy(stream_ptr(torch))
+        torch.cuda.synchronize()
+    after = snapshot(bufs)
+    assert np.array_equal(after, expected), first_diff(after, expected)
+
+
+def test_empty_and_degenerate_inputs_are_rejected(torch_cuda):
+    torch = torch_cuda
+    kv = P.shape(2, 2, 64)
+    bufs, view = device_arena(torch, 8 * kv.page_bytes())
+    with pytest.raises(P.PbeError):
+        P.copy_shared_kv(view, [], [], kv, 0, stream_ptr(torch))
+    with pytest.raises(P.PbeError):
+        P.RunList.bf16(view, view, [(0, 4, 0)], kv)           # zero-page run
+    with pytest.raises(P.PbeError):
+        P.RunList.bf16(view, view, [(0, 6, 1)], kv)           # 6 is not a page id (stride 4)
+    with pytest.raises(P.PbeError):
+        P.RunList.bf16(view, view, [(0, 0, 1)], kv)           # destination is its own source
+    with pytest.raises(P.PbeError):
+        P.RunList.bf16(view, view, [(0, 28, 2)], kv)          # runs past the arena
