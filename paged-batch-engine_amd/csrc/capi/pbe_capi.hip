@@ -814,10 +814,12 @@ int pbe_handoff_copy_fp8(const pbe_runlist* list, int scale_mode, const float* a
 // ---------------------------------------------------------------- one-call forms
 namespace {
 
-// Per-device pinned staging + device buffer for the one-call entry points.
-// A buffer is reused only after the launch that read it has completed.
-struct Staging {
-  std::mutex mu;
+// Per-device ring of pinned staging + device buffers for the one-call entry
+// points. A slot is reused only after the launch that read it has completed,
+// so back-to-back calls block the host only when the whole ring is in flight.
+constexpr int kStagingSlots = 4;
+
+struct StagingSlot {
   void* host = nullptr;
   void* dev = nullptr;
   size_t cap = 0;
@@ -825,39 +827,50 @@ struct Staging {
   bool pending = false;
 };
 
+struct Staging {
+  std::mutex mu;
+  StagingSlot slots[kStagingSlots];
+  int next = 0;
+};
+
 Staging& staging_for(int device) {
-  static Staging slots[64];
-  return slots[device & 63];
+  static Staging per_device[64];
+  return per_device[device & 63];
 }
 
-// Copies `bytes` of `data` to a device buffer that stays valid until the next
-// call on this device, ordered on `stream`. Caller holds st.mu.
-int stage(Staging& st, const void* data, size_t bytes, hipStream_t stream, void** dev_out) {
-  if (st.pending) {
-    PBE_HIP(hipEventSynchronize(st.done));
-    st.pending = false;
+// Copies `bytes` of `data` into the next ring slot's device buffer, ordered on
+// `stream`, and returns the slot. Caller holds st.mu and calls stage_done()
+// after the launch that reads the buffer.
+int stage(Staging& st, const void* data, size_t bytes, hipStream_t stream, StagingSlot** slot_out,
+          void** dev_out) {
+  StagingSlot& sl = st.slots[st.next];
+  st.next = (st.next + 1) % kStagingSlots;
+  if (sl.pending) {
+    PBE_HIP(hipEventSynchronize(sl.done));
+    sl.pending = false;
   }
-  if (bytes > st.cap) {
-    if (st.host) (void)hipHostFree(st.host);
-    if (st.dev) (void)hipFree(st.dev);
-    st.host = st.dev = nullptr;
-    st.cap = 0;
+  if (bytes > sl.cap) {
+    if (sl.host) (void)hipHostFree(sl.host);
+    if (sl.dev) (void)hipFree(sl.dev);
+    sl.host = sl.dev = nullptr;
+    sl.cap = 0;
     size_t cap = 4096;
     while (cap < bytes) cap *= 2;
-    PBE_HIP(hipHostMalloc(&st.host, cap, hipHostMallocDefault));
-    PBE_HIP(hipMalloc(&st.dev, cap));
-    st.cap = cap;
+    PBE_HIP(hipHostMalloc(&sl.host, cap, hipHostMallocDefault));
+    PBE_HIP(hipMalloc(&sl.dev, cap));
+    sl.cap = cap;
   }
-  if (!st.done) PBE_HIP(hipEventCreateWithFlags(&st.done, hipEventDisableTiming));
-  std::memcpy(st.host, data, bytes);
-  PBE_HIP(hipMemcpyAsync(st.dev, st.host, bytes, hipMemcpyHostToDevice, stream));
-  *dev_out = st.dev;
+  if (!sl.done) PBE_HIP(hipEventCreateWithFlags(&sl.done, hipEventDisableTiming));
+  std::memcpy(sl.host, data, bytes);
+  PBE_HIP(hipMemcpyAsync(sl.dev, sl.host, bytes, hipMemcpyHostToDevice, stream));
+  *slot_out = &sl;
+  *dev_out = sl.dev;
   return PBE_OK;
 }
 
-int stage_done(Staging& st, hipStream_t stream) {
-  PBE_HIP(hipEventRecord(st.done, stream));
-  st.pending = true;
+int stage_done(StagingSlot& sl, hipStream_t stream) {
+  PBE_HIP(hipEventRecord(sl.done, stream));
+  sl.pending = true;
   return PBE_OK;
 }
 
@@ -899,12 +912,13 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
   std::lock_guard<std::mutex> lock(st.mu);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   void* dev = nullptr;
-  rc = stage(st, res.runs.data(), res.runs.size() * sizeof(pbe::DevRun), s, &dev);
+  StagingSlot* slot = nullptr;
+  rc = stage(st, res.runs.data(), res.runs.size() * sizeof(pbe::DevRun), s, &slot, &dev);
   if (rc != PBE_OK) return rc;
   PBE_HIP(pbe::launch_copy_runs(static_cast<const pbe::DevRun*>(dev), (uint32_t)n_runs,
                                 (uint32_t)res.info.slices, 2ull * shape->layers * half,
                                 launch_shape(res.info.slices, device, cfg), s));
-  rc = stage_done(st, s);
+  rc = stage_done(*slot, s);
   if (rc != PBE_OK) return rc;
   if (copied) *copied = res.info.src_bytes;
   return PBE_OK;
@@ -943,10 +957,11 @@ int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream
   std::lock_guard<std::mutex> lock(st.mu);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   void* dev = nullptr;
-  int rc = stage(st, pieces.data(), pieces.size() * sizeof(pbe::DevOp), s, &dev);
+  StagingSlot* slot = nullptr;
+  int rc = stage(st, pieces.data(), pieces.size() * sizeof(pbe::DevOp), s, &slot, &dev);
   if (rc != PBE_OK) return rc;
   PBE_HIP(pbe::launch_copy_ops(static_cast<const pbe::DevOp*>(dev), (uint32_t)pieces.size(), s));
-  return stage_done(st, s);
+  return stage_done(*slot, s);
 }
 
 // ---------------------------------------------------------------- streams

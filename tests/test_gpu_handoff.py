@@ -114,6 +114,34 @@ def test_copy_shared_kv_one_call(torch_cuda):
     assert np.array_equal(after2, expected2), first_diff(after2, expected2)
 
 
+def test_copy_shared_kv_back_to_back_without_sync(torch_cuda):
+    """More one-call handoffs in flight than staging slots: the ring wraps onto
+    slots whose launch may still run, and slot buffers grow between calls."""
+    torch = torch_cuda
+    w = W.config3(0)
+    g = w.geometry
+    kv = _kv(g)
+    say(f"pbe_copy_shared_kv back-to-back config3 requests={len(w.requests)}")
+    bufs, view = device_arena(torch, w.arena_bytes, w.segment_bytes)
+    for i, b in enumerate(bufs):
+        fill_bf16(torch, b, w.sigma, 40 + i)
+    torch.cuda.synchronize()
+    expected = snapshot(bufs)
+    # chunks of 1, 2, 4, ... pages: more calls than slots, each larger than the last
+    src, dst = w.src_ids, w.dst_ids
+    total, start, k, calls = 0, 0, 1, 0
+    while start < len(src):
+        s, d = src[start:start + k], dst[start:start + k]
+        total += O.copy_handoff(expected, s, d, g.half(), g.layers)
+        total -= P.copy_shared_kv(view, s, d, kv, 0, stream_ptr(torch))
+        start, k, calls = start + k, 2 * k, calls + 1
+    assert calls > 8
+    torch.cuda.synchronize()
+    assert total == 0
+    after = snapshot(bufs)
+    assert np.array_equal(after, expected), first_diff(after, expected)
+
+
 def test_copy_shared_kv_rejects_bad_ids_before_any_write(torch_cuda):
     torch = torch_cuda
     w = W.small(seed=3, n_pages=32, handoff_pages=5)
