@@ -96,6 +96,48 @@ def _timed(torch, stream, scrub, fn, n):
     return float(np.mean(ts)), float(np.min(ts))
 
 
+def gpu_reference_pattern(torch, stream, scrub, base, runs, g, alg, n, scrub_each):
+    """Times the reference's copy loop as the reference issues it, on this GPU:
+    one hipMemcpyAsync (device to device) per coalesced run, on one stream,
+    between two events, plus the end-to-end time including the host loop and
+    the final stream synchronize. Uses the HIP runtime already loaded by torch."""
+    import ctypes as C
+    import numpy as np
+    hip = C.CDLL("libamdhip64.so.7")
+    hip.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+    hip.hipMemcpyAsync.restype = C.c_int
+    half, page = g.half(), g.page_bytes()
+    calls = [(base + d * half, base + s * half, k * page) for s, d, k in runs]
+    sp = C.c_void_p(stream.cuda_stream)
+
+    def issue():
+        for dst, src, nbytes in calls:
+            rc = hip.hipMemcpyAsync(dst, src, nbytes, 3, sp)  # hipMemcpyDeviceToDevice
+            if rc != 0:
+                raise RuntimeError(f"hipMemcpyAsync failed with {rc}")
+
+    issue()
+    torch.cuda.synchronize()
+    ev, wall = [], []
+    for i in range(n):
+        if scrub_each:
+            scrub.fill_(i & 0xff)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t = time.perf_counter()
+        a.record(stream)
+        issue()
+        b.record(stream)
+        stream.synchronize()
+        wall.append(time.perf_counter() - t)
+        ev.append(a.elapsed_time(b))
+    us = float(np.mean(ev)) * 1e3
+    return {"what": "one hipMemcpyAsync per coalesced run on this GPU (the reference's loop)",
+            "calls": len(calls), "us_mean": round(us, 2),
+            "gbps": round(alg / (us * 1e-6) / 1e9, 1),
+            "e2e_us_p50": round(float(np.median(wall)) * 1e6, 1)}
+
+
 def measure_extra_configs(torch, P, W, scrub, n: int):
     """Kernel timings of the other handoff configurations (parity-test cases,
     reported beside the headline line)."""
@@ -270,6 +312,12 @@ def main() -> int:
         lat.append(time.perf_counter() - t)
     e2e_us = float(np.median(lat) * 1e6)
 
+    # the reference's own GPU pattern on this GPU: one hipMemcpyAsync per
+    # coalesced run (split_pd_engine.cpp:102-108), then a stream sync (:110)
+    refpat = gpu_reference_pattern(torch, stream, scrub, arena.data_ptr(), runs, g, alg,
+                                   max(10, args.steps // 4), not args.no_scrub)
+    refpat["kernel_speedup"] = round(refpat["us_mean"] / (mean_ms * 1e3), 2)
+
     calib = None
     if args.calibrate:
         # one 256 MiB run (1024 pages of 256 KiB) from offset 0 to offset 256 MiB
@@ -331,6 +379,7 @@ def main() -> int:
         "wall_ms_per_step_incl_scrub": round(wall / args.steps * 1e3, 4),
         "grid_threads": int(info.slices) * 64,
     }
+    line["gpu_reference_pattern"] = refpat
     if calib:
         line["calibration_copy"] = calib
     print(json.dumps(line))
