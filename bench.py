@@ -318,6 +318,16 @@ def main() -> int:
                                    max(10, args.steps // 4), not args.no_scrub)
     refpat["kernel_speedup"] = round(refpat["us_mean"] / (mean_ms * 1e3), 2)
 
+    # the same bytes as one contiguous run, same kernel: the difference to
+    # the headline is the cost of the plan's page placement in HBM
+    stride = 2 * g.layers
+    n_arena = w.arena_bytes // g.page_bytes()
+    with P.RunList.bf16(view, view, [(0, stride * (n_arena - w.pages), w.pages)], kv) as crl:
+        c_ms = _timed(torch, stream, scrub, lambda: crl.copy(sp), max(10, args.steps // 4))
+    contiguous = {"what": "same kernel, same bytes, one contiguous run (pages 0.. -> end of arena)",
+                  "us_mean": round(c_ms[0] * 1e3, 2),
+                  "gbps": round(alg / (c_ms[0] * 1e-3) / 1e9, 1)}
+
     calib = None
     if args.calibrate:
         # one 256 MiB run (1024 pages of 256 KiB) from offset 0 to offset 256 MiB
@@ -380,6 +390,7 @@ def main() -> int:
         "grid_threads": int(info.slices) * 64,
     }
     line["gpu_reference_pattern"] = refpat
+    line["contiguous_same_bytes"] = contiguous
     if calib:
         line["calibration_copy"] = calib
     print(json.dumps(line))

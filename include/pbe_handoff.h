@@ -152,6 +152,49 @@ int pbe_build_runs(const int32_t* src_ids, const int32_t* dst_ids, int64_t n,
                    const pbe_kv_shape* shape, uint32_t elem_bytes, uint64_t segment_bytes,
                    pbe_run* out, int64_t* n_runs);
 
+/* ---- compact page-list wire form ---------------------------------------
+ * The prefill result names its KV pages once per layer as JSON integer arrays
+ * (RemotePrefillResult.layers[l].src_block_ids, serving_zmq_rpc.h:80-98,
+ * written by remote_prefill_result_to_json, serving_zmq_rpc.cpp:222-253);
+ * copy_shared_kv then requires all of them to be identical
+ * (split_pd_engine.cpp:78-79). The compact form carries the page-major list
+ * once, as spans of consecutive page ids (next id = id + 2*layers), in
+ * little-endian binary:
+ *   pbe_page_list_header (32 bytes), then n_spans x {int32 first_block, int32 pages}.
+ * `checksum` is FNV-1a (32-bit) over the header with checksum = 0 followed by
+ * the spans, so any single changed byte is rejected. */
+#define PBE_PAGE_LIST_MAGIC 0x50454250u /* bytes "PBEP" */
+#define PBE_PAGE_LIST_VERSION 1u
+
+typedef struct pbe_page_list_header {
+  uint32_t magic;
+  uint16_t version;
+  uint16_t header_bytes; /* 32 */
+  int32_t layers;
+  int32_t n_pages;
+  int32_t n_spans;
+  uint32_t checksum;
+  uint64_t epoch; /* shared_arena_epoch of the prefill result */
+} pbe_page_list_header;
+
+/* Bytes the encoding of `ids` takes (header + spans); 0 if ids are invalid
+ * (negative, not a multiple of 2*layers, or n outside [0, INT32_MAX]). */
+uint64_t pbe_page_list_bytes(const int32_t* ids, int64_t n, int32_t layers);
+
+/* Encodes page-major block ids (each >= 0 and a multiple of 2*layers, in the
+ * prefill's page order) into `out` (capacity `cap`). *out_bytes = bytes
+ * written. PBE_ERR_INVALID on bad ids or too small a buffer (nothing written). */
+int pbe_page_list_encode(const int32_t* ids, int64_t n, int32_t layers, uint64_t epoch, void* out,
+                         uint64_t cap, uint64_t* out_bytes);
+
+/* Checks and decodes a page list. Pass ids = NULL to read only the header
+ * (*n_pages, *layers, *epoch). Otherwise `ids` holds `cap` entries and
+ * receives n_pages ids. Rejects a wrong magic, version or size, a checksum
+ * mismatch, spans with no pages, ids that are negative, not multiples of
+ * 2*layers or beyond INT32_MAX, and span totals that differ from n_pages. */
+int pbe_page_list_decode(const void* data, uint64_t bytes, int32_t* ids, int64_t cap,
+                         int64_t* n_pages, int32_t* layers, uint64_t* epoch);
+
 /* ---- device-resident run lists ----------------------------------------
  * Validated on the host (every run inside one segment of its view, no source
  * range overlapping a destination range), resolved to device addresses and

@@ -53,6 +53,7 @@ ABI_HOST_SOURCES = [
     "csrc/serving/shared_kv_handoff.cpp",
     "csrc/serving/decode_kv_reservation.cpp",
     "csrc/serving/plan_kv_connector.cpp",
+    "csrc/serving/kv_page_wire.cpp",
 ]
 # Sources that call HIP (compiled by hipcc).
 HIP_SOURCES = [

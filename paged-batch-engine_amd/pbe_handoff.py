@@ -92,6 +92,11 @@ _SIGNATURES = [
                                    C.POINTER(C.c_int64)]),
     ("pbe_build_runs", C.c_int, [_P, _P, C.c_int64, C.POINTER(KvShape), C.c_uint32, C.c_uint64,
                                  C.POINTER(Run), C.POINTER(C.c_int64)]),
+    ("pbe_page_list_bytes", C.c_uint64, [_P, C.c_int64, C.c_int32]),
+    ("pbe_page_list_encode", C.c_int, [_P, C.c_int64, C.c_int32, C.c_uint64, _P, C.c_uint64,
+                                       C.POINTER(C.c_uint64)]),
+    ("pbe_page_list_decode", C.c_int, [_P, C.c_uint64, _P, C.c_int64, C.POINTER(C.c_int64),
+                                       C.POINTER(C.c_int32), C.POINTER(C.c_uint64)]),
     ("pbe_runlist_create", C.c_int, [C.POINTER(ArenaView), C.POINTER(ArenaView), C.POINTER(Run),
                                      C.c_int64, C.POINTER(KvShape), C.c_uint32, C.c_int,
                                      C.POINTER(_P)]),
@@ -174,6 +179,31 @@ def build_runs(src_ids, dst_ids, kv: KvShape, elem_bytes: int = 2, segment_bytes
     check(lib().pbe_build_runs(sp, dp, len(s), C.byref(kv), elem_bytes, segment_bytes, out,
                                C.byref(n)))
     return [(out[i].src_block, out[i].dst_block, out[i].pages) for i in range(n.value)]
+
+
+def encode_page_list(ids, layers: int, epoch: int) -> bytes:
+    """Compact wire form of a page-major id list (pbe_page_list_encode)."""
+    a, ap = _i32(ids)
+    need = lib().pbe_page_list_bytes(ap, len(a), layers)
+    if need == 0:
+        raise PbeError(PBE_ERR_INVALID, "ids are not a page-major list")
+    buf = C.create_string_buffer(need)
+    n = C.c_uint64()
+    check(lib().pbe_page_list_encode(ap, len(a), layers, epoch, buf, need, C.byref(n)))
+    return buf.raw[:n.value]
+
+
+def decode_page_list(data: bytes):
+    """(ids, layers, epoch) of a page list; raises PbeError on any defect."""
+    import numpy as np
+    n, layers, epoch = C.c_int64(), C.c_int32(), C.c_uint64()
+    src = C.create_string_buffer(bytes(data), len(data)) if data else C.create_string_buffer(1)
+    check(lib().pbe_page_list_decode(src, len(data), None, 0, C.byref(n), C.byref(layers),
+                                     C.byref(epoch)))
+    ids = np.empty(max(1, n.value), np.int32)
+    check(lib().pbe_page_list_decode(src, len(data), ids.ctypes.data_as(C.c_void_p), n.value,
+                                     C.byref(n), C.byref(layers), C.byref(epoch)))
+    return ids[:n.value], layers.value, epoch.value
 
 
 def validate_ids(ids, kv: KvShape, arena_bytes: int, elem_bytes: int = 2) -> int:

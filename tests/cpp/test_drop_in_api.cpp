@@ -20,6 +20,7 @@
 #include "base/shared_kv_arena.h"
 #include "serving/decode_kv_reservation.h"
 #include "serving/pd_handoff.h"
+#include "serving/kv_page_wire.h"
 
 using namespace cache;
 
@@ -950,6 +951,66 @@ TEST_CASE("bind manifest transfers: FP8 pools add scale components") {
   pool.scales = nullptr;
   std::vector<cache::BoundTransfer> none;
   CHECK(!serving::BindManifestTransfers(m, pool, pool, &planner, &none));
+}
+
+TEST_CASE("kv page wire: per-layer id lists round trip through the compact form") {
+  const int L = 4;
+  std::vector<int32_t> ids = {0, 8, 16, 64, 72, 24, 200, 208, 216, 224};
+  std::vector<serving::RemoteKVLayerPayload> layers;
+  for (int l = 0; l < L; ++l) layers.push_back({l, ids});
+  std::string wire;
+  REQUIRE(serving::EncodeKVPageList(77, layers, &wire));
+  CHECK_EQ(wire.size(), 32u + 4u * 8u);  // spans {0,3} {64,2} {24,1} {200,4}
+  uint64_t epoch = 0;
+  std::vector<serving::RemoteKVLayerPayload> back;
+  REQUIRE(serving::DecodeKVPageList(wire, &epoch, &back));
+  CHECK_EQ(epoch, 77u);
+  REQUIRE(back.size() == layers.size());
+  for (int l = 0; l < L; ++l) {
+    CHECK_EQ(back[l].layer_idx, l);
+    CHECK(back[l].src_block_ids == ids);
+  }
+  int32_t n_layers = 0;
+  std::vector<int32_t> flat;
+  REQUIRE(serving::DecodeKVPageIds(wire, &epoch, &n_layers, &flat));
+  CHECK_EQ(n_layers, L);
+  CHECK(flat == ids);
+  // empty prefix: header only
+  std::vector<serving::RemoteKVLayerPayload> empty{{0, {}}, {1, {}}};
+  REQUIRE(serving::EncodeKVPageList(5, empty, &wire));
+  CHECK_EQ(wire.size(), 32u);
+  REQUIRE(serving::DecodeKVPageList(wire, &epoch, &back));
+  CHECK_EQ(back.size(), 2u);
+  CHECK(back[1].src_block_ids.empty());
+}
+
+TEST_CASE("kv page wire: copy_shared_kv's layer checks and corrupt input are rejected") {
+  std::vector<int32_t> ids = {0, 4, 8};
+  std::vector<serving::RemoteKVLayerPayload> layers{{0, ids}, {1, ids}};
+  std::string wire;
+  auto bad = layers;
+  bad[1].src_block_ids[2] = 12;
+  CHECK(!serving::EncodeKVPageList(1, bad, &wire));  // layers disagree
+  CHECK(wire.empty());
+  bad = layers;
+  bad[1].layer_idx = 0;
+  CHECK(!serving::EncodeKVPageList(1, bad, &wire));  // layer order
+  bad = layers;
+  bad[0].src_block_ids[1] = bad[1].src_block_ids[1] = 6;  // not a multiple of 2L = 4
+  CHECK(!serving::EncodeKVPageList(1, bad, &wire));
+  CHECK(!serving::EncodeKVPageList(1, {}, &wire));
+  REQUIRE(serving::EncodeKVPageList(9, layers, &wire));
+  uint64_t epoch = 0;
+  std::vector<serving::RemoteKVLayerPayload> back;
+  for (size_t i = 0; i < wire.size(); ++i) {
+    std::string w = wire;
+    w[i] = static_cast<char>(w[i] ^ 0x10);
+    CHECK(!serving::DecodeKVPageList(w, &epoch, &back));
+    CHECK(back.empty());
+  }
+  CHECK(!serving::DecodeKVPageList(wire.substr(0, wire.size() - 1), &epoch, &back));
+  CHECK(!serving::DecodeKVPageList(wire + std::string(8, '\0'), &epoch, &back));
+  CHECK(!serving::DecodeKVPageList(std::string(), &epoch, &back));
 }
 
 MINITEST_MAIN()
