@@ -88,7 +88,7 @@ ChunkLease GlobalChunkAllocator::acquire(const std::string& model, const std::st
   return lease;
 }
 
-void GlobalChunkAllocator::release(const ChunkLease& lease) {
+const ChunkLease& GlobalChunkAllocator::live_lease(const ChunkLease& lease) const {
   auto live = leases_.find(lease.id);
   if (lease.epoch != epoch_ || live == leases_.end())
     throw std::invalid_argument("stale_or_duplicate_chunk_release");
@@ -96,6 +96,38 @@ void GlobalChunkAllocator::release(const ChunkLease& lease) {
   if (held.generation != lease.generation || held.model != lease.model ||
       held.layout != lease.layout || held.offset != lease.offset || held.bytes != lease.bytes)
     throw std::invalid_argument("chunk_identity_mismatch");
+  return held;
+}
+
+std::vector<ChunkLease> GlobalChunkAllocator::transfer(const std::vector<ChunkLease>& leases,
+                                                       const std::string& to_model) {
+  auto target = quotas_.find(to_model);
+  if (target == quotas_.end()) throw std::invalid_argument("invalid chunk transfer target");
+  uint64_t bytes = 0;
+  std::unordered_map<uint64_t, int> seen;
+  for (const ChunkLease& lease : leases) {
+    const ChunkLease& held = live_lease(lease);
+    if (held.model == to_model || seen[held.id]++) throw std::invalid_argument("invalid chunk transfer");
+    bytes += held.bytes;
+  }
+  if (bytes > target->second.limit - target->second.used)
+    throw ChunkAllocationError(ChunkAllocationFailure::kQuota);
+  std::vector<ChunkLease> moved;
+  moved.reserve(leases.size());
+  for (const ChunkLease& lease : leases) {
+    ChunkLease& held = leases_.at(lease.id);
+    quotas_.at(held.model).used -= held.bytes;
+    target->second.used += held.bytes;
+    held.model = to_model;
+    held.generation = next_generation_++;
+    moved.push_back(held);
+  }
+  return moved;
+}
+
+void GlobalChunkAllocator::release(const ChunkLease& lease) {
+  const ChunkLease& held = live_lease(lease);
+  auto live = leases_.find(held.id);
 
   uint64_t start = held.offset, length = held.bytes;
   quotas_.at(held.model).used -= length;

@@ -31,6 +31,17 @@ void LocalChunkOwner::release(const ChunkLease& lease) {
   allocator_.release(lease);
 }
 
+std::vector<ChunkLease> LocalChunkOwner::transfer(const std::vector<ChunkLease>& leases,
+                                                  const std::string& to_model) {
+  std::lock_guard<std::mutex> lock(mu_);
+  return allocator_.transfer(leases, to_model);
+}
+
+uint64_t LocalChunkOwner::leased_bytes(const std::string& model) const {
+  std::lock_guard<std::mutex> lock(mu_);
+  return allocator_.leased_bytes(model);
+}
+
 uint64_t LocalChunkOwner::free_bytes() const {
   std::lock_guard<std::mutex> lock(mu_);
   return allocator_.free_bytes();
@@ -68,6 +79,20 @@ ChunkLease SharedKVArenaClient::acquire(const std::string& layout, uint64_t byte
 
 void SharedKVArenaClient::release(const ChunkLease& lease) { owner_->release(lease); }
 
+std::vector<ChunkLease> SharedKVArenaClient::take_over(const std::vector<ChunkLease>& leases) {
+  std::vector<ChunkLease> moved = owner_->transfer(leases, model_);
+  if (moved.size() != leases.size()) throw std::runtime_error("invalid owner chunk descriptor");
+  for (size_t i = 0; i < moved.size(); ++i) {
+    const ChunkLease& m = moved[i];
+    const ChunkLease& o = leases[i];
+    if (m.epoch != owner_->epoch() || m.id != o.id || m.generation == o.generation || m.model != model_ ||
+        m.layout != o.layout || m.offset != o.offset || m.bytes != o.bytes || m.offset > view_.bytes ||
+        m.bytes > view_.bytes - m.offset)
+      throw std::runtime_error("invalid owner chunk descriptor");
+  }
+  return moved;
+}
+
 // ------------------------------------------------------------ SharedKVPageGroup
 
 struct SharedKVPageGroup::Impl {
@@ -92,6 +117,7 @@ struct SharedKVPageGroup::Impl {
   void* stream = nullptr;
   std::string layout;
   std::unordered_map<uint64_t, std::unique_ptr<Chunk>> chunks;  // by lease id
+  std::unordered_map<uint64_t, std::unique_ptr<Chunk>> detached;  // handed to a receiver
   std::unordered_map<int, Page*> pages;                         // by page id
   std::set<int> free_ids;
   std::deque<Page*> retiring;
@@ -300,6 +326,137 @@ void SharedKVPageGroup::retire(int layer, int id) {
     m.retiring.push_back(&p);
     m.collect_locked();
   }
+}
+
+void SharedKVPageGroup::detach_for_takeover(const std::vector<int32_t>& ids, PageTakeover* out) {
+  if (out == nullptr) throw std::invalid_argument("takeover output is null");
+  std::lock_guard<std::mutex> lock(impl_->mu);
+  Impl& m = *impl_;
+  if (m.failed) throw std::runtime_error("shared KV page group failed; stop GPU domain");
+  *out = PageTakeover{};
+  std::unordered_map<int, int> listed;
+  std::unordered_map<Impl::Chunk*, size_t> touched;
+  for (int32_t id : ids) {
+    auto found = m.pages.find(id);
+    if (found == m.pages.end()) throw std::logic_error("takeover page does not belong to this group");
+    const Impl::Page& p = *found->second;
+    if (p.active_layers != m.layers || p.retiring ||
+        std::any_of(p.reserved.begin(), p.reserved.end(), [](char r) { return r != 0; }))
+      throw std::logic_error("takeover page is not active in every layer");
+    if (listed[id]++) throw std::logic_error("takeover page listed twice");
+    ++touched[p.chunk];
+  }
+  // Decide per Chunk before changing anything.
+  std::unordered_map<Impl::Chunk*, bool> movable;
+  for (const auto& entry : touched) {
+    bool whole = true;
+    for (const Impl::Page& q : entry.first->pages) {
+      const int qid = m.id_of(q);
+      if (!listed.count(qid) && !m.free_ids.count(qid)) {
+        whole = false;
+        break;
+      }
+    }
+    movable[entry.first] = whole;
+  }
+  out->epoch = m.arena->epoch();
+  out->from_model = m.arena->model();
+  out->page_ids = ids;
+  for (int32_t id : ids) {
+    if (movable[m.pages.at(id)->chunk]) out->moved_ids.push_back(id);
+    else out->copy_ids.push_back(id);
+  }
+  for (const auto& entry : movable) {
+    if (!entry.second) continue;
+    Impl::Chunk* c = entry.first;
+    out->chunks.push_back(c->lease);
+    for (const Impl::Page& q : c->pages) {
+      m.free_ids.erase(m.id_of(q));
+      m.pages.erase(m.id_of(q));
+    }
+    m.leased -= c->lease.bytes;
+    auto node = m.chunks.find(c->lease.id);
+    m.detached.emplace(c->lease.id, std::move(node->second));
+    m.chunks.erase(node);
+  }
+  std::sort(out->chunks.begin(), out->chunks.end(),
+            [](const ChunkLease& a, const ChunkLease& b) { return a.offset < b.offset; });
+}
+
+void SharedKVPageGroup::reattach(const PageTakeover& t) {
+  std::lock_guard<std::mutex> lock(impl_->mu);
+  Impl& m = *impl_;
+  for (const ChunkLease& lease : t.chunks)
+    if (!m.detached.count(lease.id) || m.detached.at(lease.id)->lease.generation != lease.generation)
+      throw std::logic_error("reattach of a Chunk this group did not detach");
+  std::set<int> moved(t.moved_ids.begin(), t.moved_ids.end());
+  for (const ChunkLease& lease : t.chunks) {
+    auto node = m.detached.find(lease.id);
+    Impl::Chunk* c = node->second.get();
+    for (Impl::Page& q : c->pages) {
+      const int qid = m.id_of(q);
+      m.pages.emplace(qid, &q);
+      if (!moved.count(qid)) m.free_ids.insert(qid);
+    }
+    m.leased += c->lease.bytes;
+    m.chunks.emplace(lease.id, std::move(node->second));
+    m.detached.erase(node);
+  }
+}
+
+void SharedKVPageGroup::finish_takeover(const PageTakeover& t) {
+  std::lock_guard<std::mutex> lock(impl_->mu);
+  for (const ChunkLease& lease : t.chunks) impl_->detached.erase(lease.id);
+}
+
+size_t SharedKVPageGroup::adopt(const PageTakeover& t) {
+  std::lock_guard<std::mutex> lock(impl_->mu);
+  Impl& m = *impl_;
+  if (m.failed) throw std::runtime_error("shared KV page group failed; stop GPU domain");
+  if (t.epoch != m.arena->epoch()) throw std::invalid_argument("PD arena epoch mismatch");
+  uint64_t bytes = 0;
+  std::set<int> in_chunks;
+  for (const ChunkLease& lease : t.chunks) {
+    if (lease.layout != m.layout || lease.offset % m.page || !lease.bytes || lease.bytes % m.page)
+      throw std::invalid_argument("PD shared layout mismatch");
+    for (uint64_t off = lease.offset; off < lease.offset + lease.bytes; off += m.page) {
+      const int id = static_cast<int>(off / m.half);
+      if (m.pages.count(id)) throw std::logic_error("takeover Chunk overlaps this group's pages");
+      in_chunks.insert(id);
+    }
+    bytes += lease.bytes;
+  }
+  std::set<int> moved;
+  for (int32_t id : t.moved_ids)
+    if (!in_chunks.count(id) || !moved.insert(id).second)
+      throw std::invalid_argument("takeover page outside its Chunks");
+  if (bytes > m.arena->hard_limit() - m.leased) throw ChunkAllocationError(ChunkAllocationFailure::kQuota);
+  const std::vector<ChunkLease> held = m.arena->take_over(t.chunks);  // all or nothing
+  for (const ChunkLease& lease : held) {
+    auto chunk = std::make_unique<Impl::Chunk>();
+    chunk->lease = lease;
+    chunk->pages.resize(lease.bytes / m.page);
+    chunk->free_pages = 0;
+    for (size_t i = 0; i < chunk->pages.size(); ++i) {
+      Impl::Page& p = chunk->pages[i];
+      p.offset = lease.offset + i * m.page;
+      p.reserved.assign(m.layers, 0);
+      p.chunk = chunk.get();
+      const int id = m.id_of(p);
+      if (moved.count(id)) {
+        p.active.assign(m.layers, 1);
+        p.active_layers = m.layers;
+      } else {
+        p.active.assign(m.layers, 0);
+        m.free_ids.insert(id);
+        ++chunk->free_pages;
+      }
+      m.pages.emplace(id, &p);
+    }
+    m.leased += lease.bytes;
+    m.chunks.emplace(lease.id, std::move(chunk));
+  }
+  return moved.size();
 }
 
 int SharedKVPageGroup::free_blocks(int layer) const {

@@ -3,6 +3,7 @@
 #include <algorithm>
 #include <stdexcept>
 #include <string>
+#include <unordered_map>
 
 #include "serving/pd_handoff.h"
 
@@ -49,6 +50,50 @@ base::Status CopySharedKV(const SharedArenaBinding& arena, uint64_t source_epoch
   if (rc != PBE_OK) return abi_error("PD copy launch failed; discard the IPC domain");
   if (copied) *copied = bytes;
   return base::error::Success();
+}
+
+base::Status TakeOverSharedKV(base::SharedKVPageGroup* group, const SharedArenaBinding& arena,
+                              const base::SharedKVPageGroup::PageTakeover& takeover,
+                              const KVPoolDescriptor& pool, void* stream,
+                              std::vector<int32_t>* block_table, uint64_t* copied) {
+  if (copied) *copied = 0;
+  if (!group || !block_table) return InvalidArgument("takeover group or block table is null");
+  block_table->clear();
+  if (pool.layer_num != group->layers()) return InvalidArgument("PD layer count mismatch");
+  try {
+    group->adopt(takeover);
+  } catch (const base::ChunkAllocationError& e) {
+    return InvalidArgument(e.what());
+  } catch (const std::exception& e) {
+    return InvalidArgument(e.what());
+  }
+  const int layers = group->layers();
+  std::vector<int32_t> fresh;
+  for (size_t i = 0; i < takeover.copy_ids.size(); ++i) {
+    const int id = group->allocate(0);
+    if (id < 0) {
+      for (int32_t f : fresh) group->retire(0, f);  // layer 0 retire rolls back the reservations
+      return InvalidArgument("model_kv_quota_exhausted");
+    }
+    fresh.push_back(id);
+  }
+  for (int l = 1; l < layers; ++l)
+    for (size_t i = 0; i < fresh.size(); ++i) group->allocate(l);
+  std::unordered_map<int32_t, int32_t> replace;
+  for (size_t i = 0; i < fresh.size(); ++i) replace[takeover.copy_ids[i]] = fresh[i];
+  for (int32_t id : takeover.page_ids) {
+    auto r = replace.find(id);
+    block_table->push_back(r == replace.end() ? id : r->second);
+  }
+  if (fresh.empty()) return base::error::Success();
+  KVBlockManifest manifest;
+  manifest.client_request_id.value = "page-takeover";
+  manifest.handoff_id.value = 1;
+  manifest.src_pool = manifest.dst_pool = pool;
+  manifest.computed_tokens = static_cast<int32_t>(fresh.size()) * pool.block_size;
+  manifest.prompt_tokens = manifest.computed_tokens;
+  for (int l = 0; l < layers; ++l) manifest.layer_mappings.push_back({l, takeover.copy_ids, fresh});
+  return CopySharedKV(arena, takeover.epoch, manifest, stream, copied);
 }
 
 SharedArenaKVTransferConnector::SharedArenaKVTransferConnector(SharedArenaBinding arena, void* stream)

@@ -12,6 +12,7 @@
 #include <stdexcept>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 namespace base {
 
@@ -50,6 +51,15 @@ class GlobalChunkAllocator {
   // foreign epoch or unknown id and ("chunk_identity_mismatch") when any other
   // field differs from the live lease.
   void release(const ChunkLease& lease);
+  // Zero-copy page takeover (no counterpart in the reference, whose decode
+  // side always copies, docs/single-gpu-2p1d-2026-10-12.md:34): re-attributes
+  // the live Chunks `leases` (as their holder sees them) to `to_model`, all or
+  // nothing. Same identity checks as release(); std::invalid_argument for an
+  // unknown target model, a Chunk listed twice or one already held by
+  // `to_model`; ChunkAllocationError kQuota when the target's limit cannot take
+  // their bytes. Returns the new leases (same id, offset, bytes and layout, a
+  // fresh generation, model = to_model): the old identities become stale.
+  std::vector<ChunkLease> transfer(const std::vector<ChunkLease>& leases, const std::string& to_model);
   uint64_t free_bytes() const;
   uint64_t leased_bytes(const std::string& model) const;
   uint64_t epoch() const { return epoch_; }
@@ -61,6 +71,7 @@ class GlobalChunkAllocator {
     uint64_t limit = 0;
     uint64_t used = 0;
   };
+  const ChunkLease& live_lease(const ChunkLease& lease) const;  // identity checks of release()
   uint64_t bytes_, epoch_, next_generation_ = 1;
   std::map<uint64_t, uint64_t> free_;  // offset -> length, disjoint, never adjacent
   std::unordered_map<uint64_t, ChunkLease> leases_;

@@ -19,6 +19,7 @@
 #include <memory>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "base/global_chunk_allocator.h"
 #include "pbe_handoff.h"
@@ -34,6 +35,11 @@ class ChunkOwner {
                              uint64_t alignment) = 0;
   // The caller guarantees every GPU access to the Chunk has completed.
   virtual void release(const ChunkLease& lease) = 0;
+  // Re-attributes live Chunks to `to_model`, all or nothing
+  // (GlobalChunkAllocator::transfer). The caller presents the identities the
+  // current holder sees; they become stale.
+  virtual std::vector<ChunkLease> transfer(const std::vector<ChunkLease>& leases,
+                                           const std::string& to_model) = 0;
   virtual uint64_t bytes() const = 0;
   virtual uint64_t epoch() const = 0;
 };
@@ -46,7 +52,10 @@ class LocalChunkOwner final : public ChunkOwner {
   ChunkLease acquire(const std::string& model, const std::string& layout, uint64_t bytes,
                      uint64_t alignment) override;
   void release(const ChunkLease& lease) override;
+  std::vector<ChunkLease> transfer(const std::vector<ChunkLease>& leases,
+                                   const std::string& to_model) override;
   uint64_t bytes() const override { return allocator_.bytes(); }
+  uint64_t leased_bytes(const std::string& model) const;
   uint64_t epoch() const override { return allocator_.epoch(); }
   uint64_t free_bytes() const;
   size_t lease_count() const;
@@ -69,6 +78,9 @@ class SharedKVArenaClient {
   // Leases a Chunk and checks the owner's answer (shared_kv_client.cpp:102-111).
   ChunkLease acquire(const std::string& layout, uint64_t bytes, uint64_t alignment);
   void release(const ChunkLease& lease);  // caller has completed every GPU access
+  // Takes over Chunks another model holds (zero-copy page takeover) and
+  // checks the owner's answer like acquire().
+  std::vector<ChunkLease> take_over(const std::vector<ChunkLease>& leases);
   // Base of a single-segment arena (nullptr when segmented: use view()).
   void* data() const;
   const pbe_arena_view& view() const { return view_; }
@@ -118,6 +130,38 @@ class SharedKVPageGroup {
   void* value_base(int layer) const;
   // Returns completed pages, and Chunks whose pages are all free, to the owner.
   void collect();
+
+  // ---- zero-copy page takeover (no counterpart in the reference: its decode
+  // side copies every page, docs/single-gpu-2p1d-2026-10-12.md:34) ----
+  //
+  // Source side. `ids` are pages of one finished request, active in every
+  // layer. A Chunk whose every page is either in `ids` or free moves whole:
+  // the group stops using it (its pages leave the group; it is neither
+  // allocated from nor returned to the owner) and lists its lease in
+  // takeover->chunks. Pages of Chunks still shared with live pages stay here
+  // and are listed in takeover->copy_ids: the receiver copies those and this
+  // group retires them afterwards as usual. The caller orders the receiver's
+  // reads after this group's writes (a fence or signal on `stream`).
+  struct PageTakeover {
+    uint64_t epoch = 0;
+    std::string from_model;
+    std::vector<ChunkLease> chunks;  // identities as this group held them
+    std::vector<int32_t> page_ids;   // the request's pages, in order
+    std::vector<int32_t> moved_ids;  // page_ids inside moved Chunks (page order)
+    std::vector<int32_t> copy_ids;   // page_ids the receiver must copy
+  };
+  void detach_for_takeover(const std::vector<int32_t>& ids, PageTakeover* takeover);
+  // Receiver side: asks the owner to re-attribute the Chunks to this group's
+  // model (all or nothing; ChunkAllocationError kQuota propagates and nothing
+  // changes), then holds them: pages in moved_ids become active in every
+  // layer, as if allocated, and the Chunks' other pages become free pages of
+  // this group. Returns the number of pages taken over.
+  size_t adopt(const PageTakeover& takeover);
+  // Source side, when the receiver could not adopt: takes the Chunks back
+  // exactly as they were detached.
+  void reattach(const PageTakeover& takeover);
+  // Source side, once the receiver has adopted: forgets the detached Chunks.
+  void finish_takeover(const PageTakeover& takeover);
   uint64_t half_bytes() const;
   uint64_t page_bytes() const;
   int layers() const;

@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "base/base.h"
+#include "base/shared_kv_arena.h"
 #include "base/kv_cache_format.h"
 #include "cache/transfer_plan.h"
 #include "pbe_handoff.h"
@@ -100,6 +101,20 @@ struct SharedArenaBinding {
 // happens before any device work, so an error leaves the arena untouched.
 base::Status CopySharedKV(const SharedArenaBinding& arena, uint64_t source_epoch,
                           const KVBlockManifest& manifest, void* stream, uint64_t* copied);
+
+// Zero-copy handoff, receiver side (no counterpart in the reference, whose
+// decode side copies every page: docs/single-gpu-2p1d-2026-10-12.md:34).
+// `takeover` comes from the prefill group's detach_for_takeover(). The decode
+// group adopts the moved Chunks (their pages are used in place), allocates
+// its own pages for takeover.copy_ids and copies those with one kernel on
+// `stream` (CopySharedKV). *block_table = the request's page ids in order,
+// moved ids unchanged, copied ids replaced by the new ones; *copied = bytes
+// copied. On a refused adoption (receiver quota) nothing changes here and the
+// prefill side calls reattach(); the caller may then fall back to a full copy.
+base::Status TakeOverSharedKV(base::SharedKVPageGroup* decode_group, const SharedArenaBinding& arena,
+                              const base::SharedKVPageGroup::PageTakeover& takeover,
+                              const KVPoolDescriptor& pool, void* stream,
+                              std::vector<int32_t>* block_table, uint64_t* copied);
 
 // A KV pool laid out page-major in an arena mapping (the shared-arena layout):
 // the K plane of layer l of block id b is at byte (2l + b)*half, the V plane

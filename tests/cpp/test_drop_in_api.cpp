@@ -1013,4 +1013,148 @@ TEST_CASE("kv page wire: copy_shared_kv's layer checks and corrupt input are rej
   CHECK(!serving::DecodeKVPageList(std::string(), &epoch, &back));
 }
 
+namespace {
+// Prefill ("p") and decode ("d") page groups over one owner; 3 layers, page
+// 24 KiB, Chunks of 3 pages.
+struct TwoGroups {
+  static constexpr uint64_t kHalf = 4096, kPage = 6 * 4096;
+  std::shared_ptr<base::LocalChunkOwner> owner;
+  std::shared_ptr<base::SharedKVArenaClient> pc, dc;
+  std::unique_ptr<base::SharedKVPageGroup> p, d;
+  TwoGroups(uint64_t arena_pages, uint64_t p_limit, uint64_t d_limit) {
+    owner = std::make_shared<base::LocalChunkOwner>(arena_pages * kPage, 11);
+    owner->register_model("p", p_limit * kPage);
+    owner->register_model("d", d_limit * kPage);
+    pc = std::make_shared<base::SharedKVArenaClient>(owner, fake_view(arena_pages * kPage), "p",
+                                                     p_limit * kPage, -1);
+    dc = std::make_shared<base::SharedKVArenaClient>(owner, fake_view(arena_pages * kPage), "d",
+                                                     d_limit * kPage, -1);
+    p = std::make_unique<base::SharedKVPageGroup>(pc, 3, kHalf, 3 * kPage, nullptr);
+    d = std::make_unique<base::SharedKVPageGroup>(dc, 3, kHalf, 3 * kPage, nullptr);
+  }
+  // Allocates n pages in every layer of group g, as a model does.
+  static std::vector<int32_t> alloc(base::SharedKVPageGroup& g, int n) {
+    std::vector<int32_t> ids;
+    for (int i = 0; i < n; ++i) ids.push_back(g.allocate(0));
+    for (int l = 1; l < 3; ++l)
+      for (int i = 0; i < n; ++i) CHECK_EQ(g.allocate(l), ids[i]);
+    return ids;
+  }
+  static void retire_all(base::SharedKVPageGroup& g, const std::vector<int32_t>& ids) {
+    for (int32_t id : ids)
+      for (int l = 0; l < 3; ++l) g.retire(l, id);
+  }
+};
+}  // namespace
+
+TEST_CASE("chunk allocator: transfer moves quota and identity, all or nothing") {
+  base::GlobalChunkAllocator a(100, 5);
+  a.register_model("p", 60);
+  a.register_model("d", 40);
+  auto x = a.acquire("p", "L", 20, 10);
+  auto y = a.acquire("p", "L", 30, 10);
+  CHECK_THROWS_AS(a.transfer({x, y}, "d"), base::ChunkAllocationError);  // 50 > 40
+  CHECK_EQ(a.leased_bytes("p"), 50u);
+  CHECK_EQ(a.leased_bytes("d"), 0u);
+  CHECK_THROWS_AS(a.transfer({y, y}, "d"), std::invalid_argument);
+  CHECK_THROWS_AS(a.transfer({y}, "p"), std::invalid_argument);
+  CHECK_THROWS_AS(a.transfer({y}, "nobody"), std::invalid_argument);
+  auto moved = a.transfer({x}, "d");
+  REQUIRE(moved.size() == 1u);
+  CHECK_EQ(moved[0].id, x.id);
+  CHECK_EQ(moved[0].offset, x.offset);
+  CHECK_EQ(moved[0].bytes, x.bytes);
+  CHECK(moved[0].generation != x.generation);
+  CHECK_EQ(moved[0].model, std::string("d"));
+  CHECK_EQ(a.leased_bytes("p"), 30u);
+  CHECK_EQ(a.leased_bytes("d"), 20u);
+  CHECK_EQ(a.lease_count(), 2u);
+  CHECK_THROWS_AS(a.release(x), std::invalid_argument);  // the old holder's identity is stale
+  auto z = a.acquire("d", "L", 10, 10);
+  CHECK(z.id != x.id && z.id != y.id && z.id != moved[0].id);
+  a.release(moved[0]);
+  a.release(y);
+  a.release(z);
+  CHECK_EQ(a.free_bytes(), 100u);
+}
+
+TEST_CASE("page takeover: exclusive Chunks move whole, shared ones are copied") {
+  TwoGroups t(30, 15, 15);
+  // request A: 4 pages (Chunks {0,1,2} and {3,4,5}); request B: 1 page, sharing Chunk 2
+  auto a = TwoGroups::alloc(*t.p, 4);
+  auto b = TwoGroups::alloc(*t.p, 1);
+  CHECK_EQ(a[0], 0);
+  CHECK_EQ(b[0], 4 * 6);
+  CHECK_EQ(t.owner->leased_bytes("p"), 6 * TwoGroups::kPage);
+  base::SharedKVPageGroup::PageTakeover tk;
+  t.p->detach_for_takeover(a, &tk);
+  REQUIRE(tk.chunks.size() == 1u);                 // Chunk {0,1,2}; page 3 shares a Chunk with B
+  CHECK(tk.moved_ids == std::vector<int32_t>({0, 6, 12}));
+  CHECK(tk.copy_ids == std::vector<int32_t>({18}));
+  CHECK_EQ(t.p->leased_bytes(), 3 * TwoGroups::kPage);
+  CHECK_THROWS_AS(t.p->retire(0, 0), std::logic_error);  // no longer the source's page
+  CHECK_EQ(t.d->adopt(tk), 3u);
+  t.p->finish_takeover(tk);
+  CHECK_EQ(t.owner->leased_bytes("p"), 3 * TwoGroups::kPage);
+  CHECK_EQ(t.owner->leased_bytes("d"), 3 * TwoGroups::kPage);
+  CHECK_EQ(t.d->leased_bytes(), 3 * TwoGroups::kPage);
+  // the receiver uses and retires the pages like its own
+  auto more = TwoGroups::alloc(*t.d, 1);             // a fresh Chunk of its own
+  CHECK(std::find(tk.moved_ids.begin(), tk.moved_ids.end(), more[0]) == tk.moved_ids.end());
+  const size_t leases = t.owner->lease_count();
+  TwoGroups::retire_all(*t.d, tk.moved_ids);
+  t.d->collect();
+  CHECK_EQ(t.owner->lease_count(), leases - 1);      // the adopted Chunk went back to the owner
+  CHECK_EQ(t.owner->leased_bytes("d"), 3 * TwoGroups::kPage);
+  // the source still retires the copied page and B normally
+  TwoGroups::retire_all(*t.p, {18});
+  TwoGroups::retire_all(*t.p, b);
+  t.p->collect();
+  CHECK_EQ(t.owner->leased_bytes("p"), 0u);
+}
+
+TEST_CASE("page takeover: refused adoption leaves both sides as they were") {
+  TwoGroups t(30, 15, 2);                            // receiver limit: 2 pages
+  auto a = TwoGroups::alloc(*t.p, 3);
+  base::SharedKVPageGroup::PageTakeover tk;
+  t.p->detach_for_takeover(a, &tk);
+  REQUIRE(tk.chunks.size() == 1u);
+  CHECK_THROWS_AS(t.d->adopt(tk), base::ChunkAllocationError);
+  CHECK_EQ(t.owner->leased_bytes("d"), 0u);
+  CHECK_EQ(t.d->leased_bytes(), 0u);
+  t.p->reattach(tk);
+  CHECK_EQ(t.p->leased_bytes(), 3 * TwoGroups::kPage);
+  TwoGroups::retire_all(*t.p, a);                    // the source owns them again
+  t.p->collect();
+  CHECK_EQ(t.owner->leased_bytes("p"), 0u);
+  CHECK_EQ(t.owner->lease_count(), 0u);
+}
+
+TEST_CASE("page takeover: stale identities, bad inputs and geometry mismatches are rejected") {
+  TwoGroups t(30, 15, 15);
+  auto a = TwoGroups::alloc(*t.p, 3);
+  base::SharedKVPageGroup::PageTakeover tk;
+  CHECK_THROWS_AS(t.p->detach_for_takeover({a[0], a[0]}, &tk), std::logic_error);
+  CHECK_THROWS_AS(t.p->detach_for_takeover({7}, &tk), std::logic_error);
+  const int half = t.p->allocate(0);                 // layer 0 only: not a finished page
+  CHECK_THROWS_AS(t.p->detach_for_takeover({half}, &tk), std::logic_error);
+  t.p->retire(0, half);
+  t.p->detach_for_takeover(a, &tk);
+  auto old = tk.chunks;
+  REQUIRE(t.d->adopt(tk) == 3u);
+  CHECK_THROWS_AS(t.owner->release(old[0]), std::invalid_argument);  // the source's identity is stale
+  CHECK_THROWS_AS(t.d->adopt(tk), std::logic_error);                 // already held
+  auto wrong = tk;
+  wrong.epoch = 99;
+  CHECK_THROWS_AS(t.d->adopt(wrong), std::invalid_argument);
+  // a receiver with another geometry refuses the Chunk before asking the owner
+  base::SharedKVPageGroup other(t.dc, 2, TwoGroups::kHalf, 3 * TwoGroups::kPage, nullptr);
+  base::SharedKVPageGroup::PageTakeover tk2;
+  auto b = TwoGroups::alloc(*t.p, 3);
+  t.p->detach_for_takeover(b, &tk2);
+  CHECK_THROWS_AS(other.adopt(tk2), std::invalid_argument);
+  t.p->reattach(tk2);
+  TwoGroups::retire_all(*t.p, b);
+}
+
 MINITEST_MAIN()

@@ -364,4 +364,87 @@ TEST_CASE("end to end: prefill pages -> decode reservation -> connector copy -> 
   CHECK(pbe_arena_destroy(arena) == PBE_OK);
 }
 
+TEST_CASE("zero-copy takeover: moved Chunks are read in place, shared pages are copied") {
+  // Qwen2.5-0.5B geometry, 3-page Chunks: request A = 5 pages, request B = 1
+  // page in A's last Chunk, so A's pages 3-4 must be copied and 0-2 move.
+  const int layers = 24;
+  const uint64_t half = 16 * 2 * 64 * 2, page = 2 * layers * half;
+  const uint64_t arena_bytes = 48 * page;
+  pbe_arena* arena = nullptr;
+  REQUIRE(pbe_arena_create(0, arena_bytes, 16 * page, 5151, &arena) == PBE_OK);  // 3 segments
+  pbe_arena_view view{};
+  REQUIRE(pbe_arena_get_view(arena, &view) == PBE_OK);
+  auto owner = std::make_shared<base::LocalChunkOwner>(arena_bytes, 5151);
+  owner->register_model("prefill", 24 * page);
+  owner->register_model("decode", 24 * page);
+  void* p_stream = nullptr;
+  void* d_stream = nullptr;
+  REQUIRE(pbe_stream_create(0, &p_stream) == PBE_OK);
+  REQUIRE(pbe_stream_create(0, &d_stream) == PBE_OK);
+  auto addr = [&](int32_t id) {
+    const uint64_t off = static_cast<uint64_t>(id) * half;
+    return static_cast<uint8_t*>(view.base[off / view.segment_bytes]) + off % view.segment_bytes;
+  };
+  {
+    auto p_client = std::make_shared<base::SharedKVArenaClient>(owner, view, "prefill", 24 * page, 0);
+    auto d_client = std::make_shared<base::SharedKVArenaClient>(owner, view, "decode", 24 * page, 0);
+    base::SharedKVPageGroup p_pages(p_client, layers, half, 3 * page, p_stream);
+    base::SharedKVPageGroup d_pages(d_client, layers, half, 3 * page, d_stream);
+    auto alloc = [&](int n) {
+      std::vector<int32_t> ids;
+      for (int i = 0; i < n; ++i) ids.push_back(p_pages.allocate(0));
+      for (int l = 1; l < layers; ++l)
+        for (int i = 0; i < n; ++i) CHECK_EQ(p_pages.allocate(l), ids[i]);
+      return ids;
+    };
+    auto a = alloc(5);
+    auto b = alloc(1);
+    std::vector<uint8_t> host(page);
+    for (size_t i = 0; i < a.size(); ++i) {
+      for (uint64_t k = 0; k < page; ++k) host[k] = static_cast<uint8_t>((k * 7 + i * 31) >> 3);
+      HIP_OK(hipMemcpy(addr(a[i]), host.data(), page, hipMemcpyHostToDevice));
+    }
+    base::SharedKVPageGroup::PageTakeover tk;
+    p_pages.detach_for_takeover(a, &tk);
+    CHECK_EQ(tk.moved_ids.size(), 3u);
+    CHECK_EQ(tk.copy_ids.size(), 2u);
+    serving::KVPoolDescriptor pool{0, layers, 16, 2, 64, base::DataType::kDataTypeBf16,
+                                   base::BlockStorageMode::kPlain};
+    serving::SharedArenaBinding binding{view, 5151, 0};
+    std::vector<int32_t> table;
+    uint64_t copied = 0;
+    REQUIRE(serving::TakeOverSharedKV(&d_pages, binding, tk, pool, d_stream, &table, &copied));
+    p_pages.finish_takeover(tk);
+    CHECK_EQ(copied, 2 * page);
+    REQUIRE(table.size() == a.size());
+    for (int i = 0; i < 3; ++i) CHECK_EQ(table[i], a[i]);  // used in place
+    REQUIRE(pbe_stream_synchronize(0, d_stream) == PBE_OK);
+    for (size_t i = 0; i < a.size(); ++i) {
+      HIP_OK(hipMemcpy(host.data(), addr(table[i]), page, hipMemcpyDeviceToHost));
+      bool ok = true;
+      for (uint64_t k = 0; k < page && ok; ++k) ok = host[k] == static_cast<uint8_t>((k * 7 + i * 31) >> 3);
+      CHECK(ok);
+    }
+    CHECK_EQ(owner->leased_bytes("decode"), 6 * page);  // adopted Chunk + a Chunk for the 2 copies
+    CHECK_EQ(owner->leased_bytes("prefill"), 3 * page);
+    // prefill retires the copied pages and B; decode retires the whole request
+    for (int l = 0; l < layers; ++l) {
+      for (int32_t id : tk.copy_ids) p_pages.retire(l, id);
+      for (int32_t id : b) p_pages.retire(l, id);
+      for (int32_t id : table) d_pages.retire(l, id);
+    }
+    REQUIRE(pbe_stream_synchronize(0, p_stream) == PBE_OK);
+    REQUIRE(pbe_stream_synchronize(0, d_stream) == PBE_OK);
+    p_pages.collect();
+    d_pages.collect();
+    CHECK_EQ(p_pages.leased_bytes(), 0u);
+    CHECK_EQ(d_pages.leased_bytes(), 0u);
+  }
+  CHECK_EQ(owner->lease_count(), 0u);
+  CHECK_EQ(owner->free_bytes(), arena_bytes);
+  pbe_stream_destroy(0, p_stream);
+  pbe_stream_destroy(0, d_stream);
+  CHECK(pbe_arena_destroy(arena) == PBE_OK);
+}
+
 MINITEST_MAIN()
