@@ -263,6 +263,41 @@ typedef struct pbe_copy_op {
 } pbe_copy_op;
 int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream);
 
+/* ---- decode-side reader -------------------------------------------------
+ * Split-K paged attention for one query token per sequence over handed-off
+ * pages: the MI355X form of splitkv_batched_paged_mha_fp8_decode_cu and
+ * splitkv_batched_paged_mha_fast_decode_cu (paged_mha_fast_kernel.cu:902-1076,
+ * called from CudaPagedKVRuntime::decode, paged_kv_runtime.cpp:293-357), with
+ * the same arithmetic: score = (q . k) * log2(e)/sqrt(head_dim) * k_scale,
+ * base-2 online softmax, acc += v * (p * v_scale), output = acc / sum in BF16.
+ *
+ * Pages are page-major in `kv` (block id = byte offset / half, page ids are
+ * multiples of 2*layers): PBE_KV_BF16 planes of 16*H*D bf16, or
+ * PBE_KV_FP8_E4M3 planes of 16*H*D bytes with a page-major scale pool
+ * [layer][K|V][token][head] fp32 (what pbe_handoff_copy_fp8 writes in
+ * per-token-head mode). head_dim 64 or 128, page_tokens 16, q_heads a multiple
+ * of kv_heads with at most 8 query heads per KV head.
+ *
+ * queries / outputs: bf16 [batch][q_heads][head_dim], 16-byte aligned.
+ * block_tables: int32 [batch][max_blocks_per_seq]; seq_lens: int32 [batch]
+ * (device memory, read by the kernel). A sequence whose table holds an id
+ * outside the arena or not a page id, or whose length needs more than
+ * max_blocks_per_seq blocks, gets NaN outputs (its pages are not read past
+ * the failing id). splits = 0 picks pbe_paged_decode_splits(); at most 64.
+ * workspace: at least pbe_paged_decode_workspace_bytes() bytes of device
+ * memory, used by this launch until it completes. Asynchronous on `stream`. */
+#define PBE_KV_BF16 0
+#define PBE_KV_FP8_E4M3 1
+int32_t pbe_paged_decode_splits(int32_t batch, int32_t kv_heads, int32_t max_blocks_per_seq);
+uint64_t pbe_paged_decode_workspace_bytes(int32_t batch, int32_t q_heads, int32_t head_dim,
+                                          int32_t splits);
+int pbe_paged_decode(const pbe_arena_view* kv, int32_t kv_dtype, const float* scales,
+                     uint64_t scale_bytes, const pbe_kv_shape* shape, int32_t layer,
+                     const void* queries, void* outputs, int32_t batch, int32_t q_heads,
+                     const int32_t* block_tables, const int32_t* seq_lens,
+                     int32_t max_blocks_per_seq, int32_t splits, void* workspace,
+                     uint64_t workspace_bytes, int device, void* stream);
+
 /* GPU UUID of `device` (16 bytes), as compared across processes. */
 int pbe_device_uuid(int device, uint8_t out[16]);
 

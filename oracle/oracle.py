@@ -138,3 +138,63 @@ def table_scales(amax_table) -> np.ndarray:
     out = np.empty_like(t)
     lib().orc_fp8_table_scales(_p(t), _p(out), t.size)
     return out
+
+
+def e4m3_table() -> np.ndarray:
+    """float64 value of every E4M3 code (NaN for 0x7f / 0xff)."""
+    return np.array([e4m3_to_f32(c) for c in range(256)], np.float64)
+
+
+def paged_decode(arena: np.ndarray, fp8: bool, scales, layers: int, kv_heads: int, head_dim: int,
+                 layer: int, q_bf16: np.ndarray, tables: np.ndarray, seq_lens) -> np.ndarray:
+    """float64 restatement of one split-K paged-attention decode step
+    (paged_mha_fast_kernel.cu:558-799 for FP8 pages, :391-556 for BF16 pages):
+    for query head qh of sequence b and its KV head qh // (q_heads / kv_heads),
+      score_t = (q . k_t) * (1/sqrt(D) * log2(e), both as fp32) * k_scale_t
+      p_t     = 2 ** (score_t - max_t score_t)
+      out     = sum_t p_t * v_scale_t * v_t / sum_t p_t      (0 when seq_len == 0)
+    over tokens t < seq_len of the blocks tables[b][t // 16], where block id
+    `id` keeps layer l's K plane at byte (id + 2l) * half and the V plane at
+    (id + 2l + 1) * half, token-major inside ([token][kv_head][D]); FP8 scale
+    k_scale_t sits at fp32 index ((id + 2l) * 16 + tok) * kv_heads + kv_head,
+    v_scale_t one plane (16 * kv_heads floats) later. Returns float64
+    [batch][q_heads][D] (the caller rounds to BF16 for comparison)."""
+    arena = np.ascontiguousarray(arena).view(np.uint8).ravel()
+    q = np.asarray(q_bf16, np.uint16)
+    batch, q_heads, D = q.shape
+    assert D == head_dim
+    kvm = q_heads // kv_heads
+    qf = (q.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    E = 1 if fp8 else 2
+    half = 16 * kv_heads * head_dim * E
+    lut = e4m3_table() if fp8 else None
+    sc = None if scales is None else np.asarray(scales, np.float32).ravel().astype(np.float64)
+    scale = float(np.float32(np.float32(1.0) / np.sqrt(np.float32(head_dim))) * np.float32(1.4426950408889634))
+    out = np.zeros((batch, q_heads, D), np.float64)
+    for b in range(batch):
+        n = int(seq_lens[b])
+        if n <= 0:
+            continue
+        t = np.arange(n)
+        ids = np.asarray(tables[b], np.int64)[t // 16]
+        tok = t % 16
+        for kvh in range(kv_heads):
+            koff = (ids + 2 * layer) * half + (tok * kv_heads + kvh) * head_dim * E
+            voff = koff + half
+            cols = np.arange(head_dim * E)
+            kb = arena[koff[:, None] + cols[None, :]]
+            vb = arena[voff[:, None] + cols[None, :]]
+            if fp8:
+                K, V = lut[kb], lut[vb]
+                sidx = ((ids + 2 * layer) * 16 + tok) * kv_heads + kvh
+                ks, vs = sc[sidx], sc[sidx + 16 * kv_heads]
+            else:
+                K = (kb.view(np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+                V = (vb.view(np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+                ks = vs = np.ones(n)
+            for r in range(kvm):
+                qh = kvh * kvm + r
+                s = (K @ qf[b, qh]) * (scale * ks)
+                p = np.exp2(s - np.max(s))
+                out[b, qh] = (p * vs) @ V / p.sum()
+    return out

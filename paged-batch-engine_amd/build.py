@@ -58,6 +58,7 @@ ABI_HOST_SOURCES = [
 # Sources that call HIP (compiled by hipcc).
 HIP_SOURCES = [
     "csrc/kernels/handoff_kernels.hip",
+    "csrc/kernels/decode_kernels.hip",
     "csrc/capi/pbe_capi.hip",
 ]
 CPU_TESTS = ["tests/cpp/test_drop_in_api.cpp"]

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -14,6 +15,7 @@
 #include <string>
 #include <vector>
 
+#include "../kernels/decode_kernels.h"
 #include "../kernels/handoff_kernels.h"
 #include "pbe_handoff.h"
 
@@ -1050,6 +1052,97 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
   rc = stage_done(*slot, s);
   if (rc != PBE_OK) return rc;
   if (copied) *copied = res.info.src_bytes;
+  return PBE_OK;
+}
+
+int32_t pbe_paged_decode_splits(int32_t batch, int32_t kv_heads, int32_t max_blocks_per_seq) {
+  if (batch <= 0 || kv_heads <= 0 || max_blocks_per_seq <= 0) return 1;
+  // Enough waves to fill the chip several times over, at least 4 blocks
+  // (64 tokens) per split so the combine stays small.
+  const int64_t units = (int64_t)batch * kv_heads;
+  int64_t splits = (4096 + units - 1) / units;
+  splits = std::min<int64_t>(splits, (max_blocks_per_seq + 3) / 4);
+  splits = std::min<int64_t>(splits, pbe::kDecodeMaxSplits);
+  return (int32_t)std::max<int64_t>(1, splits);
+}
+
+uint64_t pbe_paged_decode_workspace_bytes(int32_t batch, int32_t q_heads, int32_t head_dim,
+                                          int32_t splits) {
+  if (batch <= 0 || q_heads <= 0 || head_dim <= 0 || splits <= 0) return 0;
+  return pbe::decode_workspace_bytes(batch, q_heads, head_dim, splits);
+}
+
+int pbe_paged_decode(const pbe_arena_view* kv, int32_t kv_dtype, const float* scales,
+                     uint64_t scale_bytes, const pbe_kv_shape* shape, int32_t layer,
+                     const void* queries, void* outputs, int32_t batch, int32_t q_heads,
+                     const int32_t* block_tables, const int32_t* seq_lens,
+                     int32_t max_blocks_per_seq, int32_t splits, void* workspace,
+                     uint64_t workspace_bytes, int device, void* stream) {
+  if (!view_ok(kv) || !shape_ok(shape)) return fail(PBE_ERR_INVALID, "invalid decode arena view or shape");
+  if (kv_dtype != PBE_KV_BF16 && kv_dtype != PBE_KV_FP8_E4M3)
+    return fail(PBE_ERR_INVALID, "unknown KV dtype %d", (int)kv_dtype);
+  const bool fp8 = kv_dtype == PBE_KV_FP8_E4M3;
+  if (shape->page_tokens != 16 || (shape->head_dim != 64 && shape->head_dim != 128))
+    return fail(PBE_ERR_UNSUPPORTED, "decode reader supports 16-token pages and head_dim 64 or 128");
+  if (layer < 0 || layer >= shape->layers) return fail(PBE_ERR_INVALID, "layer %d out of range", (int)layer);
+  if (batch <= 0 || q_heads <= 0 || max_blocks_per_seq <= 0)
+    return fail(PBE_ERR_INVALID, "batch, q_heads and max_blocks_per_seq must be positive");
+  if (q_heads % shape->kv_heads != 0 || q_heads / shape->kv_heads > pbe::kDecodeMaxKvMul)
+    return fail(PBE_ERR_UNSUPPORTED, "q_heads must be 1..%d times kv_heads", pbe::kDecodeMaxKvMul);
+  if (!queries || !outputs || !block_tables || !seq_lens || !workspace)
+    return fail(PBE_ERR_INVALID, "null decode operand");
+  if ((reinterpret_cast<uintptr_t>(queries) | reinterpret_cast<uintptr_t>(outputs)) % 16)
+    return fail(PBE_ERR_INVALID, "queries and outputs must be 16-byte aligned");
+  if (fp8 && (!scales || scale_bytes == 0)) return fail(PBE_ERR_INVALID, "FP8 pages need a scale pool");
+  if (splits == 0) splits = pbe_paged_decode_splits(batch, shape->kv_heads, max_blocks_per_seq);
+  if (splits < 0 || splits > pbe::kDecodeMaxSplits)
+    return fail(PBE_ERR_INVALID, "splits must be 0..%d", pbe::kDecodeMaxSplits);
+  const uint64_t need = pbe::decode_workspace_bytes(batch, q_heads, shape->head_dim, splits);
+  if (workspace_bytes < need)
+    return fail(PBE_ERR_INVALID, "decode workspace holds %llu of %llu bytes",
+                (unsigned long long)workspace_bytes, (unsigned long long)need);
+  const uint64_t half = half_bytes(*shape, fp8 ? 1u : 2u);
+  const uint64_t page = 2ull * shape->layers * half;
+  if (kv->nseg > 1 && kv->segment_bytes % page)
+    return fail(PBE_ERR_INVALID, "arena segments must hold whole pages");
+  const uint64_t row_bytes = (uint64_t)batch * q_heads * shape->head_dim * 2;
+  {
+    PBE_DEVICE_SCOPE(device);
+    std::vector<Range> known;
+    if (!view_accessible(*kv, device, &known) || !accessible(queries, row_bytes, device, &known) ||
+        !accessible(outputs, row_bytes, device, &known) ||
+        !accessible(block_tables, (uint64_t)batch * max_blocks_per_seq * 4, device, &known) ||
+        !accessible(seq_lens, (uint64_t)batch * 4, device, &known) ||
+        !accessible(workspace, need, device, &known) ||
+        (fp8 && !accessible(scales, scale_bytes, device, &known)))
+      return fail(PBE_ERR_INVALID, "decode operands must be memory of device %d", device);
+  }
+  pbe::DecodeParams p{};
+  for (uint32_t i = 0; i < kv->nseg; ++i) p.kv.base[i] = static_cast<const char*>(kv->base[i]);
+  p.kv.segment_bytes = kv->segment_bytes;
+  p.kv.bytes = kv->bytes;
+  p.scales = fp8 ? scales : nullptr;
+  p.scale_bytes = fp8 ? scale_bytes : 0;
+  p.q = static_cast<const uint16_t*>(queries);
+  p.out = static_cast<uint16_t*>(outputs);
+  p.tables = block_tables;
+  p.seq_lens = seq_lens;
+  const uint64_t rows = (uint64_t)batch * q_heads * splits;
+  p.part_acc = static_cast<float*>(workspace);
+  p.part_m = p.part_acc + rows * shape->head_dim;
+  p.part_l = p.part_m + rows;
+  p.batch = batch;
+  p.q_heads = q_heads;
+  p.kv_heads = shape->kv_heads;
+  p.head_dim = shape->head_dim;
+  p.layers = shape->layers;
+  p.layer = layer;
+  p.max_blocks = max_blocks_per_seq;
+  p.splits = splits;
+  p.half = half;
+  p.scale = (1.f / std::sqrt((float)shape->head_dim)) * 1.4426950408889634f;  // as launch_fp8_stage1
+  PBE_DEVICE_SCOPE(device);
+  PBE_HIP(pbe::launch_paged_decode(p, fp8, static_cast<hipStream_t>(stream)));
   return PBE_OK;
 }
 

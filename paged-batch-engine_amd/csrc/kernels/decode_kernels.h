@@ -1,0 +1,40 @@
+// Internal interface of the decode-side paged-attention reader (one query
+// token per sequence) over the page-major arena layout the handoff writes.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pbe {
+
+constexpr int kDecodeMaxSegments = 16;
+constexpr int kDecodeMaxKvMul = 8;    // query heads per KV head held in registers
+constexpr int kDecodeMaxSplits = 64;  // one lane per split in the combine kernel
+
+struct DecodeView {
+  const char* base[kDecodeMaxSegments];
+  uint64_t segment_bytes;
+  uint64_t bytes;
+};
+
+struct DecodeParams {
+  DecodeView kv;           // payload arena (FP8: int8 E4M3 planes; BF16: bf16 planes)
+  const float* scales;     // FP8 only: page-major [layer][K|V][token][kv_head] fp32
+  uint64_t scale_bytes;
+  const uint16_t* q;       // bf16 [batch][q_heads][head_dim]
+  uint16_t* out;           // bf16 [batch][q_heads][head_dim]
+  const int32_t* tables;   // [batch][max_blocks] page-major block ids
+  const int32_t* seq_lens; // [batch]
+  float* part_acc;         // [batch][q_heads][splits][head_dim]
+  float* part_m;           // [batch][q_heads][splits]
+  float* part_l;           // [batch][q_heads][splits]
+  int32_t batch, q_heads, kv_heads, head_dim, layers, layer, max_blocks, splits;
+  uint64_t half;           // bytes of one K or V plane of one block
+  float scale;             // log2(e) / sqrt(head_dim): scores in base 2
+};
+
+// Bytes of the split-K workspace (partial outputs, maxima and sums).
+uint64_t decode_workspace_bytes(int32_t batch, int32_t q_heads, int32_t head_dim, int32_t splits);
+
+hipError_t launch_paged_decode(const DecodeParams& p, bool fp8, hipStream_t stream);
+
+}  // namespace pbe

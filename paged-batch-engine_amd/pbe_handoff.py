@@ -23,6 +23,8 @@ PBE_MAX_SEGMENTS = 16
 PBE_IPC_HANDLE_BYTES = 64
 PBE_FP8_SCALE_PER_TOKEN_HEAD = 0
 PBE_FP8_SCALE_TABLE = 1
+PBE_KV_BF16 = 0
+PBE_KV_FP8_E4M3 = 1
 
 
 class KvShape(C.Structure):
@@ -110,6 +112,11 @@ _SIGNATURES = [
     ("pbe_copy_shared_kv", C.c_int, [C.POINTER(ArenaView), _P, _P, C.c_int64,
                                      C.POINTER(KvShape), C.c_int, _P, C.POINTER(C.c_uint64)]),
     ("pbe_copy_ops", C.c_int, [C.POINTER(CopyOp), C.c_int64, C.c_int, _P]),
+    ("pbe_paged_decode_splits", C.c_int32, [C.c_int32, C.c_int32, C.c_int32]),
+    ("pbe_paged_decode_workspace_bytes", C.c_uint64, [C.c_int32, C.c_int32, C.c_int32, C.c_int32]),
+    ("pbe_paged_decode", C.c_int, [C.POINTER(ArenaView), C.c_int32, _P, C.c_uint64,
+                                   C.POINTER(KvShape), C.c_int32, _P, _P, C.c_int32, C.c_int32,
+                                   _P, _P, C.c_int32, C.c_int32, _P, C.c_uint64, C.c_int, _P]),
 ]
 EXPORTED = [name for name, _, _ in _SIGNATURES]
 
@@ -428,3 +435,22 @@ def device_uuid(device: int = 0) -> bytes:
     check(lib().pbe_device_uuid(device, buf))
     return bytes(buf)
 
+
+
+def decode_splits(batch: int, kv_heads: int, max_blocks: int) -> int:
+    return int(lib().pbe_paged_decode_splits(batch, kv_heads, max_blocks))
+
+
+def decode_workspace_bytes(batch: int, q_heads: int, head_dim: int, splits: int) -> int:
+    return int(lib().pbe_paged_decode_workspace_bytes(batch, q_heads, head_dim, splits))
+
+
+def paged_decode(view: ArenaView, kv_dtype: int, scales: int, scale_bytes: int, kv: KvShape,
+                 layer: int, queries: int, outputs: int, batch: int, q_heads: int, tables: int,
+                 seq_lens: int, max_blocks: int, splits: int, workspace: int,
+                 workspace_bytes: int, stream: int = 0, device: int = 0) -> None:
+    """Device pointers in, asynchronous on `stream` (pbe_paged_decode)."""
+    check(lib().pbe_paged_decode(C.byref(view), kv_dtype, scales or None, scale_bytes, C.byref(kv),
+                                 layer, queries, outputs, batch, q_heads, tables, seq_lens,
+                                 max_blocks, splits, workspace, workspace_bytes, device,
+                                 stream or None))
