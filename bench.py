@@ -214,7 +214,72 @@ def measure_extra_configs(torch, P, W, scrub, n: int):
                lambda: rl.copy_fp8(P.PBE_FP8_SCALE_TABLE, table.data_ptr(), sp), n),
         {"pages": w.pages})
     rl.close()
+    out.extend(measure_decode(torch, P, scrub, n))
     return out
+
+
+def measure_decode(torch, P, scrub, n: int, batch: int = 64, seq: int = 5040, placement: str = "chunks"):
+    """Decode-side reader after the handoff: one decode step (one layer) of
+    `batch` sequences holding the 5040-token Qwen2.5-1.5B prefix, reading FP8
+    pages + per-token-head scales, and BF16 pages. Algorithmic bytes = the K
+    and V rows (and scales) of every valid token + queries + outputs."""
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    L, H, D, kvm = 28, 2, 128, 6
+    kv = P.shape(L, H, D)
+    blocks = (seq + 15) // 16
+    n_pages = batch * blocks
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    if placement == "one_page":  # diagnostic: every block reads page 0 (cache-resident)
+        perm = torch.zeros(n_pages, dtype=torch.int32, device=dev)
+    elif placement == "random":    # every block on a random page of the arena
+        perm = torch.randperm(n_pages, generator=g, device=dev).to(torch.int32)
+    else:                          # 5-page Chunks (the shared arena's 2 MiB Chunks), shuffled
+        chunks = torch.randperm(n_pages // 5, generator=g, device=dev).to(torch.int32)
+        perm = (chunks[:, None] * 5 + torch.arange(5, device=dev, dtype=torch.int32)).view(-1)
+    tables = (perm * (2 * L)).view(batch, blocks).contiguous()
+    seq_lens = torch.full((batch,), seq, dtype=torch.int32, device=dev)
+    q = (torch.randn(batch, H * kvm, D, generator=g, device=dev)).to(torch.bfloat16)
+    o = torch.empty_like(q)
+    splits = P.decode_splits(batch, H, blocks)
+    ws_bytes = P.decode_workspace_bytes(batch, H * kvm, D, splits)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    res = []
+    for fp8 in (True, False):
+        E = 1 if fp8 else 2
+        arena = torch.empty(n_pages * 2 * L * 16 * H * D * E, dtype=torch.uint8, device=dev)
+        if fp8:
+            arena.copy_(torch.randint(0, 0x70, arena.shape, generator=g, device=dev, dtype=torch.uint8)
+                        | (torch.randint(0, 2, arena.shape, generator=g, device=dev,
+                                         dtype=torch.uint8) << 7))
+            scales = torch.rand(n_pages * 2 * L * 16 * H, generator=g, device=dev) * 0.1 + 0.01
+        else:
+            arena.view(torch.bfloat16).normal_(generator=g)
+            scales = None
+        view = P.view_of(arena.data_ptr(), arena.numel())
+
+        def step():
+            P.paged_decode(view, P.PBE_KV_FP8_E4M3 if fp8 else P.PBE_KV_BF16,
+                           scales.data_ptr() if fp8 else 0, scales.numel() * 4 if fp8 else 0, kv,
+                           L - 1, q.data_ptr(), o.data_ptr(), batch, H * kvm, tables.data_ptr(),
+                           seq_lens.data_ptr(), blocks, splits, ws.data_ptr(), ws_bytes, sp)
+
+        ms = _timed(torch, stream, scrub, step, n)
+        alg = batch * seq * H * (2 * D * E + (8 if fp8 else 0)) + 2 * q.numel() * 2
+        r = {"workload": f"decode_reader_{'fp8' if fp8 else 'bf16'}_qwen15b_b{batch}_s{seq}",
+             "placement": placement,
+             "algorithmic_bytes": alg, "kernel_us_mean": round(ms[0] * 1e3, 2),
+             "kernel_us_min": round(ms[1] * 1e3, 2),
+             "gbps": round(alg / (ms[0] * 1e-3) / 1e9, 1),
+             "pct_of_peak": round(100 * alg / (ms[0] * 1e-3) / 1e9 / PEAK_GBPS, 1),
+             "splits": splits, "launches": 2,
+             "note": "both launches (split-K attention + combine) between the events"}
+        print(json.dumps(r), file=sys.stderr, flush=True)
+        res.append(r)
+        del arena
+    return res
 
 
 def main() -> int:

@@ -1057,10 +1057,11 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
 
 int32_t pbe_paged_decode_splits(int32_t batch, int32_t kv_heads, int32_t max_blocks_per_seq) {
   if (batch <= 0 || kv_heads <= 0 || max_blocks_per_seq <= 0) return 1;
-  // Enough waves to fill the chip several times over, at least 4 blocks
-  // (64 tokens) per split so the combine stays small.
+  // About 1024 waves (measured best on MI355X for 64 x 5040-token batches:
+  // more splits add combine work without adding bandwidth), at least 4
+  // blocks (64 tokens) per split.
   const int64_t units = (int64_t)batch * kv_heads;
-  int64_t splits = (4096 + units - 1) / units;
+  int64_t splits = (1024 + units - 1) / units;
   splits = std::min<int64_t>(splits, (max_blocks_per_seq + 3) / 4);
   splits = std::min<int64_t>(splits, pbe::kDecodeMaxSplits);
   return (int32_t)std::max<int64_t>(1, splits);
@@ -1105,6 +1106,10 @@ int pbe_paged_decode(const pbe_arena_view* kv, int32_t kv_dtype, const float* sc
   const uint64_t page = 2ull * shape->layers * half;
   if (kv->nseg > 1 && kv->segment_bytes % page)
     return fail(PBE_ERR_INVALID, "arena segments must hold whole pages");
+  if (kv->bytes < page || (kv->nseg > 1 && kv->segment_bytes < page))
+    return fail(PBE_ERR_INVALID, "decode arena must hold at least one page");
+  if (fp8 && scale_bytes < 2ull * shape->layers * 16 * shape->kv_heads * 4)
+    return fail(PBE_ERR_INVALID, "scale pool must hold at least one page of scales");
   const uint64_t row_bytes = (uint64_t)batch * q_heads * shape->head_dim * 2;
   {
     PBE_DEVICE_SCOPE(device);
@@ -1141,6 +1146,13 @@ int pbe_paged_decode(const pbe_arena_view* kv, int32_t kv_dtype, const float* sc
   p.splits = splits;
   p.half = half;
   p.scale = (1.f / std::sqrt((float)shape->head_dim)) * 1.4426950408889634f;  // as launch_fp8_stage1
+  // Largest id whose page (all 2*layers planes) fits the arena and the scale pool.
+  const int64_t stride = 2ll * shape->layers;
+  int64_t id_max = (int64_t)(kv->bytes / half) - stride;
+  if (fp8) id_max = std::min<int64_t>(id_max, (int64_t)(scale_bytes / (64ull * shape->kv_heads)) - stride);
+  p.id_max = (int32_t)std::min<int64_t>(id_max, INT32_MAX);
+  p.by_stride = pbe::make_fast_div((uint32_t)stride);
+  p.by_seg_pages = pbe::make_fast_div(kv->nseg > 1 ? (uint32_t)(kv->segment_bytes / page) : 0x7fffffffu);
   PBE_DEVICE_SCOPE(device);
   PBE_HIP(pbe::launch_paged_decode(p, fp8, static_cast<hipStream_t>(stream)));
   return PBE_OK;

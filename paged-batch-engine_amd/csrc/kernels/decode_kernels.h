@@ -16,6 +16,13 @@ struct DecodeView {
   uint64_t bytes;
 };
 
+// Division by a fixed divisor d >= 1 for numerators below 2^31:
+// q = (mulhi(n, mul) + n) >> shift (round-up reciprocal method).
+struct FastDiv {
+  uint32_t d = 1, mul = 1, shift = 0;
+};
+FastDiv make_fast_div(uint32_t d);
+
 struct DecodeParams {
   DecodeView kv;           // payload arena (FP8: int8 E4M3 planes; BF16: bf16 planes)
   const float* scales;     // FP8 only: page-major [layer][K|V][token][kv_head] fp32
@@ -30,6 +37,9 @@ struct DecodeParams {
   int32_t batch, q_heads, kv_heads, head_dim, layers, layer, max_blocks, splits;
   uint64_t half;           // bytes of one K or V plane of one block
   float scale;             // log2(e) / sqrt(head_dim): scores in base 2
+  int32_t id_max;          // largest block id whose page lies inside the arena and scale pool
+  FastDiv by_stride;       // divides by 2 * layers (page ids)
+  FastDiv by_seg_pages;    // divides page indices by pages per segment
 };
 
 // Bytes of the split-K workspace (partial outputs, maxima and sums).

@@ -28,6 +28,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWavesPerBlock = 4;
 constexpr int kBlockTokens = 16;
@@ -96,28 +97,56 @@ __device__ __forceinline__ uint16_t to_bf16(float f) {
   return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
 
-__device__ __forceinline__ const char* arena_at(const DecodeView& v, uint64_t off) {
-  const uint64_t seg = off / v.segment_bytes;
-  return v.base[seg] + (off - seg * v.segment_bytes);
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, const FastDiv& f) {
+  return (__umulhi(n, f.mul) + n) >> f.shift;
 }
 
-template <int D, bool kFp8>
-__global__ __launch_bounds__(kWavesPerBlock * 64) void paged_decode_kernel(const DecodeParams p) {
-  constexpr int E = kFp8 ? 1 : 2;  // bytes per stored element
-  constexpr int NK = D / 32;       // score MFMAs per block
-  constexpr int DG = D / 4;        // head dims per lane group in the score tile
-  constexpr int DV = D / 16;       // head dims per lane in the value sum
-  constexpr int KVM = kDecodeMaxKvMul;
-  __shared__ float lds_p[kWavesPerBlock][kBlockTokens][17];
-  __shared__ float lds_alpha[kWavesPerBlock][16];
+// Four E4M3 bytes -> four BF16 with the gfx950 scaled converter (scale 1: exact).
+__device__ __forceinline__ u32x2 e4m3x4_to_bf16x4_cvt(uint32_t w) {
+  return u32x2{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, true))};
+}
 
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t unit = (int64_t)blockIdx.x * kWavesPerBlock + w;
+// Per-lane registers of one block of 16 tokens of one KV head: the lane's
+// key run (row j, head dims g*D/4..), its quarter of a value row (token
+// lane/4, quarter lane%4) and one scale (FP8: lanes 0-15 key scale of token
+// lane, lanes 16-31 value scale of token lane-16).
+template <int D, bool kFp8>
+struct Geo {
+  static constexpr int E = kFp8 ? 1 : 2;
+  static constexpr int WORDS = D * E / 16;   // key words = value words per lane
+  static constexpr int PITCH = D * E + 16;   // LDS row pitch of the value tile
+  static constexpr int SETS = kFp8 ? 4 : 2;  // register sets: SETS-1 blocks in flight
+};
+
+template <int W>
+struct BlockRegs {
+  uint32_t k[W];
+  uint32_t v[W];
+  float scale;
+};
+
+constexpr int kDecodeWaves = 4;
+
+template <int D, bool kFp8, int KVM>
+__global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
+    const DecodeParams p, const int32_t* __restrict__ tables) {
+  using G = Geo<D, kFp8>;
+  constexpr int E = G::E;
+  constexpr int NK = D / 32;  // score MFMAs per block
+  constexpr int DG = D / 4;   // head dims per lane group in the score tile
+  constexpr int NT = D / 16;  // value MFMAs (16 head dims each) per block
+  constexpr int W = G::WORDS, SETS = G::SETS, PITCH = G::PITCH;
+  __shared__ __attribute__((aligned(16))) unsigned char lds_v[kDecodeWaves][kBlockTokens * PITCH];
+  __shared__ float lds_s[kDecodeWaves][32];
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t unit = (int64_t)blockIdx.x * kDecodeWaves + w;
   if (unit >= (int64_t)p.batch * p.kv_heads * p.splits) return;
   const int split = (int)(unit % p.splits);
   const int kvh = (int)((unit / p.splits) % p.kv_heads);
   const int b = (int)(unit / p.splits / p.kv_heads);
-  const int kvm = p.q_heads / p.kv_heads;
   const int g = lane >> 4, j = lane & 15;
   const int seq = p.seq_lens[b];
   const int nblk = seq > 0 ? (seq + kBlockTokens - 1) / kBlockTokens : 0;
@@ -126,183 +155,208 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void paged_decode_kernel(const
   // (paged_mha_fast_kernel.cu:596-601).
   const int per_split = (nblk + p.splits - 1) / p.splits;
   const int blk0 = split * per_split;
-  const int blk1 = bad ? blk0 : min(blk0 + per_split, nblk);
+  int blk1 = bad ? blk0 : min(blk0 + per_split, nblk);
 
-  // Query rows (A operand): lane (g, j) holds head j's dims g*DG + 8kk + 0..7.
+  // Query rows as the B operand of the scores: lane (g, j) holds head j's
+  // dims g*DG + 8kk + 0..7 (rows past the group's heads are zero).
   bf16x8 qa[NK];
   {
-    const bool has = j < kvm;
+    const bool has = j < KVM;
     const uint16_t* qrow =
-        p.q + ((int64_t)b * p.q_heads + (int64_t)kvh * kvm + (has ? j : 0)) * D + g * DG;
+        p.q + ((int64_t)b * p.q_heads + (int64_t)kvh * KVM + (has ? j : 0)) * D + g * DG;
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
       const u32x4 v = has ? *reinterpret_cast<const u32x4*>(qrow + kk * 8) : u32x4{0u, 0u, 0u, 0u};
       qa[kk] = __builtin_bit_cast(bf16x8, v);
     }
   }
-  float m[4], l[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m[i] = -INFINITY;
-    l[i] = 0.f;
-  }
-  float acc[KVM][DV];
-#pragma unroll
-  for (int h = 0; h < KVM; ++h)
-#pragma unroll
-    for (int e = 0; e < DV; ++e) acc[h][e] = 0.f;
 
   const uint64_t H = (uint64_t)p.kv_heads;
-  const uint64_t token_stride = H * D * E;
+  const uint32_t token_stride = (uint32_t)(H * D * E);
   const uint64_t stride = 2ull * p.layers;
-  for (int blk = blk0; blk < blk1; ++blk) {
-    const int32_t id = p.tables[(int64_t)b * p.max_blocks + blk];
-    if (id < 0 || (uint64_t)id % stride != 0 || ((uint64_t)id + stride) * p.half > p.kv.bytes ||
-        (kFp8 && ((uint64_t)id + stride) * kBlockTokens * H * 4ull > p.scale_bytes)) {
-      bad = true;
-      break;
+  // Block ids are uniform: read through the read-only table with scalar loads.
+  const int32_t* table = tables + (int64_t)b * p.max_blocks;
+  const uint64_t head_off = 2ull * p.layer * p.half + (uint64_t)kvh * D * E;
+  const uint32_t key_off = (uint32_t)j * token_stride + (uint32_t)(g * DG * E);
+  const uint32_t val_off = (uint32_t)(lane >> 2) * token_stride + (uint32_t)((lane & 3) * (D * E / 4));
+  // lanes 0-15: key scale of token lane; 16-31: value scale of token lane-16
+  // (lanes 32-63 repeat 0-31)
+  const uint32_t scale_off = (uint32_t)((2u * p.layer + ((lane >> 4) & 1)) * kBlockTokens * H +
+                                        (lane & 15) * H + kvh);
+  // Loads block `blk` into `r`. Every call issues the same loads (an
+  // unconditional count keeps the compiler's in-flight accounting exact): a
+  // block past the split's end, or whose id is not a page id inside the arena
+  // and scale pool, reads page 0 instead and reports false when it was wanted.
+  auto load = [&](int blk, BlockRegs<W>& r) -> bool {
+    const bool want = blk < blk1;
+    int32_t id = want ? table[blk] : 0;
+    uint32_t page = fast_div((uint32_t)max(id, 0), p.by_stride);
+    const bool ok = id >= 0 && id <= p.id_max && page * p.by_stride.d == (uint32_t)id;
+    if (!ok) id = 0, page = 0;
+    const uint32_t seg = fast_div(page, p.by_seg_pages);
+    const char* kplane =
+        p.kv.base[seg] + (uint64_t)(page - seg * p.by_seg_pages.d) * stride * p.half + head_off;
+#pragma unroll
+    for (int v = 0; v < W / 4; ++v) {
+      const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kplane + key_off) + v);
+      const u32x4 y =
+          __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kplane + p.half + val_off) + v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        r.k[4 * v + e] = x[e];
+        r.v[4 * v + e] = y[e];
+      }
     }
+    r.scale = 1.f;
+    if constexpr (kFp8) r.scale = p.scales[(uint64_t)id * kBlockTokens * H + scale_off];
+    return ok || !want;
+  };
+
+  float m = -INFINITY, l = 0.f;  // of head j
+  f32x4 acc[NT];                 // O^T: lane (g, j) = head j, dims 16nt + 4g + 0..3
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  unsigned char* vt_w = &lds_v[w][0];
+  auto compute = [&](int blk, const BlockRegs<W>& r) {
     const int valid = blk == nblk - 1 ? seq - kBlockTokens * (nblk - 1) : kBlockTokens;
-    const char* page = arena_at(p.kv, (uint64_t)id * p.half);
-    const char* kplane = page + 2ull * p.layer * p.half + (uint64_t)kvh * D * E;
-    const char* vplane = kplane + p.half;
-
-    // ---- scores of the block's 16 tokens (B operand: lane (g, j) = token j)
+    // Value tile -> LDS rows (tail rows zeroed: tail slots may hold anything, even NaN).
+    {
+      const int t = lane >> 2;
+      unsigned char* dst = vt_w + t * PITCH + (lane & 3) * (D * E / 4);
+#pragma unroll
+      for (int v = 0; v < W / 4; ++v) {
+        const u32x4 x = t < valid ? u32x4{r.v[4 * v], r.v[4 * v + 1], r.v[4 * v + 2], r.v[4 * v + 3]}
+                                  : u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(dst + 16 * v) = x;
+      }
+      if (lane < 32) lds_s[w][lane] = r.scale;
+    }
+    // Scores, transposed: lane (g, j) gets tokens 4g..4g+3 of head j.
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
-    const char* krow = kplane + (uint64_t)j * token_stride + (uint64_t)g * DG * E;
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) {
+      bf16x8 kb;
+      if constexpr (kFp8) {
+        const u32x2 lo = e4m3x4_to_bf16x4_cvt(r.k[2 * kk]);
+        const u32x2 hi = e4m3x4_to_bf16x4_cvt(r.k[2 * kk + 1]);
+        kb = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+      } else {
+        kb = __builtin_bit_cast(bf16x8, u32x4{r.k[4 * kk], r.k[4 * kk + 1], r.k[4 * kk + 2], r.k[4 * kk + 3]});
+      }
+      s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qa[kk], s, 0, 0, 0);
+    }
+    wave_sync();
+    float ks[4] = {1.f, 1.f, 1.f, 1.f}, vs[4] = {1.f, 1.f, 1.f, 1.f};
     if constexpr (kFp8) {
-      uint32_t words[DG / 4];
+      const f32x4 k4 = *reinterpret_cast<const f32x4*>(&lds_s[w][4 * g]);
+      const f32x4 v4 = *reinterpret_cast<const f32x4*>(&lds_s[w][16 + 4 * g]);
 #pragma unroll
-      for (int v = 0; v < DG / 16; ++v) {
-        const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(krow) + v);
-        words[4 * v] = x[0];
-        words[4 * v + 1] = x[1];
-        words[4 * v + 2] = x[2];
-        words[4 * v + 3] = x[3];
-      }
-#pragma unroll
-      for (int kk = 0; kk < NK; ++kk) {
-        const u32x2 lo = e4m3x4_to_bf16x4(words[2 * kk]);
-        const u32x2 hi = e4m3x4_to_bf16x4(words[2 * kk + 1]);
-        const bf16x8 kb = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[kk], kb, s, 0, 0, 0);
-      }
-    } else {
-#pragma unroll
-      for (int kk = 0; kk < NK; ++kk) {
-        const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(krow) + kk);
-        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[kk], __builtin_bit_cast(bf16x8, x), s, 0, 0, 0);
+      for (int i = 0; i < 4; ++i) {
+        ks[i] = k4[i];
+        vs[i] = v4[i];
       }
     }
-    const bool tok_ok = j < valid;
-    float ks = 1.f, vs = 1.f;
-    if constexpr (kFp8) {
-      if (tok_ok) {
-        const uint64_t kidx = ((uint64_t)id + 2ull * p.layer) * kBlockTokens + j;
-        ks = p.scales[kidx * H + kvh];
-        vs = p.scales[(kidx + kBlockTokens) * H + kvh];
-      }
-    }
-    const float c = p.scale * ks;
-    // ---- online softmax; lane (g, j) holds heads 4g..4g+3 of token j
+    // Online softmax of head j over the block's 16 tokens.
+    float sv[4], tmax = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float sv = tok_ok ? s[i] * c : -INFINITY;
-      const float mn = fmaxf(m[i], row_max16(sv));
-      const float alpha = mn == -INFINITY ? 1.f : exp2f(m[i] - mn);
-      const float pr = tok_ok ? exp2f(sv - mn) : 0.f;
-      l[i] = l[i] * alpha + row_sum16(pr);
-      m[i] = mn;
-      lds_p[w][j][4 * g + i] = pr * vs;
-      if (j == 0) lds_alpha[w][4 * g + i] = alpha;
+      sv[i] = 4 * g + i < valid ? s[i] * (p.scale * ks[i]) : -INFINITY;
+      tmax = fmaxf(tmax, sv[i]);
     }
-    wave_sync();
-    // ---- values: lane (g, j) takes tokens 4g..4g+3, dims j*DV..j*DV+DV-1
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float mn = fmaxf(m, tmax);
+    const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mn);
+    float psum = 0.f;
+    uint32_t phi[2], plo[2];
 #pragma unroll
-    for (int h = 0; h < KVM; ++h) {
-      if (h < kvm) {
-        const float a = lds_alpha[w][h];
-#pragma unroll
-        for (int e = 0; e < DV; ++e) acc[h][e] *= a;
-      }
+    for (int i = 0; i < 4; i += 2) {
+      const bool ok0 = 4 * g + i < valid, ok1 = 4 * g + i + 1 < valid;
+      const float p0 = ok0 ? __builtin_amdgcn_exp2f(sv[i] - mn) : 0.f;
+      const float p1 = ok1 ? __builtin_amdgcn_exp2f(sv[i + 1] - mn) : 0.f;
+      psum += p0 + p1;
+      // p * v_scale as bf16 hi + bf16 lo: the value product keeps ~16 bits.
+      const float a0 = ok0 ? p0 * vs[i] : 0.f, a1 = ok1 ? p1 * vs[i + 1] : 0.f;
+      const uint32_t h0 = to_bf16(a0), h1 = to_bf16(a1);
+      const uint32_t l0 = to_bf16(a0 - __uint_as_float(h0 << 16));
+      const uint32_t l1 = to_bf16(a1 - __uint_as_float(h1 << 16));
+      phi[i / 2] = h0 | (h1 << 16);
+      plo[i / 2] = l0 | (l1 << 16);
     }
+    psum += __shfl_xor(psum, 16);
+    psum += __shfl_xor(psum, 32);
+    l = l * alpha + psum;
+    m = mn;
+    const s16x4 p_hi = __builtin_bit_cast(s16x4, u32x2{phi[0], phi[1]});
+    const s16x4 p_lo = __builtin_bit_cast(s16x4, u32x2{plo[0], plo[1]});
+    // Rescale: the accumulators hold O^T, lane (g, j) = head j, so alpha is
+    // in-lane; skipped when no head's maximum moved (the common case).
+    if (__ballot(alpha != 1.f) != 0) {
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const int t = 4 * g + tt;
-      const bool ok = t < valid;  // tail slots may hold anything, even NaN
-      const char* vrow = vplane + (uint64_t)t * token_stride + (uint64_t)j * DV * E;
-      float vf[DV];
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[nt][i] *= alpha;
+    }
+    // O^T += V^T P^T: A = value rows 4g..4g+3 at head dim 16nt + j, B = P^T as held.
+    const unsigned char* vt = vt_w + 4 * g * PITCH;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      s16x4 va;
       if constexpr (kFp8) {
-        if constexpr (DV == 8) {
-          const u32x2 x = ok ? *reinterpret_cast<const u32x2*>(vrow) : u32x2{0u, 0u};
-          e4m3x4_to_f32(x[0], vf);
-          e4m3x4_to_f32(x[1], vf + 4);
-        } else {
-          const uint32_t x = ok ? *reinterpret_cast<const uint32_t*>(vrow) : 0u;
-          e4m3x4_to_f32(x, vf);
-        }
+        uint32_t x = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x |= (uint32_t)vt[i * PITCH + 16 * nt + j] << (8 * i);
+        va = __builtin_bit_cast(s16x4, e4m3x4_to_bf16x4_cvt(x));
       } else {
-        uint32_t x[DV / 2];
-        if constexpr (DV == 8) {
-          const u32x4 y = ok ? *reinterpret_cast<const u32x4*>(vrow) : u32x4{0u, 0u, 0u, 0u};
-          x[0] = y[0];
-          x[1] = y[1];
-          x[2] = y[2];
-          x[3] = y[3];
-        } else {
-          const u32x2 y = ok ? *reinterpret_cast<const u32x2*>(vrow) : u32x2{0u, 0u};
-          x[0] = y[0];
-          x[1] = y[1];
-        }
-#pragma unroll
-        for (int e = 0; e < DV / 2; ++e) {
-          vf[2 * e] = __uint_as_float(x[e] << 16);
-          vf[2 * e + 1] = __uint_as_float(x[e] & 0xffff0000u);
-        }
+        const uint16_t* c16 = reinterpret_cast<const uint16_t*>(vt + 32 * nt + 2 * j);
+        const uint32_t x0 = (uint32_t)c16[0] | ((uint32_t)c16[PITCH / 2] << 16);
+        const uint32_t x1 = (uint32_t)c16[PITCH] | ((uint32_t)c16[3 * PITCH / 2] << 16);
+        va = __builtin_bit_cast(s16x4, u32x2{x0, x1});
       }
-#pragma unroll
-      for (int h = 0; h < KVM; ++h) {
-        if (h < kvm) {
-          const float ph = lds_p[w][t][h];
-#pragma unroll
-          for (int e = 0; e < DV; ++e) acc[h][e] = fmaf(ph, vf[e], acc[h][e]);
-        }
-      }
+      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, p_hi, acc[nt], 0, 0, 0);
+      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, p_lo, acc[nt], 0, 0, 0);
     }
-    wave_sync();
+    wave_sync();  // the next block rewrites the tile
+  };
+
+  // SETS register sets in rotation: while one block is computed, the next
+  // SETS-1 are in flight.
+  static_assert(SETS == 2 || SETS == 4, "register rotation is written out for 2 or 4 sets");
+  BlockRegs<W> r0, r1, r2, r3;
+  auto prime = [&](int blk, BlockRegs<W>& r) {
+    if (!load(blk, r)) bad = true, blk1 = min(blk1, blk);
+  };
+  auto step = [&](int blk, BlockRegs<W>& r) {
+    if (blk < blk1) compute(blk, r);
+    if (!load(blk + SETS, r)) bad = true, blk1 = min(blk1, blk + SETS);
+  };
+  prime(blk0, r0);
+  prime(blk0 + 1, r1);
+  if constexpr (SETS == 4) {
+    prime(blk0 + 2, r2);
+    prime(blk0 + 3, r3);
+  }
+  for (int base = blk0; base < blk1; base += SETS) {
+    step(base, r0);
+    step(base + 1, r1);
+    if constexpr (SETS == 4) {
+      step(base + 2, r2);
+      step(base + 3, r3);
+    }
   }
 
-  // ---- sum the four token groups and write this split's partials
-#pragma unroll
-  for (int h = 0; h < KVM; ++h) {
-    if (h < kvm) {
-#pragma unroll
-      for (int e = 0; e < DV; ++e) {
-        acc[h][e] += __shfl_xor(acc[h][e], 16);
-        acc[h][e] += __shfl_xor(acc[h][e], 32);
-      }
-    }
-  }
-  const int64_t row0 = (int64_t)b * p.q_heads + (int64_t)kvh * kvm;
+  // ---- this split's partials (lane (g, j): head j, dims 16nt + 4g + i)
+  const int64_t row0 = (int64_t)b * p.q_heads + (int64_t)kvh * KVM;
   const float nan = __builtin_nanf("");
-  if (g == 0) {
+  if (j < KVM) {
+    float* dst = p.part_acc + ((row0 + j) * p.splits + split) * D + 4 * g;
 #pragma unroll
-    for (int h = 0; h < KVM; ++h) {
-      if (h < kvm) {
-        float* dst = p.part_acc + ((row0 + h) * p.splits + split) * D + j * DV;
-#pragma unroll
-        for (int e = 0; e < DV; ++e) dst[e] = bad ? nan : acc[h][e];
-      }
-    }
-  }
-  if (j == 0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 4 * g + i;
-      if (h < kvm) {
-        p.part_m[(row0 + h) * p.splits + split] = bad ? nan : m[i];
-        p.part_l[(row0 + h) * p.splits + split] = bad ? nan : l[i];
-      }
+    for (int nt = 0; nt < NT; ++nt)
+      *reinterpret_cast<f32x4*>(dst + 16 * nt) = bad ? f32x4{nan, nan, nan, nan} : acc[nt];
+    if (g == 0) {
+      p.part_m[(row0 + j) * p.splits + split] = bad ? nan : m;
+      p.part_l[(row0 + j) * p.splits + split] = bad ? nan : l;
     }
   }
 }
@@ -343,19 +397,44 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void decode_combine_kernel(con
   }
 }
 
-template <int D, bool kFp8>
+template <int D, bool kFp8, int KVM>
 void launch(const DecodeParams& p, hipStream_t stream) {
   const int64_t units = (int64_t)p.batch * p.kv_heads * p.splits;
   const int64_t rows = (int64_t)p.batch * p.q_heads;
-  hipLaunchKernelGGL((paged_decode_kernel<D, kFp8>),
-                     dim3((unsigned)((units + kWavesPerBlock - 1) / kWavesPerBlock)),
-                     dim3(kWavesPerBlock * 64), 0, stream, p);
+  hipLaunchKernelGGL((paged_decode_kernel<D, kFp8, KVM>),
+                     dim3((unsigned)((units + kDecodeWaves - 1) / kDecodeWaves)), dim3(kDecodeWaves * 64), 0,
+                     stream, p, p.tables);
   hipLaunchKernelGGL((decode_combine_kernel<D>),
                      dim3((unsigned)((rows + kWavesPerBlock - 1) / kWavesPerBlock)),
                      dim3(kWavesPerBlock * 64), 0, stream, p);
 }
 
+template <int D, bool kFp8>
+bool launch_kvm(const DecodeParams& p, hipStream_t stream) {
+  switch (p.q_heads / p.kv_heads) {
+    case 1: launch<D, kFp8, 1>(p, stream); return true;
+    case 2: launch<D, kFp8, 2>(p, stream); return true;
+    case 3: launch<D, kFp8, 3>(p, stream); return true;
+    case 4: launch<D, kFp8, 4>(p, stream); return true;
+    case 5: launch<D, kFp8, 5>(p, stream); return true;
+    case 6: launch<D, kFp8, 6>(p, stream); return true;
+    case 7: launch<D, kFp8, 7>(p, stream); return true;
+    case 8: launch<D, kFp8, 8>(p, stream); return true;
+    default: return false;
+  }
+}
+
 }  // namespace
+
+FastDiv make_fast_div(uint32_t d) {
+  FastDiv f;
+  f.d = d ? d : 1;
+  uint32_t s = 0;
+  while ((1ull << s) < f.d) ++s;
+  f.shift = s;
+  f.mul = (uint32_t)(((1ull << 32) * ((1ull << s) - f.d)) / f.d + 1);
+  return f;
+}
 
 uint64_t decode_workspace_bytes(int32_t batch, int32_t q_heads, int32_t head_dim, int32_t splits) {
   const uint64_t rows = (uint64_t)batch * q_heads * splits;
@@ -363,15 +442,10 @@ uint64_t decode_workspace_bytes(int32_t batch, int32_t q_heads, int32_t head_dim
 }
 
 hipError_t launch_paged_decode(const DecodeParams& p, bool fp8, hipStream_t stream) {
-  if (p.head_dim == 128) {
-    if (fp8) launch<128, true>(p, stream);
-    else launch<128, false>(p, stream);
-  } else if (p.head_dim == 64) {
-    if (fp8) launch<64, true>(p, stream);
-    else launch<64, false>(p, stream);
-  } else {
-    return hipErrorInvalidValue;
-  }
+  bool ok = false;
+  if (p.head_dim == 128) ok = fp8 ? launch_kvm<128, true>(p, stream) : launch_kvm<128, false>(p, stream);
+  else if (p.head_dim == 64) ok = fp8 ? launch_kvm<64, true>(p, stream) : launch_kvm<64, false>(p, stream);
+  if (!ok) return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

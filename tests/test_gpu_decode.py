@@ -32,7 +32,7 @@ def bf16_to_f64(u16):
 
 class DecodeCase:
     def __init__(self, torch, *, fp8, layers, H, D, kvm, seq_lens, seed, n_pages=None,
-                 segment_pages=0, layer=None):
+                 segment_pages=0, layer=None, raw_codes=False):
         self.torch = torch
         self.fp8, self.layers, self.H, self.D, self.kvm = fp8, layers, H, D, kvm
         self.layer = layers - 1 if layer is None else layer
@@ -62,6 +62,13 @@ class DecodeCase:
                                self.scales.numel() * 4, runs, self.kv) as rl:
                 rl.copy_fp8(P.PBE_FP8_SCALE_PER_TOKEN_HEAD, 0, stream_ptr(torch))
             torch.cuda.synchronize()
+            if raw_codes:  # every non-NaN E4M3 code (subnormals, +-448) and random scales
+                for x in self.bufs:
+                    codes = rng.integers(0, 254, x.numel(), dtype=np.uint8)
+                    codes[codes >= 0x7F] += 1  # skip 0x7f; 0xff is out of range
+                    x.copy_(torch.from_numpy(codes).cuda())
+                self.scales.copy_(torch.from_numpy(
+                    rng.uniform(1e-3, 0.05, self.scales.numel()).astype(np.float32)).cuda())
         else:
             self.bufs, self.view = self.bf_bufs, self.bf_view
             self.scales = None
@@ -176,6 +183,13 @@ def test_qwen05b_geometry_head_dim_64(torch_cuda, fp8):
     say(f"decode fp8={fp8} L3 H2 D64 kvm7")
     case = DecodeCase(torch_cuda, fp8=fp8, layers=3, H=2, D=64, kvm=7,
                       seq_lens=[5, 64, 65, 200, 1], seed=2, layer=1)
+    _check(case, case.run())
+
+
+def test_every_e4m3_code_dequantizes_exactly(torch_cuda):
+    say("decode fp8 raw codes")
+    case = DecodeCase(torch_cuda, fp8=True, layers=2, H=2, D=128, kvm=4,
+                      seq_lens=[200, 3, 64, 129], seed=7, raw_codes=True)
     _check(case, case.run())
 
 
