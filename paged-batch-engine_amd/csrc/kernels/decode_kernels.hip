@@ -116,7 +116,11 @@ struct Geo {
   static constexpr int E = kFp8 ? 1 : 2;
   static constexpr int WORDS = D * E / 16;   // key words = value words per lane
   static constexpr int PITCH = D * E + 16;   // LDS row pitch of the value tile
-  static constexpr int SETS = kFp8 ? 4 : 2;  // register sets: SETS-1 blocks in flight
+#ifndef PBE_DECODE_SETS_FP8
+#define PBE_DECODE_SETS_FP8 4
+#define PBE_DECODE_SETS_BF16 2
+#endif
+  static constexpr int SETS = kFp8 ? PBE_DECODE_SETS_FP8 : PBE_DECODE_SETS_BF16;  // SETS-1 blocks in flight
 };
 
 template <int W>
@@ -322,7 +326,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
 
   // SETS register sets in rotation: while one block is computed, the next
   // SETS-1 are in flight.
-  static_assert(SETS == 2 || SETS == 4, "register rotation is written out for 2 or 4 sets");
+  static_assert(SETS >= 2 && SETS <= 4, "register rotation is written out for 2 to 4 sets");
   BlockRegs<W> r0, r1, r2, r3;
   auto prime = [&](int blk, BlockRegs<W>& r) {
     if (!load(blk, r)) bad = true, blk1 = min(blk1, blk);
@@ -333,17 +337,13 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
   };
   prime(blk0, r0);
   prime(blk0 + 1, r1);
-  if constexpr (SETS == 4) {
-    prime(blk0 + 2, r2);
-    prime(blk0 + 3, r3);
-  }
+  if constexpr (SETS >= 3) prime(blk0 + 2, r2);
+  if constexpr (SETS >= 4) prime(blk0 + 3, r3);
   for (int base = blk0; base < blk1; base += SETS) {
     step(base, r0);
     step(base + 1, r1);
-    if constexpr (SETS == 4) {
-      step(base + 2, r2);
-      step(base + 3, r3);
-    }
+    if constexpr (SETS >= 3) step(base + 2, r2);
+    if constexpr (SETS >= 4) step(base + 3, r3);
   }
 
   // ---- this split's partials (lane (g, j): head j, dims 16nt + 4g + i)
