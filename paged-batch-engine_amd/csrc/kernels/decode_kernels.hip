@@ -228,11 +228,17 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
     {
       const int t = lane >> 2;
       unsigned char* dst = vt_w + t * PITCH + (lane & 3) * (D * E / 4);
+      if (valid == kBlockTokens) {  // every block but a sequence's last
 #pragma unroll
-      for (int v = 0; v < W / 4; ++v) {
-        const u32x4 x = t < valid ? u32x4{r.v[4 * v], r.v[4 * v + 1], r.v[4 * v + 2], r.v[4 * v + 3]}
-                                  : u32x4{0u, 0u, 0u, 0u};
-        *reinterpret_cast<u32x4*>(dst + 16 * v) = x;
+        for (int v = 0; v < W / 4; ++v)
+          *reinterpret_cast<u32x4*>(dst + 16 * v) = u32x4{r.v[4 * v], r.v[4 * v + 1], r.v[4 * v + 2], r.v[4 * v + 3]};
+      } else {
+#pragma unroll
+        for (int v = 0; v < W / 4; ++v) {
+          const u32x4 x = t < valid ? u32x4{r.v[4 * v], r.v[4 * v + 1], r.v[4 * v + 2], r.v[4 * v + 3]}
+                                    : u32x4{0u, 0u, 0u, 0u};
+          *reinterpret_cast<u32x4*>(dst + 16 * v) = x;
+        }
       }
       if (lane < 32) lds_s[w][lane] = r.scale;
     }
@@ -280,13 +286,15 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
       const float p0 = ok0 ? __builtin_amdgcn_exp2f(sv[i] - mn) : 0.f;
       const float p1 = ok1 ? __builtin_amdgcn_exp2f(sv[i + 1] - mn) : 0.f;
       psum += p0 + p1;
-      // p * v_scale as bf16 hi + bf16 lo: the value product keeps ~16 bits.
+      // p * v_scale as a bf16 hi + bf16 lo pair by truncation: hi keeps the
+      // top 8 significant bits, lo the next 8 of the exact remainder, so the
+      // pair is within 2^-15 of the fp32 product.
       const float a0 = ok0 ? p0 * vs[i] : 0.f, a1 = ok1 ? p1 * vs[i + 1] : 0.f;
-      const uint32_t h0 = to_bf16(a0), h1 = to_bf16(a1);
-      const uint32_t l0 = to_bf16(a0 - __uint_as_float(h0 << 16));
-      const uint32_t l1 = to_bf16(a1 - __uint_as_float(h1 << 16));
-      phi[i / 2] = h0 | (h1 << 16);
-      plo[i / 2] = l0 | (l1 << 16);
+      const uint32_t h0 = __float_as_uint(a0) & 0xffff0000u, h1 = __float_as_uint(a1) & 0xffff0000u;
+      const uint32_t l0 = __float_as_uint(a0 - __uint_as_float(h0)) & 0xffff0000u;
+      const uint32_t l1 = __float_as_uint(a1 - __uint_as_float(h1)) & 0xffff0000u;
+      phi[i / 2] = (h0 >> 16) | h1;
+      plo[i / 2] = (l0 >> 16) | l1;
     }
     psum += __shfl_xor(psum, 16);
     psum += __shfl_xor(psum, 32);
