@@ -1157,4 +1157,47 @@ TEST_CASE("page takeover: stale identities, bad inputs and geometry mismatches a
   TwoGroups::retire_all(*t.p, b);
 }
 
+TEST_CASE("TakeOverSharedKV: whole-Chunk requests move without a copy; refusals change nothing") {
+  TwoGroups t(30, 15, 15);
+  auto a = TwoGroups::alloc(*t.p, 6);  // two whole 3-page Chunks
+  base::SharedKVPageGroup::PageTakeover tk;
+  t.p->detach_for_takeover(a, &tk);
+  REQUIRE(tk.copy_ids.empty());
+  serving::KVPoolDescriptor pool{0, 3, 16, 2, 64, base::DataType::kDataTypeBf16,
+                                 base::BlockStorageMode::kPlain};
+  serving::SharedArenaBinding binding{fake_view(30 * TwoGroups::kPage), 11, -1};
+  std::vector<int32_t> table;
+  uint64_t copied = 7;
+  REQUIRE(serving::TakeOverSharedKV(t.d.get(), binding, tk, pool, nullptr, &table, &copied));
+  t.p->finish_takeover(tk);
+  CHECK(table == a);
+  CHECK_EQ(copied, 0u);
+  CHECK_EQ(t.owner->leased_bytes("d"), 6 * TwoGroups::kPage);
+  // a receiver without quota refuses; the source takes its Chunks back
+  TwoGroups u(30, 15, 2);
+  auto b = TwoGroups::alloc(*u.p, 3);
+  base::SharedKVPageGroup::PageTakeover tk2;
+  u.p->detach_for_takeover(b, &tk2);
+  serving::SharedArenaBinding ub{fake_view(30 * TwoGroups::kPage), 11, -1};
+  auto st = serving::TakeOverSharedKV(u.d.get(), ub, tk2, pool, nullptr, &table, &copied);
+  CHECK(!st);
+  CHECK(table.empty());
+  CHECK_EQ(u.d->leased_bytes(), 0u);
+  u.p->reattach(tk2);
+  TwoGroups::retire_all(*u.p, b);
+  u.p->collect();
+  CHECK_EQ(u.owner->lease_count(), 0u);
+  // layer-count mismatch is rejected before anything is adopted
+  TwoGroups v(30, 15, 15);
+  auto c = TwoGroups::alloc(*v.p, 3);
+  base::SharedKVPageGroup::PageTakeover tk3;
+  v.p->detach_for_takeover(c, &tk3);
+  auto bad_pool = pool;
+  bad_pool.layer_num = 4;
+  CHECK(!serving::TakeOverSharedKV(v.d.get(), binding, tk3, bad_pool, nullptr, &table, &copied));
+  CHECK_EQ(v.d->leased_bytes(), 0u);
+  v.p->reattach(tk3);
+  TwoGroups::retire_all(*v.p, c);
+}
+
 MINITEST_MAIN()
