@@ -52,6 +52,7 @@ HOST_SOURCES = [
 # the CPU-only unit-test binary).
 ABI_HOST_SOURCES = [
     "csrc/base/shared_kv_arena.cpp",
+    "csrc/base/block_allocator.cpp",
     "csrc/cache/hip_transfer_backend.cpp",
     "csrc/serving/shared_kv_handoff.cpp",
     "csrc/serving/decode_kv_reservation.cpp",

@@ -492,6 +492,15 @@ void* SharedKVPageGroup::key_base(int layer) const {
   return base ? static_cast<char*>(base) + 2ull * layer * impl_->half : nullptr;
 }
 
+void* SharedKVPageGroup::plane_address(int64_t index) const {
+  const pbe_arena_view& v = impl_->arena->view();
+  if (index < 0) return nullptr;
+  const uint64_t off = static_cast<uint64_t>(index) * impl_->half;
+  if (off / impl_->half != static_cast<uint64_t>(index) || off >= v.bytes) return nullptr;
+  const uint64_t seg = off / v.segment_bytes;
+  return static_cast<char*>(v.base[seg]) + (off - seg * v.segment_bytes);
+}
+
 void* SharedKVPageGroup::value_base(int layer) const {
   void* base = impl_->arena->data();
   return base ? static_cast<char*>(base) + (2ull * layer + 1) * impl_->half : nullptr;

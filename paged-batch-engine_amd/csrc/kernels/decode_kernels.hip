@@ -73,23 +73,6 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Four E4M3 bytes -> four BF16 (exact), packed in two words.
-__device__ __forceinline__ u32x2 e4m3x4_to_bf16x4(uint32_t w) {
-  const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
-  const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
-  return u32x2{(__float_as_uint(lo[0]) >> 16) | (__float_as_uint(lo[1]) & 0xffff0000u),
-               (__float_as_uint(hi[0]) >> 16) | (__float_as_uint(hi[1]) & 0xffff0000u)};
-}
-
-__device__ __forceinline__ void e4m3x4_to_f32(uint32_t w, float* out) {
-  const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
-  const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, true);
-  out[0] = lo[0];
-  out[1] = lo[1];
-  out[2] = hi[0];
-  out[3] = hi[1];
-}
-
 // fp32 -> bf16, round to nearest even; NaN stays NaN (quiet).
 __device__ __forceinline__ uint16_t to_bf16(float f) {
   const uint32_t u = __float_as_uint(f);

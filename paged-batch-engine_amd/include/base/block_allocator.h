@@ -1,0 +1,125 @@
+// Shared-arena mode of the reference's block allocator
+// (infMain/include/base/block_allocator.h:15-230, block_allocator.cpp:139-401):
+// the per-layer view of a SharedKVPageGroup that copy_shared_kv and the decode
+// runtime use. Block ids are page-major (byte offset / half), so layer l's K
+// plane of block b is half-plane b + 2l of the arena and its V plane b + 2l + 1.
+// Device pointers are plain pointers (no tensor type); the local-pool and
+// external-pool modes of the reference are model-runtime code outside this build.
+#ifndef PBE_INCLUDE_BASE_BLOCK_ALLOCATOR_H_
+#define PBE_INCLUDE_BASE_BLOCK_ALLOCATOR_H_
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <utility>
+#include <vector>
+
+#include "base/base.h"
+#include "base/kv_cache_format.h"
+#include "base/shared_kv_arena.h"
+
+namespace base {
+
+struct BlockHandle {
+  int32_t block_id = -1;
+  uint64_t generation = 0;
+  uint64_t pool_id = 0;
+};
+
+struct KVBlockPayloadPtrs {
+  void* key = nullptr;
+  void* value = nullptr;
+  void* key_scale = nullptr;
+  void* value_scale = nullptr;
+  size_t key_value_bytes = 0;
+  size_t scale_bytes = 0;
+};
+
+// Non-owning binding used by compute kernels (block_allocator.h:86-112). In
+// the shared arena, block b of this layer starts at key + b * block_stride
+// (single-segment arenas; segmented arenas resolve per block through
+// BlockAllocator::get_block_payload_ptrs).
+class KVPoolView {
+ public:
+  KVPoolView() = default;
+  KVPoolView(void* key, void* value, void* key_scale, void* value_scale, size_t block_stride,
+             KVCacheStorageSpec storage_spec, DeviceType device)
+      : key_(key), value_(value), key_scale_(key_scale), value_scale_(value_scale),
+        block_stride_(block_stride), storage_spec_(storage_spec), device_(device) {}
+  bool valid() const { return key_ != nullptr && value_ != nullptr; }
+  bool uses_fp8_storage() const { return storage_spec_.uses_fp8_storage(); }
+  DeviceType device_type() const { return device_; }
+  const KVCacheStorageSpec& storage_spec() const { return storage_spec_; }
+  void* key_pool() const { return key_; }
+  void* value_pool() const { return value_; }
+  void* key_scale_pool() const { return key_scale_; }
+  void* value_scale_pool() const { return value_scale_; }
+  size_t block_stride() const { return block_stride_; }
+
+ private:
+  void* key_ = nullptr;
+  void* value_ = nullptr;
+  void* key_scale_ = nullptr;
+  void* value_scale_ = nullptr;
+  size_t block_stride_ = 0;
+  KVCacheStorageSpec storage_spec_;
+  DeviceType device_ = DeviceType::kDeviceUnknown;
+};
+
+class BlockAllocator {
+ public:
+  // Shared-arena mode (block_allocator.cpp:139-163): BF16 plain storage, one
+  // allocator per layer over a page group whose half-plane equals
+  // block_size * num_kv_heads * head_size * 2 bytes. Throws
+  // std::invalid_argument on a mismatch.
+  BlockAllocator(int32_t block_size, int32_t num_kv_heads, int32_t head_size,
+                 std::shared_ptr<SharedKVPageGroup> group, int32_t layer);
+  BlockAllocator(const BlockAllocator&) = delete;
+  BlockAllocator& operator=(const BlockAllocator&) = delete;
+
+  // Block id of a fresh page for this layer, or -1 when the group is out of
+  // quota (block_allocator.cpp:206-216). Layers allocate in order.
+  int32_t allocate();
+  void incref(int32_t block_id);
+  // Drops one reference; the last one retires the page in the group.
+  void free(int32_t block_id);
+  int32_t ref_count(int32_t block_id) const;
+  BlockHandle handle(int32_t block_id) const;
+  bool is_current(BlockHandle handle) const;
+
+  std::pair<void*, void*> get_block_ptrs(int32_t block_id) const;
+  KVBlockPayloadPtrs get_block_payload_ptrs(int32_t block_id) const;
+
+  int32_t num_free_blocks() const;
+  int32_t num_total_blocks() const;
+  bool uses_shared_arena() const { return true; }
+  size_t shared_leased_bytes() const;
+  size_t shared_arena_bytes() const;
+  uint64_t shared_arena_epoch() const;
+
+  int32_t block_size() const { return block_size_; }
+  int32_t num_kv_heads() const { return num_kv_heads_; }
+  int32_t head_size() const { return head_size_; }
+  int32_t layer() const { return layer_; }
+  const KVCacheStorageSpec& storage_spec() const { return storage_spec_; }
+  BlockStorageMode storage_mode() const { return storage_spec_.storage_mode; }
+  bool uses_fp8_storage() const { return storage_spec_.uses_fp8_storage(); }
+  DeviceType device_type() const { return DeviceType::kDeviceHIP; }
+  size_t key_value_bytes_per_block() const;
+  size_t scale_bytes_per_block() const { return 0; }
+  KVPoolView pool_view() const;
+
+ private:
+  void check_id(int32_t block_id) const;
+  std::shared_ptr<SharedKVPageGroup> group_;
+  int32_t block_size_, num_kv_heads_, head_size_, layer_;
+  int32_t num_blocks_ = 0;
+  uint64_t pool_id_ = 0;
+  KVCacheStorageSpec storage_spec_;
+  std::vector<int32_t> ref_counts_;
+  std::vector<uint64_t> generations_;
+};
+
+}  // namespace base
+
+#endif  // PBE_INCLUDE_BASE_BLOCK_ALLOCATOR_H_

@@ -128,6 +128,9 @@ class SharedKVPageGroup {
   // K / V plane bases of a single-segment arena (shared_kv_arena.cpp:224-229).
   void* key_base(int layer) const;
   void* value_base(int layer) const;
+  // This process's address of half-plane `index` (byte offset index * half)
+  // in any arena, segmented or not; nullptr past the end.
+  void* plane_address(int64_t index) const;
   // Returns completed pages, and Chunks whose pages are all free, to the owner.
   void collect();
 

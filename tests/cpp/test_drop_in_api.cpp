@@ -21,6 +21,7 @@
 #include "serving/decode_kv_reservation.h"
 #include "serving/pd_handoff.h"
 #include "serving/kv_page_wire.h"
+#include "base/block_allocator.h"
 
 using namespace cache;
 
@@ -1198,6 +1199,54 @@ TEST_CASE("TakeOverSharedKV: whole-Chunk requests move without a copy; refusals 
   CHECK_EQ(v.d->leased_bytes(), 0u);
   v.p->reattach(tk3);
   TwoGroups::retire_all(*v.p, c);
+}
+
+TEST_CASE("block allocator (shared arena): per-layer ids, refcounts, payload pointers") {
+  auto owner = std::make_shared<base::LocalChunkOwner>(12 * Group::kPage, 9);
+  owner->register_model("d", 12 * Group::kPage);
+  // segmented mapping: 4 segments of 3 pages; group geometry: 3 layers, half 4 KiB
+  pbe_arena_view view = fake_view(12 * Group::kPage, 3 * Group::kPage);
+  auto client = std::make_shared<base::SharedKVArenaClient>(owner, view, "d", 12 * Group::kPage, -1);
+  auto group = std::make_shared<base::SharedKVPageGroup>(client, 3, Group::kHalf, 3 * Group::kPage, nullptr);
+  // block_size 16 x 1 head x 128 dims x 2 B = 4 KiB = half
+  CHECK_THROWS_AS(base::BlockAllocator(16, 2, 128, group, 0), std::invalid_argument);
+  CHECK_THROWS_AS(base::BlockAllocator(16, 1, 128, group, 3), std::invalid_argument);
+  std::vector<std::unique_ptr<base::BlockAllocator>> layers;
+  for (int l = 0; l < 3; ++l) layers.push_back(std::make_unique<base::BlockAllocator>(16, 1, 128, group, l));
+  CHECK_EQ(layers[0]->num_total_blocks(), 12);
+  const int a = layers[0]->allocate();
+  const int b = layers[0]->allocate();
+  CHECK_EQ(layers[1]->allocate(), a);
+  CHECK_EQ(layers[2]->allocate(), a);
+  CHECK_EQ(layers[1]->allocate(), b);
+  CHECK_EQ(layers[2]->allocate(), b);
+  // payload pointers: K of layer l = half-plane id + 2l, V = id + 2l + 1, through the segments
+  for (int l = 0; l < 3; ++l) {
+    for (int id : {a, b}) {
+      auto p = layers[l]->get_block_payload_ptrs(id);
+      const uint64_t koff = (uint64_t)(id + 2 * l) * Group::kHalf, voff = koff + Group::kHalf;
+      const uint64_t seg = 3 * Group::kPage;
+      CHECK(p.key == static_cast<char*>(view.base[koff / seg]) + koff % seg);
+      CHECK(p.value == static_cast<char*>(view.base[voff / seg]) + voff % seg);
+      CHECK_EQ(p.key_value_bytes, (size_t)Group::kHalf);
+      CHECK(p.key_scale == nullptr);
+    }
+  }
+  auto h = layers[0]->handle(a);
+  CHECK(layers[0]->is_current(h));
+  layers[0]->incref(a);
+  CHECK_EQ(layers[0]->ref_count(a), 2);
+  layers[0]->free(a);
+  CHECK(layers[0]->is_current(h));
+  for (int l = 0; l < 3; ++l) layers[l]->free(a);  // last references retire the page
+  CHECK(!layers[0]->is_current(h));
+  CHECK_THROWS_AS(layers[0]->free(a), std::logic_error);
+  CHECK_THROWS_AS(layers[0]->get_block_payload_ptrs(-1), std::out_of_range);
+  // the retired page is the lowest free id again, with a new generation
+  CHECK_EQ(layers[0]->allocate(), a);
+  CHECK(!layers[0]->is_current(h));
+  CHECK_EQ(layers[0]->shared_arena_epoch(), 9u);
+  CHECK_EQ(layers[0]->shared_arena_bytes(), (size_t)(12 * Group::kPage));
 }
 
 MINITEST_MAIN()
