@@ -188,6 +188,16 @@ bool view_accessible(const pbe_arena_view& v, int device, std::vector<Range>* kn
   return true;
 }
 
+// Run lists of up to kKernargRuns entries go in the kernel arguments;
+// PBE_KERNARG=0 stages them through device memory instead (measurement only).
+bool kernarg_runs_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("PBE_KERNARG");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
 // Identity-copy kernel variant. The defaults are the measured best on MI355X;
 // PBE_UNROLL / PBE_POLICY / PBE_BLOCK / PBE_LDS override them for tuning
 // experiments only.
@@ -1039,9 +1049,24 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
                     pbe::slice_bytes(pbe::KernelKind::kCopy, cfg), &res);
   if (rc != PBE_OK) return rc;
   PBE_DEVICE_SCOPE(device);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const pbe::LaunchShape shape_l = launch_shape(res.info.slices, device, cfg);
+  const pbe::CopyConfig def{};
+  if ((uint64_t)n_runs <= pbe::kKernargRuns && kernarg_runs_enabled() && shape_l.slices_per_wave == 1 &&
+      cfg.unroll == def.unroll && cfg.policy == def.policy && cfg.block == def.block &&
+      cfg.lds_bytes == def.lds_bytes) {
+    // Short lists ride in the kernel arguments: no staging copy, no fence.
+    pbe::KernargRunList list{};
+    list.n_runs = (uint32_t)n_runs;
+    list.total_slices = (uint32_t)res.info.slices;
+    list.page_bytes = 2ull * shape->layers * half;
+    std::memcpy(list.runs, res.runs.data(), res.runs.size() * sizeof(pbe::DevRun));
+    PBE_HIP(pbe::launch_copy_runs_kernarg(list, s));
+    if (copied) *copied = res.info.src_bytes;
+    return PBE_OK;
+  }
   Staging& st = staging_for(device);
   std::lock_guard<std::mutex> lock(st.mu);
-  const hipStream_t s = static_cast<hipStream_t>(stream);
   void* dev = nullptr;
   StagingSlot* slot = nullptr;
   rc = stage(st, res.runs.data(), res.runs.size() * sizeof(pbe::DevRun), s, &slot, &dev);

@@ -48,6 +48,20 @@ struct LaunchShape {
 
 uint32_t slice_bytes(KernelKind kind, const CopyConfig& cfg);
 
+// Run lists this short travel in the kernel arguments (3.6 KB of the 4 KB
+// kernarg space) instead of a staged device copy.
+constexpr uint32_t kKernargRuns = 112;
+struct KernargRunList {
+  uint32_t n_runs;
+  uint32_t total_slices;
+  uint64_t page_bytes;
+  DevRun runs[kKernargRuns];
+};
+static_assert(sizeof(KernargRunList) <= 4096 - 256, "kernel arguments are limited to 4 KiB");
+
+// Default copy variant (unroll 4, global nt, 256 threads, one slice per wave).
+hipError_t launch_copy_runs_kernarg(const KernargRunList& list, hipStream_t stream);
+
 hipError_t launch_copy_runs(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
                             uint64_t page_bytes, const LaunchShape& shape, hipStream_t stream);
 

@@ -120,9 +120,9 @@ __device__ __forceinline__ void copy_slice(uint64_t src, uint64_t dst, uint64_t 
 // cudaMemcpyAsync loop (split_pd_engine.cpp:96-108). Wave w copies the
 // contiguous slice range [w*k, (w+1)*k) (k = slices_per_wave).
 template <int kUnroll, int kPolicy, int kBlock>
-__global__ __launch_bounds__(kBlock) void copy_runs_kernel(
-    const DevRun* __restrict__ runs, uint32_t n_runs, uint32_t total_slices,
-    uint32_t slices_per_wave, uint64_t page_bytes) {
+__device__ __forceinline__ void copy_runs_body(const DevRun* __restrict__ runs, uint32_t n_runs,
+                                               uint32_t total_slices, uint32_t slices_per_wave,
+                                               uint64_t page_bytes) {
   constexpr uint32_t kSlice = kWave * 16u * kUnroll;
   const uint32_t lane = threadIdx.x % kWave;
   const uint32_t wave = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
@@ -137,6 +137,20 @@ __global__ __launch_bounds__(kBlock) void copy_runs_kernel(
     const uint64_t run_bytes = (uint64_t)run.pages * page_bytes;
     copy_slice<kUnroll, kPolicy>(run.src + rel, run.dst + rel, run_bytes - rel, lane);
   }
+}
+
+template <int kUnroll, int kPolicy, int kBlock>
+__global__ __launch_bounds__(kBlock) void copy_runs_kernel(
+    const DevRun* __restrict__ runs, uint32_t n_runs, uint32_t total_slices,
+    uint32_t slices_per_wave, uint64_t page_bytes) {
+  copy_runs_body<kUnroll, kPolicy, kBlock>(runs, n_runs, total_slices, slices_per_wave, page_bytes);
+}
+
+// The same copy with the run list in the kernel arguments (no staging copy).
+// An aggregate kernel argument stays in the kernarg segment and is read there.
+__global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_kernarg_kernel(const KernargRunList list) {
+  copy_runs_body<kCopyUnroll, 0, kThreadsPerBlock>(list.runs, list.n_runs, list.total_slices, 1u,
+                                                   list.page_bytes);
 }
 
 // ---- FP8 E4M3 (OCP v1.0, "fn": no infinities, 0x7F NaN, max 448) ----
@@ -418,6 +432,15 @@ bool pick_policy(const CopyConfig& c, const CopyArgs& a) {
   }
 }
 }  // namespace
+
+hipError_t launch_copy_runs_kernarg(const KernargRunList& list, hipStream_t stream) {
+  if (list.n_runs == 0 || list.n_runs > kKernargRuns) return hipErrorInvalidValue;
+  const uint32_t waves = list.total_slices ? list.total_slices : 1u;
+  const uint32_t per_block = kThreadsPerBlock / kWave;
+  hipLaunchKernelGGL(copy_runs_kernarg_kernel, dim3((waves + per_block - 1) / per_block),
+                     dim3(kThreadsPerBlock), 0, stream, list);
+  return hipGetLastError();
+}
 
 hipError_t launch_copy_runs(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
                             uint64_t page_bytes, const LaunchShape& shape, hipStream_t stream) {

@@ -136,6 +136,11 @@ def test_copy_shared_kv_back_to_back_without_sync(torch_cuda):
         total -= P.copy_shared_kv(view, s, d, kv, 0, stream_ptr(torch))
         start, k, calls = start + k, 2 * k, calls + 1
     assert calls > 8
+    # both launch forms ran: short run lists travel in the kernel arguments,
+    # long ones through the staging ring
+    sizes = [len(P.build_runs(src[a:a + k], dst[a:a + k], kv))
+             for a, k in ((2 ** i - 1, 2 ** i) for i in range(calls)) if a < len(src)]
+    assert min(sizes) <= 112 < max(sizes), sizes
     torch.cuda.synchronize()
     assert total == 0
     after = snapshot(bufs)
