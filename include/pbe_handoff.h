@@ -238,6 +238,15 @@ int pbe_handoff_copy(const pbe_runlist* list, void* stream);
 int pbe_handoff_copy_fp8(const pbe_runlist* list, int scale_mode, const float* amax_table,
                          void* stream);
 
+/* The same launches with two caller-created hipEvent_t (timing enabled) that
+ * the runtime stamps at the kernel's own start and end (hipExtLaunchKernel),
+ * so hipEventElapsedTime(start, stop) is the kernel's duration. For per-
+ * handoff GPU-time accounting; no counterpart in the reference. */
+int pbe_handoff_copy_timed(const pbe_runlist* list, void* stream, void* start_event,
+                           void* stop_event);
+int pbe_handoff_copy_fp8_timed(const pbe_runlist* list, int scale_mode, const float* amax_table,
+                               void* stream, void* start_event, void* stop_event);
+
 /* ---- one-call form of copy_shared_kv's data path -----------------------
  * Validates ids against the arena (as split_pd_engine.cpp:70-77), coalesces,
  * builds and uploads a run list, launches one copy and returns the copied

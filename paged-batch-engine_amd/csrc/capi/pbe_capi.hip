@@ -920,17 +920,30 @@ int pbe_runlist_destroy(pbe_runlist* list) {
   return PBE_OK;
 }
 
-int pbe_handoff_copy(const pbe_runlist* list, void* stream) {
+int pbe_handoff_copy_timed(const pbe_runlist* list, void* stream, void* start_event,
+                           void* stop_event) {
   if (!list) return fail(PBE_ERR_INVALID, "null run list");
   if (list->fp8) return fail(PBE_ERR_INVALID, "FP8 run list passed to the BF16 copy");
   PBE_DEVICE_SCOPE(list->device);
+  pbe::LaunchShape shape = list->shape;
+  shape.start = static_cast<hipEvent_t>(start_event);
+  shape.stop = static_cast<hipEvent_t>(stop_event);
   PBE_HIP(pbe::launch_copy_runs(list->runs, list->n_runs, list->total_slices, list->page_bytes,
-                                list->shape, static_cast<hipStream_t>(stream)));
+                                shape, static_cast<hipStream_t>(stream)));
   return PBE_OK;
+}
+
+int pbe_handoff_copy(const pbe_runlist* list, void* stream) {
+  return pbe_handoff_copy_timed(list, stream, nullptr, nullptr);
 }
 
 int pbe_handoff_copy_fp8(const pbe_runlist* list, int scale_mode, const float* amax_table,
                          void* stream) {
+  return pbe_handoff_copy_fp8_timed(list, scale_mode, amax_table, stream, nullptr, nullptr);
+}
+
+int pbe_handoff_copy_fp8_timed(const pbe_runlist* list, int scale_mode, const float* amax_table,
+                               void* stream, void* start_event, void* stop_event) {
   if (!list) return fail(PBE_ERR_INVALID, "null run list");
   if (!list->fp8) return fail(PBE_ERR_INVALID, "BF16 run list passed to the FP8 copy");
   if (scale_mode == PBE_FP8_SCALE_PER_TOKEN_HEAD && !list->has_scales)
@@ -942,11 +955,13 @@ int pbe_handoff_copy_fp8(const pbe_runlist* list, int scale_mode, const float* a
   PBE_DEVICE_SCOPE(list->device);
   const pbe_kv_shape& kv = list->kv;
   const uint32_t rows_per_plane = (uint32_t)(kv.page_tokens * kv.kv_heads);
+  pbe::LaunchShape shape = list->shape;
+  shape.start = static_cast<hipEvent_t>(start_event);
+  shape.stop = static_cast<hipEvent_t>(stop_event);
   PBE_HIP(pbe::launch_copy_runs_fp8(
       list->runs, list->n_runs, list->total_slices, list->page_bytes, (uint32_t)kv.head_dim / 8u,
       rows_per_plane, (uint32_t)kv.kv_heads, rows_per_plane * 2u * (uint32_t)kv.layers,
-      scale_mode == PBE_FP8_SCALE_TABLE, amax_table, list->shape,
-      static_cast<hipStream_t>(stream)));
+      scale_mode == PBE_FP8_SCALE_TABLE, amax_table, shape, static_cast<hipStream_t>(stream)));
   return PBE_OK;
 }
 

@@ -44,6 +44,9 @@ struct CopyConfig {
 struct LaunchShape {
   uint32_t slices_per_wave = 1;
   CopyConfig copy;
+  // Optional events that bracket the kernel itself (hipExtLaunchKernel).
+  hipEvent_t start = nullptr;
+  hipEvent_t stop = nullptr;
 };
 
 uint32_t slice_bytes(KernelKind kind, const CopyConfig& cfg);

@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <hip/hip_ext.h>
+
 #include "handoff_kernels.h"
 
 namespace pbe {
@@ -406,12 +408,14 @@ struct CopyArgs {
   const DevRun* runs;
   uint32_t n_runs, total_slices, slices_per_wave;
   uint64_t page_bytes;
+  hipEvent_t start, stop;
 };
 template <int U, int P, int B>
 void launch_variant(const CopyArgs& a) {
   const uint32_t blocks = (a.waves + B / kWave - 1) / (B / kWave);
-  hipLaunchKernelGGL((copy_runs_kernel<U, P, B>), dim3(blocks), dim3(B), a.lds_bytes, a.stream,
-                     a.runs, a.n_runs, a.total_slices, a.slices_per_wave, a.page_bytes);
+  hipExtLaunchKernelGGL((copy_runs_kernel<U, P, B>), dim3(blocks), dim3(B), a.lds_bytes, a.stream,
+                        a.start, a.stop, 0, a.runs, a.n_runs, a.total_slices, a.slices_per_wave,
+                        a.page_bytes);
 }
 template <int U, int P>
 bool pick_block(const CopyConfig& c, const CopyArgs& a) {
@@ -448,7 +452,7 @@ hipError_t launch_copy_runs(const DevRun* runs, uint32_t n_runs, uint32_t total_
   uint32_t waves = (total_slices + shape.slices_per_wave - 1) / shape.slices_per_wave;
   if (waves == 0) waves = 1;
   const CopyArgs a{waves, c.lds_bytes, stream, runs, n_runs, total_slices, shape.slices_per_wave,
-                   page_bytes};
+                   page_bytes, shape.start, shape.stop};
   bool ok = false;
   switch (c.unroll) {
     case 2: ok = pick_policy<2>(c, a); break;
@@ -462,28 +466,29 @@ hipError_t launch_copy_runs(const DevRun* runs, uint32_t n_runs, uint32_t total_
 
 namespace {
 template <int U, int L>
-void launch_fp8(bool table, uint32_t blocks, hipStream_t stream, const DevRun* runs,
+void launch_fp8(bool table, uint32_t blocks, hipStream_t stream, hipEvent_t start, hipEvent_t stop,
+                const DevRun* runs,
                 uint32_t n_runs, uint32_t total_slices, uint32_t spw, uint64_t page_bytes,
                 uint32_t rows_per_plane, uint32_t kv_heads, uint32_t rows_per_page,
                 const float* amax_table) {
   if (table)
-    hipLaunchKernelGGL((copy_runs_fp8_kernel<U, L, true>), dim3(blocks), dim3(kThreadsPerBlock), 0,
-                       stream, runs, n_runs, total_slices, spw, page_bytes, rows_per_plane,
-                       kv_heads, rows_per_page, amax_table);
+    hipExtLaunchKernelGGL((copy_runs_fp8_kernel<U, L, true>), dim3(blocks), dim3(kThreadsPerBlock),
+                          0, stream, start, stop, 0, runs, n_runs, total_slices, spw,
+                          page_bytes, rows_per_plane, kv_heads, rows_per_page, amax_table);
   else
-    hipLaunchKernelGGL((copy_runs_fp8_kernel<U, L, false>), dim3(blocks), dim3(kThreadsPerBlock), 0,
-                       stream, runs, n_runs, total_slices, spw, page_bytes, rows_per_plane,
-                       kv_heads, rows_per_page, amax_table);
+    hipExtLaunchKernelGGL((copy_runs_fp8_kernel<U, L, false>), dim3(blocks), dim3(kThreadsPerBlock),
+                          0, stream, start, stop, 0, runs, n_runs, total_slices, spw,
+                          page_bytes, rows_per_plane, kv_heads, rows_per_page, amax_table);
 }
 template <int U>
 bool launch_fp8_lanes(uint32_t lanes, bool table, uint32_t blocks, hipStream_t stream,
-                      const DevRun* runs, uint32_t n_runs, uint32_t total_slices, uint32_t spw,
+                      hipEvent_t start, hipEvent_t stop, const DevRun* runs, uint32_t n_runs, uint32_t total_slices, uint32_t spw,
                       uint64_t page_bytes, uint32_t rows_per_plane, uint32_t kv_heads,
                       uint32_t rows_per_page, const float* amax_table) {
 #define PBE_FP8_CASE(L)                                                                       \
   case L:                                                                                     \
-    launch_fp8<U, L>(table, blocks, stream, runs, n_runs, total_slices, spw, page_bytes,      \
-                     rows_per_plane, kv_heads, rows_per_page, amax_table);                    \
+    launch_fp8<U, L>(table, blocks, stream, start, stop, runs, n_runs, total_slices, spw,     \
+                     page_bytes, rows_per_plane, kv_heads, rows_per_page, amax_table);        \
     return true;
   switch (lanes) {
     PBE_FP8_CASE(1)
@@ -510,17 +515,20 @@ hipError_t launch_copy_runs_fp8(const DevRun* runs, uint32_t n_runs, uint32_t to
   bool ok = false;
   switch (shape.copy.unroll) {
     case 2:
-      ok = launch_fp8_lanes<2>(lanes_per_row, table, blocks, stream, runs, n_runs, total_slices,
+      ok = launch_fp8_lanes<2>(lanes_per_row, table, blocks, stream, shape.start, shape.stop, runs,
+                               n_runs, total_slices,
                                shape.slices_per_wave, page_bytes, rows_per_plane, kv_heads,
                                rows_per_page, amax_table);
       break;
     case 4:
-      ok = launch_fp8_lanes<4>(lanes_per_row, table, blocks, stream, runs, n_runs, total_slices,
+      ok = launch_fp8_lanes<4>(lanes_per_row, table, blocks, stream, shape.start, shape.stop, runs,
+                               n_runs, total_slices,
                                shape.slices_per_wave, page_bytes, rows_per_plane, kv_heads,
                                rows_per_page, amax_table);
       break;
     case 8:
-      ok = launch_fp8_lanes<8>(lanes_per_row, table, blocks, stream, runs, n_runs, total_slices,
+      ok = launch_fp8_lanes<8>(lanes_per_row, table, blocks, stream, shape.start, shape.stop, runs,
+                               n_runs, total_slices,
                                shape.slices_per_wave, page_bytes, rows_per_plane, kv_heads,
                                rows_per_page, amax_table);
       break;

@@ -109,6 +109,8 @@ _SIGNATURES = [
     ("pbe_runlist_destroy", C.c_int, [_P]),
     ("pbe_handoff_copy", C.c_int, [_P, _P]),
     ("pbe_handoff_copy_fp8", C.c_int, [_P, C.c_int, _P, _P]),
+    ("pbe_handoff_copy_timed", C.c_int, [_P, _P, _P, _P]),
+    ("pbe_handoff_copy_fp8_timed", C.c_int, [_P, C.c_int, _P, _P, _P, _P]),
     ("pbe_copy_shared_kv", C.c_int, [C.POINTER(ArenaView), _P, _P, C.c_int64,
                                      C.POINTER(KvShape), C.c_int, _P, C.POINTER(C.c_uint64)]),
     ("pbe_copy_ops", C.c_int, [C.POINTER(CopyOp), C.c_int64, C.c_int, _P]),
@@ -267,6 +269,15 @@ class RunList:
     def copy_fp8(self, mode: int, amax_table_ptr: int = 0, stream: int = 0) -> None:
         check(lib().pbe_handoff_copy_fp8(self.handle, mode, amax_table_ptr or None,
                                          stream or None))
+
+    def copy_timed(self, stream: int, start_event: int, stop_event: int) -> None:
+        """copy() with two hipEvent_t handles stamped at the kernel's start and end."""
+        check(lib().pbe_handoff_copy_timed(self.handle, stream or None, start_event, stop_event))
+
+    def copy_fp8_timed(self, mode: int, amax_table_ptr: int, stream: int, start_event: int,
+                       stop_event: int) -> None:
+        check(lib().pbe_handoff_copy_fp8_timed(self.handle, mode, amax_table_ptr or None,
+                                               stream or None, start_event, stop_event))
 
     def close(self) -> None:
         if self.handle:

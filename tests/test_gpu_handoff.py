@@ -277,3 +277,32 @@ def test_empty_and_degenerate_inputs_are_rejected(torch_cuda):
         P.RunList.bf16(view, view, [(0, 0, 1)], kv)           # destination is its own source
     with pytest.raises(P.PbeError):
         P.RunList.bf16(view, view, [(0, 28, 2)], kv)          # runs past the arena
+
+
+def test_timed_launch_copies_and_brackets_the_kernel(torch_cuda):
+    """pbe_handoff_copy_timed: same bytes as the plain launch; its events time
+    the kernel alone, so they read no more than events recorded around it."""
+    torch = torch_cuda
+    w = W.config2(3)
+    g = w.geometry
+    kv = _kv(g)
+    say("timed launch config2")
+    bufs, view = device_arena(torch, w.arena_bytes)
+    fill_bf16(torch, bufs[0], w.sigma, 9)
+    torch.cuda.synchronize()
+    expected = snapshot(bufs)
+    O.copy_handoff(expected, w.src_ids, w.dst_ids, g.half(), g.layers)
+    runs = P.build_runs(w.src_ids, w.dst_ids, kv)
+    with P.RunList.bf16(view, view, runs, kv) as rl:
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        e.record()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        rl.copy_timed(stream_ptr(torch), s.cuda_event, e.cuda_event)
+        b.record()
+        torch.cuda.synchronize()
+        inner, outer = s.elapsed_time(e), a.elapsed_time(b)
+    assert 0 < inner <= outer, (inner, outer)
+    after = snapshot(bufs)
+    assert np.array_equal(after, expected), first_diff(after, expected)
