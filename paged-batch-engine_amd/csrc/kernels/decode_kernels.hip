@@ -7,16 +7,23 @@
 // acc += v * (p * v_scale), output = acc / sum as BF16 (round to nearest even).
 //
 // gfx950 mapping. One wave owns one (sequence, KV head, split) and walks its
-// blocks of 16 tokens:
-//  - scores: one v_mfma_f32_16x16x32_bf16 per 32 head dims. A = the query
-//    heads sharing the KV head (rows, padded to 16), B = the block's 16 keys
-//    (columns). FP8 keys become BF16 exactly (an E4M3 value has at most 3
-//    mantissa bits). The contraction order over head dims is permuted the
-//    same way in A and B so each lane reads one contiguous run of its key.
-//  - softmax: row max / row sum over the 16 token lanes with DPP row ops.
-//  - values: lane (g, j) accumulates tokens 4g..4g+3 of the block for head
-//    dims j*D/16.., all query heads of the group, in fp32 registers; the
-//    four token groups are summed once at the end.
+// blocks of 16 tokens; the KV heads of one (sequence, split) are neighbouring
+// waves of a workgroup, so a block's rows are read together:
+//  - loads: every 16-byte load instruction covers 64 contiguous bytes of each
+//    row it touches; 2 to 8 register sets rotate so that the next blocks are
+//    in flight while one is computed.
+//  - scores, transposed: one v_mfma_f32_16x16x32_bf16 per 32 head dims,
+//    A = the block's 16 keys (rows), B = the query heads sharing the KV head
+//    (columns, padded to 16). FP8 keys become BF16 exactly (an E4M3 value has
+//    at most 3 mantissa bits). The contraction order over head dims follows
+//    the load order, in A and B alike. Lane (g, j) ends with tokens 4g..4g+3
+//    of query head j.
+//  - softmax: per head in-lane, across the four lane groups with the gfx950
+//    row swaps (v_permlane32_swap / v_permlane16_swap).
+//  - values: the value tile goes through LDS once and comes back transposed
+//    with ds_read_b64_tr_b8 / _b16, four tokens of one head dim per lane, as
+//    the A operand of O^T += V^T P^T (P^T as held, split into a BF16 high and
+//    low part, K = 32).
 // A second kernel combines the splits.
 #include "decode_kernels.h"
 
@@ -66,6 +73,23 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x + __shfl_xor(x, 32);
 }
 
+// Max / sum over the four lanes j, j+16, j+32, j+48 with the gfx950 row
+// swaps (VALU only, no LDS round trip). Every lane ends with the same value,
+// combined in the same order.
+__device__ __forceinline__ float group_max4(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float group_sum4(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Orders this wave's LDS writes before its other lanes' reads.
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -91,9 +115,7 @@ __device__ __forceinline__ u32x2 e4m3x4_to_bf16x4_cvt(uint32_t w) {
 }
 
 // Per-lane registers of one block of 16 tokens of one KV head: the lane's
-// key run (row j, head dims g*D/4..), its quarter of a value row (token
-// lane/4, quarter lane%4) and one scale (FP8: lanes 0-15 key scale of token
-// lane, lanes 16-31 value scale of token lane-16).
+// part of key row j, its part of value row lane/4 and one scale.
 template <int D, bool kFp8>
 struct Geo {
   static constexpr int E = kFp8 ? 1 : 2;
@@ -106,11 +128,11 @@ struct Geo {
   static constexpr int SETS = kFp8 ? PBE_DECODE_SETS_FP8 : PBE_DECODE_SETS_BF16;  // SETS-1 blocks in flight
 };
 
-template <int W>
+template <int W, bool kFp8>
 struct BlockRegs {
   uint32_t k[W];
   uint32_t v[W];
-  float scale;
+  float scale;  // FP8: lane (g, n): key scale (n < 4) / value scale (4 <= n < 8) of token 4g + n%4
 };
 
 constexpr int kDecodeWaves = 4;
@@ -121,19 +143,17 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
   using G = Geo<D, kFp8>;
   constexpr int E = G::E;
   constexpr int NK = D / 32;  // score MFMAs per block
-  constexpr int DG = D / 4;   // head dims per lane group in the score tile
   constexpr int NT = D / 16;  // value MFMAs (16 head dims each) per block
   constexpr int W = G::WORDS, SETS = G::SETS, PITCH = G::PITCH;
   __shared__ __attribute__((aligned(16))) unsigned char lds_v[kDecodeWaves][kBlockTokens * PITCH];
-  __shared__ float lds_s[kDecodeWaves][32];
 
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t unit = (int64_t)blockIdx.x * kDecodeWaves + w;
   if (unit >= (int64_t)p.batch * p.kv_heads * p.splits) return;
-  const int split = (int)(unit % p.splits);
-  const int kvh = (int)((unit / p.splits) % p.kv_heads);
-  const int b = (int)(unit / p.splits / p.kv_heads);
+  const int kvh = (int)(unit % p.kv_heads);
+  const int split = (int)((unit / p.kv_heads) % p.splits);
+  const int b = (int)(unit / p.kv_heads / p.splits);
   const int g = lane >> 4, j = lane & 15;
   const int seq = p.seq_lens[b];
   const int nblk = seq > 0 ? (seq + kBlockTokens - 1) / kBlockTokens : 0;
@@ -145,15 +165,19 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
   int blk1 = bad ? blk0 : min(blk0 + per_split, nblk);
 
   // Query rows as the B operand of the scores: lane (g, j) holds head j's
-  // dims g*DG + 8kk + 0..7 (rows past the group's heads are zero).
+  // dims matching the key bytes MFMA kk consumes (rows past the group's
+  // heads are zero).
   bf16x8 qa[NK];
   {
     const bool has = j < KVM;
     const uint16_t* qrow =
-        p.q + ((int64_t)b * p.q_heads + (int64_t)kvh * KVM + (has ? j : 0)) * D + g * DG;
+        p.q + ((int64_t)b * p.q_heads + (int64_t)kvh * KVM + (has ? j : 0)) * D;
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
-      const u32x4 v = has ? *reinterpret_cast<const u32x4*>(qrow + kk * 8) : u32x4{0u, 0u, 0u, 0u};
+      // the head dims of the key bytes this MFMA consumes (see key_off)
+      const int cb = kk * 8 * E;
+      const int dim0 = (64 / E) * (cb / 16) + (16 / E) * g + (cb % 16) / E;
+      const u32x4 v = has ? *reinterpret_cast<const u32x4*>(qrow + dim0) : u32x4{0u, 0u, 0u, 0u};
       qa[kk] = __builtin_bit_cast(bf16x8, v);
     }
   }
@@ -164,17 +188,20 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
   // Block ids are uniform: read through the read-only table with scalar loads.
   const int32_t* table = tables + (int64_t)b * p.max_blocks;
   const uint64_t head_off = 2ull * p.layer * p.half + (uint64_t)kvh * D * E;
-  const uint32_t key_off = (uint32_t)j * token_stride + (uint32_t)(g * DG * E);
-  const uint32_t val_off = (uint32_t)(lane >> 2) * token_stride + (uint32_t)((lane & 3) * (D * E / 4));
-  // lanes 0-15: key scale of token lane; 16-31: value scale of token lane-16
-  // (lanes 32-63 repeat 0-31)
-  const uint32_t scale_off = (uint32_t)((2u * p.layer + ((lane >> 4) & 1)) * kBlockTokens * H +
-                                        (lane & 15) * H + kvh);
+  // Each 16-byte load instruction covers 64 contiguous bytes of every row it
+  // touches: load v of lane (g, j) reads bytes 64v + 16g.. of key row j, and
+  // of value row lane/4 at quarter lane%4. The key's head dims are consumed
+  // in that order; the queries are read in the same order.
+  const uint32_t key_off = (uint32_t)j * token_stride + (uint32_t)(16 * g);
+  const uint32_t val_off = (uint32_t)(lane >> 2) * token_stride + (uint32_t)(16 * (lane & 3));
+  // lane (g, j): scale of token 4g + j%4 from the key (j%8 < 4) or value plane
+  const uint32_t scale_off =
+      (uint32_t)(((2u * p.layer + ((j >> 2) & 1)) * kBlockTokens + 4u * g + (j & 3)) * H + kvh);
   // Loads block `blk` into `r`. Every call issues the same loads (an
   // unconditional count keeps the compiler's in-flight accounting exact): a
   // block past the split's end, or whose id is not a page id inside the arena
   // and scale pool, reads page 0 instead and reports false when it was wanted.
-  auto load = [&](int blk, BlockRegs<W>& r) -> bool {
+  auto load = [&](int blk, BlockRegs<W, kFp8>& r) -> bool {
     const bool want = blk < blk1;
     int32_t id = want ? table[blk] : 0;
     uint32_t page = fast_div((uint32_t)max(id, 0), p.by_stride);
@@ -185,16 +212,15 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
         p.kv.base[seg] + (uint64_t)(page - seg * p.by_seg_pages.d) * stride * p.half + head_off;
 #pragma unroll
     for (int v = 0; v < W / 4; ++v) {
-      const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kplane + key_off) + v);
+      const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kplane + key_off + 64 * v));
       const u32x4 y =
-          __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kplane + p.half + val_off) + v);
+          __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kplane + p.half + val_off + 64 * v));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         r.k[4 * v + e] = x[e];
         r.v[4 * v + e] = y[e];
       }
     }
-    r.scale = 1.f;
     if constexpr (kFp8) r.scale = p.scales[(uint64_t)id * kBlockTokens * H + scale_off];
     return ok || !want;
   };
@@ -205,25 +231,24 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
   for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   unsigned char* vt_w = &lds_v[w][0];
-  auto compute = [&](int blk, const BlockRegs<W>& r) {
+  auto compute = [&](int blk, const BlockRegs<W, kFp8>& r) {
     const int valid = blk == nblk - 1 ? seq - kBlockTokens * (nblk - 1) : kBlockTokens;
     // Value tile -> LDS rows (tail rows zeroed: tail slots may hold anything, even NaN).
     {
       const int t = lane >> 2;
-      unsigned char* dst = vt_w + t * PITCH + (lane & 3) * (D * E / 4);
+      unsigned char* dst = vt_w + t * PITCH + 16 * (lane & 3);
       if (valid == kBlockTokens) {  // every block but a sequence's last
 #pragma unroll
         for (int v = 0; v < W / 4; ++v)
-          *reinterpret_cast<u32x4*>(dst + 16 * v) = u32x4{r.v[4 * v], r.v[4 * v + 1], r.v[4 * v + 2], r.v[4 * v + 3]};
+          *reinterpret_cast<u32x4*>(dst + 64 * v) = u32x4{r.v[4 * v], r.v[4 * v + 1], r.v[4 * v + 2], r.v[4 * v + 3]};
       } else {
 #pragma unroll
         for (int v = 0; v < W / 4; ++v) {
           const u32x4 x = t < valid ? u32x4{r.v[4 * v], r.v[4 * v + 1], r.v[4 * v + 2], r.v[4 * v + 3]}
                                     : u32x4{0u, 0u, 0u, 0u};
-          *reinterpret_cast<u32x4*>(dst + 16 * v) = x;
+          *reinterpret_cast<u32x4*>(dst + 64 * v) = x;
         }
       }
-      if (lane < 32) lds_s[w][lane] = r.scale;
     }
     // Scores, transposed: lane (g, j) gets tokens 4g..4g+3 of head j.
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
@@ -241,14 +266,15 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
     }
     wave_sync();
     float ks[4] = {1.f, 1.f, 1.f, 1.f}, vs[4] = {1.f, 1.f, 1.f, 1.f};
-    if constexpr (kFp8) {
-      const f32x4 k4 = *reinterpret_cast<const f32x4*>(&lds_s[w][4 * g]);
-      const f32x4 v4 = *reinterpret_cast<const f32x4*>(&lds_s[w][16 + 4 * g]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        ks[i] = k4[i];
-        vs[i] = v4[i];
-      }
+    if constexpr (kFp8) {  // broadcast within each 16-lane row
+      ks[0] = dpp<0x150>(r.scale);
+      ks[1] = dpp<0x151>(r.scale);
+      ks[2] = dpp<0x152>(r.scale);
+      ks[3] = dpp<0x153>(r.scale);
+      vs[0] = dpp<0x154>(r.scale);
+      vs[1] = dpp<0x155>(r.scale);
+      vs[2] = dpp<0x156>(r.scale);
+      vs[3] = dpp<0x157>(r.scale);
     }
     // Online softmax of head j over the block's 16 tokens.
     float sv[4], tmax = -INFINITY;
@@ -257,8 +283,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
       sv[i] = 4 * g + i < valid ? s[i] * (p.scale * ks[i]) : -INFINITY;
       tmax = fmaxf(tmax, sv[i]);
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    tmax = group_max4(tmax);
     const float mn = fmaxf(m, tmax);
     const float alpha = mn == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m - mn);
     float psum = 0.f;
@@ -279,12 +304,10 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
       phi[i / 2] = (h0 >> 16) | h1;
       plo[i / 2] = (l0 >> 16) | l1;
     }
-    psum += __shfl_xor(psum, 16);
-    psum += __shfl_xor(psum, 32);
+    psum = group_sum4(psum);
     l = l * alpha + psum;
     m = mn;
-    const s16x4 p_hi = __builtin_bit_cast(s16x4, u32x2{phi[0], phi[1]});
-    const s16x4 p_lo = __builtin_bit_cast(s16x4, u32x2{plo[0], plo[1]});
+    const bf16x8 pb = __builtin_bit_cast(bf16x8, u32x4{phi[0], phi[1], plo[0], plo[1]});
     // Rescale: the accumulators hold O^T, lane (g, j) = head j, so alpha is
     // in-lane; skipped when no head's maximum moved (the common case).
     if (__ballot(alpha != 1.f) != 0) {
@@ -294,47 +317,49 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
         for (int i = 0; i < 4; ++i) acc[nt][i] *= alpha;
     }
     // O^T += V^T P^T: A = value rows 4g..4g+3 at head dim 16nt + j, B = P^T as held.
-    const unsigned char* vt = vt_w + 4 * g * PITCH;
+    // Transposing LDS reads: lane (g, j) gets tokens 4g..4g+3 of head dim
+    // 16nt + j. ds_read_b64_tr_b8 hands lane i of a 16-lane group byte e of
+    // the row addressed by lane 2e + i/8 (at byte i%8); tr_b16 hands it
+    // element e of the row addressed by lane 4e + i/4 (at element i%4).
+    const unsigned char* vt;
+    if constexpr (kFp8) vt = vt_w + (4 * g + ((j >> 1) & 3)) * PITCH + 8 * (j & 1);
+    else vt = vt_w + (4 * g + (j >> 2)) * PITCH + 8 * (j & 3);
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      s16x4 va;
+      u32x2 vw;
       if constexpr (kFp8) {
-        uint32_t x = 0;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) x |= (uint32_t)vt[i * PITCH + 16 * nt + j] << (8 * i);
-        va = __builtin_bit_cast(s16x4, e4m3x4_to_bf16x4_cvt(x));
+        typedef int i32x2 __attribute__((ext_vector_type(2)));
+        const i32x2 t = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (__attribute__((address_space(3))) i32x2*)(vt + 16 * nt));
+        vw = e4m3x4_to_bf16x4_cvt((uint32_t)t[0]);
       } else {
-        const uint16_t* c16 = reinterpret_cast<const uint16_t*>(vt + 32 * nt + 2 * j);
-        const uint32_t x0 = (uint32_t)c16[0] | ((uint32_t)c16[PITCH / 2] << 16);
-        const uint32_t x1 = (uint32_t)c16[PITCH] | ((uint32_t)c16[3 * PITCH / 2] << 16);
-        va = __builtin_bit_cast(s16x4, u32x2{x0, x1});
+        const s16x4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(vt + 32 * nt));
+        vw = __builtin_bit_cast(u32x2, t);
       }
-      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, p_hi, acc[nt], 0, 0, 0);
-      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, p_lo, acc[nt], 0, 0, 0);
+      // K = 32: the four tokens twice, against p_hi then p_lo.
+      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, u32x4{vw[0], vw[1], vw[0], vw[1]}),
+                                                         pb, acc[nt], 0, 0, 0);
     }
     wave_sync();  // the next block rewrites the tile
   };
 
   // SETS register sets in rotation: while one block is computed, the next
   // SETS-1 are in flight.
-  static_assert(SETS >= 2 && SETS <= 4, "register rotation is written out for 2 to 4 sets");
-  BlockRegs<W> r0, r1, r2, r3;
-  auto prime = [&](int blk, BlockRegs<W>& r) {
-    if (!load(blk, r)) bad = true, blk1 = min(blk1, blk);
+  static_assert(SETS >= 2 && SETS <= 8, "2 to 8 register sets");
+  BlockRegs<W, kFp8> r[SETS];
+  auto prime = [&](int blk, BlockRegs<W, kFp8>& rr) {
+    if (!load(blk, rr)) bad = true, blk1 = min(blk1, blk);
   };
-  auto step = [&](int blk, BlockRegs<W>& r) {
-    if (blk < blk1) compute(blk, r);
-    if (!load(blk + SETS, r)) bad = true, blk1 = min(blk1, blk + SETS);
+  auto step = [&](int blk, BlockRegs<W, kFp8>& rr) {
+    if (blk < blk1) compute(blk, rr);
+    if (!load(blk + SETS, rr)) bad = true, blk1 = min(blk1, blk + SETS);
   };
-  prime(blk0, r0);
-  prime(blk0 + 1, r1);
-  if constexpr (SETS >= 3) prime(blk0 + 2, r2);
-  if constexpr (SETS >= 4) prime(blk0 + 3, r3);
+#pragma unroll
+  for (int i = 0; i < SETS; ++i) prime(blk0 + i, r[i]);
   for (int base = blk0; base < blk1; base += SETS) {
-    step(base, r0);
-    step(base + 1, r1);
-    if constexpr (SETS >= 3) step(base + 2, r2);
-    if constexpr (SETS >= 4) step(base + 3, r3);
+#pragma unroll
+    for (int i = 0; i < SETS; ++i) step(base + i, r[i]);
   }
 
   // ---- this split's partials (lane (g, j): head j, dims 16nt + 4g + i)
