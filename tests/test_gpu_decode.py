@@ -201,6 +201,16 @@ def test_segmented_arena_and_one_query_head_per_kv_head(torch_cuda):
     _check(case, case.run())
 
 
+@pytest.mark.parametrize("fp8", [True, False])
+@pytest.mark.parametrize("H,kvm,D", [(3, 2, 128), (1, 8, 64), (3, 5, 64)])
+def test_odd_kv_head_counts_and_eight_query_heads(torch_cuda, fp8, H, kvm, D):
+    """Odd KV head counts and the largest group (8 query heads per KV head)."""
+    say(f"decode fp8={fp8} H{H} kvm{kvm} D{D}")
+    case = DecodeCase(torch_cuda, fp8=fp8, layers=2, H=H, D=D, kvm=kvm,
+                      seq_lens=[33, 1, 160, 17], seed=8 + H + kvm)
+    _check(case, case.run())
+
+
 def test_5040_token_prefix_batch(torch_cuda):
     say("decode fp8 5040-token prefixes x3, 28 layers")
     case = DecodeCase(torch_cuda, fp8=True, layers=28, H=2, D=128, kvm=6,
