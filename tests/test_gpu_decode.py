@@ -103,11 +103,13 @@ class DecodeCase:
         self.t_dev = torch.from_numpy(self.tables.copy()).cuda()
         self.s_dev = torch.tensor(self.seq_lens, dtype=torch.int32, device="cuda")
 
-    def run(self, splits=0, tables=None, seq_lens=None):
+    def run(self, splits=0, tables=None, seq_lens=None, ws=None):
         torch = self.torch
         s = splits or P.decode_splits(self.batch, self.H, self.max_blocks)
         ws_bytes = P.decode_workspace_bytes(self.batch, self.H * self.kvm, self.D, s)
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+        if ws is None:
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+        assert ws.numel() >= ws_bytes
         t = self.t_dev if tables is None else tables
         sl = self.s_dev if seq_lens is None else seq_lens
         P.paged_decode(self.view, P.PBE_KV_FP8_E4M3 if self.fp8 else P.PBE_KV_BF16,
@@ -209,6 +211,25 @@ def test_odd_kv_head_counts_and_eight_query_heads(torch_cuda, fp8, H, kvm, D):
     case = DecodeCase(torch_cuda, fp8=fp8, layers=2, H=H, D=D, kvm=kvm,
                       seq_lens=[33, 1, 160, 17], seed=8 + H + kvm)
     _check(case, case.run())
+
+
+def test_workspace_contents_do_not_matter_and_reuse_is_safe(torch_cuda):
+    """The workspace may hold anything (all ones, random bytes, the previous
+    launch's partials): the output is the same, bit for bit."""
+    torch = torch_cuda
+    say("decode fp8 workspace garbage + reuse")
+    case = DecodeCase(torch, fp8=True, layers=2, H=2, D=128, kvm=6,
+                      seq_lens=[300, 17, 0, 129, 64], seed=9)
+    want = _check(case, case.run())
+    for splits in (1, 2, 8, 64):
+        n = P.decode_workspace_bytes(case.batch, case.H * case.kvm, case.D, splits)
+        first = case.run(splits, ws=torch.zeros(n, dtype=torch.uint8, device="cuda"))
+        assert close(first, want).all(), splits
+        ws = torch.full((n,), 0xFF, dtype=torch.uint8, device="cuda")
+        for rep in range(3):  # the same workspace three times in a row
+            assert np.array_equal(case.run(splits, ws=ws), first), (splits, rep)
+        ws.copy_(torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda"))
+        assert np.array_equal(case.run(splits, ws=ws), first), splits
 
 
 def test_5040_token_prefix_batch(torch_cuda):
