@@ -121,8 +121,46 @@ def build(jobs: int = 8) -> Path:
     return so
 
 
+SAN = ["-fsanitize=address,undefined", "-fno-omit-frame-pointer"]
+
+
+def build_sanitized(jobs: int = 8) -> Path:
+    """Host code under AddressSanitizer + UBSan (device code unchanged): lib/asan/
+    holds libpbe_handoff.so and pbe_cpp_tests. The C++ suite runs as is; the
+    Python CPU suite runs against the library with the runtime preloaded:
+      LD_PRELOAD=<clang>/libclang_rt.asan-x86_64.so ASAN_OPTIONS=detect_leaks=0
+    and pbe_handoff.LIB_PATH pointed at lib/asan/libpbe_handoff.so."""
+    out = LIB / "asan"
+    out.mkdir(parents=True, exist_ok=True)
+    host_flags = [f for f in CXX_FLAGS if f != "-O2"] + ["-O1", "-g", *SAN]
+    steps, objs = [], []
+    for src in HOST_SOURCES + ABI_HOST_SOURCES:
+        o = out / (src.replace("/", "_") + ".o")
+        steps.append([HIPCC, "-x", "c++", *host_flags, *INCLUDES, "-c", str(PKG / src), "-o", str(o)])
+        objs.append(str(o))
+    for src in HIP_SOURCES:
+        o = out / (src.replace("/", "_") + ".o")
+        host_san = [x for f in SAN for x in ("-Xarch_host", f)]
+        steps.append([HIPCC, *HIP_FLAGS, *host_san, *INCLUDES, "-c", str(PKG / src), "-o", str(o)])
+        objs.append(str(o))
+    t_obj = out / "test_drop_in_api.o"
+    steps.append([HIPCC, "-x", "c++", *host_flags, *INCLUDES, f"-I{ROOT / 'tests' / 'cpp'}",
+                  "-c", str(ROOT / CPU_TESTS[0]), "-o", str(t_obj)])
+    with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
+        for fut in [pool.submit(_run, s) for s in steps]:
+            fut.result()
+    link = [HIPCC, f"--offload-arch={ARCH}", *SAN, "-fno-gpu-sanitize"]
+    _run([*link, "-shared", "-fPIC", "-shared-libsan", "-o", str(out / "libpbe_handoff.so"), *objs])
+    _run([*link, "-o", str(out / "pbe_cpp_tests"), str(t_obj), *objs])
+    return out
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=8)
+    ap.add_argument("--sanitize", action="store_true",
+                    help="also build lib/asan/ (host code under ASan + UBSan)")
     args = ap.parse_args()
     print(build(args.jobs))
+    if args.sanitize:
+        print(build_sanitized(args.jobs))
