@@ -7,6 +7,10 @@ namespace pbe {
 
 constexpr int kThreadsPerBlock = 256;
 constexpr int kCopyUnroll = 4;  // 4 KiB per wave slice for the identity copy
+// Cache policy of the identity copy: buffer loads with the non-temporal bit,
+// buffer stores with sc1 + nt (measured 1-2% faster on MI355X than global
+// nt stores; stores without nt are 50% slower).
+constexpr int kCopyPolicy = 10;
 constexpr int kFp8Unroll = 4;   // 4 KiB of BF16 source per wave slice
 
 // Device form of one run: resolved addresses in this process's mapping.
@@ -36,7 +40,7 @@ enum class KernelKind { kCopy, kFp8 };
 // size, and dynamic LDS per workgroup (caps workgroups per CU).
 struct CopyConfig {
   int unroll = kCopyUnroll;
-  int policy = 0;
+  int policy = kCopyPolicy;
   int block = 256;
   uint32_t lds_bytes = 0;
 };

@@ -79,6 +79,8 @@ constexpr PolicyBits kPolicies[] = {
     {true, 0x02, 0x13},   // 6: load nt, store sc0 sc1 nt
     {true, 0x13, 0x02},   // 7: load sc0 sc1 nt, store nt
     {true, 0x00, 0x00},   // 8: buffer default policy
+    {true, 0x12, 0x02},   // 9: load sc1 nt, store nt
+    {true, 0x02, 0x12},   // 10: load nt, store sc1 nt
 };
 constexpr int kNumPolicies = sizeof(kPolicies) / sizeof(kPolicies[0]);
 
@@ -151,7 +153,7 @@ __global__ __launch_bounds__(kBlock) void copy_runs_kernel(
 // The same copy with the run list in the kernel arguments (no staging copy).
 // An aggregate kernel argument stays in the kernarg segment and is read there.
 __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_kernarg_kernel(const KernargRunList list) {
-  copy_runs_body<kCopyUnroll, 0, kThreadsPerBlock>(list.runs, list.n_runs, list.total_slices, 1u,
+  copy_runs_body<kCopyUnroll, kCopyPolicy, kThreadsPerBlock>(list.runs, list.n_runs, list.total_slices, 1u,
                                                    list.page_bytes);
 }
 
