@@ -132,7 +132,9 @@ template <int W, bool kFp8>
 struct BlockRegs {
   uint32_t k[W];
   uint32_t v[W];
-  float scale;  // FP8: lane (g, n): key scale (n < 4) / value scale (4 <= n < 8) of token 4g + n%4
+  // FP8: lane (g, n): log2(e)/sqrt(D) * key scale (n%8 < 4) or value scale
+  // (otherwise) of token 4g + n%4
+  float scale;
 };
 
 constexpr int kDecodeWaves = 4;
@@ -221,7 +223,10 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
         r.v[4 * v + e] = y[e];
       }
     }
-    if constexpr (kFp8) r.scale = p.scales[(uint64_t)id * kBlockTokens * H + scale_off];
+    if constexpr (kFp8) {  // key scales carry the score scale: p.scale * k_scale
+      const float sc = p.scales[(uint64_t)id * kBlockTokens * H + scale_off];
+      r.scale = (j & 4) ? sc : p.scale * sc;
+    }
     return ok || !want;
   };
 
@@ -265,7 +270,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
       s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qa[kk], s, 0, 0, 0);
     }
     wave_sync();
-    float ks[4] = {1.f, 1.f, 1.f, 1.f}, vs[4] = {1.f, 1.f, 1.f, 1.f};
+    float ks[4] = {p.scale, p.scale, p.scale, p.scale}, vs[4] = {1.f, 1.f, 1.f, 1.f};
     if constexpr (kFp8) {  // broadcast within each 16-lane row
       ks[0] = dpp<0x150>(r.scale);
       ks[1] = dpp<0x151>(r.scale);
@@ -280,7 +285,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
     float sv[4], tmax = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      sv[i] = 4 * g + i < valid ? s[i] * (p.scale * ks[i]) : -INFINITY;
+      sv[i] = 4 * g + i < valid ? s[i] * ks[i] : -INFINITY;
       tmax = fmaxf(tmax, sv[i]);
     }
     tmax = group_max4(tmax);
