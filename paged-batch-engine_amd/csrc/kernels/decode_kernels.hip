@@ -388,10 +388,17 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
 template <int D>
 __global__ __launch_bounds__(kWavesPerBlock * 64) void decode_combine_kernel(const DecodeParams p) {
   constexpr int PER = D / 64;
+  constexpr int kAhead = 8;  // splits whose partials are loaded before the weights are known
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + w;
   if (row >= (int64_t)p.batch * p.q_heads) return;
   const int S = p.splits;
+  const float* src = p.part_acc + row * S * D + lane * PER;
+  float x[kAhead][PER];
+#pragma unroll
+  for (int u = 0; u < kAhead; ++u)
+#pragma unroll
+    for (int e = 0; e < PER; ++e) x[u][e] = u < S ? src[u * D + e] : 0.f;
   float ms = -INFINITY, ls = 0.f;
   if (lane < S) {
     ms = p.part_m[row * S + lane];
@@ -399,17 +406,26 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void decode_combine_kernel(con
   }
   const bool any_nan = __ballot(ls != ls) != 0;
   const float m = wave_max(ms);
-  const float denom = wave_sum((lane < S && ls > 0.f) ? ls * exp2f(ms - m) : 0.f);
+  const float wgt = (lane < S && ls > 0.f) ? exp2f(ms - m) : 0.f;
+  const float denom = wave_sum(wgt > 0.f ? ls * wgt : 0.f);
   float o[PER];
 #pragma unroll
   for (int e = 0; e < PER; ++e) o[e] = 0.f;
-  for (int s = 0; s < S; ++s) {
-    const float sl = __shfl(ls, s), sm = __shfl(ms, s);
-    if (!(sl > 0.f)) continue;
-    const float a = exp2f(sm - m);
-    const float* src = p.part_acc + (row * S + s) * D + lane * PER;
+  for (int s0 = 0; s0 < S; s0 += kAhead) {
+    if (s0 > 0) {
 #pragma unroll
-    for (int e = 0; e < PER; ++e) o[e] += src[e] * a;
+      for (int u = 0; u < kAhead; ++u)
+#pragma unroll
+        for (int e = 0; e < PER; ++e) x[u][e] = s0 + u < S ? src[(s0 + u) * D + e] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kAhead; ++u) {
+      const float a = __shfl(wgt, min(s0 + u, 63));
+      if (s0 + u < S && a > 0.f) {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) o[e] += x[u][e] * a;
+      }
+    }
   }
   uint16_t* dst = p.out + row * D + lane * PER;
 #pragma unroll
