@@ -80,19 +80,64 @@ def cpu_baseline(w, host_arena, seconds: float):
                                   "sample": f"{creps} handoffs in {cel:.1f} s"}}
 
 
+class TimingEvents:
+    """HIP timing events created with hipEventDisableSystemFence. A default
+    event runs a system-scope release (L2 writeback and invalidate) when it
+    completes; that fence lands inside the measured interval and adds ~2 us to
+    a ~50 us kernel. The flag exists for events used only to measure time."""
+    FLAGS = 0x20000000  # hipEventDisableSystemFence (timing stays enabled)
+
+    def __init__(self, n: int):
+        import ctypes as C
+        self.C = C
+        self.hip = C.CDLL("libamdhip64.so.7")
+        self.hip.hipEventCreateWithFlags.argtypes = [C.POINTER(C.c_void_p), C.c_uint]
+        self.hip.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [C.c_void_p]
+        self.ev = []
+        for _ in range(n):
+            e = C.c_void_p()
+            rc = self.hip.hipEventCreateWithFlags(C.byref(e), self.FLAGS)
+            if rc != 0:
+                raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+            self.ev.append(e)
+
+    def handle(self, i: int) -> int:
+        return self.ev[i].value
+
+    def record(self, i: int, stream: int) -> None:
+        if self.hip.hipEventRecord(self.ev[i], self.C.c_void_p(stream)) != 0:
+            raise RuntimeError("hipEventRecord failed")
+
+    def elapsed_ms(self, i: int, j: int) -> float:
+        ms = self.C.c_float()
+        if self.hip.hipEventElapsedTime(self.C.byref(ms), self.ev[i], self.ev[j]) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return float(ms.value)
+
+    def close(self) -> None:
+        for e in self.ev:
+            self.hip.hipEventDestroy(e)
+        self.ev = []
+
+
 def _timed(torch, stream, scrub, fn, n):
-    """Mean/min event time (ms) of fn() over n cold launches (scrub before each)."""
+    """Mean/min event time (ms) of fn() over n cold launches (scrub before
+    each), between fence-free timing events recorded on the stream."""
     import numpy as np
+    ev = TimingEvents(2 * (n + 2))
+    sp = stream.cuda_stream
     ts = []
     for i in range(n + 2):
         scrub.fill_(i & 0xff)
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
+        ev.record(2 * i, sp)
         fn()
-        b.record(stream)
+        ev.record(2 * i + 1, sp)
         torch.cuda.synchronize()
         if i >= 2:
-            ts.append(a.elapsed_time(b))
+            ts.append(ev.elapsed_ms(2 * i, 2 * i + 1))
+    ev.close()
     return float(np.mean(ts)), float(np.min(ts))
 
 
@@ -118,19 +163,20 @@ def gpu_reference_pattern(torch, stream, scrub, base, runs, g, alg, n, scrub_eac
 
     issue()
     torch.cuda.synchronize()
+    tev = TimingEvents(2 * n)
     ev, wall = [], []
     for i in range(n):
         if scrub_each:
             scrub.fill_(i & 0xff)
         torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t = time.perf_counter()
-        a.record(stream)
+        tev.record(2 * i, stream.cuda_stream)
         issue()
-        b.record(stream)
+        tev.record(2 * i + 1, stream.cuda_stream)
         stream.synchronize()
         wall.append(time.perf_counter() - t)
-        ev.append(a.elapsed_time(b))
+        ev.append(tev.elapsed_ms(2 * i, 2 * i + 1))
+    tev.close()
     us = float(np.mean(ev)) * 1e3
     return {"what": "one hipMemcpyAsync per coalesced run on this GPU (the reference's loop)",
             "calls": len(calls), "us_mean": round(us, 2),
@@ -350,19 +396,17 @@ def main() -> int:
     # Timed region: each step's kernel is bracketed by two HIP events that
     # the runtime stamps at the kernel's own start and end (hipExtLaunchKernel
     # through pbe_handoff_copy_timed), on the stream the kernel runs on.
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    for e in starts + ends:
-        e.record(stream)  # creates the underlying hipEvent_t
+    ev = TimingEvents(2 * args.steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         if not args.no_scrub:
             scrub.fill_((i + 1) & 0xff)
-        rl.copy_timed(sp, starts[i].cuda_event, ends[i].cuda_event)
+        rl.copy_timed(sp, ev.handle(2 * i), ev.handle(2 * i + 1))
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    times_ms = np.array([s.elapsed_time(e) for s, e in zip(starts, ends)])
+    times_ms = np.array([ev.elapsed_ms(2 * i, 2 * i + 1) for i in range(args.steps)])
+    ev.close()
     mean_ms = float(times_ms.mean())
     # the same launches between events recorded on the stream around them
     # (adds the dispatch gap on both sides)
@@ -409,14 +453,15 @@ def main() -> int:
         cview = P.view_of(cbuf.data_ptr(), cbuf.numel())
         crl = P.RunList.bf16(cview, cview, [(0, (256 << 20) // ckv.half_bytes(), 1024)], ckv)
         ct = []
+        cev = TimingEvents(2)
         for i in range(args.steps):
             scrub.fill_(i & 0xff)
-            a_, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a_.record(stream)
+            cev.record(0, sp)
             crl.copy(sp)
-            b_.record(stream)
+            cev.record(1, sp)
             torch.cuda.synchronize()
-            ct.append(a_.elapsed_time(b_))
+            ct.append(cev.elapsed_ms(0, 1))
+        cev.close()
         calib = {"bytes": 256 << 20, "grid_threads": int(crl.info().slices) * 64,
                  "gbps": round(2 * (256 << 20) / (float(np.mean(ct)) * 1e-3) / 1e9, 1)}
         crl.close()
