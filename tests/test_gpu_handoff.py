@@ -306,3 +306,42 @@ def test_timed_launch_copies_and_brackets_the_kernel(torch_cuda):
     assert 0 < inner <= outer, (inner, outer)
     after = snapshot(bufs)
     assert np.array_equal(after, expected), first_diff(after, expected)
+
+
+def test_concurrent_one_call_handoffs_from_host_threads(torch_cuda):
+    """Several host threads drive one-call handoffs at once, each on its own
+    stream, through both launch forms (run lists in the kernel arguments and
+    the shared staging ring): every request lands bit-exact."""
+    import threading
+    torch = torch_cuda
+    w = W.config3(0)
+    g = w.geometry
+    kv = _kv(g)
+    say(f"concurrent one-call handoffs: {len(w.requests)} threads x 8 repeats")
+    bufs, view = device_arena(torch, w.arena_bytes, w.segment_bytes)
+    for i, b in enumerate(bufs):
+        fill_bf16(torch, b, w.sigma, 70 + i)
+    torch.cuda.synchronize()
+    expected = snapshot(bufs)
+    O.copy_handoff(expected, w.src_ids, w.dst_ids, g.half(), g.layers)
+    sizes = [len(P.build_runs(r.src_ids, r.dst_ids, kv, 2, w.segment_bytes)) for r in w.requests]
+    assert min(sizes) <= 112 < max(sizes), sizes
+    streams = [torch.cuda.Stream() for _ in w.requests]
+    errors = []
+
+    def worker(r, st):
+        try:
+            for _ in range(8):  # idempotent: the same pages again
+                P.copy_shared_kv(view, r.src_ids, r.dst_ids, kv, 0, st.cuda_stream)
+        except Exception as e:  # surfaced below
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(r, st)) for r, st in zip(w.requests, streams)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    after = snapshot(bufs)
+    assert np.array_equal(after, expected), first_diff(after, expected)
