@@ -328,6 +328,31 @@ def measure_decode(torch, P, scrub, n: int, batch: int = 64, seq: int = 5040, pl
     return res
 
 
+def calibration_copy(torch, P, scrub, steps: int, sp: int) -> dict:
+    """One plain 256 MiB run (1024 pages of 256 KiB, offset 0 to offset 256 MiB)
+    with the copy kernel: the known byte count that rocprofv3 --pmc counters
+    are scaled by."""
+    import numpy as np
+    ckv = P.shape(1, 1, 4096, 16)
+    cbuf = torch.empty(2 * (256 << 20), dtype=torch.uint8, device="cuda")
+    cview = P.view_of(cbuf.data_ptr(), cbuf.numel())
+    crl = P.RunList.bf16(cview, cview, [(0, (256 << 20) // ckv.half_bytes(), 1024)], ckv)
+    ct = []
+    cev = TimingEvents(2)
+    for i in range(steps):
+        scrub.fill_(i & 0xff)
+        cev.record(0, sp)
+        crl.copy(sp)
+        cev.record(1, sp)
+        torch.cuda.synchronize()
+        ct.append(cev.elapsed_ms(0, 1))
+    cev.close()
+    calib = {"bytes": 256 << 20, "grid_threads": int(crl.info().slices) * 64,
+             "gbps": round(2 * (256 << 20) / (float(np.mean(ct)) * 1e-3) / 1e9, 1)}
+    crl.close()
+    return calib
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -338,6 +363,8 @@ def main() -> int:
     ap.add_argument("--no-scrub", action="store_true", help="hot-cache timing (diagnostic)")
     ap.add_argument("--extra-configs", default="",
                     help="also time configs 1, 3, 4 and 5 and write them as JSON to this file")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="time only the decode reader (FP8 and BF16 pages) and print it as JSON")
     ap.add_argument("--calibrate", action="store_true",
                     help="also launch a plain contiguous copy of 256 MiB with the same kernel "
                          "(rocprofv3 --pmc byte-count calibration)")
@@ -356,6 +383,14 @@ def main() -> int:
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
+    if args.decode_only:
+        scrub = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        sp = torch.cuda.current_stream().cuda_stream
+        out = {"decode": measure_decode(torch, P, scrub, max(3, args.steps))}
+        if args.calibrate:
+            out["calibration"] = calibration_copy(torch, P, scrub, args.steps, sp)
+        print(json.dumps(out))
+        return 0
     w = W.config2(0)
     g = w.geometry
     kv = P.shape(g.layers, g.kv_heads, g.head_dim, g.page_tokens)
@@ -445,26 +480,7 @@ def main() -> int:
                   "us_mean": round(c_ms[0] * 1e3, 2),
                   "gbps": round(alg / (c_ms[0] * 1e-3) / 1e9, 1)}
 
-    calib = None
-    if args.calibrate:
-        # one 256 MiB run (1024 pages of 256 KiB) from offset 0 to offset 256 MiB
-        ckv = P.shape(1, 1, 4096, 16)
-        cbuf = torch.empty(2 * (256 << 20), dtype=torch.uint8, device=dev)
-        cview = P.view_of(cbuf.data_ptr(), cbuf.numel())
-        crl = P.RunList.bf16(cview, cview, [(0, (256 << 20) // ckv.half_bytes(), 1024)], ckv)
-        ct = []
-        cev = TimingEvents(2)
-        for i in range(args.steps):
-            scrub.fill_(i & 0xff)
-            cev.record(0, sp)
-            crl.copy(sp)
-            cev.record(1, sp)
-            torch.cuda.synchronize()
-            ct.append(cev.elapsed_ms(0, 1))
-        cev.close()
-        calib = {"bytes": 256 << 20, "grid_threads": int(crl.info().slices) * 64,
-                 "gbps": round(2 * (256 << 20) / (float(np.mean(ct)) * 1e-3) / 1e9, 1)}
-        crl.close()
+    calib = calibration_copy(torch, P, scrub, args.steps, sp) if args.calibrate else None
 
     if args.extra_configs:
         extra = measure_extra_configs(torch, P, W, scrub, max(10, args.steps // 4))

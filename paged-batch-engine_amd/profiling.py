@@ -71,12 +71,12 @@ def stats(root: str, out: str, command: str, labels=None) -> None:
     print(text)
 
 
-def _counter_per_dispatch(root: str, counter: str):
-    """{grid size: [counter value per dispatch]} for the copy kernel."""
+def _counter_per_dispatch(root: str, counter: str, kernel: str = COPY_KERNEL):
+    """{grid size: [counter value per dispatch]} for kernels whose name holds `kernel`."""
     per = defaultdict(lambda: defaultdict(float))
     grids = {}
     for r in _csv_rows(root, "counter_collection.csv"):
-        if COPY_KERNEL not in r["Kernel_Name"] or r["Counter_Name"] != counter:
+        if kernel not in r["Kernel_Name"] or r["Counter_Name"] != counter:
             continue
         did = r["Dispatch_Id"]
         per[did][counter] += float(r["Counter_Value"])
@@ -88,18 +88,21 @@ def _counter_per_dispatch(root: str, counter: str):
 
 
 def pmc(fetch_root: str, write_root: str, out: str, command: str, alg_bytes: int,
-        handoff_grid: int, calib_grid: int) -> None:
-    f = _counter_per_dispatch(fetch_root, "FETCH_SIZE")
-    w = _counter_per_dispatch(write_root, "WRITE_SIZE")
-    f_h, f_c = statistics.median(f[handoff_grid]), statistics.median(f[calib_grid])
-    w_h, w_c = statistics.median(w[handoff_grid]), statistics.median(w[calib_grid])
+        handoff_grid: int, calib_grid: int, kernel: str = COPY_KERNEL,
+        title: str = "HBM traffic of the config-2 handoff copy") -> None:
+    f = _counter_per_dispatch(fetch_root, "FETCH_SIZE", kernel)
+    w = _counter_per_dispatch(write_root, "WRITE_SIZE", kernel)
+    fc = _counter_per_dispatch(fetch_root, "FETCH_SIZE")
+    wc = _counter_per_dispatch(write_root, "WRITE_SIZE")
+    f_h, f_c = statistics.median(f[handoff_grid]), statistics.median(fc[calib_grid])
+    w_h, w_c = statistics.median(w[handoff_grid]), statistics.median(wc[calib_grid])
     f_scale = CALIB_BYTES / f_c  # bytes per counter unit (KiB nominal)
     w_scale = CALIB_BYTES / w_c
     traffic = f_h * f_scale + w_h * w_scale
     lines = [
-        "# rocprofv3 --pmc summary: HBM traffic of the config-2 handoff copy",
+        f"# rocprofv3 --pmc summary: {title}",
         f"command: {command}",
-        f"kernel: {COPY_KERNEL} (handoff grid {handoff_grid}, calibration grid {calib_grid})",
+        f"kernel: {kernel} (grid {handoff_grid}); calibration: {COPY_KERNEL} (grid {calib_grid})",
         f"FETCH_SIZE per dispatch: handoff {f_h:.1f}, plain copy of {CALIB_BYTES} B {f_c:.1f}"
         f" -> {f_scale:.2f} bytes per unit",
         f"WRITE_SIZE per dispatch: handoff {w_h:.1f}, plain copy of {CALIB_BYTES} B {w_c:.1f}"
@@ -133,6 +136,8 @@ def main() -> None:
     p.add_argument("--alg-bytes", type=int, required=True)
     p.add_argument("--handoff-grid", type=int, required=True)
     p.add_argument("--calib-grid", type=int, required=True)
+    p.add_argument("--kernel", default=COPY_KERNEL, help="substring of the measured kernel's name")
+    p.add_argument("--title", default="HBM traffic of the config-2 handoff copy")
     a = ap.parse_args()
     if a.cmd == "stats":
         labels = {}
@@ -148,7 +153,7 @@ def main() -> None:
         stats(a.root, a.out, a.command, labels)
     else:
         pmc(a.fetch_root, a.write_root, a.out, a.command, a.alg_bytes, a.handoff_grid,
-            a.calib_grid)
+            a.calib_grid, a.kernel, a.title)
 
 
 if __name__ == "__main__":
