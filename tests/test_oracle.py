@@ -95,6 +95,18 @@ def test_e4m3_decode_round_trip():
         assert back == code or (v == 0 and (back & 0x7F) == 0), (code, v, back)
 
 
+def test_e4m3_decode_matches_torch_float8_e4m3fn():
+    """Every one of the 256 codes decodes to torch's float8_e4m3fn value (the
+    OCP E4M3 'fn' format: no infinities, 0x7F/0xFF NaN)."""
+    torch = pytest.importorskip("torch")
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    want = codes.view(torch.float8_e4m3fn).to(torch.float64).numpy()
+    got = O.e4m3_table()
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan], want[~nan])
+
+
 # ------------------------------------------------------------------ BF16
 
 def test_bf16_rounding_matches_torch():
