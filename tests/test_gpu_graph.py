@@ -1,0 +1,73 @@
+"""The launches can be captured into a HIP graph (one kernel node each, no
+memset nodes) and replayed: a prebuilt run list's handoff copy and a decode
+step. Every replay is checked against the oracle, with the program's own eager
+work (fresh fills) and synchronisations between replays."""
+import numpy as np
+import pytest
+
+import pbe_handoff as P
+import workload as W
+from oracle import oracle as O
+from tests.conftest import say
+from tests.gpu_util import fill_bf16, first_diff
+
+pytestmark = pytest.mark.gpu
+
+
+def test_handoff_copy_replays_from_a_graph(torch_cuda):
+    torch = torch_cuda
+    w = W.small(seed=5, layers=3, kv_heads=2, head_dim=64, n_pages=96, handoff_pages=21, max_run=4)
+    g = w.geometry
+    kv = P.shape(g.layers, g.kv_heads, g.head_dim, g.page_tokens)
+    say(f"graph replay of the handoff copy, {w.pages} pages")
+    arena = torch.empty(w.arena_bytes, dtype=torch.uint8, device="cuda")
+    view = P.view_of(arena.data_ptr(), arena.numel())
+    rl = P.RunList.bf16(view, view, P.build_runs(w.src_ids, w.dst_ids, kv), kv)
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    fill_bf16(torch, arena, 1.0, 1)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            rl.copy(side.cuda_stream)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        fill_bf16(torch, arena, 1.0, 100 + rep)  # eager work between replays
+        torch.cuda.synchronize()
+        expected = arena.cpu().numpy().copy()
+        O.copy_handoff(expected, w.src_ids, w.dst_ids, g.half(), g.layers)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = arena.cpu().numpy()
+        assert np.array_equal(got, expected), (rep, first_diff(got, expected))
+    rl.close()
+
+
+def test_decode_step_replays_from_a_graph(torch_cuda):
+    from tests.test_gpu_decode import DecodeCase, close
+    torch = torch_cuda
+    say("graph replay of a decode step (FP8 pages)")
+    case = DecodeCase(torch, fp8=True, layers=2, H=2, D=128, kvm=6, seq_lens=[300, 17, 0, 129],
+                      seed=12)
+    want = case.oracle()
+    ws_bytes = P.decode_workspace_bytes(case.batch, case.H * case.kvm, case.D, 8)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            P.paged_decode(case.view, P.PBE_KV_FP8_E4M3, case.scales.data_ptr(),
+                           case.scales.numel() * 4, case.kv, case.layer, case.q.data_ptr(),
+                           case.out.data_ptr(), case.batch, case.H * case.kvm,
+                           case.t_dev.data_ptr(), case.s_dev.data_ptr(), case.max_blocks, 8,
+                           ws.data_ptr(), ws_bytes, side.cuda_stream)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        case.out.fill_(rep + 1)  # eager work between replays: the output is overwritten
+        ws.fill_(0xA5 + rep)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (case.out.cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+        assert close(got.astype(np.float64), want).all(), rep
