@@ -345,3 +345,37 @@ def test_concurrent_one_call_handoffs_from_host_threads(torch_cuda):
     assert not errors, errors
     after = snapshot(bufs)
     assert np.array_equal(after, expected), first_diff(after, expected)
+
+
+def test_single_allocation_beyond_4_gib(torch_cuda):
+    """A 6 GiB single-segment arena: pages above the 4 GiB offset are copied
+    from and to correctly (no 32-bit truncation of ids, offsets or addresses),
+    by a prebuilt run list and by the one-call form."""
+    torch = torch_cuda
+    g = W.Geometry(layers=28, kv_heads=2, head_dim=128)
+    kv = _kv(g)
+    page = g.page_bytes()
+    n_pages = (6 << 30) // page
+    say(f"6 GiB single arena, {n_pages} pages of {page} B")
+    arena = torch.empty(n_pages * page, dtype=torch.uint8, device="cuda")
+    fill_bf16(torch, arena, 1.0, 90)
+    view = P.view_of(arena.data_ptr(), arena.numel())
+    hi = ((4 << 30) + page - 1) // page  # first page at or above 4 GiB
+    rng = np.random.default_rng(90)
+    src_pages = np.concatenate([rng.permutation(2000)[:60] + 100, rng.permutation(n_pages - hi - 200)[:60] + hi + 100])
+    dst_pages = rng.permutation(np.setdiff1d(np.arange(hi - 50, n_pages - 1), src_pages))[:120]
+    src_ids = (src_pages * g.stride).astype(np.int32)
+    dst_ids = (dst_pages * g.stride).astype(np.int32)
+    saved = {int(s): arena[int(s) * page:(int(s) + 1) * page].clone() for s in src_pages}
+    canary = [int(p) for p in rng.permutation(np.setdiff1d(np.arange(n_pages),
+                                                        np.concatenate([dst_pages])))[:40]]
+    canary_before = {p: arena[p * page:(p + 1) * page].clone() for p in canary}
+    half = len(src_ids) // 2
+    with P.RunList.bf16(view, view, P.build_runs(src_ids[:half], dst_ids[:half], kv), kv) as rl:
+        rl.copy(stream_ptr(torch))
+    P.copy_shared_kv(view, src_ids[half:], dst_ids[half:], kv, 0, stream_ptr(torch))
+    torch.cuda.synchronize()
+    for s, d in zip(src_pages, dst_pages):
+        assert torch.equal(arena[int(d) * page:(int(d) + 1) * page], saved[int(s)]), (s, d)
+    for p in canary:
+        assert torch.equal(arena[p * page:(p + 1) * page], canary_before[p]), p
