@@ -274,3 +274,63 @@ def test_argument_errors_are_rejected_before_launch(torch_cuda):
         args.update(change)
         with pytest.raises(P.PbeError):
             P.paged_decode(**args)
+
+
+@pytest.mark.parametrize("fp8", [True, False])
+def test_pages_beyond_4_gib_of_a_single_arena(torch_cuda, fp8):
+    """The blocks of every sequence lie above the 4 GiB offset of one 6 GiB
+    allocation (and of a 100-200 MB scale pool): addresses, page indices and
+    scale offsets are computed without 32-bit truncation. The oracle runs on
+    the used pages gathered into a compact host arena."""
+    torch = torch_cuda
+    L, H, D, kvm, layer = 2, 2, 128, 6, 1
+    E = 1 if fp8 else 2
+    half = 16 * H * D * E
+    page = 2 * L * half
+    n_pages = (6 << 30) // page
+    say(f"decode fp8={fp8} over a 6 GiB arena, {n_pages} pages")
+    arena = torch.empty(n_pages * page, dtype=torch.uint8, device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(31 + fp8)
+    if fp8:  # E4M3 codes without the NaN codes
+        arena.copy_(torch.randint(0, 0x7F, arena.shape, generator=g, device="cuda", dtype=torch.uint8)
+                    | (torch.randint(0, 2, arena.shape, generator=g, device="cuda", dtype=torch.uint8) << 7))
+        scales = torch.rand(n_pages * 2 * L * 16 * H, generator=g, device="cuda") * 0.05 + 1e-3
+    else:
+        fill_bf16(torch, arena, 1.0, 31)
+        scales = None
+    seq_lens = [200, 77, 300]
+    need = [(n + 15) // 16 for n in seq_lens]
+    hi = ((4 << 30) + page - 1) // page
+    rng = np.random.default_rng(31)
+    pages = rng.permutation(n_pages - hi)[:sum(need)] + hi
+    batch, max_blocks = len(seq_lens), max(need)
+    tables = np.zeros((batch, max_blocks), np.int32)
+    compact = np.zeros((batch, max_blocks), np.int32)
+    k = 0
+    for b, nb in enumerate(need):
+        tables[b, :nb] = pages[k:k + nb] * 2 * L
+        compact[b, :nb] = np.arange(k, k + nb) * 2 * L
+        k += nb
+    view = P.view_of(arena.data_ptr(), arena.numel())
+    kv = P.shape(L, H, D)
+    qf = rng.standard_normal((batch, H * kvm, D)).astype(np.float32)
+    q_host = O.bf16_from_f32(qf)
+    q = torch.from_numpy(q_host.view(np.int16)).cuda()
+    out = torch.empty_like(q)
+    t_dev = torch.from_numpy(tables).cuda()
+    s_dev = torch.tensor(seq_lens, dtype=torch.int32, device="cuda")
+    splits = P.decode_splits(batch, H, max_blocks)
+    ws_bytes = P.decode_workspace_bytes(batch, H * kvm, D, splits)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    P.paged_decode(view, P.PBE_KV_FP8_E4M3 if fp8 else P.PBE_KV_BF16,
+                   scales.data_ptr() if fp8 else 0, scales.numel() * 4 if fp8 else 0, kv, layer,
+                   q.data_ptr(), out.data_ptr(), batch, H * kvm, t_dev.data_ptr(), s_dev.data_ptr(),
+                   max_blocks, splits, ws.data_ptr(), ws_bytes, stream_ptr(torch))
+    torch.cuda.synchronize()
+    got = bf16_to_f64(out.cpu().numpy().view(np.uint16))
+    idx = torch.from_numpy(pages.astype(np.int64)).cuda()
+    host = arena.view(n_pages, page)[idx].cpu().numpy().reshape(-1)
+    host_scales = scales.view(n_pages, -1)[idx].cpu().numpy().reshape(-1) if fp8 else None
+    want = O.paged_decode(host, fp8, host_scales, L, H, D, layer, q_host, compact, seq_lens)
+    assert close(got, want).all()
