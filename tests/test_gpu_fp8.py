@@ -146,3 +146,40 @@ def test_fp8_rejects_misuse(torch_cuda):
     with pytest.raises(P.PbeError) as e:
         P.RunList.fp8(pools.src_view, pools.dst_view, 0, 0, [(0, 4, 1)], kv)
     assert e.value.code == P.PBE_ERR_UNSUPPORTED
+
+
+def test_fp8_destination_beyond_4_gib(torch_cuda):
+    """Destination pages above the 4 GiB offset of one 6 GiB FP8 arena:
+    payload and per-token-head scales bit-exact (oracle run on the gathered
+    pages)."""
+    torch = torch_cuda
+    g = W.Geometry(28, 2, 128)
+    src_pages_n, n_dst = 64, (6 << 30) // g.page_bytes(1)
+    say(f"fp8 handoff into a 6 GiB FP8 arena ({n_dst} pages)")
+    src = torch.empty(src_pages_n * g.page_bytes(2), dtype=torch.uint8, device="cuda")
+    fill_bf16(torch, src, 1.0, 44, 0.01, 40.0)
+    dst = torch.zeros(n_dst * g.page_bytes(1), dtype=torch.uint8, device="cuda")
+    scale_page = 2 * g.layers * g.page_tokens * g.kv_heads * 4
+    scales = torch.zeros(n_dst * scale_page, dtype=torch.uint8, device="cuda")
+    kv = P.shape(g.layers, g.kv_heads, g.head_dim, g.page_tokens)
+    hi = ((4 << 30) + g.page_bytes(1) - 1) // g.page_bytes(1)
+    rng = np.random.default_rng(44)
+    sp = rng.permutation(src_pages_n)[:40]
+    dp = rng.permutation(n_dst - hi)[:40] + hi
+    runs = P.build_runs(sp.astype(np.int32) * g.stride, dp.astype(np.int32) * g.stride, kv)
+    with P.RunList.fp8(P.view_of(src.data_ptr(), src.numel()), P.view_of(dst.data_ptr(), dst.numel()),
+                       scales.data_ptr(), scales.numel(), runs, kv) as rl:
+        rl.copy_fp8(P.PBE_FP8_SCALE_PER_TOKEN_HEAD, 0, stream_ptr(torch))
+    torch.cuda.synchronize()
+    # oracle on compact copies: source pages as they are, destination slot k for dp[k]
+    src_host = src.cpu().numpy()
+    dst_exp = np.zeros(len(dp) * g.page_bytes(1), np.uint8)
+    sc_exp = np.zeros(len(dp) * scale_page, np.uint8)
+    O.fp8_handoff_token_head(src_host, dst_exp, sc_exp, sp.astype(np.int32) * g.stride,
+                             np.arange(len(dp), dtype=np.int32) * g.stride, g.layers,
+                             g.page_tokens, g.kv_heads, g.head_dim)
+    idx = torch.from_numpy(dp.astype(np.int64)).cuda()
+    got = dst.view(n_dst, g.page_bytes(1))[idx].cpu().numpy().reshape(-1)
+    got_sc = scales.view(n_dst, scale_page)[idx].cpu().numpy().reshape(-1)
+    assert np.array_equal(got, dst_exp), first_diff(got, dst_exp)
+    assert np.array_equal(got_sc, sc_exp), first_diff(got_sc, sc_exp)
