@@ -32,11 +32,14 @@ base::Status EncodeKVPageList(uint64_t shared_arena_epoch,
 }
 
 base::Status DecodeKVPageIds(const std::string& wire, uint64_t* shared_arena_epoch, int32_t* layers,
-                             std::vector<int32_t>* ids) {
+                             std::vector<int32_t>* ids, int64_t max_pages) {
   if (!shared_arena_epoch || !layers || !ids) return InvalidArgument("page list output is null");
   int64_t n = 0;
   if (pbe_page_list_decode(wire.data(), wire.size(), nullptr, 0, &n, layers, shared_arena_epoch) != PBE_OK)
     return InvalidArgument(pbe_last_error());
+  if (n > max_pages)
+    return InvalidArgument("page list claims " + std::to_string(n) + " pages, more than the " +
+                           std::to_string(max_pages) + " allowed");
   ids->assign(static_cast<size_t>(n), 0);
   if (pbe_page_list_decode(wire.data(), wire.size(), ids->data(), n, &n, layers, shared_arena_epoch) !=
       PBE_OK) {
@@ -47,12 +50,12 @@ base::Status DecodeKVPageIds(const std::string& wire, uint64_t* shared_arena_epo
 }
 
 base::Status DecodeKVPageList(const std::string& wire, uint64_t* shared_arena_epoch,
-                              std::vector<RemoteKVLayerPayload>* layers) {
+                              std::vector<RemoteKVLayerPayload>* layers, int64_t max_pages) {
   if (layers == nullptr) return InvalidArgument("page list output is null");
   layers->clear();
   int32_t n_layers = 0;
   std::vector<int32_t> ids;
-  base::Status status = DecodeKVPageIds(wire, shared_arena_epoch, &n_layers, &ids);
+  base::Status status = DecodeKVPageIds(wire, shared_arena_epoch, &n_layers, &ids, max_pages);
   if (!status) return status;
   layers->resize(static_cast<size_t>(n_layers));
   for (int32_t l = 0; l < n_layers; ++l) {

@@ -33,14 +33,22 @@ struct RemoteKVLayerPayload {
 base::Status EncodeKVPageList(uint64_t shared_arena_epoch,
                               const std::vector<RemoteKVLayerPayload>& layers, std::string* wire);
 
+constexpr int64_t kMaxWirePages = int64_t{1} << 22;
+
 // Decodes and checks a page list; fills one payload per layer, all with the
 // same ids, ready for DecodeKVReservationRequest::src_block_ids_per_layer.
+// A few bytes of spans can claim millions of pages: `max_pages` (the arena's
+// page capacity, say) bounds what is allocated for input from another
+// process; longer lists are rejected before any allocation. The default,
+// 2^22 pages, exceeds any one-GPU arena (1.8 TB of 448 KiB pages).
 base::Status DecodeKVPageList(const std::string& wire, uint64_t* shared_arena_epoch,
-                              std::vector<RemoteKVLayerPayload>* layers);
+                              std::vector<RemoteKVLayerPayload>* layers,
+                              int64_t max_pages = kMaxWirePages);
 
 // Decodes the page-major id list once (no per-layer copies).
 base::Status DecodeKVPageIds(const std::string& wire, uint64_t* shared_arena_epoch,
-                             int32_t* layers, std::vector<int32_t>* ids);
+                             int32_t* layers, std::vector<int32_t>* ids,
+                             int64_t max_pages = kMaxWirePages);
 
 }  // namespace serving
 

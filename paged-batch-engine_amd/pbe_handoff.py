@@ -202,13 +202,17 @@ def encode_page_list(ids, layers: int, epoch: int) -> bytes:
     return buf.raw[:n.value]
 
 
-def decode_page_list(data: bytes):
-    """(ids, layers, epoch) of a page list; raises PbeError on any defect."""
+def decode_page_list(data: bytes, max_pages: int = 1 << 22):
+    """(ids, layers, epoch) of a page list; raises PbeError on any defect, and
+    before allocating anything when the list claims more than max_pages pages
+    (a few bytes of spans can claim millions)."""
     import numpy as np
     n, layers, epoch = C.c_int64(), C.c_int32(), C.c_uint64()
     src = C.create_string_buffer(bytes(data), len(data)) if data else C.create_string_buffer(1)
     check(lib().pbe_page_list_decode(src, len(data), None, 0, C.byref(n), C.byref(layers),
                                      C.byref(epoch)))
+    if n.value > max_pages:
+        raise PbeError(PBE_ERR_INVALID, f"page list claims {n.value} pages (> {max_pages})")
     ids = np.empty(max(1, n.value), np.int32)
     check(lib().pbe_page_list_decode(src, len(data), ids.ctypes.data_as(C.c_void_p), n.value,
                                      C.byref(n), C.byref(layers), C.byref(epoch)))

@@ -976,6 +976,11 @@ TEST_CASE("kv page wire: per-layer id lists round trip through the compact form"
   REQUIRE(serving::DecodeKVPageIds(wire, &epoch, &n_layers, &flat));
   CHECK_EQ(n_layers, L);
   CHECK(flat == ids);
+  // a bound on the page count (the arena's capacity) is enforced before allocating
+  CHECK(!serving::DecodeKVPageIds(wire, &epoch, &n_layers, &flat, 9));
+  CHECK(!serving::DecodeKVPageList(wire, &epoch, &back, 9));
+  REQUIRE(serving::DecodeKVPageIds(wire, &epoch, &n_layers, &flat, 10));
+  CHECK(flat == ids);
   // empty prefix: header only
   std::vector<serving::RemoteKVLayerPayload> empty{{0, {}}, {1, {}}};
   REQUIRE(serving::EncodeKVPageList(5, empty, &wire));

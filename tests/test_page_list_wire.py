@@ -112,6 +112,19 @@ def test_every_single_bit_flip_truncation_and_extension_is_rejected():
         P.decode_page_list(wire + b"\0" * 8)
 
 
+def test_short_list_claiming_millions_of_pages_is_bounded():
+    """40 bytes can claim 2^22 + 1 pages: rejected before anything is
+    allocated unless the caller's bound (its arena capacity) allows them."""
+    wire = spec_bytes([(0, (1 << 22) + 1)], 1, 3)
+    assert len(wire) == 40
+    with pytest.raises(P.PbeError):
+        P.decode_page_list(wire)
+    with pytest.raises(P.PbeError):
+        P.decode_page_list(spec_bytes([(0, 1000)], 1, 3), max_pages=999)
+    ids, layers, epoch = P.decode_page_list(wire, max_pages=1 << 23)
+    assert len(ids) == (1 << 22) + 1 and ids[-1] == 2 << 22 and layers == 1 and epoch == 3
+
+
 def test_structurally_bad_lists_with_valid_checksums_are_rejected():
     cases = [
         [(0, 0)],                # span without pages
@@ -145,3 +158,32 @@ def test_config2_page_list_is_far_smaller_than_per_layer_json():
     assert len(wire) * 100 < len(layers_json)
     back, _, _ = P.decode_page_list(wire)
     assert np.array_equal(back, ids)
+
+
+def test_fuzzed_input_is_rejected_or_round_trips():
+    """Arbitrary bytes, and valid lists with random byte edits and checksums
+    recomputed over the edit: decoding either raises PbeError or yields a list
+    whose encoding is exactly the input (nothing else is accepted)."""
+    hyp = pytest.importorskip("hypothesis")
+    st = hyp.strategies
+
+    def check(data: bytes):
+        try:
+            ids, layers, epoch = P.decode_page_list(data, max_pages=1 << 16)
+        except P.PbeError:
+            return
+        assert P.encode_page_list(ids, layers, epoch) == data
+
+    @hyp.settings(max_examples=300, deadline=None, derandomize=True)
+    @hyp.given(st.binary(max_size=200))
+    def raw(data):
+        check(data)
+
+    @hyp.settings(max_examples=300, deadline=None, derandomize=True)
+    @hyp.given(st.lists(st.tuples(st.integers(-8, 1 << 20), st.integers(-2, 50)), max_size=6),
+               st.integers(1, 64), st.integers(0, 2**64 - 1))
+    def spans(sp, layers, epoch):
+        check(spec_bytes(sp, layers, epoch))
+
+    raw()
+    spans()
