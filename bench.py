@@ -238,6 +238,27 @@ def measure_extra_configs(torch, P, W, scrub, n: int):
                 x.close()
         del bufs
 
+    out.extend(measure_fp8(torch, P, W, scrub, n))
+    out.extend(measure_decode(torch, P, scrub, n))
+    return out
+
+
+def measure_fp8(torch, P, W, scrub, n: int):
+    """Config 4: the fused BF16 -> FP8 E4M3 handoff in both scale modes."""
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    out = []
+
+    def rec(name, alg, ms, extra=None):
+        r = {"workload": name, "algorithmic_bytes": alg, "kernel_us_mean": round(ms[0] * 1e3, 2),
+             "kernel_us_min": round(ms[1] * 1e3, 2),
+             "gbps": round(alg / (ms[0] * 1e-3) / 1e9, 1),
+             "pct_of_peak": round(100 * alg / (ms[0] * 1e-3) / 1e9 / PEAK_GBPS, 1)}
+        r.update(extra or {})
+        out.append(r)
+        print(json.dumps(r), file=sys.stderr, flush=True)
+
     w = W.config4(0)
     g = w.geometry
     kv = P.shape(g.layers, g.kv_heads, g.head_dim, g.page_tokens)
@@ -260,7 +281,6 @@ def measure_extra_configs(torch, P, W, scrub, n: int):
                lambda: rl.copy_fp8(P.PBE_FP8_SCALE_TABLE, table.data_ptr(), sp), n),
         {"pages": w.pages})
     rl.close()
-    out.extend(measure_decode(torch, P, scrub, n))
     return out
 
 
@@ -365,6 +385,8 @@ def main() -> int:
                     help="also time configs 1, 3, 4 and 5 and write them as JSON to this file")
     ap.add_argument("--decode-only", action="store_true",
                     help="time only the decode reader (FP8 and BF16 pages) and print it as JSON")
+    ap.add_argument("--fp8-only", action="store_true",
+                    help="time only the fused FP8 handoff (config 4, both scale modes)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also launch a plain contiguous copy of 256 MiB with the same kernel "
                          "(rocprofv3 --pmc byte-count calibration)")
@@ -383,10 +405,11 @@ def main() -> int:
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
-    if args.decode_only:
+    if args.decode_only or args.fp8_only:
         scrub = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         sp = torch.cuda.current_stream().cuda_stream
-        out = {"decode": measure_decode(torch, P, scrub, max(3, args.steps))}
+        out = {"decode": measure_decode(torch, P, scrub, max(3, args.steps))} if args.decode_only \
+            else {"fp8": measure_fp8(torch, P, W, scrub, max(3, args.steps))}
         if args.calibrate:
             out["calibration"] = calibration_copy(torch, P, scrub, args.steps, sp)
         print(json.dumps(out))
