@@ -1254,4 +1254,29 @@ TEST_CASE("block allocator (shared arena): per-layer ids, refcounts, payload poi
   CHECK_EQ(layers[0]->shared_arena_bytes(), (size_t)(12 * Group::kPage));
 }
 
+TEST_CASE("block allocator: the pool view binds the planes without owning the allocation queue") {
+  // test_kv_pool_view.cpp:5-25, in shared-arena mode over a one-segment mapping
+  Group g(12, 12 * Group::kPage);
+  std::shared_ptr<base::SharedKVPageGroup> group(std::move(g.group));
+  base::BlockAllocator layer1(16, 1, 128, group, 1);
+  const int32_t free_before = layer1.num_free_blocks();
+  const base::KVPoolView view = layer1.pool_view();
+  REQUIRE(view.valid());
+  CHECK(view.device_type() == base::DeviceType::kDeviceHIP);
+  CHECK(view.key_pool() == group->key_base(1));
+  CHECK(view.value_pool() == group->value_base(1));
+  CHECK(!view.uses_fp8_storage());
+  CHECK_EQ(view.block_stride(), (size_t)Group::kHalf);
+  CHECK_EQ(layer1.num_free_blocks(), free_before);
+  base::BlockAllocator layer0(16, 1, 128, group, 0);
+  const int32_t block = layer0.allocate();
+  REQUIRE(block >= 0);
+  CHECK_EQ(layer1.allocate(), block);
+  CHECK_EQ(layer1.num_free_blocks(), free_before - 1);
+  // copying the descriptor does not affect physical ownership
+  const base::KVPoolView imported = view;
+  CHECK(imported.key_pool() == view.key_pool());
+  CHECK_EQ(layer1.num_free_blocks(), free_before - 1);
+}
+
 MINITEST_MAIN()
