@@ -371,21 +371,24 @@ __global__ __launch_bounds__(kThreadsPerBlock) void copy_ops_kernel(
   for (uint32_t i = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave; i < n_ops; i += waves) {
     const DevOp op = ops[__builtin_amdgcn_readfirstlane(i)];
     if (((op.src | op.dst | op.bytes) & 15u) == 0) {
-      gsrc_t src = reinterpret_cast<gsrc_t>(op.src);
-      gdst_t dst = reinterpret_cast<gdst_t>(op.dst);
+      // Up to 8 KiB per round (a whole K or V plane of a 1.5B page in one
+      // round trip): all loads first, then all stores, against buffer
+      // resources clamped to the op (out-of-range lanes load 0, stores drop).
+      // A piece is at most kOpPieceBytes, so the 32-bit range holds it. Loads
+      // are non-temporal, stores sc1+nt, as in the run-list kernel.
       const uint32_t bytes = (uint32_t)op.bytes;
-      for (uint32_t base = 0; base < bytes; base += 4u * kWave * 16u) {
-        u32x4 v[4];
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)op.src, (short)0, bytes, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rd =
+          __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)op.dst, (short)0, bytes, 0x00020000);
+      for (uint32_t base = 0; base < bytes; base += 8u * kWave * 16u) {
+        u32x4 v[8];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const uint32_t off = base + (u * kWave + lane) * 16u;
-          if (off < bytes) v[u] = ld16(src, off);
-        }
+        for (int u = 0; u < 8; ++u)
+          v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, base + (u * kWave + lane) * 16u, 0, 0x02);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const uint32_t off = base + (u * kWave + lane) * 16u;
-          if (off < bytes) st16(dst, off, v[u]);
-        }
+        for (int u = 0; u < 8; ++u)
+          __builtin_amdgcn_raw_buffer_store_b128(v[u], rd, base + (u * kWave + lane) * 16u, 0, 0x12);
       }
     } else {
       const uint8_t* src = reinterpret_cast<const uint8_t*>(op.src);

@@ -214,6 +214,20 @@ def test_component_ops_match_generic_plan(torch_cuda):
     exp2 = after.copy()
     exp2[dst_off:dst_off + 37] = after[src_off:src_off + 37]
     assert np.array_equal(after2, exp2), first_diff(after2, exp2)
+    # 16-byte aligned ops of ragged sizes: partial rounds, ops split into
+    # several pieces, and the bytes around each destination left alone
+    sizes = [16, 1040, 8192 + 16, 2 * 16384 + 48]
+    ops, exp3, at = [], after2.copy(), 0
+    for n in sizes:
+        src_off, dst_off = at, 40 * half + at + 32
+        ops.append((base + src_off, base + dst_off, n))
+        exp3[dst_off:dst_off + n] = after2[src_off:src_off + n]
+        at += n + 4096
+    assert 40 * half + at < len(exp3)
+    P.copy_ops(ops, 0, stream_ptr(torch))
+    torch.cuda.synchronize()
+    after3 = snapshot(bufs)
+    assert np.array_equal(after3, exp3), first_diff(after3, exp3)
 
 
 def test_repeated_launches_are_idempotent(torch_cuda):
