@@ -68,6 +68,28 @@ def cpu_baseline(w, host_arena, seconds: float):
         if cel >= seconds / 2:
             break
     cper = cel / creps
+    # the same generic path as the reference's own code runs it: oracle/_ref
+    # (its TransferPlanner / BoundTransfer / ExecuteCpuTransfer compiled from
+    # its sources), binding included, on the same host arena and plan
+    ref = {"skipped": "oracle/_ref not built"}
+    if O.REF_LIB_PATH.exists():
+        after_port = host_arena.copy()
+        geo = (g.layers, g.kv_heads, g.head_dim)
+        t0 = time.perf_counter()
+        ok = O.ref_cpu_handoff(O.REF_LIB_PATH, host_arena, w.src_ids, w.dst_ids, *geo) == w.copied_bytes()
+        one = time.perf_counter() - t0
+        rreps = max(1, int(seconds / 2 / max(one, 1e-6)))
+        t0 = time.perf_counter()
+        ok = ok and O.ref_cpu_handoff(O.REF_LIB_PATH, host_arena, w.src_ids, w.dst_ids, *geo,
+                                      repeats=rreps) == w.copied_bytes()
+        rel = time.perf_counter() - t0
+        rper = rel / rreps
+        ref = {"value": round(w.algorithmic_bytes() / rper / 1e9, 3), "unit": "GB/s", "cores": 1,
+               "kind": "reference", "ms_per_handoff": round(rper * 1e3, 3),
+               "what": "the reference's TransferPlanner + per-page BoundTransfer::BindComponents + "
+                       "ExecuteCpuTransfer (pd_handoff.cpp:192-213), compiled from its sources",
+               "same_bytes_as_port": bool(ok and np.array_equal(host_arena, after_port)),
+               "sample": f"{rreps} handoffs in {rel:.1f} s"}
     return {"value": round(w.algorithmic_bytes() / per / 1e9, 3), "unit": "GB/s", "cores": 1,
             "kind": "port",
             "sample": f"{reps} handoffs of the config-2 plan (315 pages, {w.copied_bytes()} B "
@@ -77,7 +99,8 @@ def cpu_baseline(w, host_arena, seconds: float):
             "generic_plan_form": {"value": round(w.algorithmic_bytes() / cper / 1e9, 3),
                                   "unit": "GB/s", "ms_per_handoff": round(cper * 1e3, 3),
                                   "memcpys_per_handoff": w.pages * 2 * g.layers,
-                                  "sample": f"{creps} handoffs in {cel:.1f} s"}}
+                                  "sample": f"{creps} handoffs in {cel:.1f} s"},
+            "reference_generic_plan_form": ref}
 
 
 class TimingEvents:

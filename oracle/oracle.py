@@ -198,3 +198,20 @@ def paged_decode(arena: np.ndarray, fp8: bool, scales, layers: int, kv_heads: in
                 p = np.exp2(s - np.max(s))
                 out[b, qh] = (p * vs) @ V / p.sum()
     return out
+
+
+def ref_cpu_handoff(lib_path, arena: np.ndarray, src, dst, layers: int, kv_heads: int,
+                    head_size: int, page_tokens: int = 16, repeats: int = 1) -> int:
+    """The generic CPU plan path (bind each page's planes, ExecuteCpuTransfer)
+    from oracle/ref_driver.cpp, in the build at `lib_path`: the reference's own
+    sources (oracle/_ref) or this repository's drop-in API. In place on a uint8
+    host arena; returns the bytes one pass copies, -1 on error."""
+    assert arena.dtype == np.uint8 and arena.flags.c_contiguous
+    lib_ = C.CDLL(str(lib_path))
+    f = lib_.ref_cpu_handoff
+    f.restype = C.c_int64
+    f.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p, C.c_int64, C.c_int32, C.c_int32,
+                  C.c_int32, C.c_int32, C.c_int32]
+    s, d = _i32(src), _i32(dst)
+    return int(f(_p(arena), arena.nbytes, _p(s), _p(d), len(s), layers, kv_heads, head_size,
+                 page_tokens, repeats))

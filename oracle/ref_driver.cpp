@@ -215,3 +215,65 @@ done:
   std::memcpy(out, log.c_str(), log.size() + 1);
   return (int)log.size();
 }
+
+// ---------------------------------------------------------------------------
+// CPU handoff through the generic plan path, as the in-process block-copy
+// connector runs it between two host pools (pd_handoff.cpp:192-213 with
+// pd_handoff_common.cpp:64-140 binding the manifest): one KV page schema, one
+// kExactDirect plan, then per page a BoundTransfer over that page's planes and
+// ExecuteCpuTransfer (transfer_plan.cpp:392-403), i.e. one memcpy per (layer,
+// K|V) component. Planes live in a page-major arena: plane 2l+kind of page id p
+// starts at byte (p + 2l + kind) * half. Every binding and copy is repeated
+// `repeats` times. Returns the bytes copied by one pass, or -1 on any error.
+extern "C" int64_t ref_cpu_handoff(uint8_t* arena, uint64_t arena_bytes, const int32_t* src_ids,
+                                   const int32_t* dst_ids, int64_t n, int32_t layers,
+                                   int32_t kv_heads, int32_t head_size, int32_t page_tokens,
+                                   int32_t repeats) {
+  try {
+    const auto storage =
+        base::MakeKVCacheStorageSpec(base::DataType::kDataTypeBf16, base::BlockStorageMode::kPlain);
+    cache::PageSchema schema;
+    if (!cache::MakeKVPageSchema(1, layers, page_tokens, kv_heads, head_size, storage, &schema))
+      return -1;
+    cache::TransferPlanner planner;
+    std::shared_ptr<const cache::TransferPlan> plan;
+    if (!planner.compile(schema, schema, cache::TransferPlacement::kExactDirect, &plan)) return -1;
+    std::vector<size_t> order(schema.components.size());
+    std::iota(order.begin(), order.end(), 0);
+    cache::LayoutDescriptor src_layout, dst_layout;
+    if (!cache::MakePackedLayout(schema, "cpu-src", 1, order, {}, &src_layout) ||
+        !cache::MakePackedLayout(schema, "cpu-dst", 1, order, {}, &dst_layout))
+      return -1;
+    const uint64_t half = (uint64_t)page_tokens * kv_heads * head_size * 2u;
+    for (int64_t i = 0; i < n; ++i)
+      if (src_ids[i] < 0 || dst_ids[i] < 0 ||
+          ((uint64_t)src_ids[i] + 2ull * layers) * half > arena_bytes ||
+          ((uint64_t)dst_ids[i] + 2ull * layers) * half > arena_bytes)
+        return -1;
+    int64_t copied = 0;
+    for (int32_t rep = 0; rep < repeats; ++rep) {
+      copied = 0;
+      std::vector<cache::BoundTransfer> transfers(static_cast<size_t>(n));
+      for (int64_t i = 0; i < n; ++i) {
+        cache::ConstComponentEndpoint src;
+        cache::MutableComponentEndpoint dst;
+        src.layout = &src_layout;
+        dst.layout = &dst_layout;
+        for (const auto& c : schema.components) {
+          const uint64_t plane = 2ull * c.layer + (c.kind == cache::ComponentKind::kValue ? 1 : 0);
+          src.components.push_back({c, arena + (src_ids[i] + plane) * half, c.byte_size()});
+          dst.components.push_back({c, arena + (dst_ids[i] + plane) * half, c.byte_size()});
+        }
+        if (!cache::BoundTransfer::BindComponents(*plan, schema, src, dst, &transfers[(size_t)i]))
+          return -1;
+      }
+      for (const auto& t : transfers) {
+        if (!cache::ExecuteCpuTransfer(t)) return -1;
+        for (const auto& op : t.operations()) copied += (int64_t)op.bytes;
+      }
+    }
+    return copied;
+  } catch (const std::exception&) {
+    return -1;
+  }
+}

@@ -118,3 +118,30 @@ def test_transfer_plan_random_shards_match_reference(libs):
             spec += [a, b]
         spec += [int(rng.integers(0, 100)), int(rng.integers(0, 100))]
         assert _plan(libs[0], spec) == _plan(libs[1], spec), spec
+
+
+def test_cpu_generic_path_matches_oracle(libs):
+    """The generic CPU plan path (pd_handoff.cpp:192-213: per page a BoundTransfer
+    over its planes, ExecuteCpuTransfer) run by the reference build and by the
+    drop-in build leaves exactly the oracle's component copy, canaries included.
+    bench.py times the reference build of this path as a CPU baseline."""
+    import sys
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as O
+    layers, heads, hd = 3, 2, 64
+    half = 16 * heads * hd * 2
+    stride = 2 * layers
+    rng = np.random.default_rng(9)
+    pages = rng.permutation(24)[:10] * stride
+    src, dst = pages[:5], pages[5:]
+    base = rng.integers(0, 256, 24 * stride * half, dtype=np.uint8)
+    expected = base.copy()
+    O.copy_components(expected, src, dst, half, layers)
+    for lib_path in (REF, API):
+        arena = base.copy()
+        assert O.ref_cpu_handoff(lib_path, arena, src, dst, layers, heads, hd, repeats=2) == 5 * stride * half
+        assert np.array_equal(arena, expected), lib_path.name
+    # an id whose page runs past the arena is refused before any byte moves
+    arena = base.copy()
+    assert O.ref_cpu_handoff(REF, arena, [23 * stride + 1], [0], layers, heads, hd) == -1
+    assert np.array_equal(arena, base)
