@@ -90,6 +90,16 @@ def cpu_baseline(w, host_arena, seconds: float):
                        "ExecuteCpuTransfer (pd_handoff.cpp:192-213), compiled from its sources",
                "same_bytes_as_port": bool(ok and np.array_equal(host_arena, after_port)),
                "sample": f"{rreps} handoffs in {rel:.1f} s"}
+        # the same driver over this repository's drop-in TransferPlanner / BoundTransfer
+        api = Path(__file__).resolve().parent / "paged-batch-engine_amd" / "lib" / "libpbe_api_driver.so"
+        if api.exists():
+            t0 = time.perf_counter()
+            aok = O.ref_cpu_handoff(api, host_arena, w.src_ids, w.dst_ids, *geo,
+                                    repeats=rreps) == w.copied_bytes()
+            ael = time.perf_counter() - t0
+            ref["drop_in_build"] = {"ms_per_handoff": round(ael / rreps * 1e3, 3),
+                                    "value": round(w.algorithmic_bytes() / (ael / rreps) / 1e9, 3),
+                                    "same_bytes_as_port": bool(aok and np.array_equal(host_arena, after_port))}
     return {"value": round(w.algorithmic_bytes() / per / 1e9, 3), "unit": "GB/s", "cores": 1,
             "kind": "port",
             "sample": f"{reps} handoffs of the config-2 plan (315 pages, {w.copied_bytes()} B "

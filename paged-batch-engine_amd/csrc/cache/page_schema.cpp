@@ -2,6 +2,8 @@
 // fingerprint text formats follow :172-199 so identities match across builds.
 #include "cache/page_schema.h"
 
+#include <cstdio>
+
 #include <algorithm>
 #include <array>
 #include <limits>
@@ -49,10 +51,22 @@ size_t ComponentDescriptor::byte_size() const {
 }
 
 std::string ComponentDescriptor::semantic_key() const {
-  std::ostringstream out;
-  out << layer << ':' << static_cast<int>(kind) << ':' << token_count << ':' << head_begin << ':'
-      << head_count << ':' << elements_per_head << ':' << static_cast<int>(dtype);
-  return out.str();
+  char buf[96];
+  const int n = std::snprintf(buf, sizeof(buf), "%d:%d:%d:%d:%d:%d:%d", (int)layer, (int)kind,
+                              (int)token_count, (int)head_begin, (int)head_count,
+                              (int)elements_per_head, (int)dtype);
+  return std::string(buf, (size_t)n);
+}
+
+size_t ComponentDescriptorHash::operator()(const ComponentDescriptor& c) const noexcept {
+  uint64_t h = 1469598103934665603ull;  // FNV-1a over the seven fields
+  const int64_t f[7] = {c.layer, (int64_t)c.kind, c.token_count, c.head_begin, c.head_count,
+                        c.elements_per_head, (int64_t)c.dtype};
+  for (int64_t v : f) {
+    h ^= (uint64_t)v;
+    h *= 1099511628211ull;
+  }
+  return (size_t)h;
 }
 
 bool ComponentDescriptor::operator==(const ComponentDescriptor& o) const {
@@ -86,7 +100,7 @@ base::Status PageSchema::validate() const {
   // Head ranges seen per (layer, kind).
   std::vector<std::array<std::vector<std::pair<int32_t, int32_t>>, 4>> heads(
       static_cast<size_t>(layer_count));
-  std::unordered_set<std::string> keys;
+  std::unordered_set<ComponentDescriptor, ComponentDescriptorHash> keys;
   for (const ComponentDescriptor& c : components) {
     if (c.layer < 0 || c.token_count <= 0 || c.head_begin < 0 || c.head_count <= 0 ||
         c.elements_per_head <= 0 || c.dtype == base::DataType::kDataTypeUnknown ||
@@ -103,7 +117,7 @@ base::Status PageSchema::validate() const {
       return InvalidArgument("Page component shape or dtype disagrees with storage.");
     if (scale && !storage.has_scales())
       return InvalidArgument("Plain storage must not contain scale components.");
-    if (!keys.insert(c.semantic_key()).second)
+    if (!keys.insert(c).second)
       return InvalidArgument("Page schema contains a duplicate component.");
     heads[static_cast<size_t>(c.layer)][static_cast<size_t>(c.kind)].emplace_back(
         c.head_begin, c.head_begin + c.head_count);
@@ -141,15 +155,27 @@ std::string PageSchema::logical_fingerprint() const {
 std::string PageSchema::fingerprint() const {
   std::vector<std::string> keys;
   keys.reserve(components.size());
-  for (const auto& c : components) keys.push_back(c.semantic_key());
+  size_t total = 64;
+  for (const auto& c : components) {
+    keys.push_back(c.semantic_key());
+    total += keys.back().size() + 1;
+  }
   std::sort(keys.begin(), keys.end());
-  std::ostringstream out;
-  out << version << '|' << layer_count << '|' << page_size << '|' << kv_head_count << '|'
-      << head_size << '|' << static_cast<int>(storage.storage_mode) << '|'
-      << static_cast<int>(storage.logical_dtype) << '|' << static_cast<int>(storage.storage_dtype)
-      << '|' << static_cast<int>(storage.scale_dtype);
-  for (const auto& k : keys) out << '|' << k;
-  return out.str();
+  char head[128];
+  const int n = std::snprintf(head, sizeof(head), "%u|%d|%d|%d|%d|%d|%d|%d|%d", (unsigned)version,
+                              (int)layer_count, (int)page_size, (int)kv_head_count, (int)head_size,
+                              static_cast<int>(storage.storage_mode),
+                              static_cast<int>(storage.logical_dtype),
+                              static_cast<int>(storage.storage_dtype),
+                              static_cast<int>(storage.scale_dtype));
+  std::string out;
+  out.reserve(total);
+  out.append(head, (size_t)n);
+  for (const auto& k : keys) {
+    out.push_back('|');
+    out += k;
+  }
+  return out;
 }
 
 base::Status MakeKVPageSchema(uint32_t version, int32_t layer_count, int32_t page_size,

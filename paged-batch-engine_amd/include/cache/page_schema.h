@@ -42,6 +42,12 @@ struct ComponentDescriptor {
   bool operator==(const ComponentDescriptor& other) const;
 };
 
+// Hash over the same fields as semantic_key() and operator==, for maps keyed
+// by component without building key strings.
+struct ComponentDescriptorHash {
+  size_t operator()(const ComponentDescriptor& c) const noexcept;
+};
+
 struct PageSchema {
   uint32_t version = 1;
   int32_t layer_count = 0;
