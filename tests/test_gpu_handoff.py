@@ -230,6 +230,27 @@ def test_component_ops_match_generic_plan(torch_cuda):
     assert np.array_equal(after3, exp3), first_diff(after3, exp3)
 
 
+def test_copy_ops_beyond_one_grid(torch_cuda):
+    """More op pieces than one grid holds (16,384 workgroups x 4 waves): each
+    wave walks several pieces in the grid-stride loop."""
+    torch = torch_cuda
+    n = 70000
+    say(f"copy_ops {n} ops of 32 B")
+    src = torch.randint(0, 256, (n * 32,), dtype=torch.uint8, device="cuda")
+    dst = torch.zeros(n * 64, dtype=torch.uint8, device="cuda")
+    rng = np.random.default_rng(12)
+    perm = rng.permutation(n)  # op i writes slot perm[i] of dst, every other 32 B
+    sb, db = src.data_ptr(), dst.data_ptr()
+    ops = [(sb + 32 * i, db + 64 * int(perm[i]), 32) for i in range(n)]
+    P.copy_ops(ops, 0, stream_ptr(torch))
+    torch.cuda.synchronize()
+    s_host = src.cpu().numpy().reshape(n, 32)
+    d_host = dst.cpu().numpy().reshape(n, 64)
+    expected = np.zeros((n, 64), np.uint8)
+    expected[perm, :32] = s_host
+    assert np.array_equal(d_host, expected)
+
+
 def test_repeated_launches_are_idempotent(torch_cuda):
     torch = torch_cuda
     w = W.config2(3)
