@@ -9,8 +9,11 @@
 // gfx950 mapping. One wave owns one (sequence, KV head, split) and walks its
 // blocks of 16 tokens; the KV heads of one (sequence, split) are neighbouring
 // waves of a workgroup, so a block's rows are read together:
-//  - loads: every 16-byte load instruction covers 64 contiguous bytes of each
-//    row it touches; 2 to 8 register sets rotate so that the next blocks are
+//  - loads: a key load instruction covers 64 contiguous bytes of each of the
+//    16 rows (the MFMA wants one row per lane). A value load instruction
+//    covers whole rows, i.e. full 128-byte lines, since the value tile is
+//    rearranged in LDS anyway; requesting half lines instead costs 10% of
+//    the BF16 step. 2 to 8 register sets rotate so that the next blocks are
 //    in flight while one is computed.
 //  - scores, transposed: one v_mfma_f32_16x16x32_bf16 per 32 head dims,
 //    A = the block's 16 keys (rows), B = the query heads sharing the KV head
@@ -115,7 +118,7 @@ __device__ __forceinline__ u32x2 e4m3x4_to_bf16x4_cvt(uint32_t w) {
 }
 
 // Per-lane registers of one block of 16 tokens of one KV head: the lane's
-// part of key row j, its part of value row lane/4 and one scale.
+// part of key row j, its whole-row-mapped part of the value tile and one scale.
 template <int D, bool kFp8>
 struct Geo {
   static constexpr int E = kFp8 ? 1 : 2;
@@ -190,12 +193,15 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
   // Block ids are uniform: read through the read-only table with scalar loads.
   const int32_t* table = tables + (int64_t)b * p.max_blocks;
   const uint64_t head_off = 2ull * p.layer * p.half + (uint64_t)kvh * D * E;
-  // Each 16-byte load instruction covers 64 contiguous bytes of every row it
-  // touches: load v of lane (g, j) reads bytes 64v + 16g.. of key row j, and
-  // of value row lane/4 at quarter lane%4. The key's head dims are consumed
-  // in that order; the queries are read in the same order.
+  // Key load v of lane (g, j) reads bytes 64v + 16g.. of key row j: 64
+  // contiguous bytes of every row per instruction. The key's head dims are
+  // consumed in that order; the queries are read in the same order.
   const uint32_t key_off = (uint32_t)j * token_stride + (uint32_t)(16 * g);
-  const uint32_t val_off = (uint32_t)(lane >> 2) * token_stride + (uint32_t)(16 * (lane & 3));
+  // Value load v of lane l reads the 16 bytes at column vcol of row
+  // v * RPI + vrow0: each instruction covers RPI whole rows.
+  constexpr int LPR = D * E / 16, RPI = 64 / LPR;  // lanes per row, rows per load
+  const int vrow0 = lane / LPR, vcol = 16 * (lane % LPR);
+  const uint32_t val_off = (uint32_t)vrow0 * token_stride + (uint32_t)vcol;
   // lane (g, j): scale of token 4g + j%4 from the key (j%8 < 4) or value plane
   const uint32_t scale_off =
       (uint32_t)(((2u * p.layer + ((j >> 2) & 1)) * kBlockTokens + 4u * g + (j & 3)) * H + kvh);
@@ -215,8 +221,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
 #pragma unroll
     for (int v = 0; v < W / 4; ++v) {
       const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kplane + key_off + 64 * v));
-      const u32x4 y =
-          __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kplane + p.half + val_off + 64 * v));
+      const u32x4 y = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(kplane + p.half + val_off + (uint64_t)v * RPI * token_stride));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         r.k[4 * v + e] = x[e];
@@ -241,19 +247,13 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
     const int valid = blk == nblk - 1 ? seq - kBlockTokens * (nblk - 1) : kBlockTokens;
     // Value tile -> LDS rows (tail rows zeroed: tail slots may hold anything, even NaN).
     {
-      const int t = lane >> 2;
-      unsigned char* dst = vt_w + t * PITCH + 16 * (lane & 3);
-      if (valid == kBlockTokens) {  // every block but a sequence's last
+      unsigned char* dst = vt_w + vrow0 * PITCH + vcol;
 #pragma unroll
-        for (int v = 0; v < W / 4; ++v)
-          *reinterpret_cast<u32x4*>(dst + 64 * v) = u32x4{r.v[4 * v], r.v[4 * v + 1], r.v[4 * v + 2], r.v[4 * v + 3]};
-      } else {
-#pragma unroll
-        for (int v = 0; v < W / 4; ++v) {
-          const u32x4 x = t < valid ? u32x4{r.v[4 * v], r.v[4 * v + 1], r.v[4 * v + 2], r.v[4 * v + 3]}
-                                    : u32x4{0u, 0u, 0u, 0u};
-          *reinterpret_cast<u32x4*>(dst + 64 * v) = x;
-        }
+      for (int v = 0; v < W / 4; ++v) {
+        const u32x4 x = v * RPI + vrow0 < valid
+                            ? u32x4{r.v[4 * v], r.v[4 * v + 1], r.v[4 * v + 2], r.v[4 * v + 3]}
+                            : u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(dst + v * RPI * PITCH) = x;
       }
     }
     // Scores, transposed: lane (g, j) gets tokens 4g..4g+3 of head j.
