@@ -342,12 +342,12 @@ def measure_decode(torch, P, scrub, n: int, batch: int = 64, seq: int = 5040, pl
     seq_lens = torch.full((batch,), seq, dtype=torch.int32, device=dev)
     q = (torch.randn(batch, H * kvm, D, generator=g, device=dev)).to(torch.bfloat16)
     o = torch.empty_like(q)
-    splits = P.decode_splits(batch, H, blocks)
-    ws_bytes = P.decode_workspace_bytes(batch, H * kvm, D, splits)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     res = []
     for fp8 in (True, False):
         E = 1 if fp8 else 2
+        splits = P.decode_splits(batch, H, blocks, P.PBE_KV_FP8_E4M3 if fp8 else P.PBE_KV_BF16)
+        ws_bytes = P.decode_workspace_bytes(batch, H * kvm, D, splits)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         arena = torch.empty(n_pages * 2 * L * 16 * H * D * E, dtype=torch.uint8, device=dev)
         if fp8:
             arena.copy_(torch.randint(0, 0x70, arena.shape, generator=g, device=dev, dtype=torch.uint8)

@@ -114,7 +114,7 @@ _SIGNATURES = [
     ("pbe_copy_shared_kv", C.c_int, [C.POINTER(ArenaView), _P, _P, C.c_int64,
                                      C.POINTER(KvShape), C.c_int, _P, C.POINTER(C.c_uint64)]),
     ("pbe_copy_ops", C.c_int, [C.POINTER(CopyOp), C.c_int64, C.c_int, _P]),
-    ("pbe_paged_decode_splits", C.c_int32, [C.c_int32, C.c_int32, C.c_int32]),
+    ("pbe_paged_decode_splits", C.c_int32, [C.c_int32, C.c_int32, C.c_int32, C.c_int32]),
     ("pbe_paged_decode_workspace_bytes", C.c_uint64, [C.c_int32, C.c_int32, C.c_int32, C.c_int32]),
     ("pbe_paged_decode", C.c_int, [C.POINTER(ArenaView), C.c_int32, _P, C.c_uint64,
                                    C.POINTER(KvShape), C.c_int32, _P, _P, C.c_int32, C.c_int32,
@@ -452,8 +452,8 @@ def device_uuid(device: int = 0) -> bytes:
 
 
 
-def decode_splits(batch: int, kv_heads: int, max_blocks: int) -> int:
-    return int(lib().pbe_paged_decode_splits(batch, kv_heads, max_blocks))
+def decode_splits(batch: int, kv_heads: int, max_blocks: int, kv_dtype: int) -> int:
+    return int(lib().pbe_paged_decode_splits(batch, kv_heads, max_blocks, kv_dtype))
 
 
 def decode_workspace_bytes(batch: int, q_heads: int, head_dim: int, splits: int) -> int:

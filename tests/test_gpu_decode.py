@@ -105,7 +105,8 @@ class DecodeCase:
 
     def run(self, splits=0, tables=None, seq_lens=None, ws=None):
         torch = self.torch
-        s = splits or P.decode_splits(self.batch, self.H, self.max_blocks)
+        s = splits or P.decode_splits(self.batch, self.H, self.max_blocks,
+                                      P.PBE_KV_FP8_E4M3 if self.fp8 else P.PBE_KV_BF16)
         ws_bytes = P.decode_workspace_bytes(self.batch, self.H * self.kvm, self.D, s)
         if ws is None:
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
@@ -320,7 +321,7 @@ def test_pages_beyond_4_gib_of_a_single_arena(torch_cuda, fp8):
     out = torch.empty_like(q)
     t_dev = torch.from_numpy(tables).cuda()
     s_dev = torch.tensor(seq_lens, dtype=torch.int32, device="cuda")
-    splits = P.decode_splits(batch, H, max_blocks)
+    splits = P.decode_splits(batch, H, max_blocks, P.PBE_KV_FP8_E4M3 if fp8 else P.PBE_KV_BF16)
     ws_bytes = P.decode_workspace_bytes(batch, H * kvm, D, splits)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
     P.paged_decode(view, P.PBE_KV_FP8_E4M3 if fp8 else P.PBE_KV_BF16,

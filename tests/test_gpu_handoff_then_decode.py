@@ -75,7 +75,7 @@ def test_prefill_pages_handed_off_then_decoded(torch_cuda, fp8):
     out = torch.empty_like(q)
     t_dev = torch.from_numpy(tables).cuda()
     s_dev = torch.tensor(seq_lens, dtype=torch.int32, device="cuda")
-    splits = P.decode_splits(batch, g.kv_heads, max_blocks)
+    splits = P.decode_splits(batch, g.kv_heads, max_blocks, P.PBE_KV_FP8_E4M3 if fp8 else P.PBE_KV_BF16)
     ws_bytes = P.decode_workspace_bytes(batch, g.kv_heads * kvm, g.head_dim, splits)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
     P.paged_decode(dst_view, P.PBE_KV_FP8_E4M3 if fp8 else P.PBE_KV_BF16,
