@@ -1098,14 +1098,20 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
 int32_t pbe_paged_decode_splits(int32_t batch, int32_t kv_heads, int32_t max_blocks_per_seq,
                                 int32_t kv_dtype) {
   if (batch <= 0 || kv_heads <= 0 || max_blocks_per_seq <= 0) return 1;
-  // At most 2048 waves for FP8 pages (two per SIMD) and 1024 for BF16 (one
-  // per SIMD), rounded down so no partial extra round of waves trails the
-  // launch; at least 4 blocks (64 tokens) per split. Measured on MI355X for
-  // 64 x 5040-token batches: FP8 stage 1 takes 35.7 us at 16 splits against
-  // 40.9 us at 8 (32 splits: 45.6 us); BF16 54.6 us at 8 against 56.5 us at 16.
+  // At most 1024 waves (one per SIMD), rounded down so no partial extra round
+  // of waves trails the launch; FP8 pages take 2048 (two per SIMD) when every
+  // split still holds at least 16 blocks; at least 4 blocks (64 tokens) per
+  // split. Measured on MI355X, 5040-token sequences, both launches: FP8 batch
+  // 64 at 16 splits 35.7 us stage 1 against 40.9 us at 8; batch 128: 8 splits
+  // 66.7 us against 74.5 us at 4; batch 32: 16 splits 28.9 us against 30.8 us
+  // at 32; batch 16: 32 splits 22.9 us against 27.9 us at 64. BF16 batch 64:
+  // 54.6 us stage 1 at 8 splits against 56.5 us at 16.
   const int64_t units = (int64_t)batch * kv_heads;
-  const int64_t waves = kv_dtype == PBE_KV_FP8_E4M3 ? 2048 : 1024;
-  int64_t splits = std::max<int64_t>(1, waves / units);
+  int64_t splits = std::max<int64_t>(1, 1024 / units);
+  if (kv_dtype == PBE_KV_FP8_E4M3) {
+    const int64_t two = std::max<int64_t>(1, 2048 / units);
+    if ((max_blocks_per_seq + two - 1) / two >= 16) splits = two;
+  }
   splits = std::min<int64_t>(splits, (max_blocks_per_seq + 3) / 4);
   splits = std::min<int64_t>(splits, pbe::kDecodeMaxSplits);
   return (int32_t)std::max<int64_t>(1, splits);
