@@ -81,3 +81,21 @@ def test_invalid_arguments_are_rejected_on_the_host():
     with pytest.raises(P.PbeError) as e:
         P.build_runs([0], [4], bad)
     assert e.value.code == P.PBE_ERR_INVALID
+
+
+def test_decode_split_count_by_page_dtype():
+    """pbe_paged_decode_splits: at most 1024 waves (batch x kv_heads x splits),
+    FP8 pages 2048 while every split keeps >= 16 blocks, >= 4 blocks per
+    split, at most 64 splits. The choices at 5040 tokens (315 blocks) are the
+    ones measured fastest on MI355X."""
+    fp8, bf16 = P.PBE_KV_FP8_E4M3, P.PBE_KV_BF16
+    assert P.decode_splits(64, 2, 315, fp8) == 16
+    assert P.decode_splits(64, 2, 315, bf16) == 8
+    assert P.decode_splits(128, 2, 315, fp8) == 8
+    assert P.decode_splits(128, 2, 315, bf16) == 4
+    assert P.decode_splits(32, 2, 315, fp8) == 16   # 32 splits would leave < 16 blocks each
+    assert P.decode_splits(16, 2, 315, fp8) == 32
+    assert P.decode_splits(1, 2, 10000, fp8) == 64  # capped
+    assert P.decode_splits(1, 1, 7, bf16) == 2      # at least 4 blocks per split
+    assert P.decode_splits(4096, 8, 315, fp8) == 1
+    assert P.decode_splits(0, 2, 315, fp8) == 1
