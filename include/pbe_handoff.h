@@ -102,11 +102,17 @@ int pbe_arena_get_view(const pbe_arena* arena, pbe_arena_view* out);
 uint64_t pbe_arena_epoch(const pbe_arena* arena);
 int pbe_arena_destroy(pbe_arena* arena);
 
-/* ---- IPC completion events -------------------------------------------
- * hipEventInterprocess|hipEventDisableTiming events whose handle crosses
- * processes (pattern of demo/cuda_ipc_event_probe.cu:24-27,70-75 and
- * data/ipc_pool.h:24-26): P records "KV written", D waits on it in its
- * stream before the copy, D records "copy done", P waits before retiring. */
+/* ---- completion events ------------------------------------------------
+ * In-process fences (interprocess = 0): record on one stream, wait on another
+ * or query/synchronize from the host.
+ * interprocess = 1 asks for a hipEventInterprocess event whose handle crosses
+ * processes (the pattern of demo/cuda_ipc_event_probe.cu:24-27,70-75). The
+ * HIP runtime of ROCm 7.2 creates such events but rejects hipEventRecord on
+ * them, so they cannot carry a completion: pbe_event_create(.., 1, ..) and
+ * pbe_event_import probe the runtime once per device and return
+ * PBE_ERR_UNSUPPORTED when recording fails. Cross-process completion uses
+ * pbe_signal_* below. pbe_event_export of an in-process event is
+ * PBE_ERR_INVALID. */
 typedef struct pbe_event pbe_event;
 int pbe_event_create(int device, int interprocess, pbe_event** out);
 int pbe_event_export(const pbe_event* event, uint8_t out[PBE_IPC_HANDLE_BYTES]);
@@ -312,6 +318,10 @@ int pbe_paged_decode(const pbe_arena_view* kv, int32_t kv_dtype, const float* sc
 
 /* GPU UUID of `device` (16 bytes), as compared across processes. */
 int pbe_device_uuid(int device, uint8_t out[16]);
+/* The calling thread's current HIP device (the one a pool built without an
+ * explicit device index lives on, as the reference's CUDA allocator uses the
+ * current device: block_allocator.cpp:36-38). */
+int pbe_current_device(int* device);
 
 /* ---- streams and pointer queries for C++ host code ---------------------
  * Backends above this ABI (the HIP TransferBackend, the shared-arena

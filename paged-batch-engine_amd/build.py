@@ -53,9 +53,11 @@ HOST_SOURCES = [
 ABI_HOST_SOURCES = [
     "csrc/base/shared_kv_arena.cpp",
     "csrc/base/block_allocator.cpp",
+    "csrc/base/kv_cache_manager.cpp",
     "csrc/cache/hip_transfer_backend.cpp",
     "csrc/serving/shared_kv_handoff.cpp",
     "csrc/serving/decode_kv_reservation.cpp",
+    "csrc/serving/split_pd_handoff.cpp",
     "csrc/serving/plan_kv_connector.cpp",
     "csrc/serving/kv_page_wire.cpp",
 ]

@@ -1,14 +1,72 @@
-// Shared-arena mode of the block allocator; rules follow
-// infMain/source/base/block_allocator.cpp:139-401 (reference counts and
-// generations per block id, the page group deciding allocation and retire).
+// Block allocator in shared-arena and local-pool mode; rules follow
+// infMain/source/base/block_allocator.cpp:17-428 (reference counts and
+// generations per block id; the page group or a FIFO free queue deciding
+// allocation and reuse).
 #include "base/block_allocator.h"
 
 #include <atomic>
+#include <cstring>
 #include <limits>
 #include <stdexcept>
 #include <string>
 
 namespace base {
+namespace {
+uint64_t next_pool_id() {
+  static std::atomic<uint64_t> next{1};
+  return next.fetch_add(1);
+}
+}  // namespace
+
+BlockAllocator::BlockAllocator(int32_t num_blocks, int32_t block_size, int32_t num_kv_heads,
+                               int32_t head_size, const KVCacheStorageSpec& storage_spec,
+                               DeviceType device)
+    : block_size_(block_size), num_kv_heads_(num_kv_heads), head_size_(head_size),
+      num_blocks_(num_blocks), device_(device), storage_spec_(storage_spec) {
+  if (num_blocks <= 0 || block_size <= 0 || num_kv_heads <= 0 || head_size <= 0)
+    throw std::invalid_argument("block pool dimensions must be positive");
+  if (device != DeviceType::kDeviceHIP && device != DeviceType::kDeviceCPU)
+    throw std::invalid_argument("block pool device must be HIP or CPU");
+  const Status ok = ValidateKVCacheStorageSpec(storage_spec_, device_, storage_spec_.logical_dtype);
+  if (!ok) throw std::invalid_argument(ok.get_err_msg());
+  const uint64_t kv = static_cast<uint64_t>(num_blocks) * key_value_bytes_per_block();
+  const uint64_t sc = static_cast<uint64_t>(num_blocks) * scale_bytes_per_block();
+  // Every pool starts on a 256-byte boundary.
+  const uint64_t kv_pad = (kv + 255) / 256 * 256, sc_pad = (sc + 255) / 256 * 256;
+  const uint64_t total = 2 * kv_pad + 2 * sc_pad;
+  uint8_t* base = nullptr;
+  if (device_ == DeviceType::kDeviceHIP) {
+    if (pbe_current_device(&device_index_) != PBE_OK ||
+        pbe_arena_create(device_index_, total, 0, 1, &device_pools_) != PBE_OK)
+      throw std::runtime_error(std::string("block pool allocation: ") + pbe_last_error());
+    pbe_arena_view v;
+    pbe_arena_get_view(device_pools_, &v);
+    base = static_cast<uint8_t*>(v.base[0]);
+  } else {
+    host_pools_.assign(total, 0);
+    base = host_pools_.data();
+  }
+  key_pool_ = base;
+  value_pool_ = base + kv_pad;
+  if (sc) {
+    key_scale_pool_ = base + 2 * kv_pad;
+    value_scale_pool_ = base + 2 * kv_pad + sc_pad;
+  }
+  pool_id_ = next_pool_id();
+  ref_counts_.assign(num_blocks_, 0);
+  generations_.assign(num_blocks_, 0);
+  for (int32_t i = 0; i < num_blocks_; ++i) free_queue_.push_back(i);
+}
+
+BlockAllocator::BlockAllocator(int32_t num_blocks, int32_t block_size, int32_t num_kv_heads,
+                               int32_t head_size, DataType dtype, DeviceType device,
+                               BlockStorageMode storage_mode)
+    : BlockAllocator(num_blocks, block_size, num_kv_heads, head_size,
+                     MakeKVCacheStorageSpec(dtype, storage_mode), device) {}
+
+BlockAllocator::~BlockAllocator() {
+  if (device_pools_) pbe_arena_destroy(device_pools_);
+}
 
 BlockAllocator::BlockAllocator(int32_t block_size, int32_t num_kv_heads, int32_t head_size,
                                std::shared_ptr<SharedKVPageGroup> group, int32_t layer)
@@ -20,11 +78,12 @@ BlockAllocator::BlockAllocator(int32_t block_size, int32_t num_kv_heads, int32_t
     throw std::invalid_argument("invalid shared-arena block allocator");
   if (key_value_bytes_per_block() != group_->half_bytes())
     throw std::invalid_argument("block geometry does not match the shared page group");
+  device_ = DeviceType::kDeviceHIP;
+  device_index_ = group_->device();
   num_blocks_ = group_->addressable_blocks();
   if (num_blocks_ <= 0 || static_cast<int64_t>(num_blocks_) * block_size_ > INT32_MAX)
     throw std::invalid_argument("Shared arena exceeds int32 slot mapping range");
-  static std::atomic<uint64_t> next_pool_id{uint64_t{1} << 62};
-  pool_id_ = next_pool_id.fetch_add(1);
+  pool_id_ = next_pool_id();
   ref_counts_.assign(num_blocks_, 0);
   generations_.assign(num_blocks_, 0);
 }
@@ -34,8 +93,15 @@ void BlockAllocator::check_id(int32_t block_id) const {
 }
 
 int32_t BlockAllocator::allocate() {
-  const int32_t id = group_->allocate(layer_);
-  if (id < 0) return -1;
+  int32_t id;
+  if (group_) {
+    id = group_->allocate(layer_);
+    if (id < 0) return -1;
+  } else {
+    if (free_queue_.empty()) return -1;
+    id = free_queue_.front();
+    free_queue_.pop_front();
+  }
   check_id(id);
   if (ref_counts_[id] != 0) throw std::logic_error("allocated block still has outstanding references");
   if (generations_[id] == std::numeric_limits<uint64_t>::max())
@@ -54,7 +120,10 @@ void BlockAllocator::incref(int32_t block_id) {
 void BlockAllocator::free(int32_t block_id) {
   check_id(block_id);
   if (ref_counts_[block_id] <= 0) throw std::logic_error("Double free of block");
-  if (--ref_counts_[block_id] == 0) group_->retire(layer_, block_id);
+  if (--ref_counts_[block_id] == 0) {
+    if (group_) group_->retire(layer_, block_id);
+    else free_queue_.push_back(block_id);
+  }
 }
 
 int32_t BlockAllocator::ref_count(int32_t block_id) const {
@@ -83,26 +152,75 @@ std::pair<void*, void*> BlockAllocator::get_block_ptrs(int32_t block_id) const {
   return {p.key, p.value};
 }
 
+size_t BlockAllocator::scale_bytes_per_block() const {
+  if (!storage_spec_.has_scales()) return 0;
+  return static_cast<size_t>(block_size_) * num_kv_heads_ * DataTypeSize(storage_spec_.scale_dtype);
+}
+
 KVBlockPayloadPtrs BlockAllocator::get_block_payload_ptrs(int32_t block_id) const {
   check_id(block_id);
   KVBlockPayloadPtrs ptrs;
-  ptrs.key = group_->plane_address(static_cast<int64_t>(block_id) + 2 * layer_);
-  ptrs.value = group_->plane_address(static_cast<int64_t>(block_id) + 2 * layer_ + 1);
   ptrs.key_value_bytes = key_value_bytes_per_block();
+  if (group_) {
+    ptrs.key = group_->plane_address(static_cast<int64_t>(block_id) + 2 * layer_);
+    ptrs.value = group_->plane_address(static_cast<int64_t>(block_id) + 2 * layer_ + 1);
+    return ptrs;
+  }
+  const size_t kv = static_cast<size_t>(block_id) * ptrs.key_value_bytes;
+  ptrs.key = key_pool_ + kv;
+  ptrs.value = value_pool_ + kv;
+  ptrs.scale_bytes = scale_bytes_per_block();
+  if (ptrs.scale_bytes) {
+    const size_t s = static_cast<size_t>(block_id) * ptrs.scale_bytes;
+    ptrs.key_scale = key_scale_pool_ + s;
+    ptrs.value_scale = value_scale_pool_ + s;
+  }
   return ptrs;
 }
 
+void BlockAllocator::copy_block_payload(int32_t source_block_id, int32_t destination_block_id) const {
+  if (source_block_id == destination_block_id)
+    throw std::logic_error("block payload copy onto itself");
+  if (ref_count(source_block_id) <= 0 || ref_count(destination_block_id) <= 0)
+    throw std::logic_error("block payload copy between free blocks");
+  const KVBlockPayloadPtrs src = get_block_payload_ptrs(source_block_id);
+  const KVBlockPayloadPtrs dst = get_block_payload_ptrs(destination_block_id);
+  pbe_copy_op ops[4];
+  int n = 0;
+  auto add = [&](const void* s, void* d, size_t bytes) {
+    if (bytes) ops[n++] = {reinterpret_cast<uint64_t>(s), reinterpret_cast<uint64_t>(d), bytes};
+  };
+  add(src.key, dst.key, src.key_value_bytes);
+  add(src.value, dst.value, src.key_value_bytes);
+  add(src.key_scale, dst.key_scale, src.scale_bytes);
+  add(src.value_scale, dst.value_scale, src.scale_bytes);
+  if (device_ == DeviceType::kDeviceCPU) {
+    for (int i = 0; i < n; ++i)
+      std::memcpy(reinterpret_cast<void*>(ops[i].dst), reinterpret_cast<const void*>(ops[i].src), ops[i].bytes);
+  } else {
+    void* stream = group_ ? group_->stream() : nullptr;
+    if (pbe_copy_ops(ops, n, device_index_, stream) != PBE_OK ||
+        pbe_stream_synchronize(device_index_, stream) != PBE_OK)
+      throw std::runtime_error(std::string("block payload copy failed: ") + pbe_last_error());
+  }
+  payload_copy_bytes_ += 2 * src.key_value_bytes + 2 * src.scale_bytes;
+}
+
 int32_t BlockAllocator::num_free_blocks() const {
+  if (!group_) return static_cast<int32_t>(free_queue_.size());
   group_->collect();
   return group_->free_blocks(layer_);
 }
 
-int32_t BlockAllocator::num_total_blocks() const { return group_->capacity(); }
-size_t BlockAllocator::shared_leased_bytes() const { return group_->leased_bytes(); }
-size_t BlockAllocator::shared_arena_bytes() const { return group_->arena_bytes(); }
-uint64_t BlockAllocator::shared_arena_epoch() const { return group_->arena_epoch(); }
+int32_t BlockAllocator::num_total_blocks() const { return group_ ? group_->capacity() : num_blocks_; }
+size_t BlockAllocator::shared_leased_bytes() const { return group_ ? group_->leased_bytes() : 0; }
+size_t BlockAllocator::shared_arena_bytes() const { return group_ ? group_->arena_bytes() : 0; }
+uint64_t BlockAllocator::shared_arena_epoch() const { return group_ ? group_->arena_epoch() : 0; }
 
 KVPoolView BlockAllocator::pool_view() const {
+  if (!group_)
+    return KVPoolView(key_pool_, value_pool_, key_scale_pool_, value_scale_pool_,
+                      key_value_bytes_per_block(), storage_spec_, device_);
   return KVPoolView(group_->key_base(layer_), group_->value_base(layer_), nullptr, nullptr,
                     key_value_bytes_per_block(), storage_spec_, DeviceType::kDeviceHIP);
 }

@@ -477,6 +477,9 @@ uint64_t SharedKVPageGroup::arena_epoch() const { return impl_->arena->epoch(); 
 uint64_t SharedKVPageGroup::half_bytes() const { return impl_->half; }
 uint64_t SharedKVPageGroup::page_bytes() const { return impl_->page; }
 int SharedKVPageGroup::layers() const { return impl_->layers; }
+int SharedKVPageGroup::device() const { return impl_->arena->device(); }
+void* SharedKVPageGroup::stream() const { return impl_->stream; }
+const pbe_arena_view& SharedKVPageGroup::arena_view() const { return impl_->arena->view(); }
 
 int SharedKVPageGroup::capacity() const {
   return static_cast<int>(std::min<uint64_t>(INT32_MAX, impl_->arena->hard_limit() / impl_->page));

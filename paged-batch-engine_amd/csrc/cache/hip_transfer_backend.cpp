@@ -1,10 +1,26 @@
-// HIP TransferBackend: the contract of CudaTransferBackend
-// (infMain/source/cache/cuda_transfer_backend.cpp:19-128) with the per-op
-// cudaMemcpyAsync loop replaced by one op-list kernel launch per submission.
-// All device work goes through the C ABI in pbe_handoff.h.
+// HIP TransferBackend for the contract of infMain/include/cache/page_migration.h:13-27.
+//
+// Design: every submission is ONE gfx950 op-list kernel (pbe_copy_ops) on the
+// backend's single in-order stream, followed by one completion event. A copy
+// kernel already spreads over every CU, so parallel streams would only contend
+// for HBM; one stream makes completion monotone, which lets poll() settle
+// every earlier launch at once. Launches live in a fixed table of `slots`
+// records (the in-flight limit), found by MigrationId through a hash index.
+//
+// A record moves kQueued -> kDone (event observed) or kQueued -> kBroken (a
+// HIP call failed after work may have been queued). Outcomes:
+//   kSucceeded   event observed on a healthy record;
+//   kFailedSafe  nothing was queued (endpoint check, no free record, the ABI
+//                rejected the op list), or a broken record whose stream has
+//                since drained, so no write of it can still land;
+//   kUnknown     a broken record not yet drained, an unknown id, or a
+//                duplicate id: the caller must quarantine.
+// release() of a record whose completion is not established terminates the
+// process: the copy may still write memory the caller would reuse.
 #include <exception>
 #include <stdexcept>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "cache/page_migration.h"
@@ -13,115 +29,127 @@
 namespace cache {
 namespace {
 
-class HipTransferBackend final : public TransferBackend {
+class HipMigrationQueue final : public TransferBackend {
  public:
-  HipTransferBackend(size_t slots, int device, void* dependency)
-      : device_(device), dependency_(dependency), slots_(slots) {
-    if (slots == 0) throw std::invalid_argument("HIP migration needs at least one slot");
-    if (device_ < 0) device_ = 0;
-    for (auto& slot : slots_) {
-      if (pbe_stream_create(device_, &slot.stream) != PBE_OK ||
-          pbe_event_create(device_, 0, &slot.fence) != PBE_OK) {
-        const std::string why = pbe_last_error();
-        destroy();
-        throw std::runtime_error("HIP migration stream/event allocation failed: " + why);
-      }
+  HipMigrationQueue(size_t capacity, int device, void* dependency)
+      : device_(device < 0 ? 0 : device), dependency_(dependency), launches_(capacity) {
+    if (capacity == 0) throw std::invalid_argument("HIP migration needs at least one slot");
+    bool ok = pbe_stream_create(device_, &stream_) == PBE_OK;
+    for (auto& l : launches_) ok = ok && pbe_event_create(device_, 0, &l.done) == PBE_OK;
+    if (!ok) {
+      const std::string why = pbe_last_error();
+      teardown();
+      throw std::runtime_error("HIP migration stream/event allocation failed: " + why);
     }
+    by_id_.reserve(capacity);
   }
 
-  ~HipTransferBackend() override {
-    for (auto& slot : slots_)
-      if (slot.id && pbe_stream_synchronize(device_, slot.stream) != PBE_OK) std::terminate();
-    destroy();
+  ~HipMigrationQueue() override {
+    // Queued copies still own their destinations: wait for the stream, and
+    // if even that cannot be established the process must not continue.
+    if (!by_id_.empty() && pbe_stream_synchronize(device_, stream_) != PBE_OK) std::terminate();
+    teardown();
   }
 
-  bool supports(base::DeviceType device) const override {
-    return device == base::DeviceType::kDeviceHIP;
-  }
+  bool supports(base::DeviceType device) const override { return device == base::DeviceType::kDeviceHIP; }
 
   BackendResult submit(MigrationId id, TransferDirection direction,
                        const BoundTransfer& transfer) noexcept override {
-    if (find(id)) return BackendResult::kUnknown;
+    if (by_id_.count(id)) return BackendResult::kUnknown;
     std::vector<pbe_copy_op> ops;
+    if (!collect_ops(direction, transfer, &ops)) return BackendResult::kFailedSafe;
+    Launch* l = idle_launch();
+    if (!l) return BackendResult::kFailedSafe;
+    if (dependency_ && pbe_stream_wait_raw_event(device_, stream_, dependency_) != PBE_OK)
+      return BackendResult::kFailedSafe;  // a failed wait queues nothing
+    const int rc = pbe_copy_ops(ops.data(), static_cast<int64_t>(ops.size()), device_, stream_);
+    if (rc == PBE_ERR_INVALID) return BackendResult::kFailedSafe;  // rejected on the host
     try {
-      ops.reserve(transfer.operations().size());
+      by_id_.emplace(id, static_cast<size_t>(l - launches_.data()));
     } catch (...) {
-      return BackendResult::kFailedSafe;
+      // The copy is queued but cannot be tracked: wait for it here.
+      return pbe_stream_synchronize(device_, stream_) == PBE_OK && rc == PBE_OK ? BackendResult::kFailedSafe
+                                                                                : BackendResult::kUnknown;
     }
-    // Validate every physical endpoint before queueing anything.
-    for (const auto& op : transfer.operations()) {
-      if (op.bytes == 0 || !op.source || !op.destination) return BackendResult::kFailedSafe;
-      const bool src_gpu = direction != TransferDirection::kToGpu;
-      const bool dst_gpu = direction != TransferDirection::kToHost;
-      if (!endpoint_ok(op.source, op.bytes, src_gpu) || !endpoint_ok(op.destination, op.bytes, dst_gpu))
-        return BackendResult::kFailedSafe;
-      ops.push_back({reinterpret_cast<uint64_t>(op.source), reinterpret_cast<uint64_t>(op.destination),
-                     op.bytes});
-    }
-    Slot* slot = nullptr;
-    for (auto& candidate : slots_)
-      if (!candidate.id) {
-        slot = &candidate;
-        break;
-      }
-    if (!slot) return BackendResult::kFailedSafe;
-    slot->id = id;
-    slot->failed = false;
-    slot->safe = false;
-    if (dependency_ && pbe_stream_wait_raw_event(device_, slot->stream, dependency_) != PBE_OK) {
-      slot->failed = true;
-      return BackendResult::kUnknown;
-    }
-    const int rc = pbe_copy_ops(ops.data(), static_cast<int64_t>(ops.size()), device_, slot->stream);
-    if (rc == PBE_ERR_INVALID) {  // rejected on the host: nothing was queued by this call
-      slot->id = 0;
-      return BackendResult::kFailedSafe;
-    }
-    if (rc != PBE_OK) {
-      slot->failed = true;
-      return BackendResult::kUnknown;
-    }
-    if (pbe_event_record(slot->fence, slot->stream) != PBE_OK) {
-      slot->failed = true;
-      return BackendResult::kUnknown;
-    }
-    return BackendResult::kPending;
+    l->id = id;
+    l->seq = ++issued_;
+    l->state = (rc == PBE_OK && pbe_event_record(l->done, stream_) == PBE_OK) ? State::kQueued : State::kBroken;
+    return l->state == State::kQueued ? BackendResult::kPending : BackendResult::kUnknown;
   }
 
   BackendResult poll(MigrationId id) noexcept override {
-    Slot* slot = find(id);
-    if (!slot || slot->failed) return BackendResult::kUnknown;
-    const int rc = pbe_event_query(slot->fence);
-    if (rc == PBE_NOT_READY) return BackendResult::kPending;
-    if (rc != PBE_OK) {
-      slot->failed = true;
-      return BackendResult::kUnknown;
-    }
-    slot->safe = true;
-    return BackendResult::kSucceeded;
+    Launch* l = lookup(id);
+    if (!l) return BackendResult::kUnknown;
+    if (l->state == State::kQueued) observe(l);
+    return outcome(*l);
   }
 
   BackendResult drain(MigrationId id) noexcept override {
-    Slot* slot = find(id);
-    if (!slot || pbe_stream_synchronize(device_, slot->stream) != PBE_OK) return BackendResult::kUnknown;
-    slot->safe = true;
-    return slot->failed ? BackendResult::kFailedSafe : BackendResult::kSucceeded;
+    Launch* l = lookup(id);
+    if (!l) return BackendResult::kUnknown;
+    if (l->state == State::kQueued && pbe_event_synchronize(l->done) == PBE_OK) {
+      settle_through(l->seq);
+    } else if (l->state != State::kDone && l->state != State::kDrained) {
+      // Broken, or its event failed: only an idle stream proves no write of
+      // this launch is still in flight.
+      if (pbe_stream_synchronize(device_, stream_) != PBE_OK) {
+        l->state = State::kBroken;
+        return BackendResult::kUnknown;
+      }
+      settle_through(issued_);
+      if (l->state != State::kDone) l->state = State::kDrained;
+    }
+    return outcome(*l);
   }
 
   void release(MigrationId id) noexcept override {
-    Slot* slot = find(id);
-    if (!slot) return;  // rejected before any stream submission
-    if (!slot->safe) std::terminate();
-    slot->id = 0;
+    auto it = by_id_.find(id);
+    if (it == by_id_.end()) return;  // never queued
+    Launch& l = launches_[it->second];
+    if (l.state != State::kDone && l.state != State::kDrained) std::terminate();
+    l.state = State::kIdle;
+    l.id = 0;
+    by_id_.erase(it);
   }
 
  private:
-  struct Slot {
+  enum class State { kIdle, kQueued, kDone, kBroken, kDrained };
+  struct Launch {
     MigrationId id = 0;
-    void* stream = nullptr;
-    pbe_event* fence = nullptr;
-    bool failed = false, safe = false;
+    uint64_t seq = 0;  // submission order on the stream
+    State state = State::kIdle;
+    pbe_event* done = nullptr;
   };
+
+  static BackendResult outcome(const Launch& l) {
+    switch (l.state) {
+      case State::kQueued: return BackendResult::kPending;
+      case State::kDone: return BackendResult::kSucceeded;
+      case State::kDrained: return BackendResult::kFailedSafe;
+      default: return BackendResult::kUnknown;
+    }
+  }
+
+  // Every endpoint checked before anything is queued: the GPU side must be
+  // device memory of this backend's GPU, the host side pinned host memory.
+  bool collect_ops(TransferDirection direction, const BoundTransfer& transfer,
+                   std::vector<pbe_copy_op>* ops) const noexcept {
+    const bool src_gpu = direction != TransferDirection::kToGpu;
+    const bool dst_gpu = direction != TransferDirection::kToHost;
+    try {
+      ops->reserve(transfer.operations().size());
+      for (const auto& op : transfer.operations()) {
+        if (op.bytes == 0 || !op.source || !op.destination) return false;
+        if (!endpoint_ok(op.source, op.bytes, src_gpu) || !endpoint_ok(op.destination, op.bytes, dst_gpu))
+          return false;
+        ops->push_back({reinterpret_cast<uint64_t>(op.source), reinterpret_cast<uint64_t>(op.destination),
+                        op.bytes});
+      }
+    } catch (...) {
+      return false;
+    }
+    return true;
+  }
 
   bool endpoint_ok(const void* p, size_t bytes, bool want_device) const noexcept {
     int kind = PBE_PTR_UNKNOWN, dev = -1;
@@ -129,31 +157,48 @@ class HipTransferBackend final : public TransferBackend {
     return want_device ? (kind == PBE_PTR_DEVICE && dev == device_) : kind == PBE_PTR_PINNED_HOST;
   }
 
-  Slot* find(MigrationId id) noexcept {
-    for (auto& slot : slots_)
-      if (slot.id == id) return &slot;
+  Launch* idle_launch() noexcept {
+    for (auto& l : launches_)
+      if (l.state == State::kIdle) return &l;
     return nullptr;
   }
 
-  void destroy() noexcept {
-    for (auto& slot : slots_) {
-      if (slot.fence) pbe_event_destroy(slot.fence);
-      if (slot.stream) pbe_stream_destroy(device_, slot.stream);
-      slot.fence = nullptr;
-      slot.stream = nullptr;
-    }
+  Launch* lookup(MigrationId id) noexcept {
+    auto it = by_id_.find(id);
+    return it == by_id_.end() ? nullptr : &launches_[it->second];
+  }
+
+  // Queries one launch's event; on completion everything queued before it on
+  // the stream has completed too.
+  void observe(Launch* l) noexcept {
+    const int rc = pbe_event_query(l->done);
+    if (rc == PBE_OK) settle_through(l->seq);
+    else if (rc != PBE_NOT_READY) l->state = State::kBroken;
+  }
+
+  void settle_through(uint64_t seq) noexcept {
+    for (auto& l : launches_)
+      if (l.state == State::kQueued && l.seq <= seq) l.state = State::kDone;
+  }
+
+  void teardown() noexcept {
+    for (auto& l : launches_)
+      if (l.done) pbe_event_destroy(l.done), l.done = nullptr;
+    if (stream_) pbe_stream_destroy(device_, stream_), stream_ = nullptr;
   }
 
   int device_;
   void* dependency_;
-  std::vector<Slot> slots_;
+  void* stream_ = nullptr;
+  uint64_t issued_ = 0;
+  std::vector<Launch> launches_;
+  std::unordered_map<MigrationId, size_t> by_id_;
 };
 
 }  // namespace
 
-std::unique_ptr<TransferBackend> MakeHipTransferBackend(size_t slots, int device,
-                                                       void* dependency_event) {
-  return std::make_unique<HipTransferBackend>(slots, device, dependency_event);
+std::unique_ptr<TransferBackend> MakeHipTransferBackend(size_t slots, int device, void* dependency_event) {
+  return std::make_unique<HipMigrationQueue>(slots, device, dependency_event);
 }
 
 }  // namespace cache

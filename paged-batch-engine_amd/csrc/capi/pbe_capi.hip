@@ -249,6 +249,7 @@ struct pbe_arena {
 struct pbe_event {
   int device = 0;
   bool imported = false;
+  bool interprocess = false;
   hipEvent_t event = nullptr;
 };
 
@@ -282,6 +283,12 @@ int pbe_device_uuid(int device, uint8_t out[16]) {
   hipUUID uuid;
   PBE_HIP(hipDeviceGetUuid(&uuid, device));
   std::memcpy(out, uuid.bytes, 16);
+  return PBE_OK;
+}
+
+int pbe_current_device(int* device) {
+  if (!device) return fail(PBE_ERR_INVALID, "null output");
+  PBE_HIP(hipGetDevice(device));
   return PBE_OK;
 }
 
@@ -408,13 +415,39 @@ int pbe_arena_destroy(pbe_arena* a) {
 }
 
 // ---------------------------------------------------------------- events
+namespace {
+// Whether this runtime can record hipEventInterprocess events. ROCm 7.2 on
+// MI355X creates them but rejects hipEventRecord with hipErrorInvalidValue, so
+// they cannot carry a completion; the answer is probed once per device.
+bool interprocess_events_work(int device) {
+  static std::mutex mu;
+  static int known[64] = {};  // 0 unknown, 1 yes, -1 no
+  std::lock_guard<std::mutex> lock(mu);
+  int& k = known[device & 63];
+  if (k == 0) {
+    hipEvent_t e = nullptr;
+    bool ok = hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventInterprocess) == hipSuccess;
+    ok = ok && hipEventRecord(e, nullptr) == hipSuccess && hipEventSynchronize(e) == hipSuccess;
+    if (e) (void)hipEventDestroy(e);
+    (void)hipGetLastError();
+    k = ok ? 1 : -1;
+  }
+  return k > 0;
+}
+}  // namespace
+
 int pbe_event_create(int device, int interprocess, pbe_event** out) {
   if (!out) return fail(PBE_ERR_INVALID, "null output");
   *out = nullptr;
   PBE_DEVICE_SCOPE(device);
+  if (interprocess && !interprocess_events_work(device))
+    return fail(PBE_ERR_UNSUPPORTED,
+                "this HIP runtime cannot record interprocess events; use pbe_signal_* for "
+                "cross-process completion");
   pbe_event* ev = new (std::nothrow) pbe_event;
   if (!ev) return fail(PBE_ERR_NOMEM, "event object");
   ev->device = device;
+  ev->interprocess = interprocess != 0;
   const unsigned flags =
       hipEventDisableTiming | (interprocess ? (unsigned)hipEventInterprocess : 0u);
   const hipError_t e = hipEventCreateWithFlags(&ev->event, flags);
@@ -428,6 +461,7 @@ int pbe_event_create(int device, int interprocess, pbe_event** out) {
 
 int pbe_event_export(const pbe_event* ev, uint8_t out[PBE_IPC_HANDLE_BYTES]) {
   if (!ev || !out) return fail(PBE_ERR_INVALID, "null argument");
+  if (!ev->interprocess) return fail(PBE_ERR_INVALID, "only interprocess events are exported");
   static_assert(sizeof(hipIpcEventHandle_t) <= PBE_IPC_HANDLE_BYTES, "event handle size");
   PBE_DEVICE_SCOPE(ev->device);
   hipIpcEventHandle_t h;
@@ -441,10 +475,15 @@ int pbe_event_import(const uint8_t handle[PBE_IPC_HANDLE_BYTES], int device, pbe
   if (!handle || !out) return fail(PBE_ERR_INVALID, "null argument");
   *out = nullptr;
   PBE_DEVICE_SCOPE(device);
+  if (!interprocess_events_work(device))
+    return fail(PBE_ERR_UNSUPPORTED,
+                "this HIP runtime cannot record interprocess events; use pbe_signal_* for "
+                "cross-process completion");
   pbe_event* ev = new (std::nothrow) pbe_event;
   if (!ev) return fail(PBE_ERR_NOMEM, "event object");
   ev->device = device;
   ev->imported = true;
+  ev->interprocess = true;
   hipIpcEventHandle_t h;
   std::memcpy(&h, handle, sizeof(h));
   const hipError_t e = hipIpcOpenEventHandle(&ev->event, h);

@@ -8,10 +8,10 @@ namespace {
 using base::error::InvalidArgument;
 }
 
-DecodeKVReservationManager::DecodeKVReservationManager(base::SharedKVPageGroup* pages,
+DecodeKVReservationManager::DecodeKVReservationManager(base::KVCacheManager* kv_manager,
                                                        KVPoolDescriptor dst_pool)
-    : pages_(pages), dst_pool_(std::move(dst_pool)) {
-  if (pages_ == nullptr) throw std::invalid_argument("decode kv reservation needs a page group");
+    : kv_manager_(kv_manager), dst_pool_(std::move(dst_pool)) {
+  if (kv_manager_ == nullptr) throw std::invalid_argument("decode kv reservation needs a KV cache manager");
 }
 
 base::Status DecodeKVReservationManager::validate_request(const DecodeKVReservationRequest& r) const {
@@ -22,10 +22,14 @@ base::Status DecodeKVReservationManager::validate_request(const DecodeKVReservat
     return InvalidArgument("decode kv reservation computed_tokens is invalid");
   if (!r.src_pool.compatible_with(dst_pool_))
     return InvalidArgument("decode kv reservation source/destination pools are incompatible");
-  if (dst_pool_.layer_num != pages_->layers())
+  if (dst_pool_.layer_num != kv_manager_->num_layers())
     return InvalidArgument("decode kv reservation dst layer_num mismatch");
-  if (dst_pool_.block_size <= 0 ||
-      static_cast<uint64_t>(dst_pool_.bytes_per_block_per_layer()) != 2 * pages_->half_bytes())
+  // The reference compares block sizes only; the per-layer payload bytes are
+  // checked as well so a pool whose head geometry differs from the manager's
+  // allocators cannot be mapped.
+  if (dst_pool_.block_size != kv_manager_->block_size() ||
+      static_cast<uint64_t>(dst_pool_.bytes_per_block_per_layer()) !=
+          2 * kv_manager_->allocator(0).key_value_bytes_per_block())
     return InvalidArgument("decode kv reservation dst block_size mismatch");
   if (static_cast<int32_t>(r.src_block_ids_per_layer.size()) != dst_pool_.layer_num)
     return InvalidArgument("decode kv reservation source layer count mismatch");
@@ -53,20 +57,23 @@ base::Status DecodeKVReservationManager::reserve(const DecodeKVReservationReques
 
   const int32_t blocks = required_blocks(request.computed_tokens);
   const int32_t layers = dst_pool_.layer_num;
+  const base::RequestId id = kv_manager_->register_request();
+  if (!kv_manager_->append_slots(id, request.computed_tokens)) {
+    kv_manager_->free_request(id);
+    return base::error::InternalError("decode kv reservation failed to allocate dst KV blocks");
+  }
   DecodeKVReservation held;
-  held.decode_request_id = next_request_id_++;
+  held.decode_request_id = id;
   held.reserved_tokens = request.computed_tokens;
   held.first_token = request.first_token;
-  held.dst_block_ids_per_layer.assign(layers, {});
-  // Page by page: layer 0 picks the page, layers 1..L-1 take its reservation.
-  for (int32_t b = 0; b < blocks; ++b) {
-    const int id = pages_->allocate(0);
-    if (id < 0) {
+  held.dst_block_ids_per_layer.resize(layers);
+  for (int32_t l = 0; l < layers; ++l) {
+    const std::vector<int32_t>& got = kv_manager_->get_block_ids(id, l);
+    if (static_cast<int32_t>(got.size()) < blocks) {
       release(&held);
-      return base::error::InternalError("decode kv reservation failed to allocate dst KV blocks");
+      return base::error::InternalError("decode kv reservation dst block count is insufficient");
     }
-    held.dst_block_ids_per_layer[0].push_back(id);
-    for (int32_t l = 1; l < layers; ++l) held.dst_block_ids_per_layer[l].push_back(pages_->allocate(l));
+    held.dst_block_ids_per_layer[l].assign(got.begin(), got.begin() + blocks);
   }
 
   manifest->client_request_id = request.client_request_id;
@@ -97,13 +104,8 @@ base::Status DecodeKVReservationManager::reserve(const DecodeKVReservationReques
 
 void DecodeKVReservationManager::release(DecodeKVReservation* reservation) {
   if (reservation == nullptr || !reservation->valid()) return;
-  auto& ids = reservation->dst_block_ids_per_layer;
-  // Retire the later layers first so layer 0's retire finds nothing to roll
-  // back, then layer 0 (which fences the page once all layers are retired).
-  for (size_t l = ids.size(); l-- > 1;)
-    for (int id : ids[l]) pages_->retire(static_cast<int>(l), id);
-  if (!ids.empty())
-    for (int id : ids[0]) pages_->retire(0, id);
+  if (kv_manager_->is_valid_request(reservation->decode_request_id))
+    kv_manager_->free_request(reservation->decode_request_id);
   *reservation = {};
 }
 

@@ -1,15 +1,20 @@
-// Shared-arena mode of the reference's block allocator
-// (infMain/include/base/block_allocator.h:15-230, block_allocator.cpp:139-401):
-// the per-layer view of a SharedKVPageGroup that copy_shared_kv and the decode
-// runtime use. Block ids are page-major (byte offset / half), so layer l's K
-// plane of block b is half-plane b + 2l of the arena and its V plane b + 2l + 1.
-// Device pointers are plain pointers (no tensor type); the local-pool and
-// external-pool modes of the reference are model-runtime code outside this build.
+// The reference's block allocator (infMain/include/base/block_allocator.h:113-240,
+// block_allocator.cpp:17-428) in two of its modes:
+//  - shared-arena mode: the per-layer view of a SharedKVPageGroup that
+//    copy_shared_kv and the decode runtime use. Block ids are page-major (byte
+//    offset / half), so layer l's K plane of block b is half-plane b + 2l of
+//    the arena and its V plane b + 2l + 1;
+//  - local-pool mode: one layer's own [num_blocks][block] K and V pools (and,
+//    for FP8 storage, [num_blocks][block_size * heads] fp32 K and V scale
+//    pools) with a FIFO free queue, on the GPU or in host memory.
+// Device pointers are plain pointers (no tensor type). The external-pool
+// binding of the reference belongs to its data service, outside this build.
 #ifndef PBE_INCLUDE_BASE_BLOCK_ALLOCATOR_H_
 #define PBE_INCLUDE_BASE_BLOCK_ALLOCATOR_H_
 
 #include <cstddef>
 #include <cstdint>
+#include <deque>
 #include <memory>
 #include <utility>
 #include <vector>
@@ -68,6 +73,16 @@ class KVPoolView {
 
 class BlockAllocator {
  public:
+  // Local-pool mode (block_allocator.cpp:17-84): kDeviceHIP pools live on the
+  // calling thread's current GPU, kDeviceCPU pools in host memory. Throws
+  // std::invalid_argument for a bad geometry or an invalid storage spec and
+  // std::runtime_error when the pools cannot be allocated.
+  BlockAllocator(int32_t num_blocks, int32_t block_size, int32_t num_kv_heads, int32_t head_size,
+                 const KVCacheStorageSpec& storage_spec, DeviceType device);
+  BlockAllocator(int32_t num_blocks, int32_t block_size, int32_t num_kv_heads, int32_t head_size,
+                 DataType dtype, DeviceType device,
+                 BlockStorageMode storage_mode = BlockStorageMode::kPlain);
+  ~BlockAllocator();
   // Shared-arena mode (block_allocator.cpp:139-163): BF16 plain storage, one
   // allocator per layer over a page group whose half-plane equals
   // block_size * num_kv_heads * head_size * 2 bytes. Throws
@@ -89,13 +104,25 @@ class BlockAllocator {
 
   std::pair<void*, void*> get_block_ptrs(int32_t block_id) const;
   KVBlockPayloadPtrs get_block_payload_ptrs(int32_t block_id) const;
+  // Bitwise copy of one block's K and V payload (and scales) onto another
+  // block of this layer, both allocated (block_allocator.cpp:403-428). On the
+  // GPU it is one copy-kernel launch, ordered on the page group's stream in
+  // shared-arena mode, and returns once the copy has completed. Throws
+  // std::logic_error for equal or free blocks, std::runtime_error when the
+  // device copy fails.
+  void copy_block_payload(int32_t source_block_id, int32_t destination_block_id) const;
+  uint64_t payload_copy_bytes() const { return payload_copy_bytes_; }
 
   int32_t num_free_blocks() const;
   int32_t num_total_blocks() const;
-  bool uses_shared_arena() const { return true; }
+  bool uses_shared_arena() const { return group_ != nullptr; }
   size_t shared_leased_bytes() const;
   size_t shared_arena_bytes() const;
   uint64_t shared_arena_epoch() const;
+  // Shared-arena mode: this process's mapping of the arena and its GPU
+  // (nullptr / -1 in local-pool mode).
+  const pbe_arena_view* shared_arena_view() const { return group_ ? &group_->arena_view() : nullptr; }
+  int device_index() const { return device_index_; }
 
   int32_t block_size() const { return block_size_; }
   int32_t num_kv_heads() const { return num_kv_heads_; }
@@ -104,20 +131,31 @@ class BlockAllocator {
   const KVCacheStorageSpec& storage_spec() const { return storage_spec_; }
   BlockStorageMode storage_mode() const { return storage_spec_.storage_mode; }
   bool uses_fp8_storage() const { return storage_spec_.uses_fp8_storage(); }
-  DeviceType device_type() const { return DeviceType::kDeviceHIP; }
+  DeviceType device_type() const { return device_; }
   size_t key_value_bytes_per_block() const;
-  size_t scale_bytes_per_block() const { return 0; }
+  size_t scale_bytes_per_block() const;
   KVPoolView pool_view() const;
 
  private:
   void check_id(int32_t block_id) const;
-  std::shared_ptr<SharedKVPageGroup> group_;
-  int32_t block_size_, num_kv_heads_, head_size_, layer_;
+  std::shared_ptr<SharedKVPageGroup> group_;  // shared-arena mode only
+  int32_t block_size_, num_kv_heads_, head_size_, layer_ = 0;
   int32_t num_blocks_ = 0;
   uint64_t pool_id_ = 0;
+  DeviceType device_ = DeviceType::kDeviceHIP;
+  int device_index_ = -1;
   KVCacheStorageSpec storage_spec_;
   std::vector<int32_t> ref_counts_;
   std::vector<uint64_t> generations_;
+  // Local-pool mode: [K pool][V pool][K scales][V scales] in one allocation.
+  pbe_arena* device_pools_ = nullptr;
+  std::vector<uint8_t> host_pools_;
+  uint8_t* key_pool_ = nullptr;
+  uint8_t* value_pool_ = nullptr;
+  uint8_t* key_scale_pool_ = nullptr;
+  uint8_t* value_scale_pool_ = nullptr;
+  std::deque<int32_t> free_queue_;
+  mutable uint64_t payload_copy_bytes_ = 0;
 };
 
 }  // namespace base

@@ -168,6 +168,12 @@ class SharedKVPageGroup {
   uint64_t half_bytes() const;
   uint64_t page_bytes() const;
   int layers() const;
+  // GPU of the arena mapping (-1 for a metadata-only group) and the stream
+  // every user of the pages runs on.
+  int device() const;
+  void* stream() const;
+  // This process's mapping of the whole arena.
+  const pbe_arena_view& arena_view() const;
 
  private:
   struct Impl;

@@ -1,9 +1,10 @@
 // Decode-side reservation of destination pages for a handoff and the
 // manifest that maps them (infMain/include/serving/decode_kv_reservation.h:13-55).
-// The reference reserves through KVCacheManager::append_slots, which for a
+// Destination pages come from KVCacheManager::append_slots, which for a
 // shared arena lands in SharedKVPageGroup::allocate for every layer
 // (kv_cache_manager.cpp:644-659 -> block_allocator.cpp:205 ->
-// shared_kv_arena.cpp:115). This build reserves from the page group directly.
+// shared_kv_arena.cpp:115); the reservation is a registered decode request
+// whose first ceil(computed/block_size) pages the manifest maps.
 #ifndef PBE_INCLUDE_SERVING_DECODE_KV_RESERVATION_H_
 #define PBE_INCLUDE_SERVING_DECODE_KV_RESERVATION_H_
 
@@ -11,7 +12,7 @@
 #include <vector>
 
 #include "base/base.h"
-#include "base/shared_kv_arena.h"
+#include "base/kv_cache_manager.h"
 #include "serving/pd_handoff.h"
 
 namespace serving {
@@ -27,7 +28,7 @@ struct DecodeKVReservationRequest {
 };
 
 struct DecodeKVReservation {
-  int64_t decode_request_id = -1;
+  base::RequestId decode_request_id = -1;
   int32_t reserved_tokens = 0;
   int32_t first_token = -1;
   std::vector<std::vector<int32_t>> dst_block_ids_per_layer;
@@ -38,17 +39,19 @@ struct DecodeKVReservation {
 class DecodeKVReservationManager {
  public:
   // dst_pool describes the decode pool; its layer count and block size must
-  // match the page group.
-  DecodeKVReservationManager(base::SharedKVPageGroup* pages, KVPoolDescriptor dst_pool);
+  // match the manager's. Throws std::invalid_argument for a null manager.
+  DecodeKVReservationManager(base::KVCacheManager* kv_manager, KVPoolDescriptor dst_pool);
 
-  // Validates the request (decode_kv_reservation.cpp:14-47), reserves
-  // ceil(computed_tokens / block_size) pages for every layer and fills the
-  // manifest (src ids truncated to that count). On failure nothing stays
-  // reserved and both outputs are reset.
+  // Validates the request (decode_kv_reservation.cpp:14-47), registers a
+  // decode request holding computed_tokens slots (ceil(computed_tokens /
+  // block_size) pages in every layer) and fills the manifest (src ids
+  // truncated to that count). On failure nothing stays reserved and both
+  // outputs are reset. The caller commits the tokens with
+  // KVCacheManager::commit_kv once the copy has completed.
   base::Status reserve(const DecodeKVReservationRequest& request, DecodeKVReservation* reservation,
                        KVBlockManifest* manifest);
-  // Retires every reserved layer of every page (the pages return to the free
-  // list once the group's stream passes its completion fence).
+  // Frees the decode request (its pages return to the free list once the
+  // page group's stream passes their completion fence).
   void release(DecodeKVReservation* reservation);
 
   const KVPoolDescriptor& dst_pool() const { return dst_pool_; }
@@ -57,9 +60,8 @@ class DecodeKVReservationManager {
   base::Status validate_request(const DecodeKVReservationRequest& request) const;
   int32_t required_blocks(int32_t tokens) const;
 
-  base::SharedKVPageGroup* pages_ = nullptr;
+  base::KVCacheManager* kv_manager_ = nullptr;
   KVPoolDescriptor dst_pool_;
-  int64_t next_request_id_ = 0;
 };
 
 }  // namespace serving

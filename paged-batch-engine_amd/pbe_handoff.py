@@ -69,6 +69,7 @@ _SIGNATURES = [
     ("pbe_last_error", C.c_char_p, []),
     ("pbe_version", C.c_char_p, []),
     ("pbe_device_uuid", C.c_int, [C.c_int, C.POINTER(C.c_uint8)]),
+    ("pbe_current_device", C.c_int, [C.POINTER(C.c_int)]),
     ("pbe_arena_create", C.c_int, [C.c_int, C.c_uint64, C.c_uint64, C.c_uint64, C.POINTER(_P)]),
     ("pbe_arena_export", C.c_int, [_P, C.POINTER(ArenaIpc)]),
     ("pbe_arena_import", C.c_int, [C.POINTER(ArenaIpc), C.c_int, C.POINTER(_P)]),
@@ -369,7 +370,7 @@ class Event:
         self.handle = handle
 
     @classmethod
-    def create(cls, device: int = 0, interprocess: bool = True):
+    def create(cls, device: int = 0, interprocess: bool = False):
         h = C.c_void_p()
         check(lib().pbe_event_create(device, int(interprocess), C.byref(h)))
         return cls(h.value)

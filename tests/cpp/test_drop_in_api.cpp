@@ -22,6 +22,7 @@
 #include "serving/pd_handoff.h"
 #include "serving/kv_page_wire.h"
 #include "base/block_allocator.h"
+#include "base/kv_cache_manager.h"
 
 using namespace cache;
 
@@ -699,13 +700,13 @@ struct Group {
   static constexpr uint64_t kHalf = 4096, kPage = 6 * 4096;
   std::shared_ptr<base::LocalChunkOwner> owner;
   std::shared_ptr<base::SharedKVArenaClient> client;
-  std::unique_ptr<base::SharedKVPageGroup> group;
+  std::shared_ptr<base::SharedKVPageGroup> group;
   Group(uint64_t arena_pages, uint64_t limit_bytes, uint64_t target = 3 * kPage) {
     owner = std::make_shared<base::LocalChunkOwner>(arena_pages * kPage, 9);
     owner->register_model("d", limit_bytes);
     client = std::make_shared<base::SharedKVArenaClient>(owner, fake_view(arena_pages * kPage), "d",
                                                          limit_bytes, -1);
-    group = std::make_unique<base::SharedKVPageGroup>(client, 3, kHalf, target, nullptr);
+    group = std::make_shared<base::SharedKVPageGroup>(client, 3, kHalf, target, nullptr);
   }
   int page_id(int n) const { return n * 6; }  // block id of the n-th page
 };
@@ -808,6 +809,15 @@ serving::KVPoolDescriptor pool3() {
   return {0, 3, 16, 2, 64, base::DataType::kDataTypeBf16, base::BlockStorageMode::kPlain};
 }
 
+// One shared-arena allocator per layer over the group, 16-token blocks of
+// 2 heads x 64 dims (half = 4 KiB), as the decode runtime builds them.
+std::unique_ptr<base::KVCacheManager> manager_over(const std::shared_ptr<base::SharedKVPageGroup>& g) {
+  std::vector<std::unique_ptr<base::BlockAllocator>> layers;
+  for (int l = 0; l < g->layers(); ++l)
+    layers.push_back(std::make_unique<base::BlockAllocator>(16, 2, 64, g, l));
+  return std::make_unique<base::KVCacheManager>(16, g->layers(), std::move(layers));
+}
+
 serving::DecodeKVReservationRequest request_for(int32_t computed, int32_t prompt, int32_t pages) {
   serving::DecodeKVReservationRequest r;
   r.client_request_id.value = "r";
@@ -825,7 +835,8 @@ serving::DecodeKVReservationRequest request_for(int32_t computed, int32_t prompt
 
 TEST_CASE("decode reservation: ceil(tokens/16) page-major pages and a valid manifest") {
   Group g(24, 24 * Group::kPage);
-  serving::DecodeKVReservationManager mgr(g.group.get(), pool3());
+  auto kv = manager_over(g.group);
+  serving::DecodeKVReservationManager mgr(kv.get(), pool3());
   serving::DecodeKVReservation res;
   serving::KVBlockManifest man;
   REQUIRE(mgr.reserve(request_for(41, 50, 4), &res, &man));
@@ -849,7 +860,8 @@ TEST_CASE("decode reservation: ceil(tokens/16) page-major pages and a valid mani
 
 TEST_CASE("decode reservation: invalid requests and exhaustion reserve nothing") {
   Group g(6, 3 * Group::kPage);
-  serving::DecodeKVReservationManager mgr(g.group.get(), pool3());
+  auto kv = manager_over(g.group);
+  serving::DecodeKVReservationManager mgr(kv.get(), pool3());
   serving::DecodeKVReservation res;
   serving::KVBlockManifest man;
   auto r = request_for(41, 50, 4);
@@ -1280,3 +1292,123 @@ TEST_CASE("block allocator: the pool view binds the planes without owning the al
 }
 
 MINITEST_MAIN()
+
+// ------------------------------------------------------------ KV cache manager
+
+TEST_CASE("kv cache manager: append_slots grows page tables by ceil((n+k)/16) - ceil(n/16)") {
+  Group g(24, 24 * Group::kPage);
+  auto kv = manager_over(g.group);
+  CHECK_EQ(kv->num_layers(), 3);
+  CHECK_EQ(kv->block_size(), 16);
+  const base::RequestId a = kv->register_request();
+  CHECK(kv->is_valid_request(a));
+  CHECK(kv->append_slots(a, 41));  // 3 pages
+  CHECK_EQ(kv->get_context_len(a), 41);
+  CHECK_EQ(kv->num_tokens_in_last_block(a), 9);
+  for (int l = 0; l < 3; ++l) CHECK(kv->get_block_ids(a, l) == (std::vector<int32_t>{0, 6, 12}));
+  CHECK(kv->append_slots(a, 7));  // 48 tokens: still 3 pages
+  CHECK_EQ(kv->get_block_ids(a, 0).size(), 3u);
+  CHECK_EQ(kv->num_tokens_in_last_block(a), 16);
+  CHECK(kv->append_slot(a));      // 49: a fourth page
+  CHECK(kv->get_block_ids(a, 2) == (std::vector<int32_t>{0, 6, 12, 18}));
+  CHECK(kv->get_slot(a, 1, 17) == std::make_pair(6, 1));
+  CHECK(kv->current_slot(a, 0) == std::make_pair(18, 0));
+  CHECK(!kv->append_slots(a, 0));
+  CHECK(!kv->append_slots(a, -3));
+  // each layer's K plane of block b is plane b + 2l of the page-major arena
+  const auto p0 = kv->allocator(0).get_block_payload_ptrs(6);
+  const auto p2 = kv->allocator(2).get_block_payload_ptrs(6);
+  CHECK_EQ(static_cast<char*>(p2.key) - static_cast<char*>(p0.key), 4 * 4096);
+  const base::RequestId b = kv->register_request();
+  CHECK(kv->append_slots(b, 16));
+  CHECK(kv->build_seq_lens({a, b}) == (std::vector<int32_t>{49, 16}));
+  const auto tables = kv->build_block_tables({a, b}, 1);
+  CHECK_EQ(tables.second, 4);
+  CHECK(tables.first == (std::vector<int32_t>{0, 6, 12, 18, 24, -1, -1, -1}));
+  CHECK(kv->build_slot_mapping({a, b}, 0) == (std::vector<int32_t>{18 * 16 + 0, 24 * 16 + 15}));
+  CHECK_EQ(kv->num_active_requests(), 2);
+  kv->free_request(a);
+  kv->free_request(b);
+  CHECK_EQ(kv->num_active_requests(), 0);
+  CHECK_EQ(g.owner->lease_count(), 0u);  // every Chunk back at the owner
+}
+
+TEST_CASE("kv cache manager: commit_kv only moves forward within the appended slots") {
+  Group g(24, 24 * Group::kPage);
+  auto kv = manager_over(g.group);
+  const base::RequestId a = kv->register_request();
+  CHECK(kv->append_slots(a, 41));
+  CHECK_EQ(kv->kv_committed_tokens(a), 0);
+  CHECK(!kv->commit_kv(a, 42));
+  CHECK(kv->commit_kv(a, 41));
+  CHECK_EQ(kv->kv_committed_tokens(a), 41);
+  CHECK(!kv->commit_kv(a, 40));
+  CHECK(kv->commit_kv(a, 41));
+  kv->free_request(a);
+  CHECK(!kv->commit_kv(a, 41));  // stale id
+}
+
+TEST_CASE("kv cache manager: stale ids never alias a reused slot") {
+  Group g(24, 24 * Group::kPage);
+  auto kv = manager_over(g.group);
+  const base::RequestId a = kv->register_request();
+  kv->free_request(a);
+  const base::RequestId b = kv->register_request();  // same slot, next generation
+  CHECK(a != b);
+  CHECK(!kv->is_valid_request(a));
+  CHECK(kv->is_valid_request(b));
+  CHECK_THROWS_AS(kv->free_request(a), std::invalid_argument);
+  CHECK_THROWS_AS(kv->get_block_ids(a, 0), std::invalid_argument);
+  CHECK_THROWS_AS(kv->get_block_ids(b, 3), std::out_of_range);
+  CHECK(!kv->is_valid_request(-1));
+  CHECK(!kv->is_valid_request(12345));
+  kv->free_request(b);
+}
+
+TEST_CASE("kv cache manager: exhaustion holds nothing new") {
+  Group g(6, 3 * Group::kPage);  // limit: 3 pages
+  auto kv = manager_over(g.group);
+  const base::RequestId a = kv->register_request();
+  CHECK(kv->append_slots(a, 32));  // 2 pages
+  CHECK(!kv->append_slots(a, 33));  // would need 3 more
+  CHECK_EQ(kv->get_context_len(a), 32);
+  for (int l = 0; l < 3; ++l) CHECK_EQ(kv->get_block_ids(a, l).size(), 2u);
+  CHECK(kv->append_slots(a, 16));  // the third page still fits
+  kv->free_request(a);
+  CHECK_EQ(g.owner->lease_count(), 0u);
+  std::vector<std::unique_ptr<base::BlockAllocator>> none;
+  CHECK_THROWS_AS(base::KVCacheManager(16, 3, std::move(none)), std::invalid_argument);
+}
+
+TEST_CASE("block allocator: local pools, FIFO reuse and payload copy with scales (host)") {
+  base::BlockAllocator plain(4, 16, 2, 8, base::DataType::kDataTypeBf16, base::DeviceType::kDeviceCPU);
+  CHECK(!plain.uses_shared_arena());
+  CHECK_EQ(plain.num_total_blocks(), 4);
+  CHECK_EQ(plain.key_value_bytes_per_block(), 16u * 2 * 8 * 2);
+  CHECK_EQ(plain.scale_bytes_per_block(), 0u);
+  const int a = plain.allocate(), b = plain.allocate();
+  CHECK_EQ(a, 0);
+  CHECK_EQ(b, 1);
+  CHECK_EQ(plain.num_free_blocks(), 2);
+  auto pa = plain.get_block_payload_ptrs(a), pb = plain.get_block_payload_ptrs(b);
+  for (size_t i = 0; i < pa.key_value_bytes; ++i) {
+    static_cast<uint8_t*>(pa.key)[i] = static_cast<uint8_t>(i * 7 + 1);
+    static_cast<uint8_t*>(pa.value)[i] = static_cast<uint8_t>(i * 5 + 3);
+  }
+  plain.copy_block_payload(a, b);
+  CHECK(std::memcmp(pa.key, pb.key, pa.key_value_bytes) == 0);
+  CHECK(std::memcmp(pa.value, pb.value, pa.key_value_bytes) == 0);
+  CHECK_EQ(plain.payload_copy_bytes(), 2 * pa.key_value_bytes);
+  CHECK_THROWS_AS(plain.copy_block_payload(a, a), std::logic_error);
+  CHECK_THROWS_AS(plain.copy_block_payload(a, 2), std::logic_error);  // block 2 is free
+  plain.free(a);
+  CHECK_EQ(plain.allocate(), 2);  // FIFO: 2 and 3 were queued before 0
+  // FP8 pools need a GPU device (kv_cache_format.h rule)
+  CHECK_THROWS_AS(base::BlockAllocator(4, 16, 2, 8, base::DataType::kDataTypeBf16,
+                                       base::DeviceType::kDeviceCPU,
+                                       base::BlockStorageMode::kFp8E4M3PerTokenHead),
+                  std::invalid_argument);
+  CHECK_THROWS_AS(base::BlockAllocator(0, 16, 2, 8, base::DataType::kDataTypeBf16,
+                                       base::DeviceType::kDeviceCPU),
+                  std::invalid_argument);
+}

@@ -5,7 +5,12 @@
 // (pattern-filled pages compared element-wise after the handoff).
 #include <hip/hip_runtime.h>
 
+#include <dlfcn.h>
+#include <unistd.h>
+
 #include <algorithm>
+#include <memory>
+#include <string>
 #include <cstring>
 #include <numeric>
 #include <vector>
@@ -17,6 +22,8 @@
 #include "base/shared_kv_arena.h"
 #include "serving/decode_kv_reservation.h"
 #include "serving/pd_handoff.h"
+#include "serving/split_pd_handoff.h"
+#include "base/kv_cache_manager.h"
 
 using namespace cache;
 
@@ -145,6 +152,41 @@ TEST_CASE("hip backend: a dependency event orders the copy after the producer") 
   (void)hipStreamDestroy(producer);
   (void)hipFree(d_src);
   (void)hipFree(d_dst);
+}
+
+TEST_CASE("hip backend: completion is in submission order; settled records are reused") {
+  const auto s = schema_of(false, 8);
+  LayoutDescriptor l;
+  REQUIRE(MakePackedLayout(s, "packed", 7, iota_order(s.components.size()), {}, &l));
+  const size_t n = l.total_bytes;
+  std::vector<uint8_t*> bufs(4);
+  for (auto& b : bufs) HIP_OK(hipMalloc(&b, n));
+  HIP_OK(hipMemset(bufs[0], 0x11, n));
+  HIP_OK(hipMemset(bufs[2], 0x22, n));
+  TransferPlanner planner;
+  TransferPlan plan;
+  REQUIRE(planner.plan(s, s, &plan));
+  BoundTransfer a, b;
+  REQUIRE(BoundTransfer::Bind(plan, s, {bufs[0], n, &l}, {bufs[1], n, &l}, &a));
+  REQUIRE(BoundTransfer::Bind(plan, s, {bufs[2], n, &l}, {bufs[3], n, &l}, &b));
+  auto backend = MakeHipTransferBackend(2, 0);
+  for (int round = 0; round < 3; ++round) {
+    const MigrationId first = 10 + 2 * round, second = first + 1;
+    CHECK(backend->submit(first, TransferDirection::kGpuToGpu, a) == BackendResult::kPending);
+    CHECK(backend->submit(second, TransferDirection::kGpuToGpu, b) == BackendResult::kPending);
+    CHECK(backend->drain(second) == BackendResult::kSucceeded);
+    // the earlier launch finished before the later one on the same stream
+    CHECK(backend->poll(first) == BackendResult::kSucceeded);
+    CHECK(backend->poll(99) == BackendResult::kUnknown);
+    backend->release(second);
+    backend->release(first);
+  }
+  std::vector<uint8_t> got(n);
+  HIP_OK(hipMemcpy(got.data(), bufs[1], n, hipMemcpyDeviceToHost));
+  CHECK(std::all_of(got.begin(), got.end(), [](uint8_t v) { return v == 0x11; }));
+  HIP_OK(hipMemcpy(got.data(), bufs[3], n, hipMemcpyDeviceToHost));
+  CHECK(std::all_of(got.begin(), got.end(), [](uint8_t v) { return v == 0x22; }));
+  for (auto p : bufs) (void)hipFree(p);
 }
 
 namespace {
@@ -276,13 +318,46 @@ TEST_CASE("generic plan form: InProcKVBlockCopyConnector equals the run copy, BF
   }
 }
 
-TEST_CASE("end to end: prefill pages -> decode reservation -> connector copy -> fenced retire") {
-  // Qwen2.5-0.5B geometry: 24 layers, 2 KV heads x 64, 16-token pages (192 KiB).
+namespace {
+// The CPU oracle (oracle/liboracle.so, test infrastructure): the whole data
+// effect of copy_shared_kv on a host copy of the arena.
+using OracleCopy = uint64_t (*)(uint8_t*, const int32_t*, const int32_t*, int64_t, uint64_t, int32_t,
+                                int32_t*, int32_t*, int32_t*);
+OracleCopy oracle_copy_handoff() {
+  static OracleCopy fn = [] {
+    std::string self(4096, '\0');
+    const ssize_t n = readlink("/proc/self/exe", &self[0], self.size());
+    self.resize(n > 0 ? n : 0);
+    const std::string dir = self.substr(0, self.rfind('/'));  // .../paged-batch-engine_amd/lib
+    void* h = dlopen((dir + "/../../oracle/liboracle.so").c_str(), RTLD_NOW);
+    return h ? reinterpret_cast<OracleCopy>(dlsym(h, "orc_copy_handoff")) : nullptr;
+  }();
+  return fn;
+}
+
+std::unique_ptr<base::KVCacheManager> manager_over(const std::shared_ptr<base::SharedKVPageGroup>& g,
+                                                   int32_t heads, int32_t dim) {
+  std::vector<std::unique_ptr<base::BlockAllocator>> layers;
+  for (int l = 0; l < g->layers(); ++l)
+    layers.push_back(std::make_unique<base::BlockAllocator>(16, heads, dim, g, l));
+  return std::make_unique<base::KVCacheManager>(16, g->layers(), std::move(layers));
+}
+
+uint8_t* at(const pbe_arena_view& v, uint64_t off) {
+  return static_cast<uint8_t*>(v.base[off / v.segment_bytes]) + off % v.segment_bytes;
+}
+}  // namespace
+
+TEST_CASE("end to end: the reference's copy_shared_kv call order over KVCacheManager, bit-exact") {
+  // Qwen2.5-0.5B geometry: 24 layers, 2 KV heads x 64, 16-token pages (192 KiB),
+  // a 4-segment arena. Prefill and decode each own a KVCacheManager over their
+  // page group, built as the reference builds the shared-arena allocators.
   const int layers = 24;
   const uint64_t half = 16 * 2 * 64 * 2, page = 2 * layers * half;
   const uint64_t arena_bytes = 64 * page;
+  REQUIRE(oracle_copy_handoff() != nullptr);
   pbe_arena* arena = nullptr;
-  REQUIRE(pbe_arena_create(0, arena_bytes, 16 * page, 4242, &arena) == PBE_OK);  // 4 segments
+  REQUIRE(pbe_arena_create(0, arena_bytes, 16 * page, 4242, &arena) == PBE_OK);
   pbe_arena_view view{};
   REQUIRE(pbe_arena_get_view(arena, &view) == PBE_OK);
   auto owner = std::make_shared<base::LocalChunkOwner>(arena_bytes, 4242);
@@ -295,73 +370,161 @@ TEST_CASE("end to end: prefill pages -> decode reservation -> connector copy -> 
   {
     auto p_client = std::make_shared<base::SharedKVArenaClient>(owner, view, "prefill", 24 * page, 0);
     auto d_client = std::make_shared<base::SharedKVArenaClient>(owner, view, "decode", 40 * page, 0);
-    base::SharedKVPageGroup p_pages(p_client, layers, half, 2 * 1024 * 1024, p_stream);  // 11-page Chunks
-    base::SharedKVPageGroup d_pages(d_client, layers, half, 2 * 1024 * 1024, d_stream);
+    auto p_pages = std::make_shared<base::SharedKVPageGroup>(p_client, layers, half, 2 * 1024 * 1024, p_stream);
+    auto d_pages = std::make_shared<base::SharedKVPageGroup>(d_client, layers, half, 2 * 1024 * 1024, d_stream);
+    auto p_kv = manager_over(p_pages, 2, 64);
+    auto d_kv = manager_over(d_pages, 2, 64);
+    // a decode request already holding 2 pages, so the handoff's pages are
+    // not the arena's first ones on the decode side either
+    const base::RequestId other = d_kv->register_request();
+    REQUIRE(d_kv->append_slots(other, 20));
     // prefill: a 41-token prompt = 3 pages, every layer
-    std::vector<int32_t> src;
-    for (int i = 0; i < 3; ++i) src.push_back(p_pages.allocate(0));
-    for (int l = 1; l < layers; ++l)
-      for (int i = 0; i < 3; ++i) CHECK_EQ(p_pages.allocate(l), src[i]);
-    // write the prefill KV: byte = page index * 3 + 64 * plane + layer
-    std::vector<uint8_t> host(page);
-    for (size_t i = 0; i < src.size(); ++i) {
-      for (int l = 0; l < layers; ++l)
-        for (int plane = 0; plane < 2; ++plane)
-          std::memset(host.data() + (2 * l + plane) * half, static_cast<int>((i * 3 + 64 * plane + l) & 0xff), half);
-      const uint64_t off = static_cast<uint64_t>(src[i]) * half;
-      uint8_t* dst = static_cast<uint8_t*>(view.base[off / view.segment_bytes]) + off % view.segment_bytes;
-      HIP_OK(hipMemcpy(dst, host.data(), page, hipMemcpyHostToDevice));
-    }
-    // decode: reserve destination pages and build the manifest
+    const base::RequestId pr = p_kv->register_request();
+    REQUIRE(p_kv->append_slots(pr, 41));
+    // every arena byte random (canaries included)
+    std::vector<uint8_t> host(arena_bytes);
+    uint64_t x = 0x9e3779b97f4a7c15ull;
+    for (auto& b : host) { x ^= x << 13; x ^= x >> 7; x ^= x << 17; b = static_cast<uint8_t>(x >> 24); }
+    for (uint32_t s = 0; s < view.nseg; ++s)
+      HIP_OK(hipMemcpy(view.base[s], host.data() + s * view.segment_bytes, view.segment_bytes, hipMemcpyHostToDevice));
     serving::KVPoolDescriptor pool{0, layers, 16, 2, 64, base::DataType::kDataTypeBf16,
                                    base::BlockStorageMode::kPlain};
-    serving::DecodeKVReservationManager reservations(&d_pages, pool);
-    serving::DecodeKVReservationRequest req;
-    req.client_request_id.value = "req-41";
-    req.handoff_id.value = 1;
-    req.prompt_tokens = 41;
-    req.computed_tokens = 41;
-    req.src_pool = pool;
-    req.src_block_ids_per_layer.assign(layers, src);
+    serving::SharedKVPrefillResult result;
+    result.shared_arena_epoch = p_client->epoch();
+    result.client_request_id.value = "req-41";
+    result.handoff_id.value = 1;
+    result.prompt_tokens.assign(41, 7);
+    result.computed_tokens = 41;
+    result.first_token = 99;
+    result.src_pool = pool;
+    for (int l = 0; l < layers; ++l) result.layers.push_back({l, p_kv->get_block_ids(pr, l)});
+    // rejected inputs reserve nothing and write nothing
     serving::DecodeKVReservation res;
-    serving::KVBlockManifest manifest;
-    REQUIRE(reservations.reserve(req, &res, &manifest));
-    serving::SharedArenaBinding binding{view, 4242, 0};
-    serving::SharedArenaKVTransferConnector conn(binding, d_stream);
-    serving::HandoffId h;
-    REQUIRE(conn.submit_from(p_client->epoch(), manifest, &h));
-    CHECK(conn.drain(h).ok());
-    CHECK_EQ(conn.copied_bytes(), 3 * page);
-    // verify destination pages
-    const auto& dst_ids = manifest.layer_mappings[0].dst_block_ids;
-    for (size_t i = 0; i < dst_ids.size(); ++i) {
-      const uint64_t off = static_cast<uint64_t>(dst_ids[i]) * half;
-      const uint8_t* d = static_cast<uint8_t*>(view.base[off / view.segment_bytes]) + off % view.segment_bytes;
-      HIP_OK(hipMemcpy(host.data(), d, page, hipMemcpyDeviceToHost));
-      bool ok = true;
-      for (int l = 0; l < layers && ok; ++l)
-        for (int plane = 0; plane < 2 && ok; ++plane)
-          ok = std::all_of(host.begin() + (2 * l + plane) * half, host.begin() + (2 * l + plane + 1) * half,
-                           [&](uint8_t b) { return b == static_cast<uint8_t>((i * 3 + 64 * plane + l) & 0xff); });
-      CHECK(ok);
-    }
-    // prefill releases its pages after the copy: fences on its stream
-    for (int l = 0; l < layers; ++l)
-      for (int id : src) p_pages.retire(l, id);
+    auto bad = result;
+    bad.shared_arena_epoch = 7;
+    CHECK_THROWS_AS(serving::CopySharedKVToDecode(d_kv.get(), pool, bad, d_stream, &res), std::runtime_error);
+    bad = result;
+    bad.layers.pop_back();
+    CHECK_THROWS_AS(serving::CopySharedKVToDecode(d_kv.get(), pool, bad, d_stream, &res), std::runtime_error);
+    bad = result;
+    bad.layers[5].src_block_ids[1] += 1;  // not a page id
+    CHECK_THROWS_AS(serving::CopySharedKVToDecode(d_kv.get(), pool, bad, d_stream, &res), std::runtime_error);
+    bad = result;
+    bad.computed_tokens = 60;  // more than the prompt
+    CHECK_THROWS_AS(serving::CopySharedKVToDecode(d_kv.get(), pool, bad, d_stream, &res), std::runtime_error);
+    CHECK_EQ(d_kv->num_active_requests(), 1);
+    CHECK(!res.valid());
+    // reserve -> manifest -> one-launch copy -> sync -> commit_kv
+    const uint64_t copied = serving::CopySharedKVToDecode(d_kv.get(), pool, result, d_stream, &res);
+    CHECK_EQ(copied, 3 * page);
+    REQUIRE(res.valid());
+    CHECK_EQ(d_kv->kv_committed_tokens(res.decode_request_id), 41);
+    CHECK_EQ(d_kv->get_context_len(res.decode_request_id), 41);
+    const auto& src = p_kv->get_block_ids(pr, 0);
+    const auto& dst = d_kv->get_block_ids(res.decode_request_id, 0);
+    REQUIRE(dst.size() == 3u);
+    CHECK(dst == res.dst_block_ids_per_layer[0]);
+    CHECK(dst[0] != src[0]);
+    std::vector<int32_t> s1(3), s2(3), s3(3);
+    CHECK_EQ(oracle_copy_handoff()(host.data(), src.data(), dst.data(), 3, half, layers, s1.data(),
+                                   s2.data(), s3.data()),
+             3 * page);
+    std::vector<uint8_t> got(arena_bytes);
+    for (uint32_t s = 0; s < view.nseg; ++s)
+      HIP_OK(hipMemcpy(got.data() + s * view.segment_bytes, view.base[s], view.segment_bytes, hipMemcpyDeviceToHost));
+    CHECK(std::memcmp(got.data(), host.data(), arena_bytes) == 0);
+    // copy_block_payload in shared-arena mode: one block of one layer, on the
+    // group's stream (K and V planes of layer 3 of dst[0] onto dst[1])
+    d_kv->allocator(3).copy_block_payload(dst[0], dst[1]);
+    for (int plane = 0; plane < 2; ++plane)
+      std::memcpy(host.data() + (dst[1] + 6 + plane) * half, host.data() + (dst[0] + 6 + plane) * half, half);
+    for (uint32_t s = 0; s < view.nseg; ++s)
+      HIP_OK(hipMemcpy(got.data() + s * view.segment_bytes, view.base[s], view.segment_bytes, hipMemcpyDeviceToHost));
+    CHECK(std::memcmp(got.data(), host.data(), arena_bytes) == 0);
+    (void)at;
+    // prefill frees its request; the pages return once its stream passes the fences
+    p_kv->free_request(pr);
     REQUIRE(pbe_stream_synchronize(0, p_stream) == PBE_OK);
-    p_pages.collect();
-    CHECK_EQ(p_pages.leased_bytes(), 0u);
-    reservations.release(&res);
+    p_pages->collect();
+    CHECK_EQ(p_pages->leased_bytes(), 0u);
+    d_kv->free_request(res.decode_request_id);
+    d_kv->free_request(other);
     REQUIRE(pbe_stream_synchronize(0, d_stream) == PBE_OK);
-    d_pages.collect();
-    CHECK_EQ(d_pages.leased_bytes(), 0u);
-    conn.release(h);
+    d_pages->collect();
+    CHECK_EQ(d_pages->leased_bytes(), 0u);
   }
   CHECK_EQ(owner->lease_count(), 0u);
   CHECK_EQ(owner->free_bytes(), arena_bytes);
   pbe_stream_destroy(0, p_stream);
   pbe_stream_destroy(0, d_stream);
   CHECK(pbe_arena_destroy(arena) == PBE_OK);
+}
+
+TEST_CASE("block allocator: local HIP pools copy one block's payload, FP8 scales included") {
+  for (int fp8 = 0; fp8 < 2; ++fp8) {
+    base::BlockAllocator a(8, 16, 2, 64, base::DataType::kDataTypeBf16, base::DeviceType::kDeviceHIP,
+                           fp8 ? base::BlockStorageMode::kFp8E4M3PerTokenHead : base::BlockStorageMode::kPlain);
+    CHECK_EQ(a.key_value_bytes_per_block(), fp8 ? 2048u : 4096u);
+    CHECK_EQ(a.scale_bytes_per_block(), fp8 ? 128u : 0u);
+    int ids[8];
+    for (int i = 0; i < 8; ++i) ids[i] = a.allocate();
+    const base::KVPoolView v = a.pool_view();
+    const size_t kvb = 8 * a.key_value_bytes_per_block(), scb = 8 * a.scale_bytes_per_block();
+    // random pools (payload and scales)
+    std::vector<std::vector<uint8_t>> host;
+    void* pools[4] = {v.key_pool(), v.value_pool(), v.key_scale_pool(), v.value_scale_pool()};
+    const size_t sizes[4] = {kvb, kvb, scb, scb};
+    uint64_t x = 12345 + fp8;
+    for (int p = 0; p < 4; ++p) {
+      host.emplace_back(sizes[p]);
+      for (auto& b : host.back()) { x ^= x << 13; x ^= x >> 7; x ^= x << 17; b = static_cast<uint8_t>(x >> 32); }
+      if (sizes[p]) HIP_OK(hipMemcpy(pools[p], host[p].data(), sizes[p], hipMemcpyHostToDevice));
+    }
+    a.copy_block_payload(ids[5], ids[2]);
+    const size_t per[4] = {a.key_value_bytes_per_block(), a.key_value_bytes_per_block(),
+                           a.scale_bytes_per_block(), a.scale_bytes_per_block()};
+    for (int p = 0; p < 4; ++p) {
+      if (!sizes[p]) continue;
+      std::memcpy(host[p].data() + ids[2] * per[p], host[p].data() + ids[5] * per[p], per[p]);
+      std::vector<uint8_t> got(sizes[p]);
+      HIP_OK(hipMemcpy(got.data(), pools[p], sizes[p], hipMemcpyDeviceToHost));
+      CHECK(got == host[p]);
+    }
+    CHECK_EQ(a.payload_copy_bytes(), 2 * per[0] + 2 * per[2]);
+    CHECK_THROWS_AS(a.copy_block_payload(ids[1], ids[1]), std::logic_error);
+  }
+}
+
+TEST_CASE("interprocess events: unsupported runtimes say so at create, in-process events work") {
+  pbe_event* ev = nullptr;
+  const int rc = pbe_event_create(0, 1, &ev);
+  if (rc == PBE_ERR_UNSUPPORTED) {
+    CHECK(ev == nullptr);
+    CHECK(std::string(pbe_last_error()).find("pbe_signal_") != std::string::npos);
+    uint8_t handle[PBE_IPC_HANDLE_BYTES] = {};
+    pbe_event* imported = nullptr;
+    CHECK_EQ(pbe_event_import(handle, 0, &imported), PBE_ERR_UNSUPPORTED);
+  } else {
+    // a runtime that records interprocess events: export, import, record, wait
+    REQUIRE(rc == PBE_OK);
+    uint8_t handle[PBE_IPC_HANDLE_BYTES];
+    REQUIRE(pbe_event_export(ev, handle) == PBE_OK);
+    pbe_event* imported = nullptr;
+    REQUIRE(pbe_event_import(handle, 0, &imported) == PBE_OK);
+    REQUIRE(pbe_event_record(ev, nullptr) == PBE_OK);
+    REQUIRE(pbe_event_wait(imported, nullptr) == PBE_OK);
+    REQUIRE(pbe_event_synchronize(ev) == PBE_OK);
+    pbe_event_destroy(imported);
+    pbe_event_destroy(ev);
+  }
+  pbe_event* local = nullptr;
+  REQUIRE(pbe_event_create(0, 0, &local) == PBE_OK);
+  uint8_t handle[PBE_IPC_HANDLE_BYTES];
+  CHECK_EQ(pbe_event_export(local, handle), PBE_ERR_INVALID);
+  REQUIRE(pbe_event_record(local, nullptr) == PBE_OK);
+  CHECK_EQ(pbe_event_synchronize(local), PBE_OK);
+  CHECK_EQ(pbe_event_query(local), PBE_OK);
+  pbe_event_destroy(local);
 }
 
 TEST_CASE("zero-copy takeover: moved Chunks are read in place, shared pages are copied") {
