@@ -316,6 +316,24 @@ int pbe_paged_decode(const pbe_arena_view* kv, int32_t kv_dtype, const float* sc
                      int32_t max_blocks_per_seq, int32_t splits, void* workspace,
                      uint64_t workspace_bytes, int device, void* stream);
 
+/* Allocation-free form of pbe_paged_decode. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The split-K
+ * partials live in a static device array of PBE_DECODE_SCRATCH_BYTES per GPU
+ * (held until the process ends) instead of a caller workspace; nothing is
+ * allocated and every partial is rewritten by each call, so no clearing is
+ * needed. Launches whose partials need more (pbe_paged_decode_workspace_bytes
+ * of the split count used) are rejected with PBE_ERR_INVALID. All calls on
+ * one GPU share the array: calls that overlap in time on one GPU (different
+ * streams, or host threads racing) corrupt each other's results; serialize
+ * them on one stream. */
+#define PBE_DECODE_SCRATCH_BYTES (8u << 20)
+int pbe_paged_decode_noalloc(const pbe_arena_view* kv, int32_t kv_dtype, const float* scales,
+                             uint64_t scale_bytes, const pbe_kv_shape* shape, int32_t layer,
+                             const void* queries, void* outputs, int32_t batch, int32_t q_heads,
+                             const int32_t* block_tables, const int32_t* seq_lens,
+                             int32_t max_blocks_per_seq, int32_t splits, int device, void* stream);
+
 /* GPU UUID of `device` (16 bytes), as compared across processes. */
 int pbe_device_uuid(int device, uint8_t out[16]);
 /* The calling thread's current HIP device (the one a pool built without an

@@ -1162,12 +1162,41 @@ uint64_t pbe_paged_decode_workspace_bytes(int32_t batch, int32_t q_heads, int32_
   return pbe::decode_workspace_bytes(batch, q_heads, head_dim, splits);
 }
 
-int pbe_paged_decode(const pbe_arena_view* kv, int32_t kv_dtype, const float* scales,
-                     uint64_t scale_bytes, const pbe_kv_shape* shape, int32_t layer,
-                     const void* queries, void* outputs, int32_t batch, int32_t q_heads,
-                     const int32_t* block_tables, const int32_t* seq_lens,
-                     int32_t max_blocks_per_seq, int32_t splits, void* workspace,
-                     uint64_t workspace_bytes, int device, void* stream) {
+}  // extern "C"
+
+// The split-K partials of the allocation-free decode entry point: one copy of
+// this array per GPU, for the life of the process. Host code never uses its
+// name as an address: scratch_address() resolves the device copy once per GPU
+// (hipGetSymbolAddress, with that GPU current) and every launch passes that.
+static __device__ __align__(256) uint8_t scratch[PBE_DECODE_SCRATCH_BYTES];
+
+namespace {
+
+int scratch_address(int device, void** out) {
+  static std::mutex mu;
+  static void* per_device[64] = {};
+  if (device < 0 || device >= 64) return fail(PBE_ERR_INVALID, "device %d out of range", device);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!per_device[device]) {
+    PBE_DEVICE_SCOPE(device);
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+    per_device[device] = ptr;
+  }
+  *out = per_device[device];
+  return PBE_OK;
+}
+
+// Shared body of both decode entry points. `static_scratch`: the workspace is
+// this GPU's scratch array (known valid, not an allocation the runtime can
+// describe), so it skips the pointer check and names its limit on overflow.
+int paged_decode_call(const pbe_arena_view* kv, int32_t kv_dtype, const float* scales,
+                      uint64_t scale_bytes, const pbe_kv_shape* shape, int32_t layer,
+                      const void* queries, void* outputs, int32_t batch, int32_t q_heads,
+                      const int32_t* block_tables, const int32_t* seq_lens,
+                      int32_t max_blocks_per_seq, int32_t splits, void* workspace,
+                      uint64_t workspace_bytes, int device, void* stream, bool static_scratch) {
   if (!view_ok(kv) || !shape_ok(shape)) return fail(PBE_ERR_INVALID, "invalid decode arena view or shape");
   if (kv_dtype != PBE_KV_BF16 && kv_dtype != PBE_KV_FP8_E4M3)
     return fail(PBE_ERR_INVALID, "unknown KV dtype %d", (int)kv_dtype);
@@ -1188,9 +1217,15 @@ int pbe_paged_decode(const pbe_arena_view* kv, int32_t kv_dtype, const float* sc
   if (splits < 0 || splits > pbe::kDecodeMaxSplits)
     return fail(PBE_ERR_INVALID, "splits must be 0..%d", pbe::kDecodeMaxSplits);
   const uint64_t need = pbe::decode_workspace_bytes(batch, q_heads, shape->head_dim, splits);
-  if (workspace_bytes < need)
+  if (workspace_bytes < need) {
+    if (static_scratch)
+      return fail(PBE_ERR_INVALID,
+                  "decode needs %llu bytes of partials; the static scratch holds %llu "
+                  "(use pbe_paged_decode with a workspace, or fewer splits)",
+                  (unsigned long long)need, (unsigned long long)workspace_bytes);
     return fail(PBE_ERR_INVALID, "decode workspace holds %llu of %llu bytes",
                 (unsigned long long)workspace_bytes, (unsigned long long)need);
+  }
   const uint64_t half = half_bytes(*shape, fp8 ? 1u : 2u);
   const uint64_t page = 2ull * shape->layers * half;
   if (kv->nseg > 1 && kv->segment_bytes % page)
@@ -1207,7 +1242,7 @@ int pbe_paged_decode(const pbe_arena_view* kv, int32_t kv_dtype, const float* sc
         !accessible(outputs, row_bytes, device, &known) ||
         !accessible(block_tables, (uint64_t)batch * max_blocks_per_seq * 4, device, &known) ||
         !accessible(seq_lens, (uint64_t)batch * 4, device, &known) ||
-        !accessible(workspace, need, device, &known) ||
+        (!static_scratch && !accessible(workspace, need, device, &known)) ||
         (fp8 && !accessible(scales, scale_bytes, device, &known)))
       return fail(PBE_ERR_INVALID, "decode operands must be memory of device %d", device);
   }
@@ -1245,6 +1280,34 @@ int pbe_paged_decode(const pbe_arena_view* kv, int32_t kv_dtype, const float* sc
   PBE_DEVICE_SCOPE(device);
   PBE_HIP(pbe::launch_paged_decode(p, fp8, static_cast<hipStream_t>(stream)));
   return PBE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pbe_paged_decode(const pbe_arena_view* kv, int32_t kv_dtype, const float* scales,
+                     uint64_t scale_bytes, const pbe_kv_shape* shape, int32_t layer,
+                     const void* queries, void* outputs, int32_t batch, int32_t q_heads,
+                     const int32_t* block_tables, const int32_t* seq_lens,
+                     int32_t max_blocks_per_seq, int32_t splits, void* workspace,
+                     uint64_t workspace_bytes, int device, void* stream) {
+  return paged_decode_call(kv, kv_dtype, scales, scale_bytes, shape, layer, queries, outputs, batch,
+                           q_heads, block_tables, seq_lens, max_blocks_per_seq, splits, workspace,
+                           workspace_bytes, device, stream, false);
+}
+
+int pbe_paged_decode_noalloc(const pbe_arena_view* kv, int32_t kv_dtype, const float* scales,
+                             uint64_t scale_bytes, const pbe_kv_shape* shape, int32_t layer,
+                             const void* queries, void* outputs, int32_t batch, int32_t q_heads,
+                             const int32_t* block_tables, const int32_t* seq_lens,
+                             int32_t max_blocks_per_seq, int32_t splits, int device, void* stream) {
+  void* ws = nullptr;
+  const int rc = scratch_address(device, &ws);
+  if (rc != PBE_OK) return rc;
+  return paged_decode_call(kv, kv_dtype, scales, scale_bytes, shape, layer, queries, outputs, batch,
+                           q_heads, block_tables, seq_lens, max_blocks_per_seq, splits, ws,
+                           PBE_DECODE_SCRATCH_BYTES, device, stream, true);
 }
 
 int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream) {

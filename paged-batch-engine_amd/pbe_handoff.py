@@ -120,6 +120,9 @@ _SIGNATURES = [
     ("pbe_paged_decode", C.c_int, [C.POINTER(ArenaView), C.c_int32, _P, C.c_uint64,
                                    C.POINTER(KvShape), C.c_int32, _P, _P, C.c_int32, C.c_int32,
                                    _P, _P, C.c_int32, C.c_int32, _P, C.c_uint64, C.c_int, _P]),
+    ("pbe_paged_decode_noalloc", C.c_int, [C.POINTER(ArenaView), C.c_int32, _P, C.c_uint64,
+                                           C.POINTER(KvShape), C.c_int32, _P, _P, C.c_int32,
+                                           C.c_int32, _P, _P, C.c_int32, C.c_int32, C.c_int, _P]),
 ]
 EXPORTED = [name for name, _, _ in _SIGNATURES]
 
@@ -459,6 +462,21 @@ def decode_splits(batch: int, kv_heads: int, max_blocks: int, kv_dtype: int) -> 
 
 def decode_workspace_bytes(batch: int, q_heads: int, head_dim: int, splits: int) -> int:
     return int(lib().pbe_paged_decode_workspace_bytes(batch, q_heads, head_dim, splits))
+
+
+PBE_DECODE_SCRATCH_BYTES = 8 << 20
+
+
+def paged_decode_noalloc(view: ArenaView, kv_dtype: int, scales: int, scale_bytes: int,
+                         kv: KvShape, layer: int, queries: int, outputs: int, batch: int,
+                         q_heads: int, tables: int, seq_lens: int, max_blocks: int, splits: int,
+                         stream: int = 0, device: int = 0) -> None:
+    """pbe_paged_decode with the partials in the library's static scratch
+    (pbe_paged_decode_noalloc): allocates nothing; calls on one GPU must not overlap."""
+    check(lib().pbe_paged_decode_noalloc(C.byref(view), kv_dtype, scales or None, scale_bytes,
+                                         C.byref(kv), layer, queries, outputs, batch, q_heads,
+                                         tables, seq_lens, max_blocks, splits, device,
+                                         stream or None))
 
 
 def paged_decode(view: ArenaView, kv_dtype: int, scales: int, scale_bytes: int, kv: KvShape,
