@@ -188,53 +188,6 @@ bool view_accessible(const pbe_arena_view& v, int device, std::vector<Range>* kn
   return true;
 }
 
-// Run lists of up to kKernargRuns entries go in the kernel arguments;
-// PBE_KERNARG=0 stages them through device memory instead (measurement only).
-bool kernarg_runs_enabled() {
-  static const bool on = [] {
-    const char* e = std::getenv("PBE_KERNARG");
-    return !(e && e[0] == '0');
-  }();
-  return on;
-}
-
-// Identity-copy kernel variant. The defaults are the measured best on MI355X;
-// PBE_UNROLL / PBE_POLICY / PBE_BLOCK / PBE_LDS override them for tuning
-// experiments only.
-pbe::CopyConfig copy_config() {
-  pbe::CopyConfig c;
-  if (const char* e = std::getenv("PBE_UNROLL")) c.unroll = std::atoi(e);
-  if (c.unroll != 2 && c.unroll != 4 && c.unroll != 8) c.unroll = pbe::kCopyUnroll;
-  if (const char* e = std::getenv("PBE_POLICY")) c.policy = std::atoi(e);
-  if (const char* e = std::getenv("PBE_BLOCK")) c.block = std::atoi(e);
-  if (c.block != 64 && c.block != 256 && c.block != 1024) c.block = 256;
-  if (const char* e = std::getenv("PBE_LDS")) c.lds_bytes = (uint32_t)std::atoi(e);
-  return c;
-}
-
-// FP8 kernel variant: the 16-byte vectors per lane per slice (PBE_FP8_UNROLL
-// overrides the default for tuning experiments only).
-pbe::CopyConfig fp8_config() {
-  pbe::CopyConfig c;
-  c.unroll = pbe::kFp8Unroll;
-  if (const char* e = std::getenv("PBE_FP8_UNROLL")) c.unroll = std::atoi(e);
-  if (c.unroll != 2 && c.unroll != 4 && c.unroll != 8) c.unroll = pbe::kFp8Unroll;
-  return c;
-}
-
-pbe::LaunchShape launch_shape(uint64_t total_slices, int device, const pbe::CopyConfig& cfg) {
-  (void)total_slices;
-  (void)device;
-  pbe::LaunchShape shape;
-  shape.copy = cfg;
-  // One slice per wave measured best on MI355X: the dispatcher keeps every CU
-  // full and each wave has all of its loads in flight at once.
-  shape.slices_per_wave = 1;
-  if (const char* env = std::getenv("PBE_SLICES_PER_WAVE"))
-    shape.slices_per_wave = std::max(1, std::atoi(env));
-  return shape;
-}
-
 }  // namespace
 
 struct pbe_arena {
@@ -268,7 +221,6 @@ struct pbe_runlist {
   uint32_t total_slices = 0;
   uint64_t page_bytes = 0;      // source bytes per page
   pbe_runlist_info info{};
-  pbe::LaunchShape shape;
   pbe_kv_shape kv{};
 };
 
@@ -860,7 +812,7 @@ int resolve_runs(const pbe_arena_view& src, const pbe_arena_view& dst, uint64_t 
 }
 
 int upload_runlist(Resolved& res, int device, bool fp8, bool has_scales, uint64_t page_bytes,
-                   const pbe_kv_shape& kv, const pbe::CopyConfig& cfg, pbe_runlist** out) {
+                   const pbe_kv_shape& kv, pbe_runlist** out) {
   PBE_DEVICE_SCOPE(device);
   pbe_runlist* list = new (std::nothrow) pbe_runlist;
   if (!list) return fail(PBE_ERR_NOMEM, "run list object");
@@ -880,7 +832,6 @@ int upload_runlist(Resolved& res, int device, bool fp8, bool has_scales, uint64_
   list->page_bytes = page_bytes;
   list->info = res.info;
   list->kv = kv;
-  list->shape = launch_shape(res.info.slices, device, cfg);
   *out = list;
   return PBE_OK;
 }
@@ -905,11 +856,10 @@ int pbe_runlist_create(const pbe_arena_view* src, const pbe_arena_view* dst, con
       return fail(PBE_ERR_INVALID, "arena view is not device memory of device %d", device);
   }
   Resolved res;
-  const pbe::CopyConfig cfg = copy_config();
   int rc = resolve_runs(*src, *dst, half, half, 2 * shape->layers, runs, n_runs, 0, 0, 0,
-                        pbe::slice_bytes(pbe::KernelKind::kCopy, cfg), &res);
+                        pbe::kCopySliceBytes, &res);
   if (rc != PBE_OK) return rc;
-  return upload_runlist(res, device, false, false, 2ull * shape->layers * half, *shape, cfg, out);
+  return upload_runlist(res, device, false, false, 2ull * shape->layers * half, *shape, out);
 }
 
 int pbe_runlist_create_fp8(const pbe_arena_view* src, const pbe_arena_view* dst, void* dst_scales,
@@ -938,10 +888,10 @@ int pbe_runlist_create_fp8(const pbe_arena_view* src, const pbe_arena_view* dst,
   Resolved res;
   int rc = resolve_runs(*src, *dst, half16, half8, 2 * shape->layers, runs, n_runs,
                         reinterpret_cast<uint64_t>(dst_scales), dst_scales_bytes, scale_page,
-                        pbe::slice_bytes(pbe::KernelKind::kFp8, fp8_config()), &res);
+                        pbe::kFp8SliceBytes, &res);
   if (rc != PBE_OK) return rc;
   return upload_runlist(res, device, true, dst_scales != nullptr, 2ull * shape->layers * half16,
-                        *shape, fp8_config(), out);
+                        *shape, out);
 }
 
 int pbe_runlist_get_info(const pbe_runlist* list, pbe_runlist_info* out) {
@@ -964,11 +914,9 @@ int pbe_handoff_copy_timed(const pbe_runlist* list, void* stream, void* start_ev
   if (!list) return fail(PBE_ERR_INVALID, "null run list");
   if (list->fp8) return fail(PBE_ERR_INVALID, "FP8 run list passed to the BF16 copy");
   PBE_DEVICE_SCOPE(list->device);
-  pbe::LaunchShape shape = list->shape;
-  shape.start = static_cast<hipEvent_t>(start_event);
-  shape.stop = static_cast<hipEvent_t>(stop_event);
-  PBE_HIP(pbe::launch_copy_runs(list->runs, list->n_runs, list->total_slices, list->page_bytes,
-                                shape, static_cast<hipStream_t>(stream)));
+  const pbe::LaunchEvents ev{static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event)};
+  PBE_HIP(pbe::launch_copy_runs(list->runs, list->n_runs, list->total_slices, list->page_bytes, ev,
+                                static_cast<hipStream_t>(stream)));
   return PBE_OK;
 }
 
@@ -994,13 +942,11 @@ int pbe_handoff_copy_fp8_timed(const pbe_runlist* list, int scale_mode, const fl
   PBE_DEVICE_SCOPE(list->device);
   const pbe_kv_shape& kv = list->kv;
   const uint32_t rows_per_plane = (uint32_t)(kv.page_tokens * kv.kv_heads);
-  pbe::LaunchShape shape = list->shape;
-  shape.start = static_cast<hipEvent_t>(start_event);
-  shape.stop = static_cast<hipEvent_t>(stop_event);
+  const pbe::LaunchEvents ev{static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event)};
   PBE_HIP(pbe::launch_copy_runs_fp8(
       list->runs, list->n_runs, list->total_slices, list->page_bytes, (uint32_t)kv.head_dim / 8u,
       rows_per_plane, (uint32_t)kv.kv_heads, rows_per_plane * 2u * (uint32_t)kv.layers,
-      scale_mode == PBE_FP8_SCALE_TABLE, amax_table, shape, static_cast<hipStream_t>(stream)));
+      scale_mode == PBE_FP8_SCALE_TABLE, amax_table, ev, static_cast<hipStream_t>(stream)));
   return PBE_OK;
 }
 
@@ -1098,17 +1044,12 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
       return fail(PBE_ERR_INVALID, "arena view is not device memory of device %d", device);
   }
   Resolved res;
-  const pbe::CopyConfig cfg = copy_config();
   rc = resolve_runs(*arena, *arena, half, half, 2 * shape->layers, runs.data(), n_runs, 0, 0, 0,
-                    pbe::slice_bytes(pbe::KernelKind::kCopy, cfg), &res);
+                    pbe::kCopySliceBytes, &res);
   if (rc != PBE_OK) return rc;
   PBE_DEVICE_SCOPE(device);
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const pbe::LaunchShape shape_l = launch_shape(res.info.slices, device, cfg);
-  const pbe::CopyConfig def{};
-  if ((uint64_t)n_runs <= pbe::kKernargRuns && kernarg_runs_enabled() && shape_l.slices_per_wave == 1 &&
-      cfg.unroll == def.unroll && cfg.policy == def.policy && cfg.block == def.block &&
-      cfg.lds_bytes == def.lds_bytes) {
+  if ((uint64_t)n_runs <= pbe::kKernargRuns) {
     // Short lists ride in the kernel arguments: no staging copy, no fence.
     pbe::KernargRunList list{};
     list.n_runs = (uint32_t)n_runs;
@@ -1127,7 +1068,7 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
   if (rc != PBE_OK) return rc;
   PBE_HIP(pbe::launch_copy_runs(static_cast<const pbe::DevRun*>(dev), (uint32_t)n_runs,
                                 (uint32_t)res.info.slices, 2ull * shape->layers * half,
-                                launch_shape(res.info.slices, device, cfg), s));
+                                pbe::LaunchEvents{}, s));
   rc = stage_done(*slot, s);
   if (rc != PBE_OK) return rc;
   if (copied) *copied = res.info.src_bytes;

@@ -124,11 +124,9 @@ struct Geo {
   static constexpr int E = kFp8 ? 1 : 2;
   static constexpr int WORDS = D * E / 16;   // key words = value words per lane
   static constexpr int PITCH = D * E + 16;   // LDS row pitch of the value tile
-#ifndef PBE_DECODE_SETS_FP8
-#define PBE_DECODE_SETS_FP8 4
-#define PBE_DECODE_SETS_BF16 2
-#endif
-  static constexpr int SETS = kFp8 ? PBE_DECODE_SETS_FP8 : PBE_DECODE_SETS_BF16;  // SETS-1 blocks in flight
+  // Register sets per wave (SETS-1 blocks in flight), the measured best on
+  // MI355X: FP8 blocks are half the bytes, so more of them stay in flight.
+  static constexpr int SETS = kFp8 ? 4 : 2;
 };
 
 template <int W, bool kFp8>

@@ -6,12 +6,10 @@
 namespace pbe {
 
 constexpr int kThreadsPerBlock = 256;
-constexpr int kCopyUnroll = 4;  // 4 KiB per wave slice for the identity copy
-// Cache policy of the identity copy: buffer loads with the non-temporal bit,
-// buffer stores with sc1 + nt (measured 1-2% faster on MI355X than global
-// nt stores; stores without nt are 50% slower).
-constexpr int kCopyPolicy = 10;
-constexpr int kFp8Unroll = 4;   // 4 KiB of BF16 source per wave slice
+constexpr int kCopyUnroll = 4;  // 16-byte vectors per lane per slice of the identity copy
+constexpr uint32_t kCopySliceBytes = 64u * 16u * kCopyUnroll;  // 4 KiB per wave
+constexpr int kFp8Unroll = 4;   // 16-byte BF16 vectors per lane per slice of the FP8 copy
+constexpr uint32_t kFp8SliceBytes = 64u * 16u * kFp8Unroll;    // 4 KiB of BF16 source per wave
 
 // Device form of one run: resolved addresses in this process's mapping.
 // slice_begin is the exclusive prefix of slices over the preceding runs.
@@ -33,27 +31,12 @@ struct DevOp {
   uint64_t bytes;
 };
 
-enum class KernelKind { kCopy, kFp8 };
-
-// Identity-copy variant: 16-byte vectors per lane per slice (unroll), cache
-// policy of loads/stores (index into the kernel's policy table), workgroup
-// size, and dynamic LDS per workgroup (caps workgroups per CU).
-struct CopyConfig {
-  int unroll = kCopyUnroll;
-  int policy = kCopyPolicy;
-  int block = 256;
-  uint32_t lds_bytes = 0;
-};
-
-struct LaunchShape {
-  uint32_t slices_per_wave = 1;
-  CopyConfig copy;
-  // Optional events that bracket the kernel itself (hipExtLaunchKernel).
+// Optional events that bracket the kernel itself (hipExtLaunchKernel), for
+// timing without the launch gap.
+struct LaunchEvents {
   hipEvent_t start = nullptr;
   hipEvent_t stop = nullptr;
 };
-
-uint32_t slice_bytes(KernelKind kind, const CopyConfig& cfg);
 
 // Run lists this short travel in the kernel arguments (3.6 KB of the 4 KB
 // kernarg space) instead of a staged device copy.
@@ -66,17 +49,17 @@ struct KernargRunList {
 };
 static_assert(sizeof(KernargRunList) <= 4096 - 256, "kernel arguments are limited to 4 KiB");
 
-// Default copy variant (unroll 4, global nt, 256 threads, one slice per wave).
+// One slice of kCopySliceBytes per wave, 256-thread workgroups.
 hipError_t launch_copy_runs_kernarg(const KernargRunList& list, hipStream_t stream);
 
 hipError_t launch_copy_runs(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
-                            uint64_t page_bytes, const LaunchShape& shape, hipStream_t stream);
+                            uint64_t page_bytes, const LaunchEvents& events, hipStream_t stream);
 
 hipError_t launch_copy_runs_fp8(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
                                 uint64_t page_bytes, uint32_t lanes_per_row,
                                 uint32_t rows_per_plane, uint32_t kv_heads,
                                 uint32_t rows_per_page, bool table, const float* amax_table,
-                                const LaunchShape& shape, hipStream_t stream);
+                                const LaunchEvents& events, hipStream_t stream);
 
 hipError_t launch_copy_ops(const DevOp* ops, uint32_t n_ops, hipStream_t stream);
 

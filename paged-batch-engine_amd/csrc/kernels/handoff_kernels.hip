@@ -7,11 +7,11 @@
 // 16-byte vectors x kUnroll. A run is contiguous on both sides across all of
 // its pages (page = every layer's K and V planes, shared_kv_arena.h:35-36), so
 // a slice never needs page or layer arithmetic: it is a contiguous byte span.
-// Each wave owns a contiguous range of slices, finds its first run with a
-// wave-parallel search over the device run list and then walks runs forward.
-// Loads and stores are non-temporal: the source pages are dead after the
-// handoff and the destination is not read until the next decode step, so
-// neither should evict the decode working set from L2 / MALL.
+// Each wave copies one slice and finds its run with a wave-parallel search
+// over the device run list. Loads and stores are non-temporal: the source
+// pages are dead after the handoff and the destination is not read until the
+// next decode step, so neither should evict the decode working set from L2 /
+// MALL.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -37,9 +37,6 @@ constexpr int kWavesPerBlock = kThreadsPerBlock / kWave;
 __device__ __forceinline__ u32x4 ld16(gsrc_t p, uint32_t off) {
   return __builtin_nontemporal_load(reinterpret_cast<PBE_GLOBAL const u32x4*>(p + off));
 }
-__device__ __forceinline__ void st16(gdst_t p, uint32_t off, u32x4 v) {
-  __builtin_nontemporal_store(v, reinterpret_cast<PBE_GLOBAL u32x4*>(p + off));
-}
 __device__ __forceinline__ void st8(gdst_t p, uint32_t off, u32x2 v) {
   __builtin_nontemporal_store(v, reinterpret_cast<PBE_GLOBAL u32x2*>(p + off));
 }
@@ -61,100 +58,56 @@ __device__ __forceinline__ uint32_t find_run(const DevRun* __restrict__ runs, ui
   }
 }
 
-// Cache policy of a copy variant. kGlobalNt uses global_load/store with the
-// non-temporal bit; the others use buffer instructions with explicit gfx950
-// cache-policy bits (bit0 sc0, bit1 nt, bit4 sc1) on loads / stores.
-struct PolicyBits {
-  bool buffer;
-  int load_aux;
-  int store_aux;
-};
-constexpr PolicyBits kPolicies[] = {
-    {false, 0, 0},        // 0: global_* nt / nt
-    {true, 0x02, 0x02},   // 1: buffer nt / nt
-    {true, 0x03, 0x03},   // 2: buffer sc0 nt
-    {true, 0x12, 0x12},   // 3: buffer sc1 nt
-    {true, 0x13, 0x13},   // 4: buffer sc0 sc1 nt
-    {true, 0x11, 0x11},   // 5: buffer sc0 sc1
-    {true, 0x02, 0x13},   // 6: load nt, store sc0 sc1 nt
-    {true, 0x13, 0x02},   // 7: load sc0 sc1 nt, store nt
-    {true, 0x00, 0x00},   // 8: buffer default policy
-    {true, 0x12, 0x02},   // 9: load sc1 nt, store nt
-    {true, 0x02, 0x12},   // 10: load nt, store sc1 nt
-};
-constexpr int kNumPolicies = sizeof(kPolicies) / sizeof(kPolicies[0]);
+// Cache policy bits of gfx950 buffer instructions (bit0 sc0, bit1 nt,
+// bit4 sc1). Loads stream (nt): the source pages are dead after the handoff.
+// Stores are sc1 + nt: written through without allocating, so the copy does
+// not evict the decode working set; measured on MI355X 1-2% faster than
+// global nt stores and 50% faster than stores without nt.
+constexpr int kLoadPolicy = 0x02;
+constexpr int kStorePolicy = 0x12;
 
-template <int kUnroll, int kPolicy>
-__device__ __forceinline__ void copy_slice(uint64_t src, uint64_t dst, uint64_t nbytes,
-                                           uint32_t lane) {
-  constexpr uint32_t kSlice = kWave * 16u * kUnroll;
-  constexpr PolicyBits pol = kPolicies[kPolicy];
-  if constexpr (!pol.buffer) {
-    gsrc_t s = reinterpret_cast<gsrc_t>(src);
-    gdst_t d = reinterpret_cast<gdst_t>(dst);
-    if (nbytes >= kSlice) {
-      u32x4 v[kUnroll];
+// One slice: every lane moves kCopyUnroll 16-byte vectors, all loads issued
+// before the first store. Buffer resources clamp to the slice, so a short
+// last slice of a run needs no per-lane bound test: out-of-range lanes read 0
+// and the hardware drops their stores.
+__device__ __forceinline__ void copy_slice(uint64_t src, uint64_t dst, uint64_t nbytes, uint32_t lane) {
+  const uint32_t n = nbytes >= kCopySliceBytes ? kCopySliceBytes : (uint32_t)nbytes;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(src), (short)0, n, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rd =
+      __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(dst), (short)0, n, 0x00020000);
+  u32x4 v[kCopyUnroll];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) v[u] = ld16(s, (u * kWave + lane) * 16u);
+  for (int u = 0; u < kCopyUnroll; ++u)
+    v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, (u * kWave + lane) * 16u, 0, kLoadPolicy);
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) st16(d, (u * kWave + lane) * 16u, v[u]);
-    } else {
-      // Last, partial slice of a run: rare, so keep it small rather than wide.
-      for (uint32_t off = lane * 16u; off < nbytes; off += kWave * 16u) st16(d, off, ld16(s, off));
-    }
-  } else {
-    // Buffer resources clamp to the slice: out-of-range lanes read 0 and
-    // their stores are dropped by the hardware, so no per-lane bound test.
-    const uint32_t n = nbytes >= kSlice ? kSlice : (uint32_t)nbytes;
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(src), (short)0, n, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rd =
-        __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(dst), (short)0, n, 0x00020000);
-    u32x4 v[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
-      v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, (u * kWave + lane) * 16u, 0, pol.load_aux);
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
-      __builtin_amdgcn_raw_buffer_store_b128(v[u], rd, (u * kWave + lane) * 16u, 0, pol.store_aux);
-  }
+  for (int u = 0; u < kCopyUnroll; ++u)
+    __builtin_amdgcn_raw_buffer_store_b128(v[u], rd, (u * kWave + lane) * 16u, 0, kStorePolicy);
 }
 
 // Identity copy of every run: the device form of the reference's per-run
-// cudaMemcpyAsync loop (split_pd_engine.cpp:96-108). Wave w copies the
-// contiguous slice range [w*k, (w+1)*k) (k = slices_per_wave).
-template <int kUnroll, int kPolicy, int kBlock>
+// cudaMemcpyAsync loop (split_pd_engine.cpp:96-108). Wave w copies global
+// slice w; it finds its run with the wave-parallel search over the run list.
 __device__ __forceinline__ void copy_runs_body(const DevRun* __restrict__ runs, uint32_t n_runs,
-                                               uint32_t total_slices, uint32_t slices_per_wave,
-                                               uint64_t page_bytes) {
-  constexpr uint32_t kSlice = kWave * 16u * kUnroll;
+                                               uint32_t total_slices, uint64_t page_bytes) {
   const uint32_t lane = threadIdx.x % kWave;
-  const uint32_t wave = blockIdx.x * (kBlock / kWave) + threadIdx.x / kWave;
-  uint32_t s = wave * slices_per_wave;
-  const uint32_t s_end = min(s + slices_per_wave, total_slices);
-  if (s >= s_end) return;
-  uint32_t r = find_run(runs, 0, n_runs, s, lane);
-  for (; s < s_end; ++s) {
-    if (r + 1 < n_runs && runs[r + 1].slice_begin <= s) r = find_run(runs, r + 1, n_runs, s, lane);
-    const DevRun& run = runs[r];
-    const uint64_t rel = (uint64_t)(s - run.slice_begin) * kSlice;
-    const uint64_t run_bytes = (uint64_t)run.pages * page_bytes;
-    copy_slice<kUnroll, kPolicy>(run.src + rel, run.dst + rel, run_bytes - rel, lane);
-  }
+  const uint32_t s = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+  if (s >= total_slices) return;
+  const uint32_t r = find_run(runs, 0, n_runs, s, lane);
+  const DevRun& run = runs[r];
+  const uint64_t rel = (uint64_t)(s - run.slice_begin) * kCopySliceBytes;
+  copy_slice(run.src + rel, run.dst + rel, (uint64_t)run.pages * page_bytes - rel, lane);
 }
 
-template <int kUnroll, int kPolicy, int kBlock>
-__global__ __launch_bounds__(kBlock) void copy_runs_kernel(
-    const DevRun* __restrict__ runs, uint32_t n_runs, uint32_t total_slices,
-    uint32_t slices_per_wave, uint64_t page_bytes) {
-  copy_runs_body<kUnroll, kPolicy, kBlock>(runs, n_runs, total_slices, slices_per_wave, page_bytes);
+__global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_kernel(
+    const DevRun* __restrict__ runs, uint32_t n_runs, uint32_t total_slices, uint64_t page_bytes) {
+  copy_runs_body(runs, n_runs, total_slices, page_bytes);
 }
 
 // The same copy with the run list in the kernel arguments (no staging copy).
 // An aggregate kernel argument stays in the kernarg segment and is read there.
 __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_kernarg_kernel(const KernargRunList list) {
-  copy_runs_body<kCopyUnroll, kCopyPolicy, kThreadsPerBlock>(list.runs, list.n_runs, list.total_slices, 1u,
-                                                   list.page_bytes);
+  copy_runs_body(list.runs, list.n_runs, list.total_slices, list.page_bytes);
 }
 
 // ---- FP8 E4M3 (OCP v1.0, "fn": no infinities, 0x7F NaN, max 448) ----
@@ -254,7 +207,7 @@ __device__ __forceinline__ float group_max(float m) {
 //   per-token-head: amax over the row, scale = amax/448 | 1, inv = 448/amax | 0
 //                   (scatter_kv_kernel.cu:166-190), scale written per row;
 //   table:          amax = table[(2*layer+kv)*heads + head], nothing written.
-template <int kUnroll, int kLanesPerRow, bool kTable>
+template <int kLanesPerRow, bool kTable>
 __device__ __forceinline__ void fp8_step(const u32x4& v, uint32_t row, uint32_t lane,
                                          gdst_t dst, uint32_t dst_off, uint64_t scales,
                                          uint32_t rows_per_plane, uint32_t kv_heads,
@@ -275,23 +228,20 @@ __device__ __forceinline__ void fp8_step(const u32x4& v, uint32_t row, uint32_t 
   st8(dst, dst_off, quantise8(v, inv));
 }
 
-template <int kUnroll, int kLanesPerRow, bool kTable>
+template <int kLanesPerRow, bool kTable>
 __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_fp8_kernel(
-    const DevRun* __restrict__ runs, uint32_t n_runs, uint32_t total_slices,
-    uint32_t slices_per_wave, uint64_t page_bytes, uint32_t rows_per_plane,
-    uint32_t kv_heads, uint32_t rows_per_page, const float* __restrict__ amax_table) {
-  constexpr uint32_t kSlice = kWave * 16u * kUnroll;    // source bytes per slice
+    const DevRun* __restrict__ runs, uint32_t n_runs, uint32_t total_slices, uint64_t page_bytes,
+    uint32_t rows_per_plane, uint32_t kv_heads, uint32_t rows_per_page,
+    const float* __restrict__ amax_table) {
+  constexpr int kUnroll = kFp8Unroll;
+  constexpr uint32_t kSlice = kFp8SliceBytes;           // source bytes per slice
   constexpr uint32_t kRowBytes = kLanesPerRow * 16u;     // source bytes per row
   constexpr uint32_t kRowsPerStep = kWave / kLanesPerRow;
   const uint32_t lane = threadIdx.x % kWave;
-  const uint32_t wave = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
-  const uint32_t s_begin = wave * slices_per_wave;
-  if (s_begin >= total_slices) return;
-  const uint32_t s_end = min(s_begin + slices_per_wave, total_slices);
-  uint32_t r = find_run(runs, 0, n_runs, s_begin, lane);
-  for (uint32_t s = s_begin; s < s_end; ++s) {
-    if (r + 1 < n_runs && runs[r + 1].slice_begin <= s) r = find_run(runs, r + 1, n_runs, s, lane);
-    r = __builtin_amdgcn_readfirstlane(r);
+  const uint32_t s = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+  if (s >= total_slices) return;
+  {
+    const uint32_t r = __builtin_amdgcn_readfirstlane(find_run(runs, 0, n_runs, s, lane));
     const DevRun& run = runs[r];
     const uint64_t rel = (uint64_t)(s - run.slice_begin) * kSlice;
     const uint64_t nbytes = (uint64_t)run.pages * page_bytes - rel;
@@ -341,7 +291,7 @@ __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_fp8_kernel(
       } else {
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u)
-          fp8_step<kUnroll, kLanesPerRow, kTable>(v[u], row0 + u * kRowsPerStep, lane, dst,
+          fp8_step<kLanesPerRow, kTable>(v[u], row0 + u * kRowsPerStep, lane, dst,
                                                   (u * kWave + lane) * 8u, scales, rows_per_plane,
                                                   kv_heads, rows_per_page, amax_table);
       }
@@ -352,7 +302,7 @@ __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_fp8_kernel(
         const uint32_t off = (u * kWave + lane) * 16u;
         const u32x4 v = off < nbytes ? ld16(src, off) : u32x4{0u, 0u, 0u, 0u};
         if (off < nbytes)
-          fp8_step<kUnroll, kLanesPerRow, kTable>(v, row0 + u * kRowsPerStep, lane, dst, off / 2,
+          fp8_step<kLanesPerRow, kTable>(v, row0 + u * kRowsPerStep, lane, dst, off / 2,
                                                   scales, rows_per_plane, kv_heads,
                                                   rows_per_page, amax_table);
       }
@@ -400,102 +350,54 @@ __global__ __launch_bounds__(kThreadsPerBlock) void copy_ops_kernel(
 
 }  // namespace
 
-uint32_t slice_bytes(KernelKind kind, const CopyConfig& cfg) {
-  (void)kind;
-  return kWave * 16u * (uint32_t)cfg.unroll;
-}
-
-namespace {
-struct CopyArgs {
-  uint32_t waves;
-  uint32_t lds_bytes;
-  hipStream_t stream;
-  const DevRun* runs;
-  uint32_t n_runs, total_slices, slices_per_wave;
-  uint64_t page_bytes;
-  hipEvent_t start, stop;
-};
-template <int U, int P, int B>
-void launch_variant(const CopyArgs& a) {
-  const uint32_t blocks = (a.waves + B / kWave - 1) / (B / kWave);
-  hipExtLaunchKernelGGL((copy_runs_kernel<U, P, B>), dim3(blocks), dim3(B), a.lds_bytes, a.stream,
-                        a.start, a.stop, 0, a.runs, a.n_runs, a.total_slices, a.slices_per_wave,
-                        a.page_bytes);
-}
-template <int U, int P>
-bool pick_block(const CopyConfig& c, const CopyArgs& a) {
-  switch (c.block) {
-    case 64: launch_variant<U, P, 64>(a); return true;
-    case 256: launch_variant<U, P, 256>(a); return true;
-    case 1024: launch_variant<U, P, 1024>(a); return true;
-    default: return false;
-  }
-}
-template <int U, int P = 0>
-bool pick_policy(const CopyConfig& c, const CopyArgs& a) {
-  if constexpr (P >= kNumPolicies) {
-    return false;
-  } else {
-    if (c.policy == P) return pick_block<U, P>(c, a);
-    return pick_policy<U, P + 1>(c, a);
-  }
-}
-}  // namespace
-
 hipError_t launch_copy_runs_kernarg(const KernargRunList& list, hipStream_t stream) {
   if (list.n_runs == 0 || list.n_runs > kKernargRuns) return hipErrorInvalidValue;
   const uint32_t waves = list.total_slices ? list.total_slices : 1u;
-  const uint32_t per_block = kThreadsPerBlock / kWave;
-  hipLaunchKernelGGL(copy_runs_kernarg_kernel, dim3((waves + per_block - 1) / per_block),
+  hipLaunchKernelGGL(copy_runs_kernarg_kernel, dim3((waves + kWavesPerBlock - 1) / kWavesPerBlock),
                      dim3(kThreadsPerBlock), 0, stream, list);
   return hipGetLastError();
 }
 
 hipError_t launch_copy_runs(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
-                            uint64_t page_bytes, const LaunchShape& shape, hipStream_t stream) {
-  const CopyConfig& c = shape.copy;
-  uint32_t waves = (total_slices + shape.slices_per_wave - 1) / shape.slices_per_wave;
-  if (waves == 0) waves = 1;
-  const CopyArgs a{waves, c.lds_bytes, stream, runs, n_runs, total_slices, shape.slices_per_wave,
-                   page_bytes, shape.start, shape.stop};
-  bool ok = false;
-  switch (c.unroll) {
-    case 2: ok = pick_policy<2>(c, a); break;
-    case 4: ok = pick_policy<4>(c, a); break;
-    case 8: ok = pick_policy<8>(c, a); break;
-    default: break;
-  }
-  if (!ok) return hipErrorInvalidValue;
+                            uint64_t page_bytes, const LaunchEvents& ev, hipStream_t stream) {
+  const uint32_t waves = total_slices ? total_slices : 1u;
+  hipExtLaunchKernelGGL(copy_runs_kernel, dim3((waves + kWavesPerBlock - 1) / kWavesPerBlock),
+                        dim3(kThreadsPerBlock), 0, stream, ev.start, ev.stop, 0, runs, n_runs,
+                        total_slices, page_bytes);
   return hipGetLastError();
 }
 
 namespace {
-template <int U, int L>
-void launch_fp8(bool table, uint32_t blocks, hipStream_t stream, hipEvent_t start, hipEvent_t stop,
-                const DevRun* runs,
-                uint32_t n_runs, uint32_t total_slices, uint32_t spw, uint64_t page_bytes,
+template <int L>
+void launch_fp8(bool table, uint32_t blocks, hipStream_t stream, const LaunchEvents& ev,
+                const DevRun* runs, uint32_t n_runs, uint32_t total_slices, uint64_t page_bytes,
                 uint32_t rows_per_plane, uint32_t kv_heads, uint32_t rows_per_page,
                 const float* amax_table) {
   if (table)
-    hipExtLaunchKernelGGL((copy_runs_fp8_kernel<U, L, true>), dim3(blocks), dim3(kThreadsPerBlock),
-                          0, stream, start, stop, 0, runs, n_runs, total_slices, spw,
-                          page_bytes, rows_per_plane, kv_heads, rows_per_page, amax_table);
+    hipExtLaunchKernelGGL((copy_runs_fp8_kernel<L, true>), dim3(blocks), dim3(kThreadsPerBlock), 0,
+                          stream, ev.start, ev.stop, 0, runs, n_runs, total_slices, page_bytes,
+                          rows_per_plane, kv_heads, rows_per_page, amax_table);
   else
-    hipExtLaunchKernelGGL((copy_runs_fp8_kernel<U, L, false>), dim3(blocks), dim3(kThreadsPerBlock),
-                          0, stream, start, stop, 0, runs, n_runs, total_slices, spw,
-                          page_bytes, rows_per_plane, kv_heads, rows_per_page, amax_table);
+    hipExtLaunchKernelGGL((copy_runs_fp8_kernel<L, false>), dim3(blocks), dim3(kThreadsPerBlock), 0,
+                          stream, ev.start, ev.stop, 0, runs, n_runs, total_slices, page_bytes,
+                          rows_per_plane, kv_heads, rows_per_page, amax_table);
 }
-template <int U>
-bool launch_fp8_lanes(uint32_t lanes, bool table, uint32_t blocks, hipStream_t stream,
-                      hipEvent_t start, hipEvent_t stop, const DevRun* runs, uint32_t n_runs, uint32_t total_slices, uint32_t spw,
-                      uint64_t page_bytes, uint32_t rows_per_plane, uint32_t kv_heads,
-                      uint32_t rows_per_page, const float* amax_table) {
-#define PBE_FP8_CASE(L)                                                                       \
-  case L:                                                                                     \
-    launch_fp8<U, L>(table, blocks, stream, start, stop, runs, n_runs, total_slices, spw,     \
-                     page_bytes, rows_per_plane, kv_heads, rows_per_page, amax_table);        \
-    return true;
-  switch (lanes) {
+}  // namespace
+
+hipError_t launch_copy_runs_fp8(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
+                                uint64_t page_bytes, uint32_t lanes_per_row,
+                                uint32_t rows_per_plane, uint32_t kv_heads,
+                                uint32_t rows_per_page, bool table, const float* amax_table,
+                                const LaunchEvents& ev, hipStream_t stream) {
+  const uint32_t waves = total_slices ? total_slices : 1u;
+  const uint32_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
+  // One instantiation per row width (head_dim / 8 lanes), a shape, not a tuning choice.
+#define PBE_FP8_CASE(L)                                                                      \
+  case L:                                                                                    \
+    launch_fp8<L>(table, blocks, stream, ev, runs, n_runs, total_slices, page_bytes,         \
+                  rows_per_plane, kv_heads, rows_per_page, amax_table);                      \
+    return hipGetLastError();
+  switch (lanes_per_row) {
     PBE_FP8_CASE(1)
     PBE_FP8_CASE(2)
     PBE_FP8_CASE(4)
@@ -504,44 +406,9 @@ bool launch_fp8_lanes(uint32_t lanes, bool table, uint32_t blocks, hipStream_t s
     PBE_FP8_CASE(32)
     PBE_FP8_CASE(64)
     default:
-      return false;
+      return hipErrorInvalidValue;
   }
 #undef PBE_FP8_CASE
-}
-}  // namespace
-
-hipError_t launch_copy_runs_fp8(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
-                                uint64_t page_bytes, uint32_t lanes_per_row,
-                                uint32_t rows_per_plane, uint32_t kv_heads,
-                                uint32_t rows_per_page, bool table, const float* amax_table,
-                                const LaunchShape& shape, hipStream_t stream) {
-  const uint32_t waves = (total_slices + shape.slices_per_wave - 1) / shape.slices_per_wave;
-  const uint32_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
-  bool ok = false;
-  switch (shape.copy.unroll) {
-    case 2:
-      ok = launch_fp8_lanes<2>(lanes_per_row, table, blocks, stream, shape.start, shape.stop, runs,
-                               n_runs, total_slices,
-                               shape.slices_per_wave, page_bytes, rows_per_plane, kv_heads,
-                               rows_per_page, amax_table);
-      break;
-    case 4:
-      ok = launch_fp8_lanes<4>(lanes_per_row, table, blocks, stream, shape.start, shape.stop, runs,
-                               n_runs, total_slices,
-                               shape.slices_per_wave, page_bytes, rows_per_plane, kv_heads,
-                               rows_per_page, amax_table);
-      break;
-    case 8:
-      ok = launch_fp8_lanes<8>(lanes_per_row, table, blocks, stream, shape.start, shape.stop, runs,
-                               n_runs, total_slices,
-                               shape.slices_per_wave, page_bytes, rows_per_plane, kv_heads,
-                               rows_per_page, amax_table);
-      break;
-    default:
-      break;
-  }
-  if (!ok) return hipErrorInvalidValue;
-  return hipGetLastError();
 }
 
 hipError_t launch_copy_ops(const DevOp* ops, uint32_t n_ops, hipStream_t stream) {
