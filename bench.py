@@ -43,6 +43,17 @@ def _traffic_from_profile():
     return float(m.group(1)) if m else None
 
 
+def _cpu_model() -> str:
+    """The host CPU's model name from /proc/cpuinfo."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(w, host_arena, seconds: float):
     """Reference-faithful host copy: coalesce + one memcpy per run, 1 thread."""
     from oracle import oracle as O
@@ -85,9 +96,11 @@ def cpu_baseline(w, host_arena, seconds: float):
         rel = time.perf_counter() - t0
         rper = rel / rreps
         ref = {"value": round(w.algorithmic_bytes() / rper / 1e9, 3), "unit": "GB/s", "cores": 1,
-               "kind": "reference", "ms_per_handoff": round(rper * 1e3, 3),
+               "kind": "reference-with-glog-stub", "ms_per_handoff": round(rper * 1e3, 3),
                "what": "the reference's TransferPlanner + per-page BoundTransfer::BindComponents + "
-                       "ExecuteCpuTransfer (pd_handoff.cpp:192-213), compiled from its sources",
+                       "ExecuteCpuTransfer (pd_handoff.cpp:192-213), compiled from its sources "
+                       "against the glog stand-in of its own CPU tests (test/cache_core/stubs): "
+                       "a timing of the reference's code, not a parity pin",
                "same_bytes_as_port": bool(ok and np.array_equal(host_arena, after_port)),
                "sample": f"{rreps} handoffs in {rel:.1f} s"}
         # the same driver over this repository's drop-in TransferPlanner / BoundTransfer
@@ -546,6 +559,7 @@ def main() -> int:
     if not args.no_cpu:
         cpu = cpu_baseline(w, host_before, args.cpu_seconds)
         cpu["cores_on_host"] = os.cpu_count()
+        cpu["cpu_model"] = _cpu_model()
 
     traffic = _traffic_from_profile()
     line = {

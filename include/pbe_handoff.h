@@ -303,8 +303,12 @@ int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream
  * memory, used by this launch until it completes. Asynchronous on `stream`. */
 #define PBE_KV_BF16 0
 #define PBE_KV_FP8_E4M3 1
-/* Split count for a decode launch: kv_dtype as for pbe_paged_decode (FP8
- * pages run two waves per SIMD, BF16 pages one). Size the workspace with it. */
+/* Split count for a decode launch on the current GPU (its CU count sets the
+ * wave budget): kv_dtype as for pbe_paged_decode (FP8 pages run two waves per
+ * SIMD, BF16 pages one). max_blocks_per_seq here should be the block count of
+ * the longest live sequence, not the block-table capacity: a table sized for
+ * the maximum context would pick splits too short to keep the reader busy.
+ * Size the workspace with the result. */
 int32_t pbe_paged_decode_splits(int32_t batch, int32_t kv_heads, int32_t max_blocks_per_seq,
                                 int32_t kv_dtype);
 uint64_t pbe_paged_decode_workspace_bytes(int32_t batch, int32_t q_heads, int32_t head_dim,

@@ -238,6 +238,34 @@ int pbe_device_uuid(int device, uint8_t out[16]) {
   return PBE_OK;
 }
 
+}  // extern "C"
+
+namespace {
+// Compute units of the calling thread's current GPU (256 on MI355X), cached
+// per device; 256 when the runtime cannot say.
+int64_t decode_cus() {
+  static std::mutex mu;
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+      (void)hipGetLastError();
+      n = 256;
+    }
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+}  // namespace
+
+extern "C" {
+
 int pbe_current_device(int* device) {
   if (!device) return fail(PBE_ERR_INVALID, "null output");
   PBE_HIP(hipGetDevice(device));
@@ -1009,6 +1037,19 @@ int stage(Staging& st, const void* data, size_t bytes, hipStream_t stream, Stagi
   return PBE_OK;
 }
 
+// The staging ring reuses its buffers after four calls: a graph captured with
+// a staged list would replay stale or freed memory, so staged calls refuse a
+// stream that is being captured (prebuilt run lists are the capturable form).
+int refuse_capture(hipStream_t stream, const char* what) {
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  PBE_HIP(hipStreamIsCapturing(stream, &status));
+  if (status != hipStreamCaptureStatusNone)
+    return fail(PBE_ERR_UNSUPPORTED,
+                "%s stages its list per call and cannot be captured into a graph; capture "
+                "pbe_handoff_copy with a prebuilt run list instead", what);
+  return PBE_OK;
+}
+
 int stage_done(StagingSlot& sl, hipStream_t stream) {
   PBE_HIP(hipEventRecord(sl.done, stream));
   sl.pending = true;
@@ -1060,6 +1101,8 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
     if (copied) *copied = res.info.src_bytes;
     return PBE_OK;
   }
+  rc = refuse_capture(s, "pbe_copy_shared_kv with more than 112 runs");
+  if (rc != PBE_OK) return rc;
   Staging& st = staging_for(device);
   std::lock_guard<std::mutex> lock(st.mu);
   void* dev = nullptr;
@@ -1078,18 +1121,20 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
 int32_t pbe_paged_decode_splits(int32_t batch, int32_t kv_heads, int32_t max_blocks_per_seq,
                                 int32_t kv_dtype) {
   if (batch <= 0 || kv_heads <= 0 || max_blocks_per_seq <= 0) return 1;
-  // At most 1024 waves (one per SIMD), rounded down so no partial extra round
-  // of waves trails the launch; FP8 pages take 2048 (two per SIMD) when every
-  // split still holds at least 16 blocks; at least 4 blocks (64 tokens) per
-  // split. Measured on MI355X, 5040-token sequences, both launches: FP8 batch
-  // 64 at 16 splits 35.7 us stage 1 against 40.9 us at 8; batch 128: 8 splits
-  // 66.7 us against 74.5 us at 4; batch 32: 16 splits 28.9 us against 30.8 us
-  // at 32; batch 16: 32 splits 22.9 us against 27.9 us at 64. BF16 batch 64:
-  // 54.6 us stage 1 at 8 splits against 56.5 us at 16.
+  // One wave per SIMD (4 per CU) of the current GPU, rounded down so no
+  // partial extra round of waves trails the launch; FP8 pages take two per
+  // SIMD when every split still holds at least 16 blocks; at least 4 blocks
+  // (64 tokens) per split. Measured on MI355X (256 CUs), 5040-token
+  // sequences, both launches: FP8 batch 64 at 16 splits 35.7 us stage 1
+  // against 40.9 us at 8; batch 128: 8 splits 66.7 us against 74.5 us at 4;
+  // batch 32: 16 splits 28.9 us against 30.8 us at 32; batch 16: 32 splits
+  // 22.9 us against 27.9 us at 64. BF16 batch 64: 54.6 us stage 1 at 8
+  // splits against 56.5 us at 16.
+  const int64_t simds = 4ll * decode_cus();
   const int64_t units = (int64_t)batch * kv_heads;
-  int64_t splits = std::max<int64_t>(1, 1024 / units);
+  int64_t splits = std::max<int64_t>(1, simds / units);
   if (kv_dtype == PBE_KV_FP8_E4M3) {
-    const int64_t two = std::max<int64_t>(1, 2048 / units);
+    const int64_t two = std::max<int64_t>(1, 2 * simds / units);
     if ((max_blocks_per_seq + two - 1) / two >= 16) splits = two;
   }
   splits = std::min<int64_t>(splits, (max_blocks_per_seq + 3) / 4);
@@ -1280,12 +1325,14 @@ int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream
       pieces.push_back({ops[i].src + off, ops[i].dst + off,
                         std::min<uint64_t>(pbe::kOpPieceBytes, ops[i].bytes - off)});
   if (pieces.size() > 0xffffffffull) return fail(PBE_ERR_INVALID, "op list too large");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = refuse_capture(s, "pbe_copy_ops");
+  if (rc != PBE_OK) return rc;
   Staging& st = staging_for(device);
   std::lock_guard<std::mutex> lock(st.mu);
-  const hipStream_t s = static_cast<hipStream_t>(stream);
   void* dev = nullptr;
   StagingSlot* slot = nullptr;
-  int rc = stage(st, pieces.data(), pieces.size() * sizeof(pbe::DevOp), s, &slot, &dev);
+  rc = stage(st, pieces.data(), pieces.size() * sizeof(pbe::DevOp), s, &slot, &dev);
   if (rc != PBE_OK) return rc;
   PBE_HIP(pbe::launch_copy_ops(static_cast<const pbe::DevOp*>(dev), (uint32_t)pieces.size(), s));
   return stage_done(*slot, s);

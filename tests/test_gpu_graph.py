@@ -71,3 +71,46 @@ def test_decode_step_replays_from_a_graph(torch_cuda):
         torch.cuda.synchronize()
         got = (case.out.cpu().numpy().view(np.uint16).astype(np.uint32) << 16).view(np.float32)
         assert close(got.astype(np.float64), want).all(), rep
+
+
+def test_staged_calls_refuse_capture(torch_cuda):
+    """pbe_copy_ops and a staged pbe_copy_shared_kv (more than 112 runs) stage
+    their lists in a reused ring, so under capture they return
+    PBE_ERR_UNSUPPORTED before queueing anything; the prebuilt run list
+    captured in the same graph still replays correctly."""
+    torch = torch_cuda
+    w = W.small(seed=9, layers=2, kv_heads=2, head_dim=64, n_pages=640, handoff_pages=150,
+                max_run=1)
+    g = w.geometry
+    kv = P.shape(g.layers, g.kv_heads, g.head_dim, g.page_tokens)
+    say("staged calls under graph capture are refused")
+    arena = torch.empty(w.arena_bytes, dtype=torch.uint8, device="cuda")
+    view = P.view_of(arena.data_ptr(), arena.numel())
+    runs = P.build_runs(w.src_ids, w.dst_ids, kv)
+    assert len(runs) > 112
+    rl = P.RunList.bf16(view, view, runs, kv)
+    half = g.half()
+    base = arena.data_ptr()
+    ops = P.op_array([(base + int(s) * half, base + int(d) * half, half)
+                      for s, d in zip(w.src_ids[:4].tolist(), w.dst_ids[:4].tolist())])
+    fill_bf16(torch, arena, 1.0, 3)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            with pytest.raises(P.PbeError, match="captured"):
+                P.copy_ops(ops, 0, side.cuda_stream)
+            with pytest.raises(P.PbeError, match="captured"):
+                P.copy_shared_kv(view, w.src_ids, w.dst_ids, kv, 0, side.cuda_stream)
+            rl.copy(side.cuda_stream)
+    torch.cuda.synchronize()
+    expected = arena.cpu().numpy().copy()
+    O.copy_handoff(expected, w.src_ids, w.dst_ids, g.half(), g.layers)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert np.array_equal(arena.cpu().numpy(), expected)
+    # outside capture the same calls work
+    P.copy_ops(ops, 0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    rl.close()

@@ -249,6 +249,7 @@ def test_fp8_token_head_properties(head_dim):
     table = np.array([O.e4m3_to_f32(c) for c in range(256)], np.float32)
     sc_page = 2 * g.layers * g.page_tokens * g.kv_heads
     written = set()
+    divided = []
     for sp, dp in zip((w.src_ids // g.stride).tolist(), (w.dst_ids // g.stride).tolist()):
         x = _rows(src, g, sp, 2, np.uint16).astype(np.uint32) << 16
         x = x.view(np.float32)
@@ -265,10 +266,21 @@ def test_fp8_token_head_properties(head_dim):
         assert np.all(err <= bound)
         peak = q[np.abs(x) == amax[..., None]]
         assert np.all((peak & 0x7F) == 0x7E)
+        # element by element, in the reference's order (scatter_kv_kernel.cu:
+        # 205-206): inv = 448/amax once per row in fp32, then e4m3(x * inv)
+        # through the independently pinned scalar conversion
+        inv = np.where(amax > 0, np.float32(448) / np.where(amax > 0, amax, 1), 0).astype(np.float32)
+        prod = (x * inv[..., None]).astype(np.float32)
+        assert np.array_equal(q, O.e4m3_from_f32(prod))
+        # dividing by the stored scale instead rounds some elements differently
+        by_scale = (x / s[..., None]).astype(np.float32)
+        divided.append(O.e4m3_from_f32(by_scale) != q)
         written.add(dp)
     untouched = [p for p in range(48) if p not in written]
     for p in untouched:
         assert not _rows(dst, g, p, 1, np.uint8).any()
+    # the element-wise check above tells the two orders apart on this data
+    assert any(d.any() for d in divided)
 
 
 def test_fp8_table_mode_matches_elementwise_conversion():
