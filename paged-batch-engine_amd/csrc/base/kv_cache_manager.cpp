@@ -193,6 +193,10 @@ BlockAllocator& KVCacheManager::allocator_mut(int32_t layer_idx) {
   return *layers_[layer_idx];
 }
 
+void KVCacheManager::set_radix_cache_enabled(bool enabled) {
+  if (enabled) throw std::invalid_argument("this KV cache manager has no radix prefix cache");
+}
+
 int32_t KVCacheManager::num_free_blocks(int32_t layer_idx) const { return allocator(layer_idx).num_free_blocks(); }
 int32_t KVCacheManager::num_total_blocks(int32_t layer_idx) const { return allocator(layer_idx).num_total_blocks(); }
 

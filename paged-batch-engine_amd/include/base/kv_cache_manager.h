@@ -77,6 +77,11 @@ class KVCacheManager {
   int32_t num_free_blocks(int32_t layer_idx) const;
   int32_t num_total_blocks(int32_t layer_idx) const;
   int32_t num_active_requests() const { return active_; }
+  // This build has no radix prefix cache: the shared-arena setup's
+  // set_radix_cache_enabled(false) (qwen2.cpp:1137) is accepted, true throws
+  // std::invalid_argument.
+  void set_radix_cache_enabled(bool enabled);
+  bool radix_cache_enabled() const { return false; }
 
  private:
   struct Request {

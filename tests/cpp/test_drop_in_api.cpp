@@ -1300,6 +1300,8 @@ TEST_CASE("kv cache manager: append_slots grows page tables by ceil((n+k)/16) - 
   auto kv = manager_over(g.group);
   CHECK_EQ(kv->num_layers(), 3);
   CHECK_EQ(kv->block_size(), 16);
+  kv->set_radix_cache_enabled(false);  // the shared-arena setup's call (qwen2.cpp:1137)
+  CHECK_THROWS_AS(kv->set_radix_cache_enabled(true), std::invalid_argument);
   const base::RequestId a = kv->register_request();
   CHECK(kv->is_valid_request(a));
   CHECK(kv->append_slots(a, 41));  // 3 pages
