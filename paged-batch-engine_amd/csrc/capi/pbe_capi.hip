@@ -1300,30 +1300,49 @@ int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream
   if (n_ops < 0 || (n_ops && !ops) || n_ops > 0x7fffffff)
     return fail(PBE_ERR_INVALID, "invalid op list");
   if (!n_ops) return PBE_OK;
-  std::vector<std::pair<uint64_t, uint64_t>> dst, src;
-  for (int64_t i = 0; i < n_ops; ++i) {
-    if (!ops[i].src || !ops[i].dst || !ops[i].bytes)
-      return fail(PBE_ERR_INVALID, "op %lld: null pointer or zero bytes", (long long)i);
-    dst.emplace_back(ops[i].dst, ops[i].dst + ops[i].bytes);
-    src.emplace_back(ops[i].src, ops[i].src + ops[i].bytes);
-  }
-  if (!spans_disjoint(dst, src))
-    return fail(PBE_ERR_INVALID, "op list writes a byte twice or overwrites its own source");
   PBE_DEVICE_SCOPE(device);
+  // Every op's endpoints are checked as given; then ops that continue the
+  // previous one on both sides (the 2L component copies of one page, and
+  // consecutive pages of a run, in a bound manifest) are merged, so the
+  // overlap check, the staging and the kernel see runs instead of planes.
+  std::vector<pbe_copy_op> merged;
   {
     std::vector<Range> known;
-    for (int64_t i = 0; i < n_ops; ++i)
-      if (!accessible(reinterpret_cast<const void*>(ops[i].src), ops[i].bytes, device, &known) ||
-          !accessible(reinterpret_cast<const void*>(ops[i].dst), ops[i].bytes, device, &known))
-        return fail(PBE_ERR_INVALID, "op %lld: endpoint is not device or pinned memory",
-                    (long long)i);
+    for (int64_t i = 0; i < n_ops; ++i) {
+      const pbe_copy_op& o = ops[i];
+      if (!o.src || !o.dst || !o.bytes)
+        return fail(PBE_ERR_INVALID, "op %lld: null pointer or zero bytes", (long long)i);
+      if (o.bytes > ~0ull - o.src || o.bytes > ~0ull - o.dst)
+        return fail(PBE_ERR_INVALID, "op %lld: span wraps the address space", (long long)i);
+      if (!accessible(reinterpret_cast<const void*>(o.src), o.bytes, device, &known) ||
+          !accessible(reinterpret_cast<const void*>(o.dst), o.bytes, device, &known))
+        return fail(PBE_ERR_INVALID, "op %lld: endpoint is not device or pinned memory", (long long)i);
+      if (!merged.empty()) {
+        pbe_copy_op& last = merged.back();
+        if (last.src + last.bytes == o.src && last.dst + last.bytes == o.dst) {
+          last.bytes += o.bytes;
+          continue;
+        }
+      }
+      merged.push_back(o);
+    }
+  }
+  {
+    std::vector<std::pair<uint64_t, uint64_t>> dst, src;
+    dst.reserve(merged.size());
+    src.reserve(merged.size());
+    for (const pbe_copy_op& o : merged) {
+      dst.emplace_back(o.dst, o.dst + o.bytes);
+      src.emplace_back(o.src, o.src + o.bytes);
+    }
+    if (!spans_disjoint(dst, src))
+      return fail(PBE_ERR_INVALID, "op list writes a byte twice or overwrites its own source");
   }
   // Split large ops so that every wave moves at most kOpPieceBytes.
   std::vector<pbe::DevOp> pieces;
-  for (int64_t i = 0; i < n_ops; ++i)
-    for (uint64_t off = 0; off < ops[i].bytes; off += pbe::kOpPieceBytes)
-      pieces.push_back({ops[i].src + off, ops[i].dst + off,
-                        std::min<uint64_t>(pbe::kOpPieceBytes, ops[i].bytes - off)});
+  for (const pbe_copy_op& o : merged)
+    for (uint64_t off = 0; off < o.bytes; off += pbe::kOpPieceBytes)
+      pieces.push_back({o.src + off, o.dst + off, std::min<uint64_t>(pbe::kOpPieceBytes, o.bytes - off)});
   if (pieces.size() > 0xffffffffull) return fail(PBE_ERR_INVALID, "op list too large");
   const hipStream_t s = static_cast<hipStream_t>(stream);
   int rc = refuse_capture(s, "pbe_copy_ops");
