@@ -1064,7 +1064,7 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
                        int64_t n, const pbe_kv_shape* shape, int device, void* stream,
                        uint64_t* copied) {
   if (copied) *copied = 0;
-  if (!view_ok(arena) || !shape_ok(shape) || n <= 0 || !src_ids || !dst_ids)
+  if (!view_ok(arena) || !shape_ok(shape) || n <= 0 || !src_ids || !dst_ids || device < 0)
     return fail(PBE_ERR_INVALID, "invalid handoff arguments");
   int64_t bad = -1;
   int rc = pbe_validate_ids(src_ids, n, shape, 2, arena->bytes, &bad);

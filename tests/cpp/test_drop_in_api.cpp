@@ -21,6 +21,7 @@
 #include "serving/decode_kv_reservation.h"
 #include "serving/pd_handoff.h"
 #include "serving/kv_page_wire.h"
+#include "serving/split_pd_handoff.h"
 #include "base/block_allocator.h"
 #include "base/kv_cache_manager.h"
 
@@ -1412,5 +1413,59 @@ TEST_CASE("block allocator: local pools, FIFO reuse and payload copy with scales
                   std::invalid_argument);
   CHECK_THROWS_AS(base::BlockAllocator(0, 16, 2, 8, base::DataType::kDataTypeBf16,
                                        base::DeviceType::kDeviceCPU),
+                  std::invalid_argument);
+}
+
+// ------------------------------------------------------------ copy_shared_kv in the reference's order
+
+namespace {
+serving::SharedKVPrefillResult prefill_result(uint64_t epoch, const std::vector<int32_t>& ids) {
+  serving::SharedKVPrefillResult r;
+  r.shared_arena_epoch = epoch;
+  r.client_request_id.value = "req";
+  r.handoff_id.value = 3;
+  r.prompt_tokens.assign(40, 1);
+  r.computed_tokens = 40;  // 3 pages
+  r.src_pool = pool3();
+  for (int l = 0; l < 3; ++l) r.layers.push_back({l, ids});
+  return r;
+}
+}  // namespace
+
+TEST_CASE("copy_shared_kv order: rejected inputs reserve nothing; a refused copy releases the pages") {
+  Group g(24, 24 * Group::kPage);  // metadata-only group: no device
+  auto kv = manager_over(g.group);
+  serving::DecodeKVReservation res;
+  const std::vector<int32_t> src{60, 66, 72};
+  auto bad = prefill_result(5, src);  // the arena's epoch is 9
+  CHECK_THROWS_AS(serving::CopySharedKVToDecode(kv.get(), pool3(), bad, nullptr, &res), std::runtime_error);
+  bad = prefill_result(9, src);
+  bad.layers.pop_back();
+  CHECK_THROWS_AS(serving::CopySharedKVToDecode(kv.get(), pool3(), bad, nullptr, &res), std::runtime_error);
+  bad = prefill_result(9, src);
+  bad.layers[1].layer_idx = 2;
+  CHECK_THROWS_AS(serving::CopySharedKVToDecode(kv.get(), pool3(), bad, nullptr, &res), std::runtime_error);
+  bad = prefill_result(9, {60, 66, 73});  // not a page id
+  CHECK_THROWS_AS(serving::CopySharedKVToDecode(kv.get(), pool3(), bad, nullptr, &res), std::runtime_error);
+  bad = prefill_result(9, src);
+  bad.layers[2].src_block_ids = {60, 72, 66};  // layers disagree
+  CHECK_THROWS_AS(serving::CopySharedKVToDecode(kv.get(), pool3(), bad, nullptr, &res), std::runtime_error);
+  bad = prefill_result(9, {60, 66, 24 * 6});  // past the arena
+  CHECK_THROWS_AS(serving::CopySharedKVToDecode(kv.get(), pool3(), bad, nullptr, &res), std::runtime_error);
+  CHECK_EQ(kv->num_active_requests(), 0);
+  CHECK(!res.valid());
+  // Valid input: the reservation is made, then the copy is refused (this
+  // group has no GPU mapping), so the reservation is released again.
+  try {
+    serving::CopySharedKVToDecode(kv.get(), pool3(), prefill_result(9, src), nullptr, &res);
+    CHECK(false);
+  } catch (const std::runtime_error& e) {
+    CHECK(std::string(e.what()).find("PD copy failed") != std::string::npos);
+  }
+  CHECK(!res.valid());
+  CHECK_EQ(kv->num_active_requests(), 0);
+  g.group->collect();
+  CHECK_EQ(g.owner->lease_count(), 0u);
+  CHECK_THROWS_AS(serving::CopySharedKVToDecode(nullptr, pool3(), prefill_result(9, src), nullptr, &res),
                   std::invalid_argument);
 }
