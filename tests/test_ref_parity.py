@@ -1,7 +1,11 @@
-"""The drop-in GlobalChunkAllocator and TransferPlanner/BoundTransfer against
-the reference's own implementation, compiled from its sources into
-oracle/_ref (oracle/Makefile). One scenario driver (oracle/ref_driver.cpp) is
-built against both; every scenario must produce identical logs."""
+"""Cross-check of the drop-in GlobalChunkAllocator and TransferPlanner /
+BoundTransfer against the reference's own implementation, compiled from its
+sources into oracle/_ref (oracle/Makefile). Those sources include glog, which
+this image lacks, and are built against the glog stand-in of the reference's
+own CPU tests, so this comparison is a cross-check, not a parity pin (the
+rows are pinned by the reference's gtest known answers restated in
+tests/cpp/test_drop_in_api.cpp). One scenario driver (oracle/ref_driver.cpp)
+is built against both; every scenario must produce identical logs."""
 import ctypes as C
 from pathlib import Path
 
