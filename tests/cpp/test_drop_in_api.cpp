@@ -22,6 +22,7 @@
 #include "serving/pd_handoff.h"
 #include "serving/kv_page_wire.h"
 #include "serving/split_pd_handoff.h"
+#include "serving/split_pd_admission.h"
 #include "base/block_allocator.h"
 #include "base/kv_cache_manager.h"
 
@@ -1468,4 +1469,43 @@ TEST_CASE("copy_shared_kv order: rejected inputs reserve nothing; a refused copy
   CHECK_EQ(g.owner->lease_count(), 0u);
   CHECK_THROWS_AS(serving::CopySharedKVToDecode(nullptr, pool3(), prefill_result(9, src), nullptr, &res),
                   std::invalid_argument);
+}
+
+// ------------------------------------------------------------ split-PD admission
+// The reference's cases (test/test_split_pd_admission.cpp:4-34), restated.
+
+TEST_CASE("split PD admission: long outputs cannot consume short slots or tokens") {
+  serving::SplitPDAdmission admission({2, 1}, {512, 4096});
+  admission.acquire(1, 4096);
+  CHECK(!admission.can_acquire(1, 16));
+  CHECK(admission.can_acquire(0, 256));
+  admission.acquire(0, 256);
+  admission.acquire(0, 256);
+  CHECK(!admission.can_acquire(0, 16));  // both short slots taken
+  admission.release(0, 256);
+  CHECK(admission.can_acquire(0, 256));
+  CHECK_EQ(admission.used(1), 4096);
+}
+
+TEST_CASE("split PD admission: future output rounds to whole pages") {
+  CHECK_EQ(serving::SplitPDAdmission::charge(17, 16, 16), 48);
+  CHECK_EQ(serving::SplitPDAdmission::charge(16, 0, 16), 16);
+  CHECK_EQ(serving::SplitPDAdmission::charge(5040, 1, 16), 5056);
+  serving::SplitPDAdmission admission({4, 2}, {32, 64});
+  CHECK(!admission.fits_request(0, 48));
+  CHECK(admission.fits_request(1, 48));
+  CHECK(!admission.fits_request(1, 0));
+}
+
+TEST_CASE("split PD admission: reclaim, and reject a double release") {
+  serving::SplitPDAdmission admission({1, 1}, {128, 128});
+  for (int round = 0; round < 10; ++round) {
+    admission.acquire(0, 128);
+    CHECK_THROWS_AS(admission.acquire(0, 1), std::logic_error);
+    admission.release(0, 128);
+  }
+  CHECK_EQ(admission.active(0), 0);
+  CHECK_EQ(admission.used(0), 0);
+  CHECK_THROWS_AS(admission.release(0, 128), std::logic_error);
+  CHECK_THROWS_AS(admission.acquire(2, 1), std::out_of_range);
 }
