@@ -1293,7 +1293,6 @@ TEST_CASE("block allocator: the pool view binds the planes without owning the al
   CHECK_EQ(layer1.num_free_blocks(), free_before - 1);
 }
 
-MINITEST_MAIN()
 
 // ------------------------------------------------------------ KV cache manager
 
@@ -1509,3 +1508,25 @@ TEST_CASE("split PD admission: reclaim, and reject a double release") {
   CHECK_THROWS_AS(admission.release(0, 128), std::logic_error);
   CHECK_THROWS_AS(admission.acquire(2, 1), std::out_of_range);
 }
+
+TEST_CASE("block allocator: local pool view binds the pools without owning the allocation queue") {
+  // test_kv_pool_view.cpp:5-25 as written: a local CPU pool of 4 FP32 blocks
+  base::BlockAllocator owner(4, 16, 2, 8, base::DataType::kDataTypeFp32, base::DeviceType::kDeviceCPU);
+  const int32_t free_before = owner.num_free_blocks();
+  const base::KVPoolView view = owner.pool_view();
+  REQUIRE(view.valid());
+  CHECK(view.device_type() == base::DeviceType::kDeviceCPU);
+  CHECK(view.key_pool() == owner.get_block_payload_ptrs(0).key);
+  CHECK(view.value_pool() == owner.get_block_payload_ptrs(0).value);
+  CHECK_EQ(owner.num_free_blocks(), free_before);
+  const int32_t block = owner.allocate();
+  REQUIRE(block >= 0);
+  CHECK_EQ(owner.num_free_blocks(), free_before - 1);
+  const base::KVPoolView imported = view;  // copying the descriptor owns nothing
+  CHECK(imported.key_pool() == view.key_pool());
+  CHECK_EQ(owner.num_free_blocks(), free_before - 1);
+  owner.free(block);
+  CHECK_EQ(owner.num_free_blocks(), free_before);
+}
+
+MINITEST_MAIN()
