@@ -251,6 +251,47 @@ def test_copy_ops_beyond_one_grid(torch_cuda):
     assert np.array_equal(d_host, expected)
 
 
+def test_copy_ops_merging_keeps_every_op(torch_cuda):
+    """Ops that continue the previous op on both sides are merged before
+    staging; the result must equal the ops applied one by one. Cases: runs of
+    adjacent ops (merged), the same ops in reverse order (not merged), odd
+    sizes and offsets (byte path), and a chain whose merged span would overlap
+    its own source (rejected before anything is written)."""
+    torch = torch_cuda
+    say("copy_ops merging: adjacent, reversed, odd sizes, self-overlap")
+    rng = np.random.default_rng(21)
+    nbytes = 4 << 20
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda")
+    dst = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    sb, db = src.data_ptr(), dst.data_ptr()
+    ops, cur_s, cur_d = [], 0, 0
+    for k in range(200):
+        size = int(rng.choice([16, 4096, 8192, 24, 1000, 16 * 1024 + 16]))
+        n = int(rng.integers(1, 6))
+        chain = [(cur_s + i * size, cur_d + i * size, size) for i in range(n)]
+        if k % 3 == 1:
+            chain.reverse()             # adjacent in memory, listed backwards
+        ops.extend(chain)
+        cur_s += n * size + int(rng.integers(0, 3)) * 16 + (k % 5)   # gaps, odd offsets
+        cur_d += n * size + int(rng.integers(0, 3)) * 32
+        if cur_s + 6 * 20000 > nbytes or cur_d + 6 * 20000 > nbytes:
+            break
+    P.copy_ops([(sb + s, db + d, b) for s, d, b in ops], 0, stream_ptr(torch))
+    torch.cuda.synchronize()
+    s_host = src.cpu().numpy()
+    expected = np.zeros(nbytes, np.uint8)
+    for s, d, b in ops:
+        expected[d:d + b] = s_host[s:s + b]
+    assert np.array_equal(dst.cpu().numpy(), expected)
+    # a chain whose merged span overlaps its own source: op 1 reads what op 0 wrote
+    before = dst.cpu().numpy().copy()
+    bad = [(db + 0, db + 8192, 8192), (db + 8192, db + 16384, 8192)]
+    with pytest.raises(P.PbeError, match="overwrites its own source"):
+        P.copy_ops(bad, 0, stream_ptr(torch))
+    torch.cuda.synchronize()
+    assert np.array_equal(dst.cpu().numpy(), before)
+
+
 def test_repeated_launches_are_idempotent(torch_cuda):
     torch = torch_cuda
     w = W.config2(3)
