@@ -520,7 +520,7 @@ def main() -> int:
 
     # end-to-end handoff latency of the one-call form (validate, coalesce,
     # stage, launch, wait), as copy_shared_kv does before commit_kv
-    lat = []
+    lat, lat_stream = [], []
     src_np = np.ascontiguousarray(w.src_ids, dtype=np.int32)  # the id lists as the
     dst_np = np.ascontiguousarray(w.dst_ids, dtype=np.int32)  # engine holds them
     for i in range(20):
@@ -531,7 +531,18 @@ def main() -> int:
         P.copy_shared_kv(view, src_np, dst_np, kv, 0, sp)
         torch.cuda.synchronize()
         lat.append(time.perf_counter() - t)
+    # the same call waited on with its own stream's synchronize, as copy_shared_kv
+    # waits on the model stream (split_pd_engine.cpp:110)
+    for i in range(20):
+        if not args.no_scrub:
+            scrub.fill_(i & 0xff)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        P.copy_shared_kv(view, src_np, dst_np, kv, 0, sp)
+        P.stream_synchronize(sp)
+        lat_stream.append(time.perf_counter() - t)
     e2e_us = float(np.median(lat) * 1e6)
+    e2e_stream_us = float(np.median(lat_stream) * 1e6)
 
     # the reference's own GPU pattern on this GPU: one hipMemcpyAsync per
     # coalesced run (split_pd_engine.cpp:102-108), then a stream sync (:110)
@@ -584,7 +595,8 @@ def main() -> int:
                        "kernel_p50": round(float(np.median(times_ms)) * 1e3, 2),
                        "kernel_min": round(float(times_ms.min()) * 1e3, 2),
                        "launch_between_stream_events_mean": round(outer_ms[0] * 1e3, 2),
-                       "handoff_e2e_p50": round(e2e_us, 1)},
+                       "handoff_e2e_p50": round(e2e_us, 1),
+                       "handoff_e2e_stream_sync_p50": round(e2e_stream_us, 1)},
         "pct_of_peak": round(100 * achieved / PEAK_GBPS, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),

@@ -120,6 +120,7 @@ _SIGNATURES = [
     ("pbe_paged_decode", C.c_int, [C.POINTER(ArenaView), C.c_int32, _P, C.c_uint64,
                                    C.POINTER(KvShape), C.c_int32, _P, _P, C.c_int32, C.c_int32,
                                    _P, _P, C.c_int32, C.c_int32, _P, C.c_uint64, C.c_int, _P]),
+    ("pbe_stream_synchronize", C.c_int, [C.c_int, _P]),
     ("pbe_paged_decode_noalloc", C.c_int, [C.POINTER(ArenaView), C.c_int32, _P, C.c_uint64,
                                            C.POINTER(KvShape), C.c_int32, _P, _P, C.c_int32,
                                            C.c_int32, _P, _P, C.c_int32, C.c_int32, C.c_int, _P]),
@@ -313,6 +314,11 @@ def copy_shared_kv(view: ArenaView, src_ids, dst_ids, kv: KvShape, device: int =
     check(lib().pbe_copy_shared_kv(C.byref(view), sp, dp, len(s), C.byref(kv), device,
                                    stream or None, C.byref(copied)))
     return copied.value
+
+
+def stream_synchronize(stream: int = 0, device: int = 0) -> None:
+    """Waits for everything queued on `stream` (hipStreamSynchronize)."""
+    check(lib().pbe_stream_synchronize(device, stream or None))
 
 
 def op_array(ops):
