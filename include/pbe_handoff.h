@@ -326,8 +326,10 @@ int pbe_paged_decode(const pbe_arena_view* kv, int32_t kv_dtype, const float* sc
  * partials live in a static device array of PBE_DECODE_SCRATCH_BYTES per GPU
  * (held until the process ends) instead of a caller workspace; nothing is
  * allocated and every partial is rewritten by each call, so no clearing is
- * needed. Launches whose partials need more (pbe_paged_decode_workspace_bytes
- * of the split count used) are rejected with PBE_ERR_INVALID. All calls on
+ * needed. splits = 0 takes pbe_paged_decode_splits' count, lowered until the
+ * partials fit the array; an explicit split count whose partials need more
+ * (pbe_paged_decode_workspace_bytes) is rejected with PBE_ERR_INVALID, as is a
+ * batch too large for the array even at one split. All calls on
  * one GPU share the array: calls that overlap in time on one GPU (different
  * streams, or host threads racing) corrupt each other's results; serialize
  * them on one stream. */

@@ -63,7 +63,9 @@ class HipMigrationQueue final : public TransferBackend {
     if (dependency_ && pbe_stream_wait_raw_event(device_, stream_, dependency_) != PBE_OK)
       return BackendResult::kFailedSafe;  // a failed wait queues nothing
     const int rc = pbe_copy_ops(ops.data(), static_cast<int64_t>(ops.size()), device_, stream_);
-    if (rc == PBE_ERR_INVALID) return BackendResult::kFailedSafe;  // rejected on the host
+    // Rejected on the host (bad op list, or a stream under graph capture):
+    // nothing was queued.
+    if (rc == PBE_ERR_INVALID || rc == PBE_ERR_UNSUPPORTED) return BackendResult::kFailedSafe;
     try {
       by_id_.emplace(id, static_cast<size_t>(l - launches_.data()));
     } catch (...) {

@@ -1199,7 +1199,15 @@ int paged_decode_call(const pbe_arena_view* kv, int32_t kv_dtype, const float* s
   if ((reinterpret_cast<uintptr_t>(queries) | reinterpret_cast<uintptr_t>(outputs)) % 16)
     return fail(PBE_ERR_INVALID, "queries and outputs must be 16-byte aligned");
   if (fp8 && (!scales || scale_bytes == 0)) return fail(PBE_ERR_INVALID, "FP8 pages need a scale pool");
-  if (splits == 0) splits = pbe_paged_decode_splits(batch, shape->kv_heads, max_blocks_per_seq, kv_dtype);
+  if (splits == 0) {
+    splits = pbe_paged_decode_splits(batch, shape->kv_heads, max_blocks_per_seq, kv_dtype);
+    // The allocation-free form lowers an automatic count until the partials
+    // fit its fixed scratch (the partials grow linearly with the splits).
+    if (static_scratch) {
+      const uint64_t per_split = pbe::decode_workspace_bytes(batch, q_heads, shape->head_dim, 1);
+      splits = (int32_t)std::max<uint64_t>(1, std::min<uint64_t>(splits, workspace_bytes / per_split));
+    }
+  }
   if (splits < 0 || splits > pbe::kDecodeMaxSplits)
     return fail(PBE_ERR_INVALID, "splits must be 0..%d", pbe::kDecodeMaxSplits);
   const uint64_t need = pbe::decode_workspace_bytes(batch, q_heads, shape->head_dim, splits);

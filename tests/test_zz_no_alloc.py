@@ -66,3 +66,26 @@ def test_noalloc_decode_rejects_partials_beyond_the_scratch(torch_cuda):
                                64, stream_ptr(torch_cuda))
     torch_cuda.cuda.synchronize()
     assert bool((out == 7).all())  # nothing was launched
+
+
+def test_noalloc_decode_lowers_an_automatic_split_count_to_fit(torch_cuda):
+    # 16 sequences x 8 KV heads x 8 query heads each: the automatic FP8 count
+    # (two waves per SIMD) needs more partials than the static scratch holds,
+    # so splits = 0 must run at the largest count that fits, bit-identical to
+    # the workspace form at that count.
+    case = DecodeCase(torch_cuda, fp8=True, layers=1, H=8, D=128, kvm=8,
+                      seq_lens=[4090] * 15 + [1000], seed=21)
+    q_heads = case.H * case.kvm
+    auto = P.decode_splits(case.batch, case.H, case.max_blocks, P.PBE_KV_FP8_E4M3)
+    per_split = P.decode_workspace_bytes(case.batch, q_heads, case.D, 1)
+    fit = min(auto, P.PBE_DECODE_SCRATCH_BYTES // per_split)
+    say(f"noalloc decode automatic splits: auto={auto} fit={fit}")
+    assert P.decode_workspace_bytes(case.batch, q_heads, case.D, auto) > P.PBE_DECODE_SCRATCH_BYTES
+    assert 1 <= fit < auto
+    case.out.fill_(0)
+    case.run(splits=fit)
+    want_bits = case.out.cpu().numpy().view(np.uint16).copy()
+    case.out.fill_(0)
+    got_bits = _noalloc(case, 0).view(np.uint16)
+    assert np.array_equal(got_bits, want_bits)
+    assert not np.isnan(bf16_to_f64(got_bits)).any()
