@@ -13,6 +13,12 @@ for p in (str(ROOT), str(PKG)):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+    try:  # property tests draw the same examples on every run, and keep no database
+        from hypothesis import settings
+        settings.register_profile("repeatable", derandomize=True, database=None)
+        settings.load_profile("repeatable")
+    except ImportError:
+        pass
 
 
 @pytest.fixture(scope="session")
