@@ -1529,4 +1529,75 @@ TEST_CASE("block allocator: local pool view binds the pools without owning the a
   CHECK_EQ(owner.num_free_blocks(), free_before);
 }
 
+TEST_CASE("kv cache manager: randomized requests keep exact block accounting (model check)") {
+  // Local host pools of 20 blocks per layer; a model of each live request's
+  // token count predicts every outcome: append succeeds iff every layer has
+  // ceil((n+k)/16) - ceil(n/16) free blocks, and a refusal changes nothing.
+  constexpr int kLayers = 3, kBlocks = 20, kB = 16;
+  std::vector<std::unique_ptr<base::BlockAllocator>> pools;
+  for (int l = 0; l < kLayers; ++l)
+    pools.push_back(std::make_unique<base::BlockAllocator>(kBlocks, kB, 1, 8, base::DataType::kDataTypeBf16,
+                                                           base::DeviceType::kDeviceCPU));
+  base::KVCacheManager kv(kB, kLayers, std::move(pools));
+  struct Live { int32_t tokens = 0, committed = 0; };
+  std::vector<std::pair<base::RequestId, Live>> live;
+  std::vector<base::RequestId> dead;
+  std::mt19937_64 rng(77);
+  auto blocks = [](int32_t t) { return (t + kB - 1) / kB; };
+  int appended_ok = 0, refused = 0;
+  for (int step = 0; step < 4000; ++step) {
+    const int op = static_cast<int>(rng() % 10);
+    if (op == 0 || live.empty()) {
+      live.push_back({kv.register_request(), {}});
+    } else if (op <= 5) {
+      auto& [id, m] = live[rng() % live.size()];
+      const int32_t k = 1 + static_cast<int32_t>(rng() % 60);
+      int32_t used = 0;
+      for (auto& e : live) used += blocks(e.second.tokens);
+      const bool fits = blocks(m.tokens + k) - blocks(m.tokens) <= kBlocks - used;
+      const bool ok = kv.append_slots(id, k);
+      CHECK_EQ(ok, fits);
+      if (ok) m.tokens += k, ++appended_ok;
+      else ++refused;
+    } else if (op <= 7) {
+      auto& [id, m] = live[rng() % live.size()];
+      const int32_t t = static_cast<int32_t>(rng() % (m.tokens + 2));
+      const bool want = t >= m.committed && t <= m.tokens;
+      CHECK_EQ(kv.commit_kv(id, t), want);
+      if (want) m.committed = t;
+    } else {
+      const size_t i = rng() % live.size();
+      kv.free_request(live[i].first);
+      dead.push_back(live[i].first);
+      live.erase(live.begin() + static_cast<long>(i));
+    }
+    // invariants
+    int32_t used = 0;
+    for (auto& [id, m] : live) {
+      used += blocks(m.tokens);
+      CHECK(kv.is_valid_request(id));
+      CHECK_EQ(kv.get_context_len(id), m.tokens);
+      CHECK_EQ(kv.kv_committed_tokens(id), m.committed);
+    }
+    for (int l = 0; l < kLayers; ++l) {
+      CHECK_EQ(kv.num_free_blocks(l), kBlocks - used);
+      std::vector<char> seen(kBlocks, 0);
+      for (auto& [id, m] : live) {
+        const auto& ids = kv.get_block_ids(id, l);
+        CHECK_EQ(static_cast<int32_t>(ids.size()), blocks(m.tokens));
+        for (int32_t b : ids) {
+          CHECK(b >= 0 && b < kBlocks);
+          if (b >= 0 && b < kBlocks) CHECK(!seen[b]++);  // no block in two tables
+        }
+      }
+    }
+    for (base::RequestId d : dead) CHECK(!kv.is_valid_request(d));
+    CHECK_EQ(kv.num_active_requests(), static_cast<int32_t>(live.size()));
+  }
+  CHECK(appended_ok > 100);
+  CHECK(refused > 100);
+  for (auto& [id, m] : live) kv.free_request(id);
+  for (int l = 0; l < kLayers; ++l) CHECK_EQ(kv.num_free_blocks(l), kBlocks);
+}
+
 MINITEST_MAIN()
