@@ -549,6 +549,52 @@ TEST_CASE("transfer plan: template cache ignores addresses and stays bounded") {
   CHECK_THROWS_AS(TransferPlanner(0, 1), std::invalid_argument);
 }
 
+TEST_CASE("transfer plan: the cache evicts the least recently used plan") {
+  const auto src = shard(headed_schema(false), {{0, 2}, {2, 2}});
+  const auto dst = shard(headed_schema(false), {{0, 1}, {1, 3}});
+  auto get = [&](TransferPlanner& p, TransferPlacement where) -> const TransferPlan* {
+    std::shared_ptr<const TransferPlan> out;
+    CHECK(p.compile(src, dst, where, &out));
+    return out.get();  // the cache, or nothing, keeps it alive
+  };
+  const auto A = TransferPlacement::kSenderPack, B = TransferPlacement::kReceiverUnpack,
+             C = TransferPlacement::kExactDirect;
+  TransferPlanner lru(2, 1u << 20);
+  const TransferPlan* a = get(lru, A);
+  const TransferPlan* b = get(lru, B);
+  CHECK(get(lru, A) == a);  // A is now the most recent
+  get(lru, C);              // evicts B, not A
+  CHECK_EQ(lru.cache_evictions(), 1u);
+  CHECK(get(lru, A) == a);
+  const size_t hits = lru.cache_hits();
+  CHECK(get(lru, B) != nullptr);  // B was gone: compiled again, evicting C
+  CHECK_EQ(lru.cache_hits(), hits);
+  CHECK_EQ(lru.cache_evictions(), 2u);
+  (void)b;
+
+  // Byte budget of one plan: every new plan replaces the previous one; a
+  // budget below one plan caches nothing and still returns plans.
+  std::shared_ptr<const TransferPlan> probe;
+  REQUIRE(lru.compile(src, dst, A, &probe));
+  const size_t one = probe->template_bytes;
+  TransferPlanner tight(16, one + one / 2);
+  get(tight, A);
+  get(tight, B);
+  CHECK_EQ(tight.cache_entries(), 1u);
+  CHECK_EQ(tight.cache_bytes(), one);
+  get(tight, A);  // A was replaced by B: a miss
+  CHECK_EQ(tight.cache_hits(), 0u);
+  CHECK_EQ(tight.cache_evictions(), 2u);
+  TransferPlanner none(16, one - 1);
+  std::shared_ptr<const TransferPlan> p1, p2;
+  REQUIRE(none.compile(src, dst, A, &p1));
+  REQUIRE(none.compile(src, dst, A, &p2));
+  CHECK(p1 && p2 && p1.get() != p2.get());
+  CHECK_EQ(none.cache_entries(), 0u);
+  CHECK_EQ(none.cache_bytes(), 0u);
+  CHECK(p1->operations.size() == p2->operations.size());
+}
+
 TEST_CASE("layout codec: overlapping or non-permutation layouts are rejected") {
   const auto schema = plain_schema();
   auto order = iota_order(schema.components.size());
