@@ -177,9 +177,11 @@ def view_of(ptrs, total_bytes: int, segment_bytes: int | None = None) -> ArenaVi
 
 
 def _i32(arr):
+    """A contiguous int32 copy (or the array itself) and its address as an int
+    (an int passes to a c_void_p parameter at a fraction of data_as' cost)."""
     import numpy as np
     a = np.ascontiguousarray(arr, dtype=np.int32)
-    return a, a.ctypes.data_as(C.c_void_p)
+    return a, a.ctypes.data
 
 
 def build_runs(src_ids, dst_ids, kv: KvShape, elem_bytes: int = 2, segment_bytes: int = 0):
