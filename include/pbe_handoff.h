@@ -340,6 +340,48 @@ int pbe_paged_decode_noalloc(const pbe_arena_view* kv, int32_t kv_dtype, const f
                              const int32_t* block_tables, const int32_t* seq_lens,
                              int32_t max_blocks_per_seq, int32_t splits, int device, void* stream);
 
+/* ---- page writer ---------------------------------------------------------
+ * Writes n_tokens new tokens' K and V rows into their page slots: the MI355X
+ * form of scatter_kv_batch_to_pages_cu and scatter_kv_batch_to_pages_fp8_e4m3_cu
+ * (scatter_kv_kernel.cuh:27-57, called from CudaPagedKVRuntime::scatter,
+ * paged_kv_runtime.cpp:207-245).
+ *   keys, values: [n_tokens][kv_heads*head_dim] of in_dtype (PBE_IN_BF16 or
+ *     PBE_IN_F32) in device memory, 16-byte aligned, rows a multiple of 16 bytes.
+ *   slot_mapping: int32 [n_tokens] in device memory, slot = block * block_size
+ *     + offset. Head h of token t lands at
+ *     pool + block*block_size*kv_dim*E + (offset*kv_dim + h*head_dim)*E,
+ *     E the bytes of one stored element. A negative slot, or one whose row or
+ *     scale would end beyond the pool sizes given, writes nothing.
+ *   kv_dtype PBE_KV_BF16: plain copy, the pools hold the input type (BF16 or
+ *     FP32). PBE_KV_FP8_E4M3: E4M3 bytes plus one fp32 scale per (token, head)
+ *     at scales[(block*block_size + offset)*kv_heads + head]; scale = amax/448,
+ *     q = E4M3(x * (448/amax)) saturated, and an all-zero row stores scale 1 and
+ *     zero codes (scatter_kv_kernel.cu:166-211). FP8 needs head_dim*E_in/16 to
+ *     be a power of two up to 64 (BF16 head_dim 8..512, FP32 4..256).
+ * Over the shared page-major arena, a layer's planes are key_pool = arena +
+ * 2*layer*half and value_pool = key_pool + half, with block ids the
+ * KVCacheManager's page-major ids (its build_slot_mapping gives the slots).
+ * Asynchronous on `stream`; n_tokens = 0 queues nothing. */
+#define PBE_IN_BF16 0
+#define PBE_IN_F32 1
+int pbe_scatter_kv(const void* keys, const void* values, int32_t in_dtype, int32_t n_tokens,
+                   const int32_t* slot_mapping, int32_t block_size, int32_t kv_heads,
+                   int32_t head_dim, int32_t kv_dtype, void* key_pool, uint64_t key_pool_bytes,
+                   void* value_pool, uint64_t value_pool_bytes, float* key_scales,
+                   uint64_t key_scale_bytes, float* value_scales, uint64_t value_scale_bytes,
+                   int device, void* stream);
+/* One token at a slot given by value: scatter_kv_to_page_cu
+ * (scatter_kv_kernel.cuh:13-24) with the block and offset as host integers, the
+ * same rules as pbe_scatter_kv (FP8 pools too, which the reference routes
+ * through its batched FP8 form). */
+int pbe_scatter_kv_to_page(const void* keys, const void* values, int32_t in_dtype,
+                           int32_t physical_block_id, int32_t offset_in_block,
+                           int32_t block_size, int32_t kv_heads, int32_t head_dim,
+                           int32_t kv_dtype, void* key_pool, uint64_t key_pool_bytes,
+                           void* value_pool, uint64_t value_pool_bytes, float* key_scales,
+                           uint64_t key_scale_bytes, float* value_scales,
+                           uint64_t value_scale_bytes, int device, void* stream);
+
 /* GPU UUID of `device` (16 bytes), as compared across processes. */
 int pbe_device_uuid(int device, uint8_t out[16]);
 /* The calling thread's current HIP device (the one a pool built without an

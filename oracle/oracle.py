@@ -52,6 +52,10 @@ def lib() -> C.CDLL:
                                             C.c_int32, C.c_int32]
         L.orc_fp8_table_scales.restype = None
         L.orc_fp8_table_scales.argtypes = [P, P, C.c_int64]
+        L.orc_scatter_kv.restype = None
+        L.orc_scatter_kv.argtypes = [P, P, C.c_int32, C.c_int64, P, C.c_int32, C.c_int32,
+                                     C.c_int32, C.c_int32, P, C.c_uint64, P, C.c_uint64, P,
+                                     C.c_uint64, P, C.c_uint64]
         _lib = L
     return _lib
 
@@ -138,6 +142,25 @@ def table_scales(amax_table) -> np.ndarray:
     out = np.empty_like(t)
     lib().orc_fp8_table_scales(_p(t), _p(out), t.size)
     return out
+
+
+def scatter_kv(keys, values, slots, block_size: int, heads: int, head_dim: int, fp8: bool,
+               key_pool: np.ndarray, value_pool: np.ndarray, key_scales=None,
+               value_scales=None) -> None:
+    """orc_scatter_kv in place. keys/values: [n][heads*head_dim] uint16 (BF16 bits)
+    or float32; pools: uint8 arrays; scales: float32 arrays (FP8 only)."""
+    k, v = np.ascontiguousarray(keys), np.ascontiguousarray(values)
+    assert k.dtype == v.dtype and k.dtype in (np.uint16, np.float32) and k.shape == v.shape
+    s = _i32(slots)
+    assert key_pool.dtype == np.uint8 and value_pool.dtype == np.uint8
+    assert key_pool.flags.c_contiguous and value_pool.flags.c_contiguous
+    ks = key_scales if fp8 else np.zeros(1, np.float32)
+    vs = value_scales if fp8 else np.zeros(1, np.float32)
+    assert ks.dtype == np.float32 and vs.dtype == np.float32
+    lib().orc_scatter_kv(_p(k), _p(v), int(k.dtype == np.float32), len(s), _p(s), block_size,
+                         heads, head_dim, int(fp8), _p(key_pool), key_pool.nbytes, _p(value_pool),
+                         value_pool.nbytes, _p(ks), ks.size if fp8 else 0, _p(vs),
+                         vs.size if fp8 else 0)
 
 
 def e4m3_table() -> np.ndarray:

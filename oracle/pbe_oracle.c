@@ -22,6 +22,12 @@
  *   orc_fp8_*               per-row reduction checked against a numpy restatement
  *                           on small pools; FP8 rounding parity against CUDA's
  *                           __nv_cvt_float_to_fp8 is pinned by the OCP spec only.
+ *   orc_scatter_kv          plain form: pages it writes, read back by the pinned
+ *                           paged-decode oracle, give the attention torch computes
+ *                           on the unpaged K/V; FP8 form: byte-identical to the
+ *                           pinned FP8 handoff of the plain pages it would write
+ *                           (same rows, same per-(token, head) rule); FP32 input
+ *                           checked element-wise against numpy x*inv + E4M3.
  */
 #include <math.h>
 #include <stdint.h>
@@ -187,21 +193,31 @@ void orc_e4m3_from_f32_array(const float* in, uint8_t* out, int64_t n) {
  * Source: BF16 page-major arena, half16 = T*H*D*2 bytes, ids = offset/half16.
  * Destination: FP8 page-major arena, half8 = T*H*D bytes, ids = offset/half8;
  * scale page of dst id d is at scales + (d / (2L)) * (2L*T*H*4). */
-static void fp8_row(const uint16_t* x, uint8_t* q, int32_t d_count, float inv_given,
-                    int use_given, float* scale_out) {
+/* One row of d_count values: amax, scale = amax/448 (1 for amax 0),
+ * inv = 448/amax (0 for amax 0), q = E4M3(x * inv) (scatter_kv_kernel.cu:166-211).
+ * fmaxf drops NaN inputs from the amax, as the reference's reduction does. */
+static void fp8_row_f32(const float* x, uint8_t* q, int32_t d_count, float inv_given,
+                        int use_given, float* scale_out) {
   float amax = 0.f;
   float inv;
   if (use_given) {
     inv = inv_given;
   } else {
-    for (int32_t d = 0; d < d_count; ++d) amax = fmaxf(amax, fabsf(orc_f32_from_bf16(x[d])));
+    for (int32_t d = 0; d < d_count; ++d) amax = fmaxf(amax, fabsf(x[d]));
     *scale_out = amax > 0.f ? amax / 448.f : 1.f;
     inv = amax > 0.f ? 448.f / amax : 0.f;
   }
   for (int32_t d = 0; d < d_count; ++d) {
-    volatile float v = inv > 0.f ? orc_f32_from_bf16(x[d]) * inv : 0.f;
+    volatile float v = inv > 0.f ? x[d] * inv : 0.f;
     q[d] = orc_e4m3_from_f32(v);
   }
+}
+
+static void fp8_row(const uint16_t* x, uint8_t* q, int32_t d_count, float inv_given,
+                    int use_given, float* scale_out) {
+  float row[1024];
+  for (int32_t d = 0; d < d_count; ++d) row[d] = orc_f32_from_bf16(x[d]);
+  fp8_row_f32(row, q, d_count, inv_given, use_given, scale_out);
 }
 
 void orc_fp8_handoff_token_head(const uint8_t* src_arena, uint8_t* dst_arena,
@@ -256,4 +272,55 @@ void orc_fp8_handoff_table(const uint8_t* src_arena, uint8_t* dst_arena,
 /* scale = amax/448 (or 1) for each table entry, as the decode side reads it. */
 void orc_fp8_table_scales(const float* amax_table, float* scales, int64_t n) {
   for (int64_t i = 0; i < n; ++i) scales[i] = amax_table[i] > 0.f ? amax_table[i] / 448.f : 1.f;
+}
+
+/* ---- page writer: scatter_kv_kernel.cu:99-127 (plain), :128-216 (FP8) ----
+ * keys/values: n rows of kv_dim = heads*head_dim elements, BF16 (in_f32 = 0)
+ * or FP32 (in_f32 = 1). Row t goes to slot s = slots[t], block s/B and offset
+ * s%B. Plain pools hold the input type, head h of the row at
+ *   pool + ((s/B)*B*kv_dim + (s%B)*kv_dim + h*head_dim) * E;
+ * FP8 pools hold E4M3 bytes (E = 1) and the (token, head) scale at
+ * scales[((s/B)*B + s%B)*heads + h]. A negative slot, a row that would end
+ * beyond its pool, or (FP8) a head whose scale would fall beyond its scale
+ * pool, is skipped; the reference skips negative slots in its FP8 form
+ * (:147-149) and does not check bounds. */
+void orc_scatter_kv(const uint8_t* keys, const uint8_t* values, int32_t in_f32, int64_t n,
+                    const int32_t* slots, int32_t block_size, int32_t heads, int32_t head_dim,
+                    int32_t fp8, uint8_t* key_pool, uint64_t key_pool_bytes, uint8_t* value_pool,
+                    uint64_t value_pool_bytes, float* key_scales, uint64_t key_scale_count,
+                    float* value_scales, uint64_t value_scale_count) {
+  const uint64_t kv_dim = (uint64_t)heads * (uint64_t)head_dim;
+  const uint64_t e_in = in_f32 ? 4u : 2u, e_out = fp8 ? 1u : e_in;
+  float row[1024];
+  for (int64_t t = 0; t < n; ++t) {
+    const int32_t s = slots[t];
+    if (s < 0) continue;
+    const uint64_t block = (uint64_t)s / (uint64_t)block_size, off = (uint64_t)s % (uint64_t)block_size;
+    const uint64_t out_row = (block * (uint64_t)block_size + off) * kv_dim * e_out;
+    for (int kv = 0; kv < 2; ++kv) {
+      const uint8_t* in = (kv ? values : keys) + (uint64_t)t * kv_dim * e_in;
+      uint8_t* pool = kv ? value_pool : key_pool;
+      if (out_row + kv_dim * e_out > (kv ? value_pool_bytes : key_pool_bytes)) continue;
+      if (!fp8) {
+        memcpy(pool + out_row, in, kv_dim * e_in);
+        continue;
+      }
+      float* scales = kv ? value_scales : key_scales;
+      for (int32_t h = 0; h < heads; ++h) {
+        const uint64_t idx = (block * (uint64_t)block_size + off) * (uint64_t)heads + (uint64_t)h;
+        if (idx >= (kv ? value_scale_count : key_scale_count)) continue;
+        for (int32_t d = 0; d < head_dim; ++d) {
+          const uint64_t i = (uint64_t)h * (uint64_t)head_dim + (uint64_t)d;
+          if (in_f32) memcpy(&row[d], in + i * 4u, 4);
+          else {
+            uint16_t b;
+            memcpy(&b, in + i * 2u, 2);
+            row[d] = orc_f32_from_bf16(b);
+          }
+        }
+        fp8_row_f32(row, pool + out_row + (uint64_t)h * (uint64_t)head_dim, head_dim, 0.f, 0,
+                    &scales[idx]);
+      }
+    }
+  }
 }

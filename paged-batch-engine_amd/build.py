@@ -65,6 +65,7 @@ ABI_HOST_SOURCES = [
 HIP_SOURCES = [
     "csrc/kernels/handoff_kernels.hip",
     "csrc/kernels/decode_kernels.hip",
+    "csrc/kernels/scatter_kernels.hip",
     "csrc/capi/pbe_capi.hip",
 ]
 CPU_TESTS = ["tests/cpp/test_drop_in_api.cpp"]

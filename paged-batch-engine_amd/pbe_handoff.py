@@ -124,6 +124,13 @@ _SIGNATURES = [
     ("pbe_paged_decode_noalloc", C.c_int, [C.POINTER(ArenaView), C.c_int32, _P, C.c_uint64,
                                            C.POINTER(KvShape), C.c_int32, _P, _P, C.c_int32,
                                            C.c_int32, _P, _P, C.c_int32, C.c_int32, C.c_int, _P]),
+    ("pbe_scatter_kv", C.c_int, [_P, _P, C.c_int32, C.c_int32, _P, C.c_int32, C.c_int32,
+                                 C.c_int32, C.c_int32, _P, C.c_uint64, _P, C.c_uint64, _P,
+                                 C.c_uint64, _P, C.c_uint64, C.c_int, _P]),
+    ("pbe_scatter_kv_to_page", C.c_int, [_P, _P, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                         C.c_int32, C.c_int32, C.c_int32, _P, C.c_uint64, _P,
+                                         C.c_uint64, _P, C.c_uint64, _P, C.c_uint64, C.c_int,
+                                         _P]),
 ]
 EXPORTED = [name for name, _, _ in _SIGNATURES]
 
@@ -485,6 +492,39 @@ def paged_decode_noalloc(view: ArenaView, kv_dtype: int, scales: int, scale_byte
                                          C.byref(kv), layer, queries, outputs, batch, q_heads,
                                          tables, seq_lens, max_blocks, splits, device,
                                          stream or None))
+
+
+PBE_IN_BF16 = 0
+PBE_IN_F32 = 1
+
+
+def scatter_kv(keys: int, values: int, in_dtype: int, n_tokens: int, slots: int, block_size: int,
+               kv_heads: int, head_dim: int, kv_dtype: int, key_pool: int, key_pool_bytes: int,
+               value_pool: int, value_pool_bytes: int, key_scales: int = 0,
+               key_scale_bytes: int = 0, value_scales: int = 0, value_scale_bytes: int = 0,
+               stream: int = 0, device: int = 0) -> None:
+    """New tokens' K/V rows into their page slots (pbe_scatter_kv); device
+    pointers in, asynchronous on `stream`."""
+    check(lib().pbe_scatter_kv(keys or None, values or None, in_dtype, n_tokens, slots or None,
+                               block_size, kv_heads, head_dim, kv_dtype, key_pool or None,
+                               key_pool_bytes, value_pool or None, value_pool_bytes,
+                               key_scales or None, key_scale_bytes, value_scales or None,
+                               value_scale_bytes, device, stream or None))
+
+
+def scatter_kv_to_page(keys: int, values: int, in_dtype: int, block_id: int, offset: int,
+                       block_size: int, kv_heads: int, head_dim: int, kv_dtype: int,
+                       key_pool: int, key_pool_bytes: int, value_pool: int,
+                       value_pool_bytes: int, key_scales: int = 0, key_scale_bytes: int = 0,
+                       value_scales: int = 0, value_scale_bytes: int = 0, stream: int = 0,
+                       device: int = 0) -> None:
+    """One token at (block_id, offset) (pbe_scatter_kv_to_page)."""
+    check(lib().pbe_scatter_kv_to_page(keys or None, values or None, in_dtype, block_id, offset,
+                                       block_size, kv_heads, head_dim, kv_dtype,
+                                       key_pool or None, key_pool_bytes, value_pool or None,
+                                       value_pool_bytes, key_scales or None, key_scale_bytes,
+                                       value_scales or None, value_scale_bytes, device,
+                                       stream or None))
 
 
 def paged_decode(view: ArenaView, kv_dtype: int, scales: int, scale_bytes: int, kv: KvShape,
