@@ -286,6 +286,61 @@ def measure_extra_configs(torch, P, W, scrub, n: int):
 
     out.extend(measure_fp8(torch, P, W, scrub, n))
     out.extend(measure_decode(torch, P, scrub, n))
+    out.extend(measure_scatter(torch, P, scrub, n))
+    return out
+
+
+def measure_scatter(torch, P, scrub, n: int):
+    """The page writer (pbe_scatter_kv) on Qwen2.5-1.5B geometry (H=2, D=128,
+    28 layers): the C2 prompt's 5040 tokens of one layer written to random
+    page-major slots (BF16 pages, FP8 pages + scales), and one decode token for
+    each of 64 sequences. Algorithmic bytes: K and V read, rows written (+ FP8
+    scales), slot ids read."""
+    import numpy as np
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    out = []
+    L, H, D, B, layer, pages = 28, 2, 128, 16, 27, 400
+    rng = np.random.default_rng(17)
+    for tokens, fp8, name in ((5040, False, "scatter_c2_prompt_bf16_pages"),
+                              (5040, True, "scatter_c2_prompt_fp8_pages"),
+                              (64, True, "scatter_decode_b64_fp8_pages")):
+        e_out = 1 if fp8 else 2
+        half = B * H * D * e_out
+        arena = torch.empty(pages * 2 * L * half, dtype=torch.uint8, device=dev)
+        plane = B * H
+        sc = torch.empty(pages * 2 * L * plane, dtype=torch.float32, device=dev)
+        if tokens >= B:  # one sequence: consecutive slots of shuffled pages
+            ids = rng.permutation(pages)[: (tokens + B - 1) // B] * 2 * L
+            slots = np.array([ids[t // B] * B + t % B for t in range(tokens)], np.int32)
+        else:  # one token of each sequence, each on its own page
+            ids = rng.permutation(pages)[:tokens] * 2 * L
+            slots = (ids * B + rng.integers(0, B, tokens)).astype(np.int32)
+        kv = torch.randn((2, tokens, H * D), device=dev).to(torch.bfloat16)
+        d_slots = torch.from_numpy(slots).to(dev)
+        k_off, v_off = 2 * layer * half, (2 * layer + 1) * half
+        s_args = ([sc.data_ptr() + 4 * 2 * layer * plane, 4 * (sc.numel() - 2 * layer * plane),
+                   sc.data_ptr() + 4 * (2 * layer + 1) * plane,
+                   4 * (sc.numel() - (2 * layer + 1) * plane)] if fp8 else [0, 0, 0, 0])
+        alg = 2 * tokens * H * D * 2 + 2 * tokens * H * D * e_out + tokens * 4
+        if fp8:
+            alg += 2 * tokens * H * 4
+        fn = lambda: P.scatter_kv(kv[0].data_ptr(), kv[1].data_ptr(), P.PBE_IN_BF16, tokens,
+                                  d_slots.data_ptr(), B, H, D,
+                                  P.PBE_KV_FP8_E4M3 if fp8 else P.PBE_KV_BF16,
+                                  arena.data_ptr() + k_off, arena.numel() - k_off,
+                                  arena.data_ptr() + v_off, arena.numel() - v_off, *s_args,
+                                  stream=sp)
+        ms = _timed(torch, stream, scrub, fn, n)
+        r = {"workload": name, "algorithmic_bytes": alg, "kernel_us_mean": round(ms[0] * 1e3, 2),
+             "kernel_us_min": round(ms[1] * 1e3, 2),
+             "gbps": round(alg / (ms[0] * 1e-3) / 1e9, 1),
+             "pct_of_peak": round(100 * alg / (ms[0] * 1e-3) / 1e9 / PEAK_GBPS, 1),
+             "tokens": tokens, "launches": 1}
+        out.append(r)
+        print(json.dumps(r), file=sys.stderr, flush=True)
+        del arena, sc, kv
     return out
 
 
@@ -433,6 +488,8 @@ def main() -> int:
                     help="time only the decode reader (FP8 and BF16 pages) and print it as JSON")
     ap.add_argument("--fp8-only", action="store_true",
                     help="time only the fused FP8 handoff (config 4, both scale modes)")
+    ap.add_argument("--scatter-only", action="store_true",
+                    help="time only the page writer (prompt and decode-token scatters)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also launch a plain contiguous copy of 256 MiB with the same kernel "
                          "(rocprofv3 --pmc byte-count calibration)")
@@ -451,11 +508,15 @@ def main() -> int:
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
-    if args.decode_only or args.fp8_only:
+    if args.decode_only or args.fp8_only or args.scatter_only:
         scrub = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         sp = torch.cuda.current_stream().cuda_stream
-        out = {"decode": measure_decode(torch, P, scrub, max(3, args.steps))} if args.decode_only \
-            else {"fp8": measure_fp8(torch, P, W, scrub, max(3, args.steps))}
+        if args.decode_only:
+            out = {"decode": measure_decode(torch, P, scrub, max(3, args.steps))}
+        elif args.fp8_only:
+            out = {"fp8": measure_fp8(torch, P, W, scrub, max(3, args.steps))}
+        else:
+            out = {"scatter": measure_scatter(torch, P, scrub, max(3, args.steps))}
         if args.calibrate:
             out["calibration"] = calibration_copy(torch, P, scrub, args.steps, sp)
         print(json.dumps(out))

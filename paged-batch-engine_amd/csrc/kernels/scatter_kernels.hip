@@ -9,9 +9,8 @@
 // skip-or-write decision; for FP8 a (token, K|V, head) group of lanes shares
 // one amax through DPP, and the group's first lane writes the scale.
 //
-// Memory: the inputs were just written by the K/V projection and the pages are
-// read by this layer's attention next, so loads and stores keep the default
-// cache policy.
+// Memory: each input vector is read once (non-temporal load); the pages are
+// read by this layer's attention next, so stores keep the default policy.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -33,15 +32,17 @@ __global__ __launch_bounds__(kThreadsPerBlock) void scatter_kv_kernel(const Scat
   const uint32_t in_pair = u - token * 2u * p.vecs_per_row;
   const uint32_t kv = in_pair >= p.vecs_per_row ? 1u : 0u;
   const uint32_t vec = in_pair - kv * p.vecs_per_row;
+  // The input vector does not depend on the slot: both loads go out together,
+  // so a wave waits for one memory round trip before its store, not two.
+  const uint8_t* in = (kv ? p.values : p.keys) + (uint64_t)token * p.row_in_bytes;
+  const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(in + (uint64_t)vec * 16u));
   const int32_t slot = p.slots ? p.slots[token] : p.fixed_slot;
   if (slot < 0) return;  // scatter_kv_kernel.cu:147-149
   const uint32_t block = div_by((uint32_t)slot, p.by_block_size);
   const uint32_t offset = (uint32_t)slot - block * p.block_size;
   const uint64_t out_row = (uint64_t)block * p.block_out_bytes + (uint64_t)offset * p.row_out_bytes;
   if (out_row + p.row_out_bytes > (kv ? p.value_pool_bytes : p.key_pool_bytes)) return;
-  const uint8_t* in = (kv ? p.values : p.keys) + (uint64_t)token * p.row_in_bytes;
   uint8_t* out = (kv ? p.value_pool : p.key_pool) + out_row;
-  const u32x4 x = *reinterpret_cast<const u32x4*>(in + (uint64_t)vec * 16u);
   if constexpr (!kFp8) {
     *reinterpret_cast<u32x4*>(out + (uint64_t)vec * 16u) = x;  // plain: the pool holds the input type
   } else {
@@ -61,6 +62,10 @@ __global__ __launch_bounds__(kThreadsPerBlock) void scatter_kv_kernel(const Scat
 template <bool kF32, bool kFp8>
 hipError_t launch_lanes(const ScatterParams& p, uint32_t lanes_per_head, hipStream_t stream) {
   const dim3 grid((p.units + kThreadsPerBlock - 1) / kThreadsPerBlock), block(kThreadsPerBlock);
+  if constexpr (!kFp8) {  // plain rows need no per-head grouping
+    hipLaunchKernelGGL((scatter_kv_kernel<kF32, false, 1>), grid, block, 0, stream, p);
+    return hipGetLastError();
+  }
   switch (lanes_per_head) {
     case 1: hipLaunchKernelGGL((scatter_kv_kernel<kF32, kFp8, 1>), grid, block, 0, stream, p); break;
     case 2: hipLaunchKernelGGL((scatter_kv_kernel<kF32, kFp8, 2>), grid, block, 0, stream, p); break;
