@@ -60,6 +60,7 @@ ABI_HOST_SOURCES = [
     "csrc/serving/split_pd_handoff.cpp",
     "csrc/serving/plan_kv_connector.cpp",
     "csrc/serving/kv_page_wire.cpp",
+    "csrc/model/paged_kv_runtime.cpp",
 ]
 # Sources that call HIP (compiled by hipcc).
 HIP_SOURCES = [

@@ -218,11 +218,21 @@ size_t BlockAllocator::shared_arena_bytes() const { return group_ ? group_->aren
 uint64_t BlockAllocator::shared_arena_epoch() const { return group_ ? group_->arena_epoch() : 0; }
 
 KVPoolView BlockAllocator::pool_view() const {
-  if (!group_)
-    return KVPoolView(key_pool_, value_pool_, key_scale_pool_, value_scale_pool_,
-                      key_value_bytes_per_block(), storage_spec_, device_);
-  return KVPoolView(group_->key_base(layer_), group_->value_base(layer_), nullptr, nullptr,
-                    key_value_bytes_per_block(), storage_spec_, DeviceType::kDeviceHIP);
+  const size_t half = key_value_bytes_per_block();
+  if (!group_) {
+    const size_t n = static_cast<size_t>(num_blocks_);
+    return KVPoolView(key_pool_, value_pool_, key_scale_pool_, value_scale_pool_, half, storage_spec_,
+                      device_, n * half, n * half, n * scale_bytes_per_block());
+  }
+  // Shared arena: this layer's K plane of block b at key_base + b * half, up to
+  // the end of the arena (flat single-segment arenas only; otherwise no base).
+  void* key = group_->key_base(layer_);
+  void* value = group_->value_base(layer_);
+  const size_t arena = group_->arena_bytes();
+  const size_t k_off = 2 * static_cast<size_t>(layer_) * half;
+  return KVPoolView(key, value, nullptr, nullptr, half, storage_spec_, DeviceType::kDeviceHIP,
+                    key && arena > k_off ? arena - k_off : 0,
+                    value && arena > k_off + half ? arena - k_off - half : 0, 0);
 }
 
 }  // namespace base

@@ -1,0 +1,71 @@
+// CudaPagedKVRuntime::scatter / scatter_single_token (paged_kv_runtime.cpp:207-290)
+// over the C ABI's page writer.
+#include "model/paged_kv_runtime.h"
+
+#include <stdexcept>
+#include <string>
+
+#include "pbe_handoff.h"
+
+namespace model {
+namespace {
+
+struct Operands {
+  int32_t in_dtype;
+  int32_t kv_dtype;
+  float* key_scales;
+  float* value_scales;
+  uint64_t scale_bytes;
+};
+
+Operands check(const base::KVPoolView& pool, base::DataType input_dtype) {
+  if (!pool.valid()) throw std::invalid_argument("KV pool view is not bound");
+  if (!pool.key_pool_bytes() || !pool.value_pool_bytes())
+    throw std::invalid_argument("KV pool view carries no pool sizes");
+  if (input_dtype != base::DataType::kDataTypeBf16 && input_dtype != base::DataType::kDataTypeFp32)
+    throw std::invalid_argument("K/V input must be BF16 or FP32");
+  Operands o{input_dtype == base::DataType::kDataTypeFp32 ? PBE_IN_F32 : PBE_IN_BF16, PBE_KV_BF16,
+             nullptr, nullptr, 0};
+  if (pool.uses_fp8_storage()) {
+    if (!pool.key_scale_pool() || !pool.value_scale_pool() || !pool.scale_pool_bytes())
+      throw std::invalid_argument("FP8 KV pool view has no scale pools");
+    o.kv_dtype = PBE_KV_FP8_E4M3;
+    o.key_scales = static_cast<float*>(pool.key_scale_pool());
+    o.value_scales = static_cast<float*>(pool.value_scale_pool());
+    o.scale_bytes = pool.scale_pool_bytes();
+  }
+  return o;
+}
+
+void raise_if_failed(int rc) {
+  if (rc != PBE_OK) throw std::runtime_error(std::string("KV scatter launch failed: ") + pbe_last_error());
+}
+
+}  // namespace
+
+void HipPagedKVRuntime::scatter(const void* key, const void* value, base::DataType input_dtype,
+                                const base::KVPoolView& pool, const int32_t* slot_mapping,
+                                int32_t block_size, int32_t num_kv_heads, int32_t head_size,
+                                int32_t batch_tokens) const {
+  const Operands o = check(pool, input_dtype);
+  raise_if_failed(pbe_scatter_kv(key, value, o.in_dtype, batch_tokens, slot_mapping, block_size,
+                                 num_kv_heads, head_size, o.kv_dtype, pool.key_pool(),
+                                 pool.key_pool_bytes(), pool.value_pool(), pool.value_pool_bytes(),
+                                 o.key_scales, o.scale_bytes, o.value_scales, o.scale_bytes, device_,
+                                 stream_));
+}
+
+void HipPagedKVRuntime::scatter_single_token(const void* key, const void* value,
+                                             base::DataType input_dtype, const base::KVPoolView& pool,
+                                             int32_t physical_block_id, int32_t offset_in_block,
+                                             int32_t block_size, int32_t num_kv_heads,
+                                             int32_t head_size) const {
+  const Operands o = check(pool, input_dtype);
+  raise_if_failed(pbe_scatter_kv_to_page(key, value, o.in_dtype, physical_block_id, offset_in_block,
+                                         block_size, num_kv_heads, head_size, o.kv_dtype,
+                                         pool.key_pool(), pool.key_pool_bytes(), pool.value_pool(),
+                                         pool.value_pool_bytes(), o.key_scales, o.scale_bytes,
+                                         o.value_scales, o.scale_bytes, device_, stream_));
+}
+
+}  // namespace model

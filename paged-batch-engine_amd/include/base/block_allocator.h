@@ -51,6 +51,16 @@ class KVPoolView {
              KVCacheStorageSpec storage_spec, DeviceType device)
       : key_(key), value_(value), key_scale_(key_scale), value_scale_(value_scale),
         block_stride_(block_stride), storage_spec_(storage_spec), device_(device) {}
+  // With the bytes addressable from each pool pointer (the reference's pool
+  // tensors carry their sizes; kernels bound their writes by them).
+  KVPoolView(void* key, void* value, void* key_scale, void* value_scale, size_t block_stride,
+             KVCacheStorageSpec storage_spec, DeviceType device, size_t key_bytes,
+             size_t value_bytes, size_t scale_bytes)
+      : KVPoolView(key, value, key_scale, value_scale, block_stride, storage_spec, device) {
+    key_bytes_ = key_bytes;
+    value_bytes_ = value_bytes;
+    scale_bytes_ = scale_bytes;
+  }
   bool valid() const { return key_ != nullptr && value_ != nullptr; }
   bool uses_fp8_storage() const { return storage_spec_.uses_fp8_storage(); }
   DeviceType device_type() const { return device_; }
@@ -60,6 +70,10 @@ class KVPoolView {
   void* key_scale_pool() const { return key_scale_; }
   void* value_scale_pool() const { return value_scale_; }
   size_t block_stride() const { return block_stride_; }
+  // 0 when unknown.
+  size_t key_pool_bytes() const { return key_bytes_; }
+  size_t value_pool_bytes() const { return value_bytes_; }
+  size_t scale_pool_bytes() const { return scale_bytes_; }  // each of the K and V scale pools
 
  private:
   void* key_ = nullptr;
@@ -69,6 +83,9 @@ class KVPoolView {
   size_t block_stride_ = 0;
   KVCacheStorageSpec storage_spec_;
   DeviceType device_ = DeviceType::kDeviceUnknown;
+  size_t key_bytes_ = 0;
+  size_t value_bytes_ = 0;
+  size_t scale_bytes_ = 0;
 };
 
 class BlockAllocator {

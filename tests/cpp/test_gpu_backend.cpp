@@ -24,6 +24,7 @@
 #include "serving/pd_handoff.h"
 #include "serving/split_pd_handoff.h"
 #include "base/kv_cache_manager.h"
+#include "model/paged_kv_runtime.h"
 
 using namespace cache;
 
@@ -608,6 +609,167 @@ TEST_CASE("zero-copy takeover: moved Chunks are read in place, shared pages are 
   pbe_stream_destroy(0, p_stream);
   pbe_stream_destroy(0, d_stream);
   CHECK(pbe_arena_destroy(arena) == PBE_OK);
+}
+
+namespace {
+// orc_scatter_kv of the CPU oracle (test infrastructure), the page writer's restatement.
+using OracleScatter = void (*)(const uint8_t*, const uint8_t*, int32_t, int64_t, const int32_t*, int32_t,
+                               int32_t, int32_t, int32_t, uint8_t*, uint64_t, uint8_t*, uint64_t, float*,
+                               uint64_t, float*, uint64_t);
+OracleScatter oracle_scatter() {
+  static OracleScatter fn = [] {
+    std::string self(4096, '\0');
+    const ssize_t n = readlink("/proc/self/exe", &self[0], self.size());
+    self.resize(n > 0 ? n : 0);
+    const std::string dir = self.substr(0, self.rfind('/'));
+    void* h = dlopen((dir + "/../../oracle/liboracle.so").c_str(), RTLD_NOW);
+    return h ? reinterpret_cast<OracleScatter>(dlsym(h, "orc_scatter_kv")) : nullptr;
+  }();
+  return fn;
+}
+
+std::vector<uint8_t> random_bytes(size_t n, uint64_t seed) {
+  std::vector<uint8_t> v(n);
+  for (auto& b : v) { seed ^= seed << 13; seed ^= seed >> 7; seed ^= seed << 17; b = static_cast<uint8_t>(seed >> 24); }
+  return v;
+}
+
+// BF16 values N(0,1)-like from random bytes: keep sign and a small exponent range.
+std::vector<uint8_t> random_bf16(size_t elems, uint64_t seed) {
+  std::vector<uint8_t> raw = random_bytes(2 * elems, seed);
+  for (size_t i = 0; i < elems; ++i) {
+    uint16_t h = static_cast<uint16_t>(raw[2 * i] | (raw[2 * i + 1] << 8));
+    h = static_cast<uint16_t>((h & 0x807f) | ((0x7a + (h >> 7) % 8) << 7));  // |x| in [2^-5, 2^3)
+    raw[2 * i] = static_cast<uint8_t>(h);
+    raw[2 * i + 1] = static_cast<uint8_t>(h >> 8);
+  }
+  return raw;
+}
+
+template <typename T>
+T* to_device(const std::vector<T>& v) {
+  T* d = nullptr;
+  if (hipMalloc(&d, v.size() * sizeof(T)) != hipSuccess) return nullptr;
+  if (hipMemcpy(d, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+  return d;
+}
+
+std::vector<uint8_t> to_host(const void* d, size_t n) {
+  std::vector<uint8_t> v(n);
+  if (n && hipMemcpy(v.data(), d, n, hipMemcpyDeviceToHost) != hipSuccess) v.clear();
+  return v;
+}
+}  // namespace
+
+TEST_CASE("model runtime: prompt K/V written through KVCacheManager slots, shared arena and FP8 pools") {
+  REQUIRE(oracle_scatter() != nullptr);
+  const int layers = 24, H = 2, D = 64, B = 16;
+  const uint64_t half = B * H * D * 2, page = 2 * layers * half, arena_bytes = 32 * page;
+  void* stream = nullptr;
+  REQUIRE(pbe_stream_create(0, &stream) == PBE_OK);
+  const model::HipPagedKVRuntime runtime(0, stream);
+  {
+    // (1) shared page-major arena, BF16: the slots of a 41-token prompt of
+    // layer 7, from the manager's page tables, as the model's forward builds them.
+    pbe_arena* arena = nullptr;
+    REQUIRE(pbe_arena_create(0, arena_bytes, arena_bytes, 77, &arena) == PBE_OK);
+    pbe_arena_view view{};
+    REQUIRE(pbe_arena_get_view(arena, &view) == PBE_OK);
+    auto owner = std::make_shared<base::LocalChunkOwner>(arena_bytes, 77);
+    owner->register_model("decode", arena_bytes);
+    {
+      auto client = std::make_shared<base::SharedKVArenaClient>(owner, view, "decode", arena_bytes, 0);
+      auto pages = std::make_shared<base::SharedKVPageGroup>(client, layers, half, 2 * 1024 * 1024, stream);
+      auto kv = manager_over(pages, H, D);
+      const base::RequestId first = kv->register_request();
+      REQUIRE(kv->append_slots(first, 33));  // pages ahead of the prompt's
+      const base::RequestId req = kv->register_request();
+      REQUIRE(kv->append_slots(req, 41));
+      const int layer = 7;
+      std::vector<int32_t> slots;
+      for (int t = 0; t < 41; ++t) {
+        const auto s = kv->get_slot(req, layer, t);
+        slots.push_back(s.first * B + s.second);
+      }
+      std::vector<uint8_t> host = random_bytes(arena_bytes, 5);
+      HIP_OK(hipMemcpy(view.base[0], host.data(), arena_bytes, hipMemcpyHostToDevice));
+      const auto K = random_bf16(41 * H * D, 11), V = random_bf16(41 * H * D, 12);
+      uint8_t* dK = to_device(K);
+      uint8_t* dV = to_device(V);
+      int32_t* dS = to_device(slots);
+      REQUIRE(dK && dV && dS);
+      const base::KVPoolView pool = kv->allocator(layer).pool_view();
+      CHECK_EQ(pool.key_pool_bytes(), arena_bytes - 2 * layer * half);
+      runtime.scatter(dK, dV, base::DataType::kDataTypeBf16, pool, dS, B, H, D, 41);
+      REQUIRE(pbe_stream_synchronize(0, stream) == PBE_OK);
+      const uint64_t k_off = 2 * layer * half, v_off = k_off + half;
+      float none = 0.f;
+      oracle_scatter()(K.data(), V.data(), 0, 41, slots.data(), B, H, D, 0, host.data() + k_off,
+                       arena_bytes - k_off, host.data() + v_off, arena_bytes - v_off, &none, 0, &none, 0);
+      CHECK(to_host(view.base[0], arena_bytes) == host);
+      // a slot-less view is refused before any launch
+      CHECK_THROWS_AS(runtime.scatter(dK, dV, base::DataType::kDataTypeBf16, base::KVPoolView(), dS, B, H, D,
+                                      41),
+                      std::invalid_argument);
+      CHECK_THROWS_AS(runtime.scatter(dK, dV, base::DataType::kDataTypeInt8, pool, dS, B, H, D, 41),
+                      std::invalid_argument);
+      HIP_OK(hipFree(dK));
+      HIP_OK(hipFree(dV));
+      HIP_OK(hipFree(dS));
+      kv->free_request(req);
+      kv->free_request(first);
+    }
+    REQUIRE(pbe_arena_destroy(arena) == PBE_OK);
+  }
+  {
+    // (2) local HIP pools with FP8 storage: a batch of tokens in shuffled
+    // slots, then one more token at a host-known block and offset.
+    base::BlockAllocator pools(8, B, H, D, base::DataType::kDataTypeBf16, base::DeviceType::kDeviceHIP,
+                               base::BlockStorageMode::kFp8E4M3PerTokenHead);
+    const base::KVPoolView pool = pools.pool_view();
+    REQUIRE(pool.uses_fp8_storage());
+    const size_t kvb = pool.key_pool_bytes(), scb = pool.scale_pool_bytes();
+    CHECK_EQ(kvb, 8u * B * H * D);
+    CHECK_EQ(scb, 8u * B * H * 4);
+    std::vector<std::vector<uint8_t>> host;
+    void* ptr[4] = {pool.key_pool(), pool.value_pool(), pool.key_scale_pool(), pool.value_scale_pool()};
+    const size_t size[4] = {kvb, kvb, scb, scb};
+    for (int p = 0; p < 4; ++p) {
+      host.push_back(random_bytes(size[p], 40 + p));
+      HIP_OK(hipMemcpy(ptr[p], host[p].data(), size[p], hipMemcpyHostToDevice));
+    }
+    const int n = 50;
+    std::vector<int32_t> slots(8 * B);
+    std::iota(slots.begin(), slots.end(), 0);
+    uint64_t x = 99;
+    for (size_t i = slots.size() - 1; i > 0; --i) {
+      x ^= x << 13; x ^= x >> 7; x ^= x << 17;
+      std::swap(slots[i], slots[x % (i + 1)]);
+    }
+    slots.resize(n);
+    slots[3] = -1;
+    const auto K = random_bf16(n * H * D, 21), V = random_bf16(n * H * D, 22);
+    uint8_t* dK = to_device(K);
+    uint8_t* dV = to_device(V);
+    int32_t* dS = to_device(slots);
+    REQUIRE(dK && dV && dS);
+    runtime.scatter(dK, dV, base::DataType::kDataTypeBf16, pool, dS, B, H, D, n);
+    runtime.scatter_single_token(dK + 7 * H * D * 2, dV + 7 * H * D * 2, base::DataType::kDataTypeBf16, pool, 2, 9,
+                                 B, H, D);
+    REQUIRE(pbe_stream_synchronize(0, stream) == PBE_OK);
+    auto* ks = reinterpret_cast<float*>(host[2].data());
+    auto* vs = reinterpret_cast<float*>(host[3].data());
+    oracle_scatter()(K.data(), V.data(), 0, n, slots.data(), B, H, D, 1, host[0].data(), kvb, host[1].data(), kvb,
+                     ks, scb / 4, vs, scb / 4);
+    const int32_t one = 2 * B + 9;
+    oracle_scatter()(K.data() + 7 * H * D * 2, V.data() + 7 * H * D * 2, 0, 1, &one, B, H, D, 1, host[0].data(),
+                     kvb, host[1].data(), kvb, ks, scb / 4, vs, scb / 4);
+    for (int p = 0; p < 4; ++p) CHECK(to_host(ptr[p], size[p]) == host[p]);
+    HIP_OK(hipFree(dK));
+    HIP_OK(hipFree(dV));
+    HIP_OK(hipFree(dS));
+  }
+  REQUIRE(pbe_stream_destroy(0, stream) == PBE_OK);
 }
 
 MINITEST_MAIN()
