@@ -340,6 +340,29 @@ int pbe_paged_decode_noalloc(const pbe_arena_view* kv, int32_t kv_dtype, const f
                              const int32_t* block_tables, const int32_t* seq_lens,
                              int32_t max_blocks_per_seq, int32_t splits, int device, void* stream);
 
+/* Decode over per-layer K/V pools: the calling convention of the reference's
+ * decode kernels (splitkv_batched_paged_mha_fast_decode_cu /
+ * splitkv_batched_paged_mha_fp8_decode_cu, paged_mha_fast_kernel.cu:902-1076,
+ * as CudaPagedKVRuntime::decode passes a KVPoolView, paged_kv_runtime.cpp:293-357).
+ * Block b of the layer has its 16 token rows of K at key_pool + b*half and of V
+ * at value_pool + b*half (half = 16*kv_heads*head_dim*E, rows [token][head][dim]),
+ * and, for FP8, its scales at key_scales + b*16*kv_heads and
+ * value_scales + b*16*kv_heads ([token][head] fp32). pool_bytes and
+ * scale_pool_bytes are the bytes addressable from each pointer; a block id whose
+ * rows or scales would end beyond them gives its sequence NaN outputs, as a bad
+ * id does in pbe_paged_decode. Local pools (ids 0..n-1, separate K and V
+ * allocations) and a shared arena's layer views (key_pool = arena +
+ * 2*layer*half, value_pool = key_pool + half, page-major ids) both work. Pools
+ * 16-byte aligned, scale pools 4-byte aligned; everything else as
+ * pbe_paged_decode. */
+int pbe_paged_decode_pools(const void* key_pool, const void* value_pool, uint64_t pool_bytes,
+                           const float* key_scales, const float* value_scales,
+                           uint64_t scale_pool_bytes, int32_t kv_dtype, int32_t kv_heads,
+                           int32_t head_dim, const void* queries, void* outputs, int32_t batch,
+                           int32_t q_heads, const int32_t* block_tables, const int32_t* seq_lens,
+                           int32_t max_blocks_per_seq, int32_t splits, void* workspace,
+                           uint64_t workspace_bytes, int device, void* stream);
+
 /* ---- page writer ---------------------------------------------------------
  * Writes n_tokens new tokens' K and V rows into their page slots: the MI355X
  * form of scatter_kv_batch_to_pages_cu and scatter_kv_batch_to_pages_fp8_e4m3_cu

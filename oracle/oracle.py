@@ -168,6 +168,39 @@ def e4m3_table() -> np.ndarray:
     return np.array([e4m3_to_f32(c) for c in range(256)], np.float64)
 
 
+def _decode(fetch, fp8: bool, kv_heads: int, head_dim: int, q_bf16, tables, seq_lens) -> np.ndarray:
+    """float64 split-K decode over rows that fetch(ids, tok, kvh) returns as
+    (K bytes [n, D*E], V bytes, k_scale [n], v_scale [n])."""
+    q = np.asarray(q_bf16, np.uint16)
+    batch, q_heads, D = q.shape
+    assert D == head_dim
+    kvm = q_heads // kv_heads
+    qf = (q.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    lut = e4m3_table() if fp8 else None
+    scale = float(np.float32(np.float32(1.0) / np.sqrt(np.float32(head_dim))) * np.float32(1.4426950408889634))
+    out = np.zeros((batch, q_heads, D), np.float64)
+    for b in range(batch):
+        n = int(seq_lens[b])
+        if n <= 0:
+            continue
+        t = np.arange(n)
+        ids = np.asarray(tables[b], np.int64)[t // 16]
+        tok = t % 16
+        for kvh in range(kv_heads):
+            kb, vb, ks, vs = fetch(ids, tok, kvh)
+            if fp8:
+                K, V = lut[kb], lut[vb]
+            else:
+                K = (kb.view(np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+                V = (vb.view(np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+            for r in range(kvm):
+                qh = kvh * kvm + r
+                s = (K @ qf[b, qh]) * (scale * ks)
+                p = np.exp2(s - np.max(s))
+                out[b, qh] = (p * vs) @ V / p.sum()
+    return out
+
+
 def paged_decode(arena: np.ndarray, fp8: bool, scales, layers: int, kv_heads: int, head_dim: int,
                  layer: int, q_bf16: np.ndarray, tables: np.ndarray, seq_lens) -> np.ndarray:
     """float64 restatement of one split-K paged-attention decode step
@@ -183,44 +216,48 @@ def paged_decode(arena: np.ndarray, fp8: bool, scales, layers: int, kv_heads: in
     v_scale_t one plane (16 * kv_heads floats) later. Returns float64
     [batch][q_heads][D] (the caller rounds to BF16 for comparison)."""
     arena = np.ascontiguousarray(arena).view(np.uint8).ravel()
-    q = np.asarray(q_bf16, np.uint16)
-    batch, q_heads, D = q.shape
-    assert D == head_dim
-    kvm = q_heads // kv_heads
-    qf = (q.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
     E = 1 if fp8 else 2
     half = 16 * kv_heads * head_dim * E
-    lut = e4m3_table() if fp8 else None
     sc = None if scales is None else np.asarray(scales, np.float32).ravel().astype(np.float64)
-    scale = float(np.float32(np.float32(1.0) / np.sqrt(np.float32(head_dim))) * np.float32(1.4426950408889634))
-    out = np.zeros((batch, q_heads, D), np.float64)
-    for b in range(batch):
-        n = int(seq_lens[b])
-        if n <= 0:
-            continue
-        t = np.arange(n)
-        ids = np.asarray(tables[b], np.int64)[t // 16]
-        tok = t % 16
-        for kvh in range(kv_heads):
-            koff = (ids + 2 * layer) * half + (tok * kv_heads + kvh) * head_dim * E
-            voff = koff + half
-            cols = np.arange(head_dim * E)
-            kb = arena[koff[:, None] + cols[None, :]]
-            vb = arena[voff[:, None] + cols[None, :]]
-            if fp8:
-                K, V = lut[kb], lut[vb]
-                sidx = ((ids + 2 * layer) * 16 + tok) * kv_heads + kvh
-                ks, vs = sc[sidx], sc[sidx + 16 * kv_heads]
-            else:
-                K = (kb.view(np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
-                V = (vb.view(np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
-                ks = vs = np.ones(n)
-            for r in range(kvm):
-                qh = kvh * kvm + r
-                s = (K @ qf[b, qh]) * (scale * ks)
-                p = np.exp2(s - np.max(s))
-                out[b, qh] = (p * vs) @ V / p.sum()
-    return out
+    cols = np.arange(head_dim * E)
+
+    def fetch(ids, tok, kvh):
+        koff = (ids + 2 * layer) * half + (tok * kv_heads + kvh) * head_dim * E
+        kb = arena[koff[:, None] + cols[None, :]]
+        vb = arena[(koff + half)[:, None] + cols[None, :]]
+        if not fp8:
+            return kb, vb, np.ones(len(ids)), np.ones(len(ids))
+        sidx = ((ids + 2 * layer) * 16 + tok) * kv_heads + kvh
+        return kb, vb, sc[sidx], sc[sidx + 16 * kv_heads]
+
+    return _decode(fetch, fp8, kv_heads, head_dim, q_bf16, tables, seq_lens)
+
+
+def paged_decode_pools(key_pool: np.ndarray, value_pool: np.ndarray, fp8: bool, key_scales,
+                       value_scales, kv_heads: int, head_dim: int, q_bf16: np.ndarray,
+                       tables: np.ndarray, seq_lens) -> np.ndarray:
+    """The same step over per-layer pools, the reference kernels' addressing
+    (paged_mha_fast_kernel.cu:671-694): block b's K row of token tok and head h
+    at key_pool byte b*half + (tok*H + h)*D*E, its V row likewise in value_pool,
+    FP8 scales at key_scales / value_scales [b*16*H + tok*H + h]."""
+    kp = np.ascontiguousarray(key_pool).view(np.uint8).ravel()
+    vp = np.ascontiguousarray(value_pool).view(np.uint8).ravel()
+    E = 1 if fp8 else 2
+    half = 16 * kv_heads * head_dim * E
+    ks_ = None if key_scales is None else np.asarray(key_scales, np.float32).ravel().astype(np.float64)
+    vs_ = None if value_scales is None else np.asarray(value_scales, np.float32).ravel().astype(np.float64)
+    cols = np.arange(head_dim * E)
+
+    def fetch(ids, tok, kvh):
+        off = ids * half + (tok * kv_heads + kvh) * head_dim * E
+        kb = kp[off[:, None] + cols[None, :]]
+        vb = vp[off[:, None] + cols[None, :]]
+        if not fp8:
+            return kb, vb, np.ones(len(ids)), np.ones(len(ids))
+        sidx = ids * 16 * kv_heads + tok * kv_heads + kvh
+        return kb, vb, ks_[sidx], vs_[sidx]
+
+    return _decode(fetch, fp8, kv_heads, head_dim, q_bf16, tables, seq_lens)
 
 
 def ref_cpu_handoff(lib_path, arena: np.ndarray, src, dst, layers: int, kv_heads: int,

@@ -36,9 +36,11 @@ struct DecodeParams {
   float* part_l;           // [batch][q_heads][splits]
   int32_t batch, q_heads, kv_heads, head_dim, layers, layer, max_blocks, splits;
   uint64_t half;           // bytes of one K or V plane of one block
+  int64_t v_delta;         // V rows of a block relative to its K rows (bytes): half page-major
+  int64_t vscale_delta;    // V scales relative to K scales (floats): one plane page-major
   float scale;             // log2(e) / sqrt(head_dim): scores in base 2
-  int32_t id_max;          // largest block id whose page lies inside the arena and scale pool
-  FastDiv by_stride;       // divides by 2 * layers (page ids)
+  int32_t id_max;          // largest valid block id (rows and scales inside the pools)
+  FastDiv by_stride;       // block ids per page: 2 * layers page-major, 1 for per-layer pools
   FastDiv by_seg_pages;    // divides page indices by pages per segment
 };
 

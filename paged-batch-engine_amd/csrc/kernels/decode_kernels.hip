@@ -187,7 +187,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
 
   const uint64_t H = (uint64_t)p.kv_heads;
   const uint32_t token_stride = (uint32_t)(H * D * E);
-  const uint64_t stride = 2ull * p.layers;
+  const uint64_t stride = p.by_stride.d;
   // Block ids are uniform: read through the read-only table with scalar loads.
   const int32_t* table = tables + (int64_t)b * p.max_blocks;
   const uint64_t head_off = 2ull * p.layer * p.half + (uint64_t)kvh * D * E;
@@ -201,8 +201,8 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
   const int vrow0 = lane / LPR, vcol = 16 * (lane % LPR);
   const uint32_t val_off = (uint32_t)vrow0 * token_stride + (uint32_t)vcol;
   // lane (g, j): scale of token 4g + j%4 from the key (j%8 < 4) or value plane
-  const uint32_t scale_off =
-      (uint32_t)(((2u * p.layer + ((j >> 2) & 1)) * kBlockTokens + 4u * g + (j & 3)) * H + kvh);
+  const int64_t scale_off =
+      (int64_t)((2u * p.layer * kBlockTokens + 4u * g + (j & 3)) * H + kvh) + ((j >> 2) & 1 ? p.vscale_delta : 0);
   // Loads block `blk` into `r`. Every call issues the same loads (an
   // unconditional count keeps the compiler's in-flight accounting exact): a
   // block past the split's end, or whose id is not a page id inside the arena
@@ -220,7 +220,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
     for (int v = 0; v < W / 4; ++v) {
       const u32x4 x = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kplane + key_off + 64 * v));
       const u32x4 y = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4*>(kplane + p.half + val_off + (uint64_t)v * RPI * token_stride));
+          reinterpret_cast<const u32x4*>(kplane + p.v_delta + val_off + (uint64_t)v * RPI * token_stride));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         r.k[4 * v + e] = x[e];

@@ -1,7 +1,8 @@
-// CudaPagedKVRuntime::scatter / scatter_single_token (paged_kv_runtime.cpp:207-290)
-// over the C ABI's page writer.
+// CudaPagedKVRuntime::scatter / scatter_single_token / decode
+// (paged_kv_runtime.cpp:207-357) over the C ABI's page writer and decode reader.
 #include "model/paged_kv_runtime.h"
 
+#include <algorithm>
 #include <stdexcept>
 #include <string>
 
@@ -66,6 +67,30 @@ void HipPagedKVRuntime::scatter_single_token(const void* key, const void* value,
                                          pool.key_pool(), pool.key_pool_bytes(), pool.value_pool(),
                                          pool.value_pool_bytes(), o.key_scales, o.scale_bytes,
                                          o.value_scales, o.scale_bytes, device_, stream_));
+}
+
+bool HipPagedKVRuntime::decode(const base::KVPoolView& pool, const PagedKVDecodeRuntimeArgs& args) const {
+  if (!pool.valid() || !pool.key_pool_bytes() || !pool.value_pool_bytes())
+    throw std::invalid_argument("KV pool view is not bound or carries no pool sizes");
+  if (!args.queries || !args.outputs || !args.block_tables || !args.seq_lens || !args.workspace)
+    throw std::invalid_argument("decode arguments hold a null tensor");
+  if (args.num_kv_heads <= 0 || args.kv_mul <= 0 || args.head_num != args.kv_mul * args.num_kv_heads)
+    throw std::invalid_argument("head_num must equal kv_mul * num_kv_heads");
+  if (args.block_size != 16) return false;
+  const bool fp8 = pool.uses_fp8_storage();
+  if (fp8 && (!pool.key_scale_pool() || !pool.value_scale_pool() || !pool.scale_pool_bytes()))
+    throw std::invalid_argument("FP8 KV pool view has no scale pools");
+  const uint64_t bytes = std::min(pool.key_pool_bytes(), pool.value_pool_bytes());
+  const int rc = pbe_paged_decode_pools(
+      pool.key_pool(), pool.value_pool(), bytes, fp8 ? static_cast<const float*>(pool.key_scale_pool()) : nullptr,
+      fp8 ? static_cast<const float*>(pool.value_scale_pool()) : nullptr, fp8 ? pool.scale_pool_bytes() : 0,
+      fp8 ? PBE_KV_FP8_E4M3 : PBE_KV_BF16, args.num_kv_heads, args.head_size, args.queries, args.outputs,
+      args.batch_size, args.head_num, args.block_tables, args.seq_lens, args.max_blocks_per_seq, args.splits,
+      args.workspace, args.workspace_bytes, device_, stream_);
+  if (rc == PBE_ERR_UNSUPPORTED) return false;
+  if (rc == PBE_ERR_INVALID) throw std::invalid_argument(std::string("decode rejected: ") + pbe_last_error());
+  raise_if_failed(rc);
+  return true;
 }
 
 }  // namespace model

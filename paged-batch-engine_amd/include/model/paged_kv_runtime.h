@@ -9,8 +9,8 @@
 // Plain pools hold the input type; FP8 pools (pool.uses_fp8_storage()) get E4M3
 // bytes and one fp32 scale per (token, head). Writes are bounded by the pool
 // sizes the view carries; negative slots are skipped. Launches are asynchronous
-// on the runtime's stream. decode() is pbe_paged_decode in this build, and
-// prefill attention is outside it.
+// on the runtime's stream. decode() reads any KVPoolView through
+// pbe_paged_decode_pools; prefill attention is outside this build.
 #ifndef PBE_INCLUDE_MODEL_PAGED_KV_RUNTIME_H_
 #define PBE_INCLUDE_MODEL_PAGED_KV_RUNTIME_H_
 
@@ -20,6 +20,27 @@
 #include "base/block_allocator.h"
 
 namespace model {
+
+// PagedKVDecodeRuntimeArgs (paged_kv_runtime.h:12-27) with device pointers for
+// the tensors. The reference's partial_out / partial_max / partial_sum become
+// one workspace of pbe_paged_decode_workspace_bytes(batch_size, head_num,
+// head_size, splits) bytes; splits = 0 lets the library choose.
+struct PagedKVDecodeRuntimeArgs {
+  int32_t batch_size = 0;
+  int32_t head_num = 0;       // query heads
+  int32_t head_size = 0;
+  int32_t kv_mul = 0;         // head_num / num_kv_heads
+  int32_t max_blocks_per_seq = 0;
+  int32_t block_size = 0;     // 16
+  int32_t num_kv_heads = 0;
+  const void* queries = nullptr;       // bf16 [batch][head_num][head_size]
+  void* outputs = nullptr;             // bf16 [batch][head_num][head_size]
+  const int32_t* block_tables = nullptr;  // [batch][max_blocks_per_seq]
+  const int32_t* seq_lens = nullptr;      // [batch]
+  void* workspace = nullptr;
+  uint64_t workspace_bytes = 0;
+  int32_t splits = 0;
+};
 
 class HipPagedKVRuntime {
  public:
@@ -36,6 +57,14 @@ class HipPagedKVRuntime {
                             const base::KVPoolView& pool, int32_t physical_block_id,
                             int32_t offset_in_block, int32_t block_size, int32_t num_kv_heads,
                             int32_t head_size) const;
+
+  // One decode step over the pool (CudaPagedKVRuntime::decode,
+  // paged_kv_runtime.cpp:293-357). Returns false, launching nothing, for a
+  // shape the reader does not cover (head_size other than 64/128, block_size
+  // other than 16, more than 8 query heads per KV head), so the caller keeps
+  // its own path; throws std::invalid_argument for an inconsistent call and
+  // std::runtime_error when the launch fails.
+  bool decode(const base::KVPoolView& pool, const PagedKVDecodeRuntimeArgs& args) const;
 
   int device() const { return device_; }
   void* stream() const { return stream_; }

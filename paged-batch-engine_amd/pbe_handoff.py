@@ -124,6 +124,9 @@ _SIGNATURES = [
     ("pbe_paged_decode_noalloc", C.c_int, [C.POINTER(ArenaView), C.c_int32, _P, C.c_uint64,
                                            C.POINTER(KvShape), C.c_int32, _P, _P, C.c_int32,
                                            C.c_int32, _P, _P, C.c_int32, C.c_int32, C.c_int, _P]),
+    ("pbe_paged_decode_pools", C.c_int, [_P, _P, C.c_uint64, _P, _P, C.c_uint64, C.c_int32,
+                                         C.c_int32, C.c_int32, _P, _P, C.c_int32, C.c_int32, _P,
+                                         _P, C.c_int32, C.c_int32, _P, C.c_uint64, C.c_int, _P]),
     ("pbe_scatter_kv", C.c_int, [_P, _P, C.c_int32, C.c_int32, _P, C.c_int32, C.c_int32,
                                  C.c_int32, C.c_int32, _P, C.c_uint64, _P, C.c_uint64, _P,
                                  C.c_uint64, _P, C.c_uint64, C.c_int, _P]),
@@ -492,6 +495,20 @@ def paged_decode_noalloc(view: ArenaView, kv_dtype: int, scales: int, scale_byte
                                          C.byref(kv), layer, queries, outputs, batch, q_heads,
                                          tables, seq_lens, max_blocks, splits, device,
                                          stream or None))
+
+
+def paged_decode_pools(key_pool: int, value_pool: int, pool_bytes: int, key_scales: int,
+                       value_scales: int, scale_pool_bytes: int, kv_dtype: int, kv_heads: int,
+                       head_dim: int, queries: int, outputs: int, batch: int, q_heads: int,
+                       tables: int, seq_lens: int, max_blocks: int, splits: int, workspace: int,
+                       workspace_bytes: int, stream: int = 0, device: int = 0) -> None:
+    """Decode over per-layer K/V pools (pbe_paged_decode_pools); device pointers in,
+    asynchronous on `stream`."""
+    check(lib().pbe_paged_decode_pools(key_pool or None, value_pool or None, pool_bytes,
+                                       key_scales or None, value_scales or None, scale_pool_bytes,
+                                       kv_dtype, kv_heads, head_dim, queries, outputs, batch,
+                                       q_heads, tables, seq_lens, max_blocks, splits, workspace,
+                                       workspace_bytes, device, stream or None))
 
 
 PBE_IN_BF16 = 0

@@ -661,7 +661,7 @@ std::vector<uint8_t> to_host(const void* d, size_t n) {
 }
 }  // namespace
 
-TEST_CASE("model runtime: prompt K/V written through KVCacheManager slots, shared arena and FP8 pools") {
+TEST_CASE("model runtime: prompt K/V written through KVCacheManager slots, then decoded from the pool views") {
   REQUIRE(oracle_scatter() != nullptr);
   const int layers = 24, H = 2, D = 64, B = 16;
   const uint64_t half = B * H * D * 2, page = 2 * layers * half, arena_bytes = 32 * page;
@@ -707,6 +707,54 @@ TEST_CASE("model runtime: prompt K/V written through KVCacheManager slots, share
       oracle_scatter()(K.data(), V.data(), 0, 41, slots.data(), B, H, D, 0, host.data() + k_off,
                        arena_bytes - k_off, host.data() + v_off, arena_bytes - v_off, &none, 0, &none, 0);
       CHECK(to_host(view.base[0], arena_bytes) == host);
+      {
+        // decode over the layer's pool view == decode over the page-major arena
+        const int kvm = 6, batch = 2;
+        const std::vector<base::RequestId> ids{first, req};
+        const auto tables = kv->build_block_tables(ids, layer);
+        const auto lens = kv->build_seq_lens(ids);
+        const auto q = random_bf16(batch * kvm * H * D, 13);
+        uint8_t* dq = to_device(q);
+        int32_t* dt = to_device(tables.first);
+        int32_t* dl = to_device(lens);
+        uint8_t *out_pool = nullptr, *out_arena = nullptr, *ws = nullptr;
+        const int32_t splits = 4;
+        const uint64_t ws_bytes = pbe_paged_decode_workspace_bytes(batch, kvm * H, D, splits);
+        HIP_OK(hipMalloc(&out_pool, q.size()));
+        HIP_OK(hipMalloc(&out_arena, q.size()));
+        HIP_OK(hipMalloc(&ws, ws_bytes));
+        model::PagedKVDecodeRuntimeArgs a;
+        a.batch_size = batch;
+        a.head_num = kvm * H;
+        a.head_size = D;
+        a.kv_mul = kvm;
+        a.max_blocks_per_seq = tables.second;
+        a.block_size = B;
+        a.num_kv_heads = H;
+        a.queries = dq;
+        a.outputs = out_pool;
+        a.block_tables = dt;
+        a.seq_lens = dl;
+        a.workspace = ws;
+        a.workspace_bytes = ws_bytes;
+        a.splits = splits;
+        CHECK(runtime.decode(pool, a));
+        const pbe_kv_shape shape{layers, H, D, B};
+        REQUIRE(pbe_paged_decode(&view, PBE_KV_BF16, nullptr, 0, &shape, layer, dq, out_arena, batch, kvm * H, dt,
+                                 dl, tables.second, splits, ws, ws_bytes, 0, stream) == PBE_OK);
+        REQUIRE(pbe_stream_synchronize(0, stream) == PBE_OK);
+        const auto got = to_host(out_pool, q.size());
+        CHECK(got == to_host(out_arena, q.size()));
+        CHECK(std::any_of(got.begin(), got.end(), [](uint8_t b) { return b != 0; }));
+        a.block_size = 32;
+        CHECK(!runtime.decode(pool, a));  // not a shape the reader covers: the caller keeps its path
+        a.block_size = B;
+        a.kv_mul = 5;
+        CHECK_THROWS_AS(runtime.decode(pool, a), std::invalid_argument);
+        for (void* d : {static_cast<void*>(dq), static_cast<void*>(dt), static_cast<void*>(dl),
+                        static_cast<void*>(out_pool), static_cast<void*>(out_arena), static_cast<void*>(ws)})
+          HIP_OK(hipFree(d));
+      }
       // a slot-less view is refused before any launch
       CHECK_THROWS_AS(runtime.scatter(dK, dV, base::DataType::kDataTypeBf16, base::KVPoolView(), dS, B, H, D,
                                       41),
@@ -765,6 +813,68 @@ TEST_CASE("model runtime: prompt K/V written through KVCacheManager slots, share
     oracle_scatter()(K.data() + 7 * H * D * 2, V.data() + 7 * H * D * 2, 0, 1, &one, B, H, D, 1, host[0].data(),
                      kvb, host[1].data(), kvb, ks, scb / 4, vs, scb / 4);
     for (int p = 0; p < 4; ++p) CHECK(to_host(ptr[p], size[p]) == host[p]);
+    {
+      // decode over the local FP8 pools == decode over a page-major FP8 arena
+      // (one layer) holding block b's K and V planes as page b
+      const uint64_t half8 = B * H * D, plane = B * H;
+      std::vector<uint8_t> arena8(8 * 2 * half8);
+      std::vector<float> sc8(8 * 2 * plane);
+      for (int b = 0; b < 8; ++b) {
+        std::memcpy(&arena8[(2 * b) * half8], host[0].data() + b * half8, half8);
+        std::memcpy(&arena8[(2 * b + 1) * half8], host[1].data() + b * half8, half8);
+        std::memcpy(&sc8[(2 * b) * plane], ks + b * plane, plane * 4);
+        std::memcpy(&sc8[(2 * b + 1) * plane], vs + b * plane, plane * 4);
+      }
+      const int kvm = 4, batch = 3, max_blocks = 3;
+      const std::vector<int32_t> local{5, 2, 7, 0, 3, -1, 6, 1, 4};
+      std::vector<int32_t> paged(local);
+      for (auto& id : paged) id = id < 0 ? -1 : 2 * id;
+      const std::vector<int32_t> lens{40, 17, 48};
+      uint8_t* da = to_device(arena8);
+      float* dsc = to_device(sc8);
+      int32_t* dtl = to_device(local);
+      int32_t* dtp = to_device(paged);
+      int32_t* dl = to_device(lens);
+      const auto q = random_bf16(batch * kvm * H * D, 31);
+      uint8_t* dq = to_device(q);
+      uint8_t *o1 = nullptr, *o2 = nullptr, *ws = nullptr;
+      const int32_t splits = 2;
+      const uint64_t ws_bytes = pbe_paged_decode_workspace_bytes(batch, kvm * H, D, splits);
+      HIP_OK(hipMalloc(&o1, q.size()));
+      HIP_OK(hipMalloc(&o2, q.size()));
+      HIP_OK(hipMalloc(&ws, ws_bytes));
+      model::PagedKVDecodeRuntimeArgs a;
+      a.batch_size = batch;
+      a.head_num = kvm * H;
+      a.head_size = D;
+      a.kv_mul = kvm;
+      a.max_blocks_per_seq = max_blocks;
+      a.block_size = B;
+      a.num_kv_heads = H;
+      a.queries = dq;
+      a.outputs = o1;
+      a.block_tables = dtl;
+      a.seq_lens = dl;
+      a.workspace = ws;
+      a.workspace_bytes = ws_bytes;
+      a.splits = splits;
+      CHECK(runtime.decode(pool, a));
+      pbe_arena_view v8{};
+      v8.base[0] = da;
+      v8.bytes = v8.segment_bytes = arena8.size();
+      v8.nseg = 1;
+      const pbe_kv_shape shape{1, H, D, B};
+      REQUIRE(pbe_paged_decode(&v8, PBE_KV_FP8_E4M3, dsc, sc8.size() * 4, &shape, 0, dq, o2, batch, kvm * H, dtp,
+                               dl, max_blocks, splits, ws, ws_bytes, 0, stream) == PBE_OK);
+      REQUIRE(pbe_stream_synchronize(0, stream) == PBE_OK);
+      const auto got = to_host(o1, q.size());
+      CHECK(got == to_host(o2, q.size()));
+      CHECK(std::any_of(got.begin(), got.end(), [](uint8_t b) { return b != 0; }));
+      for (void* d : {static_cast<void*>(da), static_cast<void*>(dsc), static_cast<void*>(dtl),
+                      static_cast<void*>(dtp), static_cast<void*>(dl), static_cast<void*>(dq),
+                      static_cast<void*>(o1), static_cast<void*>(o2), static_cast<void*>(ws)})
+        HIP_OK(hipFree(d));
+    }
     HIP_OK(hipFree(dK));
     HIP_OK(hipFree(dV));
     HIP_OK(hipFree(dS));

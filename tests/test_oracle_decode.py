@@ -106,3 +106,43 @@ def test_closed_forms_single_token_empty_and_identical_keys():
             off = vid * half + tok * D
             vals.append(lut[arena[off: off + D]] * scales[vid * 16 + tok])
     assert np.allclose(out[2, 0], np.mean(vals, axis=0), rtol=1e-9)
+
+
+@pytest.mark.parametrize("fp8", [True, False])
+def test_pool_addressing_equals_page_major_on_layer_views_and_moved_blocks(fp8):
+    """oracle.paged_decode_pools (per-layer pools, the reference kernels'
+    addressing) against the pinned page-major form: (1) over a shared arena's
+    layer views (key = arena + 2l*half, value = key + half) with the same ids;
+    (2) over separate local K and V pools into which every used block was moved
+    to a new id, with the tables renumbered. Both must be exactly equal."""
+    rng = np.random.default_rng(41 + fp8)
+    layers, H, D, kvm, layer = 3, 2, 64, 3, 1
+    seq_lens = [40, 17, 0, 33]
+    arena, scales, tables, q = make_case(rng, fp8, layers, H, D, kvm, seq_lens)
+    E = 1 if fp8 else 2
+    half = 16 * H * D * E
+    plane = 16 * H
+    want = O.paged_decode(arena, fp8, scales, layers, H, D, layer, q, tables, seq_lens)
+    views = O.paged_decode_pools(arena[2 * layer * half:], arena[(2 * layer + 1) * half:], fp8,
+                                 scales[2 * layer * plane:] if fp8 else None,
+                                 scales[(2 * layer + 1) * plane:] if fp8 else None, H, D, q, tables,
+                                 seq_lens)
+    assert np.array_equal(views, want)
+    # local pools: block ids renumbered 0..n-1 in a shuffled order
+    used = sorted(set(tables.ravel().tolist()))
+    new_id = dict(zip(used, rng.permutation(len(used)).tolist()))
+    kp = np.zeros(len(used) * half, np.uint8)
+    vp = np.zeros(len(used) * half, np.uint8)
+    ks = np.zeros(len(used) * plane, np.float32)
+    vs = np.zeros(len(used) * plane, np.float32)
+    for old, new in new_id.items():
+        k_plane, v_plane = old + 2 * layer, old + 2 * layer + 1
+        kp[new * half:(new + 1) * half] = arena[k_plane * half:(k_plane + 1) * half]
+        vp[new * half:(new + 1) * half] = arena[v_plane * half:(v_plane + 1) * half]
+        if fp8:
+            ks[new * plane:(new + 1) * plane] = scales[k_plane * plane:(k_plane + 1) * plane]
+            vs[new * plane:(new + 1) * plane] = scales[v_plane * plane:(v_plane + 1) * plane]
+    local_tables = np.vectorize(new_id.get)(tables).astype(np.int32)
+    moved = O.paged_decode_pools(kp, vp, fp8, ks if fp8 else None, vs if fp8 else None, H, D, q,
+                                 local_tables, seq_lens)
+    assert np.array_equal(moved, want)
