@@ -114,3 +114,72 @@ def test_staged_calls_refuse_capture(torch_cuda):
     P.copy_ops(ops, 0, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     rl.close()
+
+
+def test_decode_loop_step_replays_from_a_graph(torch_cuda):
+    """One decode step of a serving loop, captured once: the new token's K/V
+    written to its page slot (pbe_scatter_kv, FP8 local pools) and attention
+    over the pools (pbe_paged_decode_pools). Between replays the host writes the
+    next token's K/V, slots, lengths and queries into the captured buffers, as a
+    loop would. Each replay's pools equal the oracle's bit for bit and its output
+    is within the reader's tolerance of the float64 oracle."""
+    from tests.test_gpu_decode import bf16_to_f64, close
+    torch = torch_cuda
+    say("graph replay of scatter + decode over FP8 pools")
+    rng = np.random.default_rng(61)
+    H, D, kvm, B, n_blocks = 2, 128, 6, 16, 24
+    half, plane = B * H * D, B * H
+    lens = [30, 15, 47]                       # two of them cross a block boundary below
+    batch = len(lens)
+    tables = rng.permutation(n_blocks)[: batch * 4].reshape(batch, 4).astype(np.int32)
+    kp = rng.integers(0, 0x7F, n_blocks * half, dtype=np.uint8)   # no NaN codes
+    vp = rng.integers(0, 0x7F, n_blocks * half, dtype=np.uint8)
+    ks = rng.uniform(1e-3, 0.05, n_blocks * plane).astype(np.float32)
+    vs = rng.uniform(1e-3, 0.05, n_blocks * plane).astype(np.float32)
+    d = {k: torch.from_numpy(v.copy()).cuda() for k, v in
+         dict(kp=kp, vp=vp, ks=ks, vs=vs, tab=tables).items()}
+    new_k = torch.zeros((batch, H * D), dtype=torch.int16, device="cuda")
+    new_v = torch.zeros_like(new_k)
+    slots = torch.zeros(batch, dtype=torch.int32, device="cuda")
+    seq = torch.zeros(batch, dtype=torch.int32, device="cuda")
+    q = torch.zeros((batch, H * kvm, D), dtype=torch.int16, device="cuda")
+    out = torch.zeros_like(q)
+    splits = 2
+    ws_bytes = P.decode_workspace_bytes(batch, H * kvm, D, splits)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            P.scatter_kv(new_k.data_ptr(), new_v.data_ptr(), P.PBE_IN_BF16, batch, slots.data_ptr(),
+                         B, H, D, P.PBE_KV_FP8_E4M3, d["kp"].data_ptr(), n_blocks * half,
+                         d["vp"].data_ptr(), n_blocks * half, d["ks"].data_ptr(), n_blocks * plane * 4,
+                         d["vs"].data_ptr(), n_blocks * plane * 4, stream=side.cuda_stream)
+            P.paged_decode_pools(d["kp"].data_ptr(), d["vp"].data_ptr(), n_blocks * half,
+                                 d["ks"].data_ptr(), d["vs"].data_ptr(), n_blocks * plane * 4,
+                                 P.PBE_KV_FP8_E4M3, H, D, q.data_ptr(), out.data_ptr(), batch,
+                                 H * kvm, d["tab"].data_ptr(), seq.data_ptr(), 4, splits,
+                                 ws.data_ptr(), ws_bytes, side.cuda_stream)
+    torch.cuda.synchronize()
+    for step in range(4):
+        K = O.bf16_from_f32(rng.standard_normal((batch, H * D)).astype(np.float32))
+        V = O.bf16_from_f32(rng.standard_normal((batch, H * D)).astype(np.float32))
+        qh = O.bf16_from_f32(rng.standard_normal((batch, H * kvm, D)).astype(np.float32))
+        s = np.array([tables[b, lens[b] // B] * B + lens[b] % B for b in range(batch)], np.int32)
+        lens = [n + 1 for n in lens]
+        new_k.copy_(torch.from_numpy(K.view(np.int16)))
+        new_v.copy_(torch.from_numpy(V.view(np.int16)))
+        slots.copy_(torch.from_numpy(s))
+        seq.copy_(torch.tensor(lens, dtype=torch.int32))
+        q.copy_(torch.from_numpy(qh.view(np.int16)))
+        out.fill_(step + 1)
+        torch.cuda.synchronize()
+        O.scatter_kv(K, V, s, B, H, D, True, kp, vp, ks, vs)
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, host in (("kp", kp), ("vp", vp), ("ks", ks), ("vs", vs)):
+            assert np.array_equal(d[name].cpu().numpy().view(np.uint8), host.view(np.uint8)), (step, name)
+        want = O.paged_decode_pools(kp, vp, True, ks, vs, H, D, qh, tables, lens)
+        got = bf16_to_f64(out.cpu().numpy().view(np.uint16))
+        assert close(got, want).all(), step
