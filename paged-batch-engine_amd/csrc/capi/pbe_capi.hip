@@ -1525,14 +1525,50 @@ int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream
     if (!spans_disjoint(dst, src))
       return fail(PBE_ERR_INVALID, "op list writes a byte twice or overwrites its own source");
   }
-  // Split large ops so that every wave moves at most kOpPieceBytes.
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  // Spans whose addresses and sizes are all 16-byte multiples are runs of
+  // 16-byte pages for the run kernel: 4 KiB per wave, one launch, and up to
+  // kKernargRuns spans in the kernel arguments (no staging, so capturable).
+  const bool aligned = std::all_of(merged.begin(), merged.end(), [](const pbe_copy_op& o) {
+    return ((o.src | o.dst | o.bytes) & 15u) == 0 && o.bytes / 16 <= 0xffffffffull;
+  });
+  if (aligned) {
+    std::vector<pbe::DevRun> runs(merged.size());
+    uint64_t slices = 0;
+    for (size_t i = 0; i < merged.size(); ++i) {
+      const pbe_copy_op& o = merged[i];
+      runs[i] = pbe::DevRun{o.src, o.dst, 0, (uint32_t)slices, (uint32_t)(o.bytes / 16)};
+      slices += (o.bytes + pbe::kCopySliceBytes - 1) / pbe::kCopySliceBytes;
+      if (slices > 0xfffffff0ull) return fail(PBE_ERR_INVALID, "op list too large for one launch");
+    }
+    if (runs.size() <= pbe::kKernargRuns) {
+      pbe::KernargRunList list{};
+      list.n_runs = (uint32_t)runs.size();
+      list.total_slices = (uint32_t)slices;
+      list.page_bytes = 16;
+      std::memcpy(list.runs, runs.data(), runs.size() * sizeof(pbe::DevRun));
+      PBE_HIP(pbe::launch_copy_runs_kernarg(list, s));
+      return PBE_OK;
+    }
+    int rc = refuse_capture(s, "pbe_copy_ops with more than 112 spans");
+    if (rc != PBE_OK) return rc;
+    Staging& st = staging_for(device);
+    std::lock_guard<std::mutex> lock(st.mu);
+    void* dev = nullptr;
+    StagingSlot* slot = nullptr;
+    rc = stage(st, runs.data(), runs.size() * sizeof(pbe::DevRun), s, &slot, &dev);
+    if (rc != PBE_OK) return rc;
+    PBE_HIP(pbe::launch_copy_runs(static_cast<const pbe::DevRun*>(dev), (uint32_t)runs.size(),
+                                  (uint32_t)slices, 16, pbe::LaunchEvents{}, s));
+    return stage_done(*slot, s);
+  }
+  // Otherwise: split ops so that every wave moves at most kOpPieceBytes.
   std::vector<pbe::DevOp> pieces;
   for (const pbe_copy_op& o : merged)
     for (uint64_t off = 0; off < o.bytes; off += pbe::kOpPieceBytes)
       pieces.push_back({o.src + off, o.dst + off, std::min<uint64_t>(pbe::kOpPieceBytes, o.bytes - off)});
   if (pieces.size() > 0xffffffffull) return fail(PBE_ERR_INVALID, "op list too large");
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  int rc = refuse_capture(s, "pbe_copy_ops");
+  int rc = refuse_capture(s, "pbe_copy_ops with unaligned spans");
   if (rc != PBE_OK) return rc;
   Staging& st = staging_for(device);
   std::lock_guard<std::mutex> lock(st.mu);

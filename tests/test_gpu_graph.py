@@ -74,10 +74,11 @@ def test_decode_step_replays_from_a_graph(torch_cuda):
 
 
 def test_staged_calls_refuse_capture(torch_cuda):
-    """pbe_copy_ops and a staged pbe_copy_shared_kv (more than 112 runs) stage
-    their lists in a reused ring, so under capture they return
+    """pbe_copy_ops and pbe_copy_shared_kv with more than 112 spans / runs
+    stage their lists in a reused ring, so under capture they return
     PBE_ERR_UNSUPPORTED before queueing anything; the prebuilt run list
-    captured in the same graph still replays correctly."""
+    captured in the same graph still replays correctly. A short op list rides
+    in the kernel arguments and is captured like a prebuilt run list."""
     torch = torch_cuda
     w = W.small(seed=9, layers=2, kv_heads=2, head_dim=64, n_pages=640, handoff_pages=150,
                 max_run=1)
@@ -91,8 +92,14 @@ def test_staged_calls_refuse_capture(torch_cuda):
     rl = P.RunList.bf16(view, view, runs, kv)
     half = g.half()
     base = arena.data_ptr()
+    # every page's first plane only: 150 spans that do not merge
     ops = P.op_array([(base + int(s) * half, base + int(d) * half, half)
-                      for s, d in zip(w.src_ids[:4].tolist(), w.dst_ids[:4].tolist())])
+                      for s, d in zip(w.src_ids.tolist(), w.dst_ids.tolist())])
+    assert ops[1] > 112
+    # source plane s of four pages onto plane d+1 of their destination pages,
+    # which the handoff in the same graph first fills with plane s+1
+    few = [(base + int(s) * half, base + (int(d) + 1) * half, half)
+           for s, d in zip(w.src_ids[:4].tolist(), w.dst_ids[:4].tolist())]
     fill_bf16(torch, arena, 1.0, 3)
     torch.cuda.synchronize()
     side = torch.cuda.Stream()
@@ -104,12 +111,18 @@ def test_staged_calls_refuse_capture(torch_cuda):
             with pytest.raises(P.PbeError, match="captured"):
                 P.copy_shared_kv(view, w.src_ids, w.dst_ids, kv, 0, side.cuda_stream)
             rl.copy(side.cuda_stream)
+            P.copy_ops(few, 0, side.cuda_stream)  # kernel-argument form: captured
     torch.cuda.synchronize()
-    expected = arena.cpu().numpy().copy()
-    O.copy_handoff(expected, w.src_ids, w.dst_ids, g.half(), g.layers)
-    graph.replay()
-    torch.cuda.synchronize()
-    assert np.array_equal(arena.cpu().numpy(), expected)
+    for rep in range(3):
+        fill_bf16(torch, arena, 1.0, 40 + rep)
+        torch.cuda.synchronize()
+        expected = arena.cpu().numpy().copy()
+        O.copy_handoff(expected, w.src_ids, w.dst_ids, g.half(), g.layers)
+        for s_, d_, n_ in few:
+            expected[d_ - base:d_ - base + n_] = expected[s_ - base:s_ - base + n_]
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(arena.cpu().numpy(), expected), rep
     # outside capture the same calls work
     P.copy_ops(ops, 0, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
