@@ -99,3 +99,40 @@ def test_decode_split_count_by_page_dtype():
     assert P.decode_splits(1, 1, 7, bf16) == 2      # at least 4 blocks per split
     assert P.decode_splits(4096, 8, 315, fp8) == 1
     assert P.decode_splits(0, 2, 315, fp8) == 1
+
+
+def test_page_writer_and_pool_reader_reject_bad_arguments_on_the_host():
+    """pbe_scatter_kv / pbe_scatter_kv_to_page / pbe_paged_decode_pools check
+    dtypes, shapes and slots before any HIP call; an empty scatter is a no-op."""
+    fake = 1 << 40  # never dereferenced: every case fails (or returns) first
+    common = dict(keys=fake, values=fake, n_tokens=4, slots=fake, block_size=16, kv_heads=2,
+                  head_dim=64, key_pool=fake, key_pool_bytes=1 << 20, value_pool=fake,
+                  value_pool_bytes=1 << 20)
+
+    def scatter(**kw):
+        a = dict(common, in_dtype=P.PBE_IN_BF16, kv_dtype=P.PBE_KV_BF16)
+        a.update(kw)
+        P.scatter_kv(**a)
+
+    for kw, code in [(dict(in_dtype=7), P.PBE_ERR_INVALID), (dict(kv_dtype=9), P.PBE_ERR_INVALID),
+                     (dict(n_tokens=-1), P.PBE_ERR_INVALID), (dict(slots=0), P.PBE_ERR_INVALID),
+                     (dict(block_size=0), P.PBE_ERR_INVALID),
+                     (dict(kv_dtype=P.PBE_KV_FP8_E4M3, head_dim=48), P.PBE_ERR_UNSUPPORTED),
+                     (dict(kv_dtype=P.PBE_KV_FP8_E4M3), P.PBE_ERR_INVALID),  # no scale pools
+                     (dict(head_dim=3), P.PBE_ERR_INVALID)]:                  # 12-byte rows
+        with pytest.raises(P.PbeError) as e:
+            scatter(**kw)
+        assert e.value.code == code, kw
+    scatter(n_tokens=0)  # nothing to write: no device work, no error
+    with pytest.raises(P.PbeError) as e:
+        P.scatter_kv_to_page(fake, fake, P.PBE_IN_BF16, 3, 16, 16, 2, 64, P.PBE_KV_BF16, fake,
+                             1 << 20, fake, 1 << 20)
+    assert e.value.code == P.PBE_ERR_INVALID  # offset == block_size is not a slot
+    with pytest.raises(P.PbeError) as e:
+        P.paged_decode_pools(fake, fake, 1 << 20, 0, 0, 0, 9, 2, 128, fake, fake, 1, 12, fake,
+                             fake, 4, 0, fake, 1 << 20)
+    assert e.value.code == P.PBE_ERR_INVALID
+    with pytest.raises(P.PbeError) as e:
+        P.paged_decode_pools(fake, fake, 1 << 20, 0, 0, 0, P.PBE_KV_BF16, 2, 96, fake, fake, 1, 12,
+                             fake, fake, 4, 0, fake, 1 << 20)
+    assert e.value.code == P.PBE_ERR_UNSUPPORTED
