@@ -67,7 +67,12 @@ HIP_SOURCES = [
     "csrc/kernels/handoff_kernels.hip",
     "csrc/kernels/decode_kernels.hip",
     "csrc/kernels/scatter_kernels.hip",
-    "csrc/capi/pbe_capi.hip",
+    "csrc/capi/capi_core.hip",
+    "csrc/capi/capi_arena.hip",
+    "csrc/capi/capi_plan.hip",
+    "csrc/capi/capi_copy.hip",
+    "csrc/capi/capi_decode.hip",
+    "csrc/capi/capi_scatter.hip",
 ]
 CPU_TESTS = ["tests/cpp/test_drop_in_api.cpp"]
 GPU_TESTS = ["tests/cpp/test_gpu_backend.cpp"]
