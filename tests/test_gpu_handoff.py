@@ -292,6 +292,36 @@ def test_copy_ops_merging_keeps_every_op(torch_cuda):
     assert np.array_equal(dst.cpu().numpy(), before)
 
 
+def test_aligned_op_lists_on_both_sides_of_the_kernel_argument_limit(torch_cuda):
+    """16-byte aligned op lists run on the run-list kernel: up to 112 spans in
+    the kernel arguments, more through the staging ring. Spans of any 16-byte
+    multiple (a partial last 4 KiB slice is clamped by the buffer resource),
+    scattered destinations, at 1, 112 and 113 spans."""
+    torch = torch_cuda
+    rng = np.random.default_rng(33)
+    nbytes = 8 << 20
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda")
+    dst = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    sb, db = src.data_ptr(), dst.data_ptr()
+    for n_spans in (1, 112, 113):
+        say(f"copy_ops aligned, {n_spans} spans")
+        dst.zero_()
+        sizes = (rng.integers(1, 2500, n_spans) * 16).tolist()
+        slot = 40000  # destinations in disjoint slots, shuffled; sources back to back with gaps
+        order = rng.permutation(n_spans)
+        ops, s_off = [], 0
+        for i, size in enumerate(sizes):
+            ops.append((s_off, int(order[i]) * slot, size))
+            s_off += size + 16 * int(rng.integers(1, 4))
+        P.copy_ops([(sb + s, db + d, b) for s, d, b in ops], 0, stream_ptr(torch))
+        torch.cuda.synchronize()
+        s_host = src.cpu().numpy()
+        expected = np.zeros(nbytes, np.uint8)
+        for s, d, b in ops:
+            expected[d:d + b] = s_host[s:s + b]
+        assert np.array_equal(dst.cpu().numpy(), expected), n_spans
+
+
 def test_repeated_launches_are_idempotent(torch_cuda):
     torch = torch_cuda
     w = W.config2(3)
