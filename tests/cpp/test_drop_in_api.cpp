@@ -1646,4 +1646,63 @@ TEST_CASE("kv cache manager: randomized requests keep exact block accounting (mo
   for (int l = 0; l < kLayers; ++l) CHECK_EQ(kv.num_free_blocks(l), kBlocks);
 }
 
+TEST_CASE("kv cache manager over a shared page group: randomized requests keep page-major tables (model check)") {
+  // 30-page arena, this model limited to 18 pages, Chunks of 3 pages. Every
+  // live request's table is identical in all layers, holds page ids only, and
+  // no page serves two requests; leases cover the held pages and respect the
+  // limit; a refused append changes nothing; freeing everything returns every
+  // Chunk to the owner.
+  Group g(30, 18 * Group::kPage);
+  auto kv = manager_over(g.group);
+  constexpr int B = 16;
+  auto pages_for = [](int32_t t) { return (t + B - 1) / B; };
+  std::vector<std::pair<base::RequestId, int32_t>> live;
+  std::mt19937_64 rng(5);
+  int grew = 0, refused = 0;
+  for (int step = 0; step < 3000; ++step) {
+    const int op = static_cast<int>(rng() % 10);
+    if (op == 0 || live.empty()) {
+      live.push_back({kv->register_request(), 0});
+    } else if (op <= 6) {
+      auto& [id, tokens] = live[rng() % live.size()];
+      const int32_t k = 1 + static_cast<int32_t>(rng() % 70);
+      std::vector<std::vector<int32_t>> before;
+      for (int l = 0; l < 3; ++l) before.push_back(kv->get_block_ids(id, l));
+      const size_t leased = g.group->leased_bytes();
+      if (kv->append_slots(id, k)) {
+        tokens += k;
+        ++grew;
+      } else {
+        ++refused;
+        for (int l = 0; l < 3; ++l) CHECK(kv->get_block_ids(id, l) == before[l]);
+        CHECK_EQ(kv->get_context_len(id), tokens);
+        CHECK(g.group->leased_bytes() <= std::max<size_t>(leased, 18 * Group::kPage));
+      }
+    } else {
+      const size_t i = rng() % live.size();
+      kv->free_request(live[i].first);
+      live.erase(live.begin() + static_cast<long>(i));
+    }
+    std::vector<char> used(30, 0);
+    int held = 0;
+    for (auto& [id, tokens] : live) {
+      const auto& ids0 = kv->get_block_ids(id, 0);
+      CHECK_EQ(static_cast<int>(ids0.size()), pages_for(tokens));
+      for (int l = 1; l < 3; ++l) CHECK(kv->get_block_ids(id, l) == ids0);
+      for (int32_t b : ids0) {
+        CHECK(b >= 0 && b % 6 == 0 && b / 6 < 30);
+        if (b >= 0 && b % 6 == 0 && b / 6 < 30) CHECK(!used[b / 6]++);
+      }
+      held += static_cast<int>(ids0.size());
+    }
+    CHECK(g.group->leased_bytes() <= 18 * Group::kPage);
+    CHECK(g.group->leased_bytes() >= static_cast<size_t>(held) * Group::kPage);
+  }
+  CHECK(grew > 200);
+  CHECK(refused > 20);
+  for (auto& [id, tokens] : live) kv->free_request(id);
+  CHECK_EQ(kv->num_active_requests(), 0);
+  CHECK_EQ(g.owner->lease_count(), 0u);
+}
+
 MINITEST_MAIN()
