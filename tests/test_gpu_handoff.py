@@ -45,12 +45,15 @@ def _run_runlist_case(torch, w: W.Workload, seed: int, batched: bool = True):
     assert np.array_equal(after, expected), first_diff(after, expected)
 
 
-@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("seed", range(16))
 def test_small_random_plans(torch_cuda, seed):
-    shapes = [(3, 2, 64), (1, 1, 8), (5, 4, 128), (2, 2, 16), (7, 1, 32), (4, 8, 64)]
+    shapes = [(3, 2, 64), (1, 1, 8), (5, 4, 128), (2, 2, 16), (7, 1, 32), (4, 8, 64),
+              (28, 2, 128), (24, 2, 64), (1, 3, 24), (9, 5, 40), (2, 1, 256), (6, 6, 8),
+              (11, 2, 96), (4, 16, 16), (1, 1, 1024), (3, 7, 56)]
     L, H, D = shapes[seed]
-    w = W.small(seed=seed, layers=L, kv_heads=H, head_dim=D, n_pages=96, handoff_pages=13 + seed,
-                max_run=1 + seed)
+    n = 13 + seed
+    w = W.small(seed=seed, layers=L, kv_heads=H, head_dim=D, n_pages=max(96, 4 * n + 12),
+                handoff_pages=n, max_run=1 + seed % 6)
     say(f"small seed={seed} L={L} H={H} D={D} pages={w.pages}")
     _run_runlist_case(torch_cuda, w, seed)
 
