@@ -105,16 +105,19 @@ def test_per_token_head_special_rows(torch_cuda):
 
 
 @pytest.mark.parametrize("mode", [P.PBE_FP8_SCALE_PER_TOKEN_HEAD, P.PBE_FP8_SCALE_TABLE])
-@pytest.mark.parametrize("head_dim", [8, 64, 128, 256])
-def test_small_random_fp8(torch_cuda, mode, head_dim):
+@pytest.mark.parametrize("layers,kv_heads,head_dim", [
+    (3, 2, 8), (3, 2, 64), (3, 2, 128), (3, 2, 256), (1, 1, 512), (28, 2, 128), (5, 3, 64),
+    (2, 8, 32), (4, 1, 16)])
+def test_small_random_fp8(torch_cuda, mode, layers, kv_heads, head_dim):
     torch = torch_cuda
-    w = W.small(seed=head_dim, layers=3, kv_heads=2, head_dim=head_dim, n_pages=48,
+    seed = layers * 1000 + kv_heads * 100 + head_dim
+    w = W.small(seed=seed, layers=layers, kv_heads=kv_heads, head_dim=head_dim, n_pages=48,
                 handoff_pages=9, max_run=3)
     g = w.geometry
     pools = Fp8Pools(torch, g, 48)
-    fill_bf16(torch, pools.src, 1.0, head_dim, 0.01, 40.0)
-    amax = np.random.default_rng(head_dim).uniform(2.5, 5.0, (2 * g.layers, g.kv_heads))
-    say(f"fp8 small mode={mode} D={head_dim}")
+    fill_bf16(torch, pools.src, 1.0, seed, 0.01, 40.0)
+    amax = np.random.default_rng(seed).uniform(2.5, 5.0, (2 * g.layers, g.kv_heads))
+    say(f"fp8 small mode={mode} L={layers} H={kv_heads} D={head_dim}")
     _check(torch, pools, w.src_ids, w.dst_ids, mode, amax)
 
 
