@@ -298,7 +298,7 @@ int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream
  * (device memory, read by the kernel). A sequence whose table holds an id
  * outside the arena or not a page id, or whose length needs more than
  * max_blocks_per_seq blocks, gets NaN outputs (its pages are not read past
- * the failing id). splits = 0 picks pbe_paged_decode_splits(); at most 64.
+ * the failing id). splits = 0 picks pbe_paged_decode_splits(); at most 1024.
  * workspace: at least pbe_paged_decode_workspace_bytes() bytes of device
  * memory, used by this launch until it completes. Asynchronous on `stream`. */
 #define PBE_KV_BF16 0

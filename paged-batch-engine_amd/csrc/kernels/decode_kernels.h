@@ -8,7 +8,7 @@ namespace pbe {
 
 constexpr int kDecodeMaxSegments = 16;
 constexpr int kDecodeMaxKvMul = 8;    // query heads per KV head held in registers
-constexpr int kDecodeMaxSplits = 64;  // one lane per split in the combine kernel
+constexpr int kDecodeMaxSplits = 1024;  // split weights of one row held in LDS by the combine
 
 struct DecodeView {
   const char* base[kDecodeMaxSegments];

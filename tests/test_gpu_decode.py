@@ -267,7 +267,7 @@ def test_argument_errors_are_rejected_before_launch(torch_cuda):
                 tables=case.t_dev.data_ptr(), seq_lens=case.s_dev.data_ptr(),
                 max_blocks=case.max_blocks, splits=0, workspace=ws.data_ptr(),
                 workspace_bytes=ws.numel())
-    bad = [dict(layer=2), dict(q_heads=13), dict(q_heads=18), dict(splits=65), dict(kv_dtype=7),
+    bad = [dict(layer=2), dict(q_heads=13), dict(q_heads=18), dict(splits=1025), dict(kv_dtype=7),
            dict(scales=0), dict(workspace_bytes=16), dict(queries=case.q.data_ptr() + 2),
            dict(kv=P.shape(2, 2, 96)), dict(tables=0)]
     for change in bad:
