@@ -335,3 +335,19 @@ def test_pages_beyond_4_gib_of_a_single_arena(torch_cuda, fp8):
     host_scales = scales.view(n_pages, -1)[idx].cpu().numpy().reshape(-1) if fp8 else None
     want = O.paged_decode(host, fp8, host_scales, L, H, D, layer, q_host, compact, seq_lens)
     assert close(got, want).all()
+
+
+@pytest.mark.parametrize("fp8", [True, False])
+def test_one_long_sequence_uses_hundreds_of_splits(torch_cuda, fp8):
+    """A small batch of long sequences takes hundreds of splits (one wave per
+    SIMD, at least 4 blocks each) and the column-grouped combine; 1024 explicit
+    splits leave most of them empty. Both against the float64 oracle."""
+    say(f"decode fp8={fp8} one 20000-token sequence + a short one, many splits")
+    case = DecodeCase(torch_cuda, fp8=fp8, layers=2, H=2, D=128, kvm=6, seq_lens=[20000, 37],
+                      seed=71, layer=1)
+    dtype = P.PBE_KV_FP8_E4M3 if fp8 else P.PBE_KV_BF16
+    auto = P.decode_splits(case.batch, case.H, case.max_blocks, dtype)
+    assert auto > 64
+    want = _check(case, case.run())
+    say(f"decode fp8={fp8} splits=1024")
+    assert close(case.run(1024), want).all()
