@@ -486,6 +486,10 @@ def main() -> int:
                     help="also time configs 1, 3, 4 and 5 and write them as JSON to this file")
     ap.add_argument("--decode-only", action="store_true",
                     help="time only the decode reader (FP8 and BF16 pages) and print it as JSON")
+    ap.add_argument("--decode-batch", type=int, default=64,
+                    help="with --decode-only: sequences per decode step")
+    ap.add_argument("--decode-seq", type=int, default=5040,
+                    help="with --decode-only: tokens per sequence")
     ap.add_argument("--fp8-only", action="store_true",
                     help="time only the fused FP8 handoff (config 4, both scale modes)")
     ap.add_argument("--scatter-only", action="store_true",
@@ -512,7 +516,10 @@ def main() -> int:
         scrub = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         sp = torch.cuda.current_stream().cuda_stream
         if args.decode_only:
-            out = {"decode": measure_decode(torch, P, scrub, max(3, args.steps))}
+            placement = "chunks" if (args.decode_batch * ((args.decode_seq + 15) // 16)) % 5 == 0 \
+                else "random"
+            out = {"decode": measure_decode(torch, P, scrub, max(3, args.steps), args.decode_batch,
+                                            args.decode_seq, placement)}
         elif args.fp8_only:
             out = {"fp8": measure_fp8(torch, P, W, scrub, max(3, args.steps))}
         else:
