@@ -290,6 +290,71 @@ def measure_extra_configs(torch, P, W, scrub, n: int):
     return out
 
 
+def measure_decode_loop(torch, P, scrub, n: int, batch: int = 64, seq: int = 5040):
+    """The KV side of one whole decode step of a 28-layer Qwen2.5-1.5B over
+    FP8 pages: per layer, the new token of every sequence written to its slot
+    (pbe_scatter_kv) and the decode reader (split-K pass + combine), i.e. 84
+    kernels per step. Timed eagerly and as one captured HIP graph replayed per
+    step (the launch-bound small-batch case is where the graph pays)."""
+    import numpy as np
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    L, H, D, kvm, B = 28, 2, 128, 6, 16
+    blocks = (seq + 1 + B - 1) // B
+    n_pages = batch * blocks
+    half = B * H * D
+    plane = B * H
+    g = torch.Generator(device=dev)
+    g.manual_seed(23)
+    arena = torch.randint(0, 0x70, (n_pages * 2 * L * half,), generator=g, device=dev,
+                          dtype=torch.uint8)
+    scales = torch.rand(n_pages * 2 * L * plane, generator=g, device=dev) * 0.1 + 0.01
+    perm = torch.randperm(n_pages, generator=g, device=dev).to(torch.int32)
+    tables = (perm * (2 * L)).view(batch, blocks).contiguous()
+    lens = torch.full((batch,), seq + 1, dtype=torch.int32, device=dev)
+    slots = (tables[:, seq // B] * B + seq % B).contiguous()
+    new_kv = torch.randn((2, batch, H * D), generator=g, device=dev).to(torch.bfloat16)
+    q = torch.randn((batch, H * kvm, D), generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    view = P.view_of(arena.data_ptr(), arena.numel())
+    kv = P.shape(L, H, D)
+    splits = P.decode_splits(batch, H, blocks, P.PBE_KV_FP8_E4M3)
+    ws_bytes = P.decode_workspace_bytes(batch, H * kvm, D, splits)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    total, total_sc = arena.numel(), scales.numel() * 4
+
+    def step(sp):
+        for layer in range(L):
+            ko, vo = 2 * layer * half, (2 * layer + 1) * half
+            so, svo = 4 * 2 * layer * plane, 4 * (2 * layer + 1) * plane
+            P.scatter_kv(new_kv[0].data_ptr(), new_kv[1].data_ptr(), P.PBE_IN_BF16, batch,
+                         slots.data_ptr(), B, H, D, P.PBE_KV_FP8_E4M3, arena.data_ptr() + ko,
+                         total - ko, arena.data_ptr() + vo, total - vo, scales.data_ptr() + so,
+                         total_sc - so, scales.data_ptr() + svo, total_sc - svo, stream=sp)
+            P.paged_decode(view, P.PBE_KV_FP8_E4M3, scales.data_ptr(), total_sc, kv, layer,
+                           q.data_ptr(), out.data_ptr(), batch, H * kvm, tables.data_ptr(),
+                           lens.data_ptr(), blocks, splits, ws.data_ptr(), ws_bytes, sp)
+
+    eager_ms = _timed(torch, stream, scrub, lambda: step(stream.cuda_stream), n)
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            step(side.cuda_stream)
+    torch.cuda.synchronize()
+    graph_ms = _timed(torch, stream, scrub, graph.replay, n)
+    alg = L * (batch * (seq + 1) * H * (2 * D + 8) + 2 * q.numel() * 2 + batch * H * D * 2 * 2)
+    r = {"workload": f"decode_step_28_layers_fp8_b{batch}_s{seq}", "algorithmic_bytes": alg,
+         "splits": splits, "kernels_per_step": 3 * L,
+         "eager_us_per_step": round(eager_ms[0] * 1e3, 1),
+         "graph_us_per_step": round(graph_ms[0] * 1e3, 1),
+         "graph_gbps": round(alg / (graph_ms[0] * 1e-3) / 1e9, 1)}
+    print(json.dumps(r), file=sys.stderr, flush=True)
+    del graph
+    return [r]
+
+
 def measure_scatter(torch, P, scrub, n: int):
     """The page writer (pbe_scatter_kv) on Qwen2.5-1.5B geometry (H=2, D=128,
     28 layers): the C2 prompt's 5040 tokens of one layer written to random
@@ -492,6 +557,8 @@ def main() -> int:
                     help="with --decode-only: tokens per sequence")
     ap.add_argument("--fp8-only", action="store_true",
                     help="time only the fused FP8 handoff (config 4, both scale modes)")
+    ap.add_argument("--decode-loop-only", action="store_true",
+                    help="time only a 28-layer decode step (page write + reader), eager and graph")
     ap.add_argument("--scatter-only", action="store_true",
                     help="time only the page writer (prompt and decode-token scatters)")
     ap.add_argument("--calibrate", action="store_true",
@@ -512,7 +579,7 @@ def main() -> int:
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
-    if args.decode_only or args.fp8_only or args.scatter_only:
+    if args.decode_only or args.fp8_only or args.scatter_only or args.decode_loop_only:
         scrub = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         sp = torch.cuda.current_stream().cuda_stream
         if args.decode_only:
@@ -520,6 +587,9 @@ def main() -> int:
                 else "random"
             out = {"decode": measure_decode(torch, P, scrub, max(3, args.steps), args.decode_batch,
                                             args.decode_seq, placement)}
+        elif args.decode_loop_only:
+            out = {"decode_loop": measure_decode_loop(torch, P, scrub, max(3, args.steps // 4),
+                                                      args.decode_batch, args.decode_seq)}
         elif args.fp8_only:
             out = {"fp8": measure_fp8(torch, P, W, scrub, max(3, args.steps))}
         else:
