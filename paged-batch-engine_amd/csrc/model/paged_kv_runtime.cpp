@@ -25,6 +25,12 @@ Operands check(const base::KVPoolView& pool, base::DataType input_dtype) {
     throw std::invalid_argument("KV pool view carries no pool sizes");
   if (input_dtype != base::DataType::kDataTypeBf16 && input_dtype != base::DataType::kDataTypeFp32)
     throw std::invalid_argument("K/V input must be BF16 or FP32");
+  // A plain pool holds the input type (the reference's kernels are templated
+  // on one element type for both): BF16 input into an FP32 pool, or the
+  // reverse, would store the wrong bytes.
+  if (!pool.uses_fp8_storage() && pool.storage_spec().storage_dtype != base::DataType::kDataTypeUnknown &&
+      pool.storage_spec().storage_dtype != input_dtype)
+    throw std::invalid_argument("K/V input dtype differs from the plain pool's element type");
   Operands o{input_dtype == base::DataType::kDataTypeFp32 ? PBE_IN_F32 : PBE_IN_BF16, PBE_KV_BF16,
              nullptr, nullptr, 0};
   if (pool.uses_fp8_storage()) {
@@ -78,6 +84,9 @@ bool HipPagedKVRuntime::decode(const base::KVPoolView& pool, const PagedKVDecode
     throw std::invalid_argument("head_num must equal kv_mul * num_kv_heads");
   if (args.block_size != 16) return false;
   const bool fp8 = pool.uses_fp8_storage();
+  // The reader takes BF16 or FP8 E4M3 pages; other plain pools (FP32) keep
+  // the caller's path.
+  if (!fp8 && pool.storage_spec().storage_dtype != base::DataType::kDataTypeBf16) return false;
   if (fp8 && (!pool.key_scale_pool() || !pool.value_scale_pool() || !pool.scale_pool_bytes()))
     throw std::invalid_argument("FP8 KV pool view has no scale pools");
   const uint64_t bytes = std::min(pool.key_pool_bytes(), pool.value_pool_bytes());

@@ -47,9 +47,10 @@ class HipPagedKVRuntime {
   // `stream`: a hipStream_t of `device` (nullptr: the null stream).
   HipPagedKVRuntime(int device, void* stream) : device_(device), stream_(stream) {}
 
-  // Throws std::invalid_argument for an invalid view, a view without pool sizes
-  // or an input dtype other than BF16/FP32, and std::runtime_error when the
-  // library rejects the launch (the reference aborts on CHECK in both cases).
+  // Throws std::invalid_argument for an invalid view, a view without pool sizes,
+  // an input dtype other than BF16/FP32 or one that differs from a plain pool's
+  // element type, and std::runtime_error when the library rejects the launch
+  // (the reference aborts on CHECK in both cases).
   void scatter(const void* key, const void* value, base::DataType input_dtype,
                const base::KVPoolView& pool, const int32_t* slot_mapping, int32_t block_size,
                int32_t num_kv_heads, int32_t head_size, int32_t batch_tokens) const;
@@ -60,9 +61,9 @@ class HipPagedKVRuntime {
 
   // One decode step over the pool (CudaPagedKVRuntime::decode,
   // paged_kv_runtime.cpp:293-357). Returns false, launching nothing, for a
-  // shape the reader does not cover (head_size other than 64/128, block_size
-  // other than 16, more than 8 query heads per KV head), so the caller keeps
-  // its own path; throws std::invalid_argument for an inconsistent call and
+  // pool or shape the reader does not cover (plain pools other than BF16,
+  // head_size other than 64/128, block_size other than 16, more than 8 query
+  // heads per KV head), so the caller keeps its own path; throws std::invalid_argument for an inconsistent call and
   // std::runtime_error when the launch fails.
   bool decode(const base::KVPoolView& pool, const PagedKVDecodeRuntimeArgs& args) const;
 

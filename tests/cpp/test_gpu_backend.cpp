@@ -879,6 +879,51 @@ TEST_CASE("model runtime: prompt K/V written through KVCacheManager slots, then 
     HIP_OK(hipFree(dV));
     HIP_OK(hipFree(dS));
   }
+  {
+    // (3) a plain FP32 pool: FP32 input is written as is; BF16 input, which the
+    // pool's element type does not match, is refused; the reader declines it.
+    base::BlockAllocator f32(4, B, H, D, base::DataType::kDataTypeFp32, base::DeviceType::kDeviceHIP);
+    const base::KVPoolView pool = f32.pool_view();
+    const size_t kvb = pool.key_pool_bytes();
+    CHECK_EQ(kvb, 4u * B * H * D * 4);
+    std::vector<uint8_t> hk = random_bytes(kvb, 61), hv = random_bytes(kvb, 62);
+    HIP_OK(hipMemcpy(pool.key_pool(), hk.data(), kvb, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(pool.value_pool(), hv.data(), kvb, hipMemcpyHostToDevice));
+    const int n = 5;
+    const std::vector<int32_t> slots{17, 3, 63, -1, 40};
+    const auto K = random_bytes(n * H * D * 4, 63), V = random_bytes(n * H * D * 4, 64);
+    uint8_t* dK = to_device(K);
+    uint8_t* dV = to_device(V);
+    int32_t* dS = to_device(slots);
+    REQUIRE(dK && dV && dS);
+    runtime.scatter(dK, dV, base::DataType::kDataTypeFp32, pool, dS, B, H, D, n);
+    REQUIRE(pbe_stream_synchronize(0, stream) == PBE_OK);
+    float none = 0.f;
+    oracle_scatter()(K.data(), V.data(), 1, n, slots.data(), B, H, D, 0, hk.data(), kvb, hv.data(), kvb, &none, 0,
+                     &none, 0);
+    CHECK(to_host(pool.key_pool(), kvb) == hk);
+    CHECK(to_host(pool.value_pool(), kvb) == hv);
+    CHECK_THROWS_AS(runtime.scatter(dK, dV, base::DataType::kDataTypeBf16, pool, dS, B, H, D, n),
+                    std::invalid_argument);
+    model::PagedKVDecodeRuntimeArgs a;
+    a.batch_size = 1;
+    a.head_num = 2 * H;
+    a.head_size = D;
+    a.kv_mul = 2;
+    a.max_blocks_per_seq = 1;
+    a.block_size = B;
+    a.num_kv_heads = H;
+    a.queries = dK;
+    a.outputs = dV;
+    a.block_tables = dS;
+    a.seq_lens = dS;
+    a.workspace = dK;
+    a.workspace_bytes = K.size();
+    CHECK(!runtime.decode(pool, a));  // FP32 pages: not a reader dtype, nothing launched
+    HIP_OK(hipFree(dK));
+    HIP_OK(hipFree(dV));
+    HIP_OK(hipFree(dS));
+  }
   REQUIRE(pbe_stream_destroy(0, stream) == PBE_OK);
 }
 
