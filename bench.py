@@ -295,7 +295,8 @@ def measure_decode_loop(torch, P, scrub, n: int, batch: int = 64, seq: int = 504
     FP8 pages: per layer, the new token of every sequence written to its slot
     (pbe_scatter_kv) and the decode reader (split-K pass + combine), i.e. 84
     kernels per step. Timed eagerly and as one captured HIP graph replayed per
-    step (the launch-bound small-batch case is where the graph pays)."""
+    step, and eagerly in the fused form (pbe_paged_decode_append: the reader
+    writes the new token itself, 56 kernels per step)."""
     import numpy as np
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
@@ -335,7 +336,19 @@ def measure_decode_loop(torch, P, scrub, n: int, batch: int = 64, seq: int = 504
                            q.data_ptr(), out.data_ptr(), batch, H * kvm, tables.data_ptr(),
                            lens.data_ptr(), blocks, splits, ws.data_ptr(), ws_bytes, sp)
 
+    def fused_step(sp):
+        for layer in range(L):
+            ko, vo = 2 * layer * half, (2 * layer + 1) * half
+            so, svo = 4 * 2 * layer * plane, 4 * (2 * layer + 1) * plane
+            P.paged_decode_append(arena.data_ptr() + ko, arena.data_ptr() + vo, total - vo,
+                                  scales.data_ptr() + so, scales.data_ptr() + svo, total_sc - svo,
+                                  P.PBE_KV_FP8_E4M3, H, D, new_kv[0].data_ptr(),
+                                  new_kv[1].data_ptr(), q.data_ptr(), out.data_ptr(), batch,
+                                  H * kvm, tables.data_ptr(), lens.data_ptr(), blocks, splits,
+                                  ws.data_ptr(), ws_bytes, sp)
+
     eager_ms = _timed(torch, stream, scrub, lambda: step(stream.cuda_stream), n)
+    fused_ms = _timed(torch, stream, scrub, lambda: fused_step(stream.cuda_stream), n)
     side = torch.cuda.Stream()
     graph = torch.cuda.CUDAGraph()
     torch.cuda.synchronize()
@@ -349,6 +362,7 @@ def measure_decode_loop(torch, P, scrub, n: int, batch: int = 64, seq: int = 504
          "splits": splits, "kernels_per_step": 3 * L,
          "eager_us_per_step": round(eager_ms[0] * 1e3, 1),
          "graph_us_per_step": round(graph_ms[0] * 1e3, 1),
+         "fused_eager_us_per_step": round(fused_ms[0] * 1e3, 1), "fused_kernels_per_step": 2 * L,
          "graph_gbps": round(alg / (graph_ms[0] * 1e-3) / 1e9, 1)}
     print(json.dumps(r), file=sys.stderr, flush=True)
     del graph

@@ -362,6 +362,28 @@ int pbe_paged_decode_pools(const void* key_pool, const void* value_pool, uint64_
                            int32_t q_heads, const int32_t* block_tables, const int32_t* seq_lens,
                            int32_t max_blocks_per_seq, int32_t splits, void* workspace,
                            uint64_t workspace_bytes, int device, void* stream);
+/* One decode step of a layer in one launch pair: each sequence's new token is
+ * written into its page slot and then read with the rest, as
+ * pbe_scatter_kv (BF16 input) followed by pbe_paged_decode_pools would do,
+ * with identical page bytes, scales and outputs. The reference runs the two
+ * as separate kernels (CudaPagedKVRuntime::scatter, then the decode kernels,
+ * paged_kv_runtime.cpp:207-245,293-357); this form has no counterpart there.
+ *   new_keys, new_values: bf16 [batch][kv_heads][head_dim] in device memory,
+ *     16-byte aligned: the K and V of each sequence's token at position
+ *     seq_lens[b] - 1, i.e. row (seq_lens[b]-1) % 16 of block
+ *     block_tables[b][(seq_lens[b]-1) / 16] (the slot the KVCacheManager's
+ *     append_slots hands out for the step's token).
+ *   Pools, scales and every other argument as pbe_paged_decode_pools; the
+ *   pools are written. A sequence of length 0 writes nothing and reads as
+ *   zeros; one whose last block id fails the reader's checks writes nothing
+ *   and reads as NaN. */
+int pbe_paged_decode_append(void* key_pool, void* value_pool, uint64_t pool_bytes,
+                            float* key_scales, float* value_scales, uint64_t scale_pool_bytes,
+                            int32_t kv_dtype, int32_t kv_heads, int32_t head_dim, const void* new_keys,
+                            const void* new_values, const void* queries, void* outputs, int32_t batch,
+                            int32_t q_heads, const int32_t* block_tables, const int32_t* seq_lens,
+                            int32_t max_blocks_per_seq, int32_t splits, void* workspace,
+                            uint64_t workspace_bytes, int device, void* stream);
 
 /* ---- page writer ---------------------------------------------------------
  * Writes n_tokens new tokens' K and V rows into their page slots: the MI355X

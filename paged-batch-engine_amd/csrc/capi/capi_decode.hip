@@ -125,7 +125,8 @@ int paged_decode_call(const pbe_arena_view* kv, int32_t kv_dtype, const float* s
                       const int32_t* block_tables, const int32_t* seq_lens,
                       int32_t max_blocks_per_seq, int32_t splits, void* workspace,
                       uint64_t workspace_bytes, int device, void* stream, bool static_scratch,
-                      const DecodePools* pools = nullptr) {
+                      const DecodePools* pools = nullptr, const void* new_keys = nullptr,
+                      const void* new_values = nullptr) {
   if ((!pools && !view_ok(kv)) || !shape_ok(shape))
     return fail(PBE_ERR_INVALID, "invalid decode arena view or shape");
   if (kv_dtype != PBE_KV_BF16 && kv_dtype != PBE_KV_FP8_E4M3)
@@ -142,6 +143,11 @@ int paged_decode_call(const pbe_arena_view* kv, int32_t kv_dtype, const float* s
     return fail(PBE_ERR_INVALID, "null decode operand");
   if ((reinterpret_cast<uintptr_t>(queries) | reinterpret_cast<uintptr_t>(outputs)) % 16)
     return fail(PBE_ERR_INVALID, "queries and outputs must be 16-byte aligned");
+  const bool append = new_keys || new_values;
+  if (append && (!new_keys || !new_values))
+    return fail(PBE_ERR_INVALID, "the new token needs both its keys and its values");
+  if (append && (reinterpret_cast<uintptr_t>(new_keys) | reinterpret_cast<uintptr_t>(new_values)) % 16)
+    return fail(PBE_ERR_INVALID, "new keys and values must be 16-byte aligned");
   if (fp8 && !pools && (!scales || scale_bytes == 0))
     return fail(PBE_ERR_INVALID, "FP8 pages need a scale pool");
   if (fp8 && pools && (!pools->key_scales || !pools->value_scales || pools->scale_bytes == 0))
@@ -188,6 +194,7 @@ int paged_decode_call(const pbe_arena_view* kv, int32_t kv_dtype, const float* s
       return fail(PBE_ERR_INVALID, "scale pool must hold at least one page of scales");
   }
   const uint64_t row_bytes = (uint64_t)batch * q_heads * shape->head_dim * 2;
+  const uint64_t new_bytes = (uint64_t)batch * shape->kv_heads * shape->head_dim * 2;
   {
     PBE_DEVICE_SCOPE(device);
     std::vector<Range> known;
@@ -202,7 +209,9 @@ int paged_decode_call(const pbe_arena_view* kv, int32_t kv_dtype, const float* s
         !accessible(outputs, row_bytes, device, &known) ||
         !accessible(block_tables, (uint64_t)batch * max_blocks_per_seq * 4, device, &known) ||
         !accessible(seq_lens, (uint64_t)batch * 4, device, &known) ||
-        (!static_scratch && !accessible(workspace, need, device, &known)))
+        (!static_scratch && !accessible(workspace, need, device, &known)) ||
+        (append && (!accessible(new_keys, new_bytes, device, &known) ||
+                    !accessible(new_values, new_bytes, device, &known))))
       return fail(PBE_ERR_INVALID, "decode operands must be memory of device %d", device);
   }
   pbe::DecodeParams p{};
@@ -226,6 +235,8 @@ int paged_decode_call(const pbe_arena_view* kv, int32_t kv_dtype, const float* s
   p.out = static_cast<uint16_t*>(outputs);
   p.tables = block_tables;
   p.seq_lens = seq_lens;
+  p.new_k = static_cast<const uint16_t*>(new_keys);
+  p.new_v = static_cast<const uint16_t*>(new_values);
   const uint64_t rows = (uint64_t)batch * q_heads * splits;
   p.part_acc = static_cast<float*>(workspace);
   p.part_m = p.part_acc + rows * shape->head_dim;
@@ -296,6 +307,21 @@ int pbe_paged_decode_pools(const void* key_pool, const void* value_pool, uint64_
   return paged_decode_call(nullptr, kv_dtype, nullptr, 0, &shape, 0, queries, outputs, batch, q_heads,
                            block_tables, seq_lens, max_blocks_per_seq, splits, workspace,
                            workspace_bytes, device, stream, false, &pools);
+}
+
+int pbe_paged_decode_append(void* key_pool, void* value_pool, uint64_t pool_bytes,
+                            float* key_scales, float* value_scales, uint64_t scale_pool_bytes,
+                            int32_t kv_dtype, int32_t kv_heads, int32_t head_dim, const void* new_keys,
+                            const void* new_values, const void* queries, void* outputs, int32_t batch,
+                            int32_t q_heads, const int32_t* block_tables, const int32_t* seq_lens,
+                            int32_t max_blocks_per_seq, int32_t splits, void* workspace,
+                            uint64_t workspace_bytes, int device, void* stream) {
+  if (!new_keys || !new_values) return fail(PBE_ERR_INVALID, "null new keys or values");
+  const pbe_kv_shape shape{1, kv_heads, head_dim, 16};
+  const DecodePools pools{key_pool, value_pool, pool_bytes, key_scales, value_scales, scale_pool_bytes};
+  return paged_decode_call(nullptr, kv_dtype, nullptr, 0, &shape, 0, queries, outputs, batch, q_heads,
+                           block_tables, seq_lens, max_blocks_per_seq, splits, workspace,
+                           workspace_bytes, device, stream, false, &pools, new_keys, new_values);
 }
 
 }  // extern "C"

@@ -42,6 +42,11 @@ struct DecodeParams {
   int32_t id_max;          // largest valid block id (rows and scales inside the pools)
   FastDiv by_stride;       // block ids per page: 2 * layers page-major, 1 for per-layer pools
   FastDiv by_seg_pages;    // divides page indices by pages per segment
+  // Append form (both set or both null): bf16 [batch][kv_heads][head_dim] K and V
+  // of each sequence's new token, written at its last position before it is
+  // read; the payload and scale pools above are then written as well.
+  const uint16_t* new_k;
+  const uint16_t* new_v;
 };
 
 // Bytes of the split-K workspace (partial outputs, maxima and sums).

@@ -27,8 +27,17 @@
 //    with ds_read_b64_tr_b8 / _b16, four tokens of one head dim per lane, as
 //    the A operand of O^T += V^T P^T (P^T as held, split into a BF16 high and
 //    low part, K = 32).
-// A second kernel combines the splits, one workgroup per output row.
+// A second kernel combines the splits.
+//
+// Append variant (kAppend): the step's new token of every sequence, at its
+// last position, is written into its page slot by the one wave that reads
+// that block (per KV head only one wave reads a given row), with the page
+// writer's arithmetic (scatter_kv_kernel.cu:128-216). The wave takes the row
+// from its registers rather than from memory, so no ordering between the
+// store and any load is needed, and the result equals writing the row first
+// and reading the pages afterwards, byte for byte.
 #include "decode_kernels.h"
+#include "fp8_device.h"
 
 namespace pbe {
 namespace {
@@ -36,8 +45,6 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBlockTokens = 16;
@@ -139,7 +146,7 @@ struct BlockRegs {
 
 constexpr int kDecodeWaves = 4;
 
-template <int D, bool kFp8, int KVM>
+template <int D, bool kFp8, int KVM, bool kAppend>
 __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
     const DecodeParams p, const int32_t* __restrict__ tables) {
   using G = Geo<D, kFp8>;
@@ -197,6 +204,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
   // Value load v of lane l reads the 16 bytes at column vcol of row
   // v * RPI + vrow0: each instruction covers RPI whole rows.
   constexpr int LPR = D * E / 16, RPI = 64 / LPR;  // lanes per row, rows per load
+  constexpr int RL = D / 8;  // append: 16-byte BF16 input vectors per head row
   const int vrow0 = lane / LPR, vcol = 16 * (lane % LPR);
   const uint32_t val_off = (uint32_t)vrow0 * token_stride + (uint32_t)vcol;
   // lane (g, j): scale of token 4g + j%4 from the key (j%8 < 4) or value plane
@@ -239,9 +247,17 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Append: the new token's row of this KV head as lane (g, j) holds key row
+  // j (nk), as the value writer lanes computed it (nv), its scales, and the
+  // block it lands in (-1: nothing to write here).
+  uint32_t nk[kAppend ? W : 1], nv[kAppend ? 4 : 1];
+  float nks = 0.f, nvs = 0.f;
+  int patch_blk = -1, slot_row = 0;
+
   unsigned char* vt_w = &lds_v[w][0];
   auto compute = [&](int blk, const BlockRegs<W, kFp8>& r) {
     const int valid = blk == nblk - 1 ? seq - kBlockTokens * (nblk - 1) : kBlockTokens;
+    const bool patch = kAppend && blk == patch_blk;
     // Value tile -> LDS rows (tail rows zeroed: tail slots may hold anything, even NaN).
     {
       unsigned char* dst = vt_w + vrow0 * PITCH + vcol;
@@ -252,32 +268,53 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
                             : u32x4{0u, 0u, 0u, 0u};
         *reinterpret_cast<u32x4*>(dst + v * RPI * PITCH) = x;
       }
+      // The new row replaces what was read (LDS writes of one wave land in
+      // issue order).
+      if constexpr (kAppend) {
+        if (patch && lane >= 32 && (lane & 31) < RL) {
+          unsigned char* row = vt_w + slot_row * PITCH + (kFp8 ? 8 : 16) * (lane & 31);
+          if constexpr (kFp8) *reinterpret_cast<u32x2*>(row) = u32x2{nv[0], nv[1]};
+          else *reinterpret_cast<u32x4*>(row) = u32x4{nv[0], nv[1], nv[2], nv[3]};
+        }
+      }
     }
     // Scores, transposed: lane (g, j) gets tokens 4g..4g+3 of head j.
+    uint32_t kw[W];
+#pragma unroll
+    for (int i = 0; i < W; ++i) kw[i] = r.k[i];
+    float rscale = kFp8 ? r.scale : 0.f;
+    if constexpr (kAppend) {
+      if (patch) {
+        const bool mine = j == slot_row;
+#pragma unroll
+        for (int i = 0; i < W; ++i) kw[i] = mine ? nk[i] : kw[i];
+        if (4 * g + (j & 3) == slot_row) rscale = (j & 4) ? nvs : p.scale * nks;
+      }
+    }
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
       bf16x8 kb;
       if constexpr (kFp8) {
-        const u32x2 lo = e4m3x4_to_bf16x4_cvt(r.k[2 * kk]);
-        const u32x2 hi = e4m3x4_to_bf16x4_cvt(r.k[2 * kk + 1]);
+        const u32x2 lo = e4m3x4_to_bf16x4_cvt(kw[2 * kk]);
+        const u32x2 hi = e4m3x4_to_bf16x4_cvt(kw[2 * kk + 1]);
         kb = __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
       } else {
-        kb = __builtin_bit_cast(bf16x8, u32x4{r.k[4 * kk], r.k[4 * kk + 1], r.k[4 * kk + 2], r.k[4 * kk + 3]});
+        kb = __builtin_bit_cast(bf16x8, u32x4{kw[4 * kk], kw[4 * kk + 1], kw[4 * kk + 2], kw[4 * kk + 3]});
       }
       s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qa[kk], s, 0, 0, 0);
     }
     wave_sync();
     float ks[4] = {p.scale, p.scale, p.scale, p.scale}, vs[4] = {1.f, 1.f, 1.f, 1.f};
     if constexpr (kFp8) {  // broadcast within each 16-lane row
-      ks[0] = dpp<0x150>(r.scale);
-      ks[1] = dpp<0x151>(r.scale);
-      ks[2] = dpp<0x152>(r.scale);
-      ks[3] = dpp<0x153>(r.scale);
-      vs[0] = dpp<0x154>(r.scale);
-      vs[1] = dpp<0x155>(r.scale);
-      vs[2] = dpp<0x156>(r.scale);
-      vs[3] = dpp<0x157>(r.scale);
+      ks[0] = dpp<0x150>(rscale);
+      ks[1] = dpp<0x151>(rscale);
+      ks[2] = dpp<0x152>(rscale);
+      ks[3] = dpp<0x153>(rscale);
+      vs[0] = dpp<0x154>(rscale);
+      vs[1] = dpp<0x155>(rscale);
+      vs[2] = dpp<0x156>(rscale);
+      vs[3] = dpp<0x157>(rscale);
     }
     // Online softmax of head j over the block's 16 tokens.
     float sv[4], tmax = -INFINITY;
@@ -360,6 +397,53 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
   };
 #pragma unroll
   for (int i = 0; i < SETS; ++i) prime(blk0 + i, r[i]);
+  if constexpr (kAppend) {
+    // The wave whose split holds the sequence's last block writes the new
+    // token there (while its first blocks are in flight). Lanes 0..RL-1 take
+    // the key row, lanes 32..32+RL-1 the value row, 16 input bytes each, as
+    // the page writer does with D/8 lanes per head.
+    const int last = nblk - 1;
+    if (seq > 0 && nblk <= p.max_blocks && last >= blk0 && last < blk0 + per_split) {
+      const int32_t id = table[last];
+      const uint32_t page = fast_div((uint32_t)max(id, 0), p.by_stride);
+      if (id >= 0 && id <= p.id_max && page * p.by_stride.d == (uint32_t)id) {
+        const int row = seq - 1 - kBlockTokens * last;
+        const uint32_t seg = fast_div(page, p.by_seg_pages);
+        char* krow = const_cast<char*>(p.kv.base[seg]) + (uint64_t)(page - seg * p.by_seg_pages.d) * stride * p.half +
+                     head_off + (uint64_t)row * token_stride;
+        const bool is_v = lane >= 32;
+        const int li = lane & 31;
+        const bool act = li < RL;
+        const uint16_t* src = (is_v ? p.new_v : p.new_k) + ((int64_t)b * p.kv_heads + kvh) * D + 8 * (act ? li : 0);
+        const u32x4 x = act ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src)) : u32x4{0u, 0u, 0u, 0u};
+        char* dst = krow + (is_v ? p.v_delta : 0);
+        if constexpr (kFp8) {
+          const float mx = group_max<RL>(amax8(x));
+          const float inv = mx > 0.f ? 448.f / mx : 0.f;
+          const float sc = mx > 0.f ? mx / 448.f : 1.f;
+          const u32x2 c = quantise8(x, inv);
+          if (act) *reinterpret_cast<u32x2*>(dst + 8 * li) = c;
+          if (act && li == 0)
+            const_cast<float*>(p.scales)[(uint64_t)id * kBlockTokens * H +
+                                         (2u * p.layer * kBlockTokens + row) * H + kvh + (is_v ? p.vscale_delta : 0)] = sc;
+          nks = __shfl(sc, 0);
+          nvs = __shfl(sc, 32);
+#pragma unroll
+          for (int i = 0; i < W; ++i) nk[i] = __shfl(c[i & 1], (64 * (i / 4) + 16 * g + 4 * (i % 4)) / 8);
+          nv[0] = c[0];
+          nv[1] = c[1];
+        } else {
+          if (act) *reinterpret_cast<u32x4*>(dst + 16 * li) = x;
+#pragma unroll
+          for (int i = 0; i < W; ++i) nk[i] = __shfl(x[i % 4], 4 * (i / 4) + g);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) nv[e] = x[e];
+        }
+        patch_blk = last;
+        slot_row = row;
+      }
+    }
+  }
   for (int base = blk0; base < blk1; base += SETS) {
 #pragma unroll
     for (int i = 0; i < SETS; ++i) step(base + i, r[i]);
@@ -480,9 +564,11 @@ template <int D, bool kFp8, int KVM>
 void launch(const DecodeParams& p, hipStream_t stream) {
   const int64_t units = (int64_t)p.batch * p.kv_heads * p.splits;
   const int64_t rows = (int64_t)p.batch * p.q_heads;
-  hipLaunchKernelGGL((paged_decode_kernel<D, kFp8, KVM>),
-                     dim3((unsigned)((units + kDecodeWaves - 1) / kDecodeWaves)), dim3(kDecodeWaves * 64), 0,
-                     stream, p, p.tables);
+  const dim3 grid((unsigned)((units + kDecodeWaves - 1) / kDecodeWaves)), block(kDecodeWaves * 64);
+  if (p.new_k)
+    hipLaunchKernelGGL((paged_decode_kernel<D, kFp8, KVM, true>), grid, block, 0, stream, p, p.tables);
+  else
+    hipLaunchKernelGGL((paged_decode_kernel<D, kFp8, KVM, false>), grid, block, 0, stream, p, p.tables);
   hipLaunchKernelGGL((decode_combine_kernel<D>), dim3((unsigned)rows, (unsigned)combine_groups(rows, D)),
                      dim3(kCombineThreads), 0, stream, p);
 }

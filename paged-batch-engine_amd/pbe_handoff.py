@@ -127,6 +127,10 @@ _SIGNATURES = [
     ("pbe_paged_decode_pools", C.c_int, [_P, _P, C.c_uint64, _P, _P, C.c_uint64, C.c_int32,
                                          C.c_int32, C.c_int32, _P, _P, C.c_int32, C.c_int32, _P,
                                          _P, C.c_int32, C.c_int32, _P, C.c_uint64, C.c_int, _P]),
+    ("pbe_paged_decode_append", C.c_int, [_P, _P, C.c_uint64, _P, _P, C.c_uint64, C.c_int32,
+                                          C.c_int32, C.c_int32, _P, _P, _P, _P, C.c_int32,
+                                          C.c_int32, _P, _P, C.c_int32, C.c_int32, _P, C.c_uint64,
+                                          C.c_int, _P]),
     ("pbe_scatter_kv", C.c_int, [_P, _P, C.c_int32, C.c_int32, _P, C.c_int32, C.c_int32,
                                  C.c_int32, C.c_int32, _P, C.c_uint64, _P, C.c_uint64, _P,
                                  C.c_uint64, _P, C.c_uint64, C.c_int, _P]),
@@ -509,6 +513,23 @@ def paged_decode_pools(key_pool: int, value_pool: int, pool_bytes: int, key_scal
                                        kv_dtype, kv_heads, head_dim, queries, outputs, batch,
                                        q_heads, tables, seq_lens, max_blocks, splits, workspace,
                                        workspace_bytes, device, stream or None))
+
+
+def paged_decode_append(key_pool: int, value_pool: int, pool_bytes: int, key_scales: int,
+                        value_scales: int, scale_pool_bytes: int, kv_dtype: int, kv_heads: int,
+                        head_dim: int, new_keys: int, new_values: int, queries: int, outputs: int,
+                        batch: int, q_heads: int, tables: int, seq_lens: int, max_blocks: int,
+                        splits: int, workspace: int, workspace_bytes: int, stream: int = 0,
+                        device: int = 0) -> None:
+    """One decode step over per-layer pools that first writes each sequence's new
+    token (bf16 [batch][kv_heads][head_dim]) at its last position
+    (pbe_paged_decode_append); device pointers in, asynchronous on `stream`."""
+    check(lib().pbe_paged_decode_append(key_pool or None, value_pool or None, pool_bytes,
+                                        key_scales or None, value_scales or None, scale_pool_bytes,
+                                        kv_dtype, kv_heads, head_dim, new_keys or None,
+                                        new_values or None, queries, outputs, batch, q_heads,
+                                        tables, seq_lens, max_blocks, splits, workspace,
+                                        workspace_bytes, device, stream or None))
 
 
 PBE_IN_BF16 = 0
