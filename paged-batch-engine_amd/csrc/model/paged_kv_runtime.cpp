@@ -76,6 +76,17 @@ void HipPagedKVRuntime::scatter_single_token(const void* key, const void* value,
 }
 
 bool HipPagedKVRuntime::decode(const base::KVPoolView& pool, const PagedKVDecodeRuntimeArgs& args) const {
+  return read(pool, args, nullptr, nullptr);
+}
+
+bool HipPagedKVRuntime::decode_append(const base::KVPoolView& pool, const PagedKVDecodeRuntimeArgs& args,
+                                      const void* new_keys, const void* new_values) const {
+  if (!new_keys || !new_values) throw std::invalid_argument("decode_append needs the new token's K and V");
+  return read(pool, args, new_keys, new_values);
+}
+
+bool HipPagedKVRuntime::read(const base::KVPoolView& pool, const PagedKVDecodeRuntimeArgs& args,
+                             const void* new_keys, const void* new_values) const {
   if (!pool.valid() || !pool.key_pool_bytes() || !pool.value_pool_bytes())
     throw std::invalid_argument("KV pool view is not bound or carries no pool sizes");
   if (!args.queries || !args.outputs || !args.block_tables || !args.seq_lens || !args.workspace)
@@ -90,12 +101,20 @@ bool HipPagedKVRuntime::decode(const base::KVPoolView& pool, const PagedKVDecode
   if (fp8 && (!pool.key_scale_pool() || !pool.value_scale_pool() || !pool.scale_pool_bytes()))
     throw std::invalid_argument("FP8 KV pool view has no scale pools");
   const uint64_t bytes = std::min(pool.key_pool_bytes(), pool.value_pool_bytes());
-  const int rc = pbe_paged_decode_pools(
-      pool.key_pool(), pool.value_pool(), bytes, fp8 ? static_cast<const float*>(pool.key_scale_pool()) : nullptr,
-      fp8 ? static_cast<const float*>(pool.value_scale_pool()) : nullptr, fp8 ? pool.scale_pool_bytes() : 0,
-      fp8 ? PBE_KV_FP8_E4M3 : PBE_KV_BF16, args.num_kv_heads, args.head_size, args.queries, args.outputs,
-      args.batch_size, args.head_num, args.block_tables, args.seq_lens, args.max_blocks_per_seq, args.splits,
-      args.workspace, args.workspace_bytes, device_, stream_);
+  float* ks = fp8 ? static_cast<float*>(pool.key_scale_pool()) : nullptr;
+  float* vs = fp8 ? static_cast<float*>(pool.value_scale_pool()) : nullptr;
+  const uint64_t sb = fp8 ? pool.scale_pool_bytes() : 0;
+  const int32_t dt = fp8 ? PBE_KV_FP8_E4M3 : PBE_KV_BF16;
+  const int rc =
+      new_keys ? pbe_paged_decode_append(pool.key_pool(), pool.value_pool(), bytes, ks, vs, sb, dt, args.num_kv_heads,
+                                         args.head_size, new_keys, new_values, args.queries, args.outputs,
+                                         args.batch_size, args.head_num, args.block_tables, args.seq_lens,
+                                         args.max_blocks_per_seq, args.splits, args.workspace, args.workspace_bytes,
+                                         device_, stream_)
+               : pbe_paged_decode_pools(pool.key_pool(), pool.value_pool(), bytes, ks, vs, sb, dt, args.num_kv_heads,
+                                        args.head_size, args.queries, args.outputs, args.batch_size, args.head_num,
+                                        args.block_tables, args.seq_lens, args.max_blocks_per_seq, args.splits,
+                                        args.workspace, args.workspace_bytes, device_, stream_);
   if (rc == PBE_ERR_UNSUPPORTED) return false;
   if (rc == PBE_ERR_INVALID) throw std::invalid_argument(std::string("decode rejected: ") + pbe_last_error());
   raise_if_failed(rc);

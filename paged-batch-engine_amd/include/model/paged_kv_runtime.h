@@ -10,7 +10,8 @@
 // bytes and one fp32 scale per (token, head). Writes are bounded by the pool
 // sizes the view carries; negative slots are skipped. Launches are asynchronous
 // on the runtime's stream. decode() reads any KVPoolView through
-// pbe_paged_decode_pools; prefill attention is outside this build.
+// pbe_paged_decode_pools, and decode_append() writes the step's new tokens in
+// the same launch; prefill attention is outside this build.
 #ifndef PBE_INCLUDE_MODEL_PAGED_KV_RUNTIME_H_
 #define PBE_INCLUDE_MODEL_PAGED_KV_RUNTIME_H_
 
@@ -67,10 +68,23 @@ class HipPagedKVRuntime {
   // std::runtime_error when the launch fails.
   bool decode(const base::KVPoolView& pool, const PagedKVDecodeRuntimeArgs& args) const;
 
+  // decode() preceded by writing each sequence's new token (bf16
+  // [batch][num_kv_heads][head_size] K and V) at its last position,
+  // seq_lens[b] - 1, in one launch pair (pbe_paged_decode_append): the same
+  // pool bytes and outputs as scatter() of those tokens at the slots
+  // append_slots handed out, then decode(). The reference runs the two
+  // separately (paged_kv_runtime.cpp:207-245,293-357). Same return and throw
+  // rules as decode().
+  bool decode_append(const base::KVPoolView& pool, const PagedKVDecodeRuntimeArgs& args, const void* new_keys,
+                     const void* new_values) const;
+
   int device() const { return device_; }
   void* stream() const { return stream_; }
 
  private:
+  bool read(const base::KVPoolView& pool, const PagedKVDecodeRuntimeArgs& args, const void* new_keys,
+            const void* new_values) const;
+
   int device_;
   void* stream_;
 };

@@ -924,6 +924,81 @@ TEST_CASE("model runtime: prompt K/V written through KVCacheManager slots, then 
     HIP_OK(hipFree(dV));
     HIP_OK(hipFree(dS));
   }
+  {
+    // (4) decode_append over twin FP8 pools == scatter of the step's tokens
+    // at their last positions, then decode: all four pools and the outputs.
+    const int nblk = 12, kvm = 6, batch = 4, max_blocks = 4;
+    base::BlockAllocator one(nblk, B, H, D, base::DataType::kDataTypeBf16, base::DeviceType::kDeviceHIP,
+                             base::BlockStorageMode::kFp8E4M3PerTokenHead);
+    base::BlockAllocator two(nblk, B, H, D, base::DataType::kDataTypeBf16, base::DeviceType::kDeviceHIP,
+                             base::BlockStorageMode::kFp8E4M3PerTokenHead);
+    const base::KVPoolView p1 = one.pool_view(), p2 = two.pool_view();
+    const size_t kvb = p1.key_pool_bytes(), scb = p1.scale_pool_bytes();
+    for (int p = 0; p < 4; ++p) {
+      std::vector<uint8_t> h = random_bytes(p < 2 ? kvb : scb, 70 + p);
+      if (p < 2) {
+        for (auto& c : h) c = (c & 0x7f) == 0x7f ? 0 : c;  // no NaN codes
+      } else {
+        auto* f = reinterpret_cast<float*>(h.data());
+        for (size_t i = 0; i < scb / 4; ++i) f[i] = 0.001f + 0.01f * (h[4 * i] / 255.f);
+      }
+      void* d1[4] = {p1.key_pool(), p1.value_pool(), p1.key_scale_pool(), p1.value_scale_pool()};
+      void* d2[4] = {p2.key_pool(), p2.value_pool(), p2.key_scale_pool(), p2.value_scale_pool()};
+      HIP_OK(hipMemcpy(d1[p], h.data(), h.size(), hipMemcpyHostToDevice));
+      HIP_OK(hipMemcpy(d2[p], h.data(), h.size(), hipMemcpyHostToDevice));
+    }
+    const std::vector<int32_t> table{3, 7, 1, 10, 0, -1, -1, -1, 5, 9, 2, -1, 11, 4, 8, 6};
+    const std::vector<int32_t> lens{64, 1, 33, 50};
+    std::vector<int32_t> slots;
+    for (int b = 0; b < batch; ++b) slots.push_back(table[b * max_blocks + (lens[b] - 1) / B] * B + (lens[b] - 1) % B);
+    const auto K = random_bf16(batch * H * D, 81), V = random_bf16(batch * H * D, 82);
+    const auto q = random_bf16(batch * kvm * H * D, 83);
+    uint8_t* dK = to_device(K);
+    uint8_t* dV = to_device(V);
+    uint8_t* dq = to_device(q);
+    int32_t* dS = to_device(slots);
+    int32_t* dt = to_device(table);
+    int32_t* dl = to_device(lens);
+    REQUIRE(dK && dV && dq && dS && dt && dl);
+    const int32_t splits = 2;
+    const uint64_t ws_bytes = pbe_paged_decode_workspace_bytes(batch, kvm * H, D, splits);
+    uint8_t *o1 = nullptr, *o2 = nullptr, *ws = nullptr;
+    HIP_OK(hipMalloc(&o1, q.size()));
+    HIP_OK(hipMalloc(&o2, q.size()));
+    HIP_OK(hipMalloc(&ws, ws_bytes));
+    model::PagedKVDecodeRuntimeArgs a;
+    a.batch_size = batch;
+    a.head_num = kvm * H;
+    a.head_size = D;
+    a.kv_mul = kvm;
+    a.max_blocks_per_seq = max_blocks;
+    a.block_size = B;
+    a.num_kv_heads = H;
+    a.queries = dq;
+    a.outputs = o1;
+    a.block_tables = dt;
+    a.seq_lens = dl;
+    a.workspace = ws;
+    a.workspace_bytes = ws_bytes;
+    a.splits = splits;
+    runtime.scatter(dK, dV, base::DataType::kDataTypeBf16, p1, dS, B, H, D, batch);
+    CHECK(runtime.decode(p1, a));
+    a.outputs = o2;
+    CHECK(runtime.decode_append(p2, a, dK, dV));
+    REQUIRE(pbe_stream_synchronize(0, stream) == PBE_OK);
+    CHECK(to_host(p1.key_pool(), kvb) == to_host(p2.key_pool(), kvb));
+    CHECK(to_host(p1.value_pool(), kvb) == to_host(p2.value_pool(), kvb));
+    CHECK(to_host(p1.key_scale_pool(), scb) == to_host(p2.key_scale_pool(), scb));
+    CHECK(to_host(p1.value_scale_pool(), scb) == to_host(p2.value_scale_pool(), scb));
+    const auto got = to_host(o2, q.size());
+    CHECK(got == to_host(o1, q.size()));
+    CHECK(std::any_of(got.begin(), got.end(), [](uint8_t b) { return b != 0; }));
+    CHECK_THROWS_AS(runtime.decode_append(p2, a, dK, nullptr), std::invalid_argument);
+    for (void* d : {static_cast<void*>(dK), static_cast<void*>(dV), static_cast<void*>(dq), static_cast<void*>(dS),
+                    static_cast<void*>(dt), static_cast<void*>(dl), static_cast<void*>(o1), static_cast<void*>(o2),
+                    static_cast<void*>(ws)})
+      HIP_OK(hipFree(d));
+  }
   REQUIRE(pbe_stream_destroy(0, stream) == PBE_OK);
 }
 
