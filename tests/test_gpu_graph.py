@@ -129,16 +129,18 @@ def test_staged_calls_refuse_capture(torch_cuda):
     rl.close()
 
 
-def test_decode_loop_step_replays_from_a_graph(torch_cuda):
+@pytest.mark.parametrize("fused", [False, True])
+def test_decode_loop_step_replays_from_a_graph(torch_cuda, fused):
     """One decode step of a serving loop, captured once: the new token's K/V
     written to its page slot (pbe_scatter_kv, FP8 local pools) and attention
-    over the pools (pbe_paged_decode_pools). Between replays the host writes the
+    over the pools (pbe_paged_decode_pools), or both in the reader's launch
+    (pbe_paged_decode_append, fused). Between replays the host writes the
     next token's K/V, slots, lengths and queries into the captured buffers, as a
     loop would. Each replay's pools equal the oracle's bit for bit and its output
     is within the reader's tolerance of the float64 oracle."""
     from tests.test_gpu_decode import bf16_to_f64, close
     torch = torch_cuda
-    say("graph replay of scatter + decode over FP8 pools")
+    say(f"graph replay of scatter + decode over FP8 pools, fused={fused}")
     rng = np.random.default_rng(61)
     H, D, kvm, B, n_blocks = 2, 128, 6, 16, 24
     half, plane = B * H * D, B * H
@@ -165,15 +167,22 @@ def test_decode_loop_step_replays_from_a_graph(torch_cuda):
     torch.cuda.synchronize()
     with torch.cuda.stream(side):
         with torch.cuda.graph(graph, stream=side):
-            P.scatter_kv(new_k.data_ptr(), new_v.data_ptr(), P.PBE_IN_BF16, batch, slots.data_ptr(),
-                         B, H, D, P.PBE_KV_FP8_E4M3, d["kp"].data_ptr(), n_blocks * half,
-                         d["vp"].data_ptr(), n_blocks * half, d["ks"].data_ptr(), n_blocks * plane * 4,
-                         d["vs"].data_ptr(), n_blocks * plane * 4, stream=side.cuda_stream)
-            P.paged_decode_pools(d["kp"].data_ptr(), d["vp"].data_ptr(), n_blocks * half,
-                                 d["ks"].data_ptr(), d["vs"].data_ptr(), n_blocks * plane * 4,
-                                 P.PBE_KV_FP8_E4M3, H, D, q.data_ptr(), out.data_ptr(), batch,
-                                 H * kvm, d["tab"].data_ptr(), seq.data_ptr(), 4, splits,
-                                 ws.data_ptr(), ws_bytes, side.cuda_stream)
+            if fused:
+                P.paged_decode_append(d["kp"].data_ptr(), d["vp"].data_ptr(), n_blocks * half,
+                                      d["ks"].data_ptr(), d["vs"].data_ptr(), n_blocks * plane * 4,
+                                      P.PBE_KV_FP8_E4M3, H, D, new_k.data_ptr(), new_v.data_ptr(),
+                                      q.data_ptr(), out.data_ptr(), batch, H * kvm, d["tab"].data_ptr(),
+                                      seq.data_ptr(), 4, splits, ws.data_ptr(), ws_bytes, side.cuda_stream)
+            else:
+                P.scatter_kv(new_k.data_ptr(), new_v.data_ptr(), P.PBE_IN_BF16, batch, slots.data_ptr(),
+                             B, H, D, P.PBE_KV_FP8_E4M3, d["kp"].data_ptr(), n_blocks * half,
+                             d["vp"].data_ptr(), n_blocks * half, d["ks"].data_ptr(), n_blocks * plane * 4,
+                             d["vs"].data_ptr(), n_blocks * plane * 4, stream=side.cuda_stream)
+                P.paged_decode_pools(d["kp"].data_ptr(), d["vp"].data_ptr(), n_blocks * half,
+                                     d["ks"].data_ptr(), d["vs"].data_ptr(), n_blocks * plane * 4,
+                                     P.PBE_KV_FP8_E4M3, H, D, q.data_ptr(), out.data_ptr(), batch,
+                                     H * kvm, d["tab"].data_ptr(), seq.data_ptr(), 4, splits,
+                                     ws.data_ptr(), ws_bytes, side.cuda_stream)
     torch.cuda.synchronize()
     for step in range(4):
         K = O.bf16_from_f32(rng.standard_normal((batch, H * D)).astype(np.float32))
