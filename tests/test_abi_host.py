@@ -138,3 +138,25 @@ def test_page_writer_and_pool_reader_reject_bad_arguments_on_the_host():
         P.paged_decode_pools(fake, fake, 1 << 20, 0, 0, 0, P.PBE_KV_BF16, 2, 96, fake, fake, 1, 12,
                              fake, fake, 4, 0, fake, 1 << 20)
     assert e.value.code == P.PBE_ERR_UNSUPPORTED
+
+
+def test_append_reader_rejects_bad_arguments_on_the_host():
+    """pbe_paged_decode_append checks the new token's operands, and everything
+    pbe_paged_decode_pools checks, before any HIP call."""
+    fake = 1 << 40
+    args = dict(key_pool=fake, value_pool=fake, pool_bytes=1 << 20, key_scales=0, value_scales=0,
+                scale_pool_bytes=0, kv_dtype=P.PBE_KV_BF16, kv_heads=2, head_dim=128,
+                new_keys=fake, new_values=fake, queries=fake, outputs=fake, batch=1, q_heads=12,
+                tables=fake, seq_lens=fake, max_blocks=4, splits=0, workspace=fake,
+                workspace_bytes=1 << 20)
+    for kw, code in [(dict(new_keys=0), P.PBE_ERR_INVALID), (dict(new_values=0), P.PBE_ERR_INVALID),
+                     (dict(new_keys=fake + 8), P.PBE_ERR_INVALID),  # not 16-byte aligned
+                     (dict(kv_dtype=9), P.PBE_ERR_INVALID),
+                     (dict(head_dim=96), P.PBE_ERR_UNSUPPORTED),
+                     (dict(kv_dtype=P.PBE_KV_FP8_E4M3), P.PBE_ERR_INVALID),  # no scale pools
+                     (dict(q_heads=13), P.PBE_ERR_UNSUPPORTED)]:
+        a = dict(args)
+        a.update(kw)
+        with pytest.raises(P.PbeError) as e:
+            P.paged_decode_append(**a)
+        assert e.value.code == code, kw
