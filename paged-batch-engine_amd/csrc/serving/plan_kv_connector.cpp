@@ -95,6 +95,8 @@ base::Status BindManifestTransfers(const KVBlockManifest& manifest, const ArenaK
   for (size_t page = 0; page < pages; ++page) {
     cache::ConstComponentEndpoint src{{}, &src_layout};
     cache::MutableComponentEndpoint dst{{}, &dst_layout};
+    src.components.reserve(src_schema.components.size());
+    dst.components.reserve(dst_schema.components.size());
     for (const auto& c : src_schema.components) {
       uint8_t* a = nullptr;
       if (!component_address(source, c, by_layer[c.layer]->src_block_ids[page], &a))
