@@ -370,6 +370,60 @@ TEST_CASE("transfer plan: a missing or corrupt component fails before any write"
   CHECK(dst == original);
 }
 
+TEST_CASE("transfer plan: a schema or layout changed in place is checked again") {
+  // Binding keeps the facts of recently seen schemas and layouts; a change to
+  // the same object must give what a first binding of the new contents gives.
+  auto schema = fp8_schema();
+  const auto order = iota_order(schema.components.size());
+  LayoutDescriptor src_l, dst_l;
+  REQUIRE(MakePackedLayout(schema, "source", 1, order, {}, &src_l));
+  REQUIRE(MakePackedLayout(schema, "destination", 2, order, {}, &dst_l));
+  std::vector<uint8_t> src(src_l.total_bytes, 0x27), dst(dst_l.total_bytes, 0xa5);
+  TransferPlanner planner;
+  TransferPlan plan;
+  REQUIRE(planner.plan(schema, schema, &plan));
+  auto bind = [&](const PageSchema& s) {
+    BoundTransfer b;
+    return static_cast<bool>(BoundTransfer::Bind(plan, s, {src.data(), src.size(), &src_l},
+                                                 {dst.data(), dst.size(), &dst_l}, &b));
+  };
+  CHECK(bind(schema));
+  schema.components[0].head_count += 1;  // beyond the schema's heads: invalid
+  CHECK(!schema.validate());
+  CHECK(!bind(schema));
+  schema.components[0].head_count -= 1;
+  CHECK(bind(schema));
+  const size_t offset = dst_l.components[1].offset_bytes;
+  dst_l.components[1].offset_bytes = dst_l.components[0].offset_bytes;  // overlapping entries
+  CHECK(!dst_l.validate(schema));
+  CHECK(!bind(schema));
+  dst_l.components[1].offset_bytes = offset;
+  CHECK(bind(schema));
+  auto other = schema;
+  other.version = 2;  // same components, another plan: the fingerprints differ
+  CHECK(!bind(other));
+  // more distinct schemas than are remembered, each bound twice in turn
+  for (int round = 0; round < 2; ++round)
+    for (int layers = 1; layers <= 7; ++layers) {
+      PageSchema s;
+      REQUIRE(MakeKVPageSchema(1, layers, 16, 2, 64,
+                               base::MakeKVCacheStorageSpec(base::DataType::kDataTypeBf16,
+                                                            base::BlockStorageMode::kPlain),
+                               &s));
+      LayoutDescriptor a, b;
+      REQUIRE(MakePackedLayout(s, "a", 1, iota_order(s.components.size()), {}, &a));
+      REQUIRE(MakePackedLayout(s, "b", 2, iota_order(s.components.size()), {}, &b));
+      std::vector<uint8_t> x(a.total_bytes, 1), y(b.total_bytes, 2);
+      TransferPlan p;
+      REQUIRE(planner.plan(s, s, &p));
+      BoundTransfer t;
+      REQUIRE(BoundTransfer::Bind(p, s, {x.data(), x.size(), &a}, {y.data(), y.size(), &b}, &t));
+      CHECK_EQ(t.operations().size(), static_cast<size_t>(2 * layers));
+      REQUIRE(ExecuteCpuTransfer(t));
+      CHECK(x == y);
+    }
+}
+
 TEST_CASE("transfer plan: shape and dtype mismatches fail before any write") {
   const auto schema = plain_schema();
   const auto order = iota_order(schema.components.size());
