@@ -3,6 +3,7 @@
 // and InProcKVBlockCopyConnector (infMain/source/serving/pd_handoff.cpp:80-213),
 // with the per-op memcpy loop replaced by one op-list kernel per handoff.
 #include <algorithm>
+#include <memory>
 #include <numeric>
 #include <stdexcept>
 #include <string>
@@ -25,27 +26,127 @@ bool address_of(const pbe_arena_view& v, uint64_t offset, uint64_t len, uint8_t*
   return true;
 }
 
-// Component address of (layer, kind) of block `id` in a page-major pool.
-bool component_address(const ArenaKVPool& p, const cache::ComponentDescriptor& c, int32_t id,
-                       uint8_t** out) {
+// Byte geometry of a page-major pool.
+struct PoolGeometry {
+  uint64_t half = 0;        // one K or V plane of one block
+  uint64_t scale_rows = 0;  // fp32 scales per plane: block_size * kv_heads
+  int64_t stride = 0;       // block ids per page: 2 * layers
+};
+
+PoolGeometry geometry_of(const ArenaKVPool& p) {
   const KVPoolDescriptor& d = p.pool;
   const auto storage = base::MakeKVCacheStorageSpec(d.dtype, d.storage_mode);
-  const uint64_t half = static_cast<uint64_t>(d.block_size) * d.kv_head_num * d.head_size *
-                        base::DataTypeSize(storage.storage_dtype);
+  PoolGeometry g;
+  g.half = static_cast<uint64_t>(d.block_size) * d.kv_head_num * d.head_size *
+           base::DataTypeSize(storage.storage_dtype);
+  g.scale_rows = static_cast<uint64_t>(d.block_size) * d.kv_head_num;
+  g.stride = 2ll * d.layer_num;
+  return g;
+}
+
+// Component address of (layer, kind) of block `id` in a page-major pool.
+bool component_address(const ArenaKVPool& p, const PoolGeometry& g, const cache::ComponentDescriptor& c,
+                       int32_t id, uint8_t** out) {
   const uint64_t plane = 2ull * c.layer + (c.kind == cache::ComponentKind::kValue ||
                                             c.kind == cache::ComponentKind::kValueScale);
-  if (id < 0 || id % (2 * d.layer_num)) return false;
+  if (id < 0 || id % g.stride) return false;
   if (c.kind == cache::ComponentKind::kKey || c.kind == cache::ComponentKind::kValue)
-    return address_of(p.view, (static_cast<uint64_t>(id) + plane) * half, half, out);
+    return address_of(p.view, (static_cast<uint64_t>(id) + plane) * g.half, g.half, out);
   // scales: [page][layer][K|V][token][head] fp32
   if (!p.scales) return false;
-  const uint64_t rows = static_cast<uint64_t>(d.block_size) * d.kv_head_num;
-  const uint64_t page = static_cast<uint64_t>(id) / (2ull * d.layer_num);
-  const uint64_t off = (page * 2ull * d.layer_num + plane) * rows * 4u;
-  if (off > p.scale_bytes || rows * 4u > p.scale_bytes - off) return false;
+  const uint64_t page = static_cast<uint64_t>(id) / static_cast<uint64_t>(g.stride);
+  const uint64_t off = (page * static_cast<uint64_t>(g.stride) + plane) * g.scale_rows * 4u;
+  if (off > p.scale_bytes || g.scale_rows * 4u > p.scale_bytes - off) return false;
   *out = static_cast<uint8_t*>(p.scales) + off;
   return true;
 }
+}  // namespace
+
+namespace {
+
+// What every page of a manifest shares: its layer mappings, both schemas,
+// the compiled plan and both packed layouts.
+struct ManifestBinding {
+  PoolGeometry src_geo, dst_geo;
+  std::vector<const KVBlockMapping*> by_layer;
+  size_t pages = 0;
+  cache::PageSchema src_schema, dst_schema;
+  std::shared_ptr<const cache::TransferPlan> plan;
+  cache::LayoutDescriptor src_layout, dst_layout;
+};
+
+base::Status prepare(const KVBlockManifest& manifest, const ArenaKVPool& source,
+                     const ArenaKVPool& destination, cache::TransferPlanner* planner, ManifestBinding* b) {
+  const int32_t layers = source.pool.layer_num;
+  if (layers != destination.pool.layer_num || static_cast<int32_t>(manifest.layer_mappings.size()) != layers)
+    return InvalidArgument("semantic transfer layer coverage mismatch");
+  b->by_layer.assign(layers, nullptr);
+  for (const auto& m : manifest.layer_mappings) {
+    if (m.layer_idx < 0 || m.layer_idx >= layers || b->by_layer[m.layer_idx] ||
+        m.src_block_ids.size() != m.dst_block_ids.size())
+      return InvalidArgument("semantic transfer mapping is incomplete or duplicate");
+    if (b->pages && b->pages != m.src_block_ids.size())
+      return InvalidArgument("semantic transfer page coverage mismatch");
+    b->pages = m.src_block_ids.size();
+    b->by_layer[m.layer_idx] = &m;
+  }
+  if (!b->pages) return InvalidArgument("semantic transfer has no pages");
+  b->src_geo = geometry_of(source);
+  b->dst_geo = geometry_of(destination);
+
+  auto schema_of = [](const KVPoolDescriptor& d, cache::PageSchema* out) {
+    return cache::MakeKVPageSchema(1, d.layer_num, d.block_size, d.kv_head_num, d.head_size,
+                                   base::MakeKVCacheStorageSpec(d.dtype, d.storage_mode), out);
+  };
+  base::Status status = schema_of(source.pool, &b->src_schema);
+  if (!status) return status;
+  status = schema_of(destination.pool, &b->dst_schema);
+  if (!status) return status;
+  status = planner->compile(b->src_schema, b->dst_schema, cache::TransferPlacement::kExactDirect, &b->plan);
+  if (!status) return status;
+  std::vector<size_t> src_order(b->src_schema.components.size()), dst_order(b->dst_schema.components.size());
+  std::iota(src_order.begin(), src_order.end(), 0);
+  std::iota(dst_order.begin(), dst_order.end(), 0);
+  status = cache::MakePackedLayout(b->src_schema, "pd-source", 1, src_order, {}, &b->src_layout);
+  if (!status) return status;
+  return cache::MakePackedLayout(b->dst_schema, "pd-destination", 1, dst_order, {}, &b->dst_layout);
+}
+
+// Component endpoints of one page: its blocks' component addresses.
+base::Status endpoints(const ManifestBinding& b, const ArenaKVPool& source, const ArenaKVPool& destination,
+                       size_t page, cache::ConstComponentEndpoint* src, cache::MutableComponentEndpoint* dst) {
+  src->layout = &b.src_layout;
+  dst->layout = &b.dst_layout;
+  src->components.clear();
+  dst->components.clear();
+  src->components.reserve(b.src_schema.components.size());
+  dst->components.reserve(b.dst_schema.components.size());
+  for (const auto& c : b.src_schema.components) {
+    uint8_t* a = nullptr;
+    if (!component_address(source, b.src_geo, c, b.by_layer[c.layer]->src_block_ids[page], &a))
+      return InvalidArgument("source block outside its page-major arena");
+    src->components.push_back({c, a, c.byte_size()});
+  }
+  for (const auto& c : b.dst_schema.components) {
+    uint8_t* a = nullptr;
+    if (!component_address(destination, b.dst_geo, c, b.by_layer[c.layer]->dst_block_ids[page], &a))
+      return InvalidArgument("destination block outside its page-major arena");
+    dst->components.push_back({c, a, c.byte_size()});
+  }
+  return base::error::Success();
+}
+
+// Index of the span holding [p, p + bytes).
+template <typename Span>
+size_t span_holding(const std::vector<Span>& spans, const uint8_t* p, size_t bytes) {
+  for (size_t i = 0; i < spans.size(); ++i) {
+    const uint8_t* begin = spans[i].data;
+    if (p >= begin && bytes <= spans[i].bytes && static_cast<size_t>(p - begin) <= spans[i].bytes - bytes)
+      return i;
+  }
+  return spans.size();
+}
+
 }  // namespace
 
 base::Status BindManifestTransfers(const KVBlockManifest& manifest, const ArenaKVPool& source,
@@ -53,68 +154,67 @@ base::Status BindManifestTransfers(const KVBlockManifest& manifest, const ArenaK
                                    std::vector<cache::BoundTransfer>* transfers) {
   if (!planner || !transfers || !transfers->empty())
     return InvalidArgument("invalid semantic transfer binding arguments");
-  const int32_t layers = source.pool.layer_num;
-  if (layers != destination.pool.layer_num || static_cast<int32_t>(manifest.layer_mappings.size()) != layers)
-    return InvalidArgument("semantic transfer layer coverage mismatch");
-  std::vector<const KVBlockMapping*> by_layer(layers, nullptr);
-  size_t pages = 0;
-  for (const auto& m : manifest.layer_mappings) {
-    if (m.layer_idx < 0 || m.layer_idx >= layers || by_layer[m.layer_idx] ||
-        m.src_block_ids.size() != m.dst_block_ids.size())
-      return InvalidArgument("semantic transfer mapping is incomplete or duplicate");
-    if (pages && pages != m.src_block_ids.size())
-      return InvalidArgument("semantic transfer page coverage mismatch");
-    pages = m.src_block_ids.size();
-    by_layer[m.layer_idx] = &m;
-  }
-  if (!pages) return InvalidArgument("semantic transfer has no pages");
-
-  cache::PageSchema src_schema, dst_schema;
-  auto schema_of = [](const KVPoolDescriptor& d, cache::PageSchema* out) {
-    return cache::MakeKVPageSchema(1, d.layer_num, d.block_size, d.kv_head_num, d.head_size,
-                                   base::MakeKVCacheStorageSpec(d.dtype, d.storage_mode), out);
-  };
-  base::Status status = schema_of(source.pool, &src_schema);
+  ManifestBinding b;
+  base::Status status = prepare(manifest, source, destination, planner, &b);
   if (!status) return status;
-  status = schema_of(destination.pool, &dst_schema);
-  if (!status) return status;
-  std::shared_ptr<const cache::TransferPlan> plan;
-  status = planner->compile(src_schema, dst_schema, cache::TransferPlacement::kExactDirect, &plan);
-  if (!status) return status;
-  std::vector<size_t> src_order(src_schema.components.size()), dst_order(dst_schema.components.size());
-  std::iota(src_order.begin(), src_order.end(), 0);
-  std::iota(dst_order.begin(), dst_order.end(), 0);
-  cache::LayoutDescriptor src_layout, dst_layout;
-  status = cache::MakePackedLayout(src_schema, "pd-source", 1, src_order, {}, &src_layout);
-  if (!status) return status;
-  status = cache::MakePackedLayout(dst_schema, "pd-destination", 1, dst_order, {}, &dst_layout);
-  if (!status) return status;
-
   std::vector<cache::BoundTransfer> bound;
-  bound.reserve(pages);
-  for (size_t page = 0; page < pages; ++page) {
-    cache::ConstComponentEndpoint src{{}, &src_layout};
-    cache::MutableComponentEndpoint dst{{}, &dst_layout};
-    src.components.reserve(src_schema.components.size());
-    dst.components.reserve(dst_schema.components.size());
-    for (const auto& c : src_schema.components) {
-      uint8_t* a = nullptr;
-      if (!component_address(source, c, by_layer[c.layer]->src_block_ids[page], &a))
-        return InvalidArgument("source block outside its page-major arena");
-      src.components.push_back({c, a, c.byte_size()});
-    }
-    for (const auto& c : dst_schema.components) {
-      uint8_t* a = nullptr;
-      if (!component_address(destination, c, by_layer[c.layer]->dst_block_ids[page], &a))
-        return InvalidArgument("destination block outside its page-major arena");
-      dst.components.push_back({c, a, c.byte_size()});
-    }
+  bound.reserve(b.pages);
+  cache::ConstComponentEndpoint src;
+  cache::MutableComponentEndpoint dst;
+  for (size_t page = 0; page < b.pages; ++page) {
+    status = endpoints(b, source, destination, page, &src, &dst);
+    if (!status) return status;
     cache::BoundTransfer t;
-    status = cache::BoundTransfer::BindComponents(*plan, src_schema, dst_schema, src, dst, &t);
+    status = cache::BoundTransfer::BindComponents(*b.plan, b.src_schema, b.dst_schema, src, dst, &t);
     if (!status) return status;
     bound.push_back(std::move(t));
   }
   *transfers = std::move(bound);
+  return base::error::Success();
+}
+
+base::Status BindManifestCopyOps(const KVBlockManifest& manifest, const ArenaKVPool& source,
+                                 const ArenaKVPool& destination, cache::TransferPlanner* planner,
+                                 std::vector<pbe_copy_op>* ops) {
+  if (!planner || !ops || !ops->empty()) return InvalidArgument("invalid semantic transfer binding arguments");
+  ManifestBinding b;
+  base::Status status = prepare(manifest, source, destination, planner, &b);
+  if (!status) return status;
+  // The first page is bound in full; its operations, as (span, offset)
+  // pairs, are the template every page follows.
+  cache::ConstComponentEndpoint src;
+  cache::MutableComponentEndpoint dst;
+  status = endpoints(b, source, destination, 0, &src, &dst);
+  if (!status) return status;
+  cache::BoundTransfer first;
+  status = cache::BoundTransfer::BindComponents(*b.plan, b.src_schema, b.dst_schema, src, dst, &first);
+  if (!status) return status;
+  struct Piece {
+    size_t src_span, dst_span;
+    uint64_t src_off, dst_off, bytes;
+  };
+  std::vector<Piece> pieces;
+  pieces.reserve(first.operations().size());
+  for (const auto& op : first.operations()) {
+    const size_t si = span_holding(src.components, op.source, op.bytes);
+    const size_t di = span_holding(dst.components, op.destination, op.bytes);
+    if (si == src.components.size() || di == dst.components.size())
+      return base::error::InternalError("bound operation outside its component span");
+    pieces.push_back({si, di, static_cast<uint64_t>(op.source - src.components[si].data),
+                      static_cast<uint64_t>(op.destination - dst.components[di].data), op.bytes});
+  }
+  std::vector<pbe_copy_op> out;
+  out.reserve(b.pages * pieces.size());
+  for (size_t page = 0; page < b.pages; ++page) {
+    if (page) {
+      status = endpoints(b, source, destination, page, &src, &dst);
+      if (!status) return status;
+    }
+    for (const Piece& p : pieces)
+      out.push_back({reinterpret_cast<uint64_t>(src.components[p.src_span].data) + p.src_off,
+                     reinterpret_cast<uint64_t>(dst.components[p.dst_span].data) + p.dst_off, p.bytes});
+  }
+  *ops = std::move(out);
   return base::error::Success();
 }
 
@@ -140,17 +240,11 @@ base::Status InProcKVBlockCopyConnector::submit(const KVBlockManifest& manifest,
   base::Status status = manifest.validate();
   if (!status) return status;
   *handle = {next_handoff_id_++};
-  std::vector<cache::BoundTransfer> transfers;
-  status = BindManifestTransfers(manifest, source_, destination_, &planner_, &transfers);
   std::vector<pbe_copy_op> ops;
+  status = BindManifestCopyOps(manifest, source_, destination_, &planner_, &ops);
   uint64_t bytes = 0;
   if (status) {
-    for (const auto& t : transfers)
-      for (const auto& op : t.operations()) {
-        ops.push_back({reinterpret_cast<uint64_t>(op.source), reinterpret_cast<uint64_t>(op.destination),
-                       op.bytes});
-        bytes += op.bytes;
-      }
+    for (const auto& op : ops) bytes += op.bytes;
     const int rc = pbe_copy_ops(ops.data(), static_cast<int64_t>(ops.size()), device_, stream_);
     if (rc == PBE_ERR_INVALID) status = InvalidArgument(pbe_last_error());
     else if (rc != PBE_OK) status = base::error::InternalError(pbe_last_error());

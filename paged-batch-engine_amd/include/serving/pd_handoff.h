@@ -137,6 +137,16 @@ base::Status BindManifestTransfers(const KVBlockManifest& manifest, const ArenaK
                                    const ArenaKVPool& destination, cache::TransferPlanner* planner,
                                    std::vector<cache::BoundTransfer>* transfers);
 
+// The same binding as a flat list of device copy operations (the concatenated
+// operations of BindManifestTransfers' transfers, in order), for
+// pbe_copy_ops. No counterpart in the reference: every page of a manifest
+// shares its schemas, plan and layouts, so the first page is bound in full
+// and the others follow its operations at their own component addresses,
+// with the same per-page bounds checks and errors.
+base::Status BindManifestCopyOps(const KVBlockManifest& manifest, const ArenaKVPool& source,
+                                 const ArenaKVPool& destination, cache::TransferPlanner* planner,
+                                 std::vector<pbe_copy_op>* ops);
+
 // InProcKVBlockCopyConnector (pd_handoff.cpp:80-213) over arena pools: each
 // handoff is bound through the TransferPlan and all of its component copies
 // (2*layers per page, plus scales for FP8 pools) run as one op-list kernel on

@@ -1037,6 +1037,66 @@ TEST_CASE("bind manifest transfers: 2L component ops per page at page-major addr
   CHECK(!serving::BindManifestTransfers(m, pool, fp8, &planner, &none));  // conversion: no plan
 }
 
+TEST_CASE("bind manifest copy ops: the flattened transfers, page after page, with the same errors") {
+  std::mt19937 rng(31);
+  for (bool fp8 : {false, true})
+    for (uint64_t segment : {uint64_t{0}, uint64_t{4 * Group::kPage}}) {
+      serving::ArenaKVPool pool;
+      pool.pool = pool3();
+      if (fp8) pool.pool.storage_mode = base::BlockStorageMode::kFp8E4M3PerTokenHead;
+      const uint64_t page = fp8 ? Group::kPage / 2 : Group::kPage;
+      pool.view = fake_view(40 * page, segment ? segment / (fp8 ? 2 : 1) : 0);
+      std::vector<uint8_t> scales(40 * 2 * 3 * 16 * 2 * 4);
+      if (fp8) {
+        pool.scales = scales.data();
+        pool.scale_bytes = scales.size();
+      }
+      std::vector<int32_t> ids(40);
+      std::iota(ids.begin(), ids.end(), 0);
+      std::shuffle(ids.begin(), ids.end(), rng);
+      std::vector<int32_t> src, dst;
+      for (int i = 0; i < 13; ++i) {
+        src.push_back(ids[i] * 6);
+        dst.push_back(ids[20 + i] * 6);
+      }
+      auto m = good_manifest();
+      m.src_pool = m.dst_pool = pool.pool;
+      m.layer_mappings.clear();
+      for (int l = 0; l < 3; ++l) m.layer_mappings.push_back({l, src, dst});
+      cache::TransferPlanner planner;
+      std::vector<cache::BoundTransfer> t;
+      REQUIRE(serving::BindManifestTransfers(m, pool, pool, &planner, &t));
+      std::vector<pbe_copy_op> want;
+      for (const auto& x : t)
+        for (const auto& op : x.operations())
+          want.push_back({reinterpret_cast<uint64_t>(op.source), reinterpret_cast<uint64_t>(op.destination), op.bytes});
+      std::vector<pbe_copy_op> got;
+      REQUIRE(serving::BindManifestCopyOps(m, pool, pool, &planner, &got));
+      REQUIRE(got.size() == want.size());
+      CHECK_EQ(got.size(), 13u * 6u * (fp8 ? 2u : 1u));
+      for (size_t i = 0; i < got.size(); ++i) {
+        CHECK_EQ(got[i].src, want[i].src);
+        CHECK_EQ(got[i].dst, want[i].dst);
+        CHECK_EQ(got[i].bytes, want[i].bytes);
+      }
+      // a bad id on the first or a later page fails both forms with one message
+      for (size_t bad_page : {size_t{0}, size_t{7}}) {
+        for (bool on_dst : {false, true}) {
+          auto b = m;
+          for (auto& lm : b.layer_mappings) (on_dst ? lm.dst_block_ids : lm.src_block_ids)[bad_page] = 40 * 6;
+          std::vector<cache::BoundTransfer> none;
+          std::vector<pbe_copy_op> no_ops;
+          const auto e1 = serving::BindManifestTransfers(b, pool, pool, &planner, &none);
+          const auto e2 = serving::BindManifestCopyOps(b, pool, pool, &planner, &no_ops);
+          CHECK(!e1);
+          CHECK(!e2);
+          CHECK(e1.get_err_msg() == e2.get_err_msg());
+          CHECK(no_ops.empty());
+        }
+      }
+    }
+}
+
 TEST_CASE("bind manifest transfers: FP8 pools add scale components") {
   serving::ArenaKVPool pool;
   pool.pool = pool3();
