@@ -111,6 +111,29 @@ int32_t BlockAllocator::allocate() {
   return id;
 }
 
+bool BlockAllocator::allocate_many(int32_t n, std::vector<int32_t>* out) {
+  if (!group_) {
+    for (int32_t k = 0; k < n; ++k) {
+      const int32_t id = allocate();
+      if (id < 0) return false;
+      out->push_back(id);
+    }
+    return true;
+  }
+  const size_t first = out->size();
+  const bool all = group_->allocate_many(layer_, n, out);
+  for (size_t i = first; i < out->size(); ++i) {
+    const int32_t id = (*out)[i];
+    check_id(id);
+    if (ref_counts_[id] != 0) throw std::logic_error("allocated block still has outstanding references");
+    if (generations_[id] == std::numeric_limits<uint64_t>::max())
+      throw std::logic_error("block generation exhausted");
+    ++generations_[id];
+    ref_counts_[id] = 1;
+  }
+  return all;
+}
+
 void BlockAllocator::incref(int32_t block_id) {
   check_id(block_id);
   if (ref_counts_[block_id] <= 0) throw std::logic_error("Cannot incref a free block");

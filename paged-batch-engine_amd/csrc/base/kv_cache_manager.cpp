@@ -98,14 +98,10 @@ bool KVCacheManager::append_slots(RequestId id, int32_t num_tokens) {
     std::vector<std::vector<int32_t>> fresh(num_layers_);
     for (int32_t l = 0; l < num_layers_; ++l) {
       fresh[l].reserve(need);
-      for (int32_t k = 0; k < need; ++k) {
-        const int32_t b = layers_[l]->allocate();
-        if (b < 0) {
-          for (int32_t m = l; m >= 0; --m)
-            for (int32_t got : fresh[m]) layers_[m]->free(got);
-          return false;
-        }
-        fresh[l].push_back(b);
+      if (!layers_[l]->allocate_many(need, &fresh[l])) {
+        for (int32_t m = l; m >= 0; --m)
+          for (int32_t got : fresh[m]) layers_[m]->free(got);
+        return false;
       }
     }
     for (int32_t l = 0; l < num_layers_; ++l)

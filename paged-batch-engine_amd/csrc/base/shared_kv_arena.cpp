@@ -122,7 +122,7 @@ struct SharedKVPageGroup::Impl {
   std::set<int> free_ids;
   std::deque<Page*> retiring;
   std::vector<pbe_event*> spare_fences;
-  std::vector<std::deque<int>> pending;  // per layer: ids reserved by layer 0
+  std::vector<std::deque<Page*>> pending;  // per layer: pages reserved by layer 0
   uint64_t leased = 0;
   bool failed = false;  // an unacknowledged release can never become reusable
   mutable std::mutex mu;
@@ -170,6 +170,9 @@ struct SharedKVPageGroup::Impl {
     }
   }
 
+  // allocate() with the mutex held.
+  int allocate_locked(int layer);
+
   int reserve(Page& p) {
     const int id = id_of(p);
     std::fill(p.active.begin(), p.active.end(), 1);
@@ -178,7 +181,7 @@ struct SharedKVPageGroup::Impl {
     free_ids.erase(id);
     for (int l = 1; l < layers; ++l) {
       p.reserved[l] = 1;
-      pending[l].push_back(id);
+      pending[l].push_back(&p);
     }
     return id;
   }
@@ -251,16 +254,30 @@ void SharedKVPageGroup::collect() {
 
 int SharedKVPageGroup::allocate(int layer) {
   std::lock_guard<std::mutex> lock(impl_->mu);
-  Impl& m = *impl_;
+  return impl_->allocate_locked(layer);
+}
+
+bool SharedKVPageGroup::allocate_many(int layer, int n, std::vector<int32_t>* out) {
+  std::lock_guard<std::mutex> lock(impl_->mu);
+  for (int k = 0; k < n; ++k) {
+    const int id = impl_->allocate_locked(layer);
+    if (id < 0) return false;
+    out->push_back(id);
+  }
+  return true;
+}
+
+int SharedKVPageGroup::Impl::allocate_locked(int layer) {
+  Impl& m = *this;
   if (m.failed) throw std::runtime_error("shared KV page group failed; stop GPU domain");
   if (layer < 0 || layer >= m.layers) throw std::invalid_argument("invalid layer");
   if (layer > 0) {
     auto& q = m.pending[layer];
     if (q.empty()) throw std::logic_error("Allocate shared pages in layer order");
-    const int id = q.front();
+    Page* p = q.front();
     q.pop_front();
-    m.pages.at(id)->reserved[layer] = 0;
-    return id;
+    p->reserved[layer] = 0;
+    return m.id_of(*p);
   }
   m.collect_locked();
   if (!m.free_ids.empty()) return m.reserve(*m.pages.at(*m.free_ids.begin()));
@@ -312,7 +329,7 @@ void SharedKVPageGroup::retire(int layer, int id) {
     for (int l = 1; l < m.layers; ++l) {
       if (!p.reserved[l]) continue;
       auto& q = m.pending[l];
-      q.erase(std::remove(q.begin(), q.end(), id), q.end());
+      q.erase(std::remove(q.begin(), q.end(), &p), q.end());
       p.reserved[l] = 0;
       p.active[l] = 0;
       --p.active_layers;

@@ -112,6 +112,10 @@ class BlockAllocator {
   // Block id of a fresh page for this layer, or -1 when the group is out of
   // quota (block_allocator.cpp:206-216). Layers allocate in order.
   int32_t allocate();
+  // allocate() up to n times, appending the ids to *out; false at the first
+  // -1 (ids already appended stay allocated). One page-group lock per call in
+  // shared-arena mode. No counterpart in the reference.
+  bool allocate_many(int32_t n, std::vector<int32_t>* out);
   void incref(int32_t block_id);
   // Drops one reference; the last one retires the page in the group.
   void free(int32_t block_id);

@@ -115,6 +115,11 @@ class SharedKVPageGroup {
   // reserves the same id for layers 1..L-1, which must allocate in order.
   // Returns -1 when the model's limit or the arena is exhausted.
   int allocate(int layer);
+  // allocate(layer) up to n times under one lock, appending the ids to *out;
+  // returns false at the first -1 (ids already appended stay allocated).
+  // No counterpart in the reference: a request's pages for one layer in one
+  // call, as KVCacheManager::append_slots takes them.
+  bool allocate_many(int layer, int n, std::vector<int32_t>* out);
   // Releases one layer of a page. Retiring layer 0 first rolls back the
   // unconsumed layer reservations. When the last layer retires, a fence is
   // recorded on the stream; the page is reused only after it completes.
