@@ -28,15 +28,18 @@ class DeviceScope {
       err_ = hipErrorNoDevice;
       return;
     }
+    if (old_ == device) return;  // already current: nothing to switch or restore
     err_ = hipSetDevice(device);
+    switched_ = err_ == hipSuccess;
   }
   ~DeviceScope() {
-    if (err_ == hipSuccess) (void)hipSetDevice(old_);
+    if (switched_) (void)hipSetDevice(old_);
   }
   hipError_t error() const { return err_; }
 
  private:
   int old_ = 0;
+  bool switched_ = false;
   hipError_t err_ = hipSuccess;
 };
 
