@@ -9,6 +9,9 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <thread>
+#include <chrono>
+#include <atomic>
 #include <memory>
 #include <string>
 #include <cstring>
@@ -153,6 +156,68 @@ TEST_CASE("hip backend: a dependency event orders the copy after the producer") 
   (void)hipStreamDestroy(producer);
   (void)hipFree(d_src);
   (void)hipFree(d_dst);
+}
+
+namespace {
+// Holds a stream until the test lets it go (the gate of
+// test_page_migration_cuda.cpp:8-12), with a bound so that a failed test can
+// never leave the host function waiting.
+std::atomic<bool> g_gate_open{false};
+void hold_stream(void*) {
+  const auto until = std::chrono::steady_clock::now() + std::chrono::seconds(20);
+  while (!g_gate_open.load() && std::chrono::steady_clock::now() < until) std::this_thread::yield();
+}
+}  // namespace
+
+TEST_CASE("hip backend: a gated dependency keeps the copy pending and its destination untouched") {
+  for (bool fp8 : {false, true}) {
+    const auto s = schema_of(fp8);
+    LayoutDescriptor l;
+    REQUIRE(MakePackedLayout(s, "packed", 7, iota_order(s.components.size()), {}, &l));
+    const size_t n = l.total_bytes;
+    uint8_t *d_src = nullptr, *h_dst = nullptr;
+    HIP_OK(hipMalloc(&d_src, n));
+    HIP_OK(hipHostMalloc(&h_dst, n, hipHostMallocDefault));  // before the gate: may synchronize
+    HIP_OK(hipMemset(d_src, 0x21, n));
+    std::memset(h_dst, 0, n);
+    HIP_OK(hipDeviceSynchronize());
+    TransferPlanner planner;
+    TransferPlan plan;
+    REQUIRE(planner.plan(s, s, &plan));
+    BoundTransfer d2h;
+    REQUIRE(BoundTransfer::Bind(plan, s, {d_src, n, &l}, {h_dst, n, &l}, &d2h));
+    hipStream_t producer;
+    hipEvent_t dependency;
+    HIP_OK(hipStreamCreateWithFlags(&producer, hipStreamNonBlocking));
+    HIP_OK(hipEventCreateWithFlags(&dependency, hipEventDisableTiming));
+    {
+      auto backend = MakeHipTransferBackend(1, 0, dependency);
+      g_gate_open.store(false);
+      const bool gated = hipLaunchHostFunc(producer, hold_stream, nullptr) == hipSuccess &&
+                         hipEventRecord(dependency, producer) == hipSuccess;
+      CHECK(gated);
+      const BackendResult submitted = backend->submit(1, TransferDirection::kToHost, d2h);
+      CHECK(submitted == BackendResult::kPending);
+      if (gated && submitted == BackendResult::kPending) {
+        const auto until = std::chrono::steady_clock::now() + std::chrono::milliseconds(50);
+        bool pending = true;
+        while (std::chrono::steady_clock::now() < until) pending = pending && backend->poll(1) == BackendResult::kPending;
+        CHECK(pending);
+        CHECK(std::all_of(h_dst, h_dst + n, [](uint8_t b) { return b == 0; }));
+      }
+      g_gate_open.store(true);  // always, whatever failed above
+      HIP_OK(hipStreamSynchronize(producer));
+      if (submitted == BackendResult::kPending) {
+        CHECK(backend->drain(1) == BackendResult::kSucceeded);
+        backend->release(1);
+      }
+      CHECK(std::all_of(h_dst, h_dst + n, [](uint8_t b) { return b == 0x21; }));
+    }
+    (void)hipEventDestroy(dependency);
+    (void)hipStreamDestroy(producer);
+    (void)hipFree(d_src);
+    (void)hipHostFree(h_dst);
+  }
 }
 
 TEST_CASE("hip backend: completion is in submission order; settled records are reused") {
