@@ -526,6 +526,53 @@ TEST_CASE("end to end: the reference's copy_shared_kv call order over KVCacheMan
   CHECK(pbe_arena_destroy(arena) == PBE_OK);
 }
 
+TEST_CASE("page group: a retired page is not handed out again until its fence has passed") {
+  // The deferred unpin of shared_kv_reuse_probe.cpp, with the stream held by
+  // a host-function gate: the page's fence is queued behind the gate.
+  const int layers = 2;
+  const uint64_t half = 16 * 2 * 64 * 2, page = 2 * layers * half, arena_bytes = 12 * page;
+  pbe_arena* arena = nullptr;
+  REQUIRE(pbe_arena_create(0, arena_bytes, arena_bytes, 515, &arena) == PBE_OK);
+  pbe_arena_view view{};
+  REQUIRE(pbe_arena_get_view(arena, &view) == PBE_OK);
+  auto owner = std::make_shared<base::LocalChunkOwner>(arena_bytes, 515);
+  owner->register_model("m", arena_bytes);
+  hipStream_t stream;
+  HIP_OK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+  {
+    auto client = std::make_shared<base::SharedKVArenaClient>(owner, view, "m", arena_bytes, 0);
+    auto group = std::make_shared<base::SharedKVPageGroup>(client, layers, half, 3 * page, stream);
+    const int a = group->allocate(0);
+    REQUIRE(a >= 0);
+    CHECK_EQ(group->allocate(1), a);
+    g_gate_open.store(false);
+    const bool gated = hipLaunchHostFunc(stream, hold_stream, nullptr) == hipSuccess;
+    CHECK(gated);
+    group->retire(1, a);
+    group->retire(0, a);  // the last layer: the fence is recorded behind the gate
+    group->collect();
+    const int b = group->allocate(0);
+    CHECK(b >= 0);
+    CHECK(b != a);  // a is still fenced
+    group->allocate(1);
+    g_gate_open.store(true);  // always, whatever failed above
+    HIP_OK(hipStreamSynchronize(stream));
+    group->collect();
+    const int c = group->allocate(0);  // the lowest free id again
+    CHECK_EQ(c, a);
+    group->allocate(1);
+    for (int id : {b, c}) {
+      group->retire(1, id);
+      group->retire(0, id);
+    }
+    HIP_OK(hipStreamSynchronize(stream));
+    group->collect();
+    CHECK_EQ(group->leased_bytes(), 0u);
+  }
+  (void)hipStreamDestroy(stream);
+  CHECK(pbe_arena_destroy(arena) == PBE_OK);
+}
+
 TEST_CASE("block allocator: local HIP pools copy one block's payload, FP8 scales included") {
   for (int fp8 = 0; fp8 < 2; ++fp8) {
     base::BlockAllocator a(8, 16, 2, 64, base::DataType::kDataTypeBf16, base::DeviceType::kDeviceHIP,
