@@ -774,7 +774,9 @@ def main() -> int:
         "pct_of_peak": round(100 * achieved / PEAK_GBPS, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
-                     "traffic": traffic, "algorithmic_bytes": alg},
+                     "traffic": traffic, "algorithmic_bytes": alg,
+                     "traffic_source": "profiles/handoff_copy_c2_pmc.txt (rocprofv3 --pmc FETCH_SIZE, "
+                                       "WRITE_SIZE of the same kernel and plan, scaled by a plain copy)"},
         "cpu_baseline": cpu,
         "parity_vs_oracle": parity,
         "wall_ms_per_step_incl_scrub": round(wall / args.steps * 1e3, 4),
