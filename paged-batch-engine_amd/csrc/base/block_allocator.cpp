@@ -149,6 +149,26 @@ void BlockAllocator::free(int32_t block_id) {
   }
 }
 
+void BlockAllocator::free_many(const std::vector<int32_t>& block_ids) {
+  if (!group_) {
+    for (int32_t id : block_ids) free(id);
+    return;
+  }
+  std::vector<int32_t> released;
+  released.reserve(block_ids.size());
+  try {
+    for (int32_t id : block_ids) {
+      check_id(id);
+      if (ref_counts_[id] <= 0) throw std::logic_error("Double free of block");
+      if (--ref_counts_[id] == 0) released.push_back(id);
+    }
+  } catch (...) {
+    group_->retire_many(layer_, released);
+    throw;
+  }
+  group_->retire_many(layer_, released);
+}
+
 int32_t BlockAllocator::ref_count(int32_t block_id) const {
   check_id(block_id);
   return ref_counts_[block_id];

@@ -78,8 +78,7 @@ void KVCacheManager::free_request(RequestId id) {
   Request& r = live_request(id);
   // Later layers first: for a shared page group, layer 0's release is the one
   // that fences the page once every other layer has let go of it.
-  for (int32_t l = num_layers_; l-- > 0;)
-    for (int32_t b : r.blocks[l]) layers_[l]->free(b);
+  for (int32_t l = num_layers_; l-- > 0;) layers_[l]->free_many(r.blocks[l]);
   r.blocks.assign(num_layers_, {});
   r.tokens = r.committed = 0;
   r.live = false;

@@ -122,6 +122,8 @@ struct SharedKVPageGroup::Impl {
   std::set<int> free_ids;
   std::deque<Page*> retiring;
   std::vector<pbe_event*> spare_fences;
+  // Pages still holding each recorded fence: pages retired together share one.
+  std::unordered_map<pbe_event*, size_t> fence_users;
   std::vector<std::deque<Page*>> pending;  // per layer: pages reserved by layer 0
   uint64_t leased = 0;
   bool failed = false;  // an unacknowledged release can never become reusable
@@ -138,7 +140,13 @@ struct SharedKVPageGroup::Impl {
       failed = true;
       throw std::runtime_error(std::string("shared KV page fence failed: ") + pbe_last_error());
     }
-    spare_fences.push_back(p.fence);
+    // The event is recorded again only once every page that shares it has
+    // seen it pass.
+    auto users = fence_users.find(p.fence);
+    if (users != fence_users.end() && --users->second == 0) {
+      fence_users.erase(users);
+      spare_fences.push_back(p.fence);
+    }
     p.fence = nullptr;
     return true;
   }
@@ -186,20 +194,53 @@ struct SharedKVPageGroup::Impl {
     return id;
   }
 
-  void record_fence(Page& p) {
-    if (arena->device() < 0) return;  // metadata-only group: nothing runs on a GPU
-    pbe_event* ev = nullptr;
-    if (!spare_fences.empty()) {
-      ev = spare_fences.back();
-      spare_fences.pop_back();
-    } else if (pbe_event_create(arena->device(), 0, &ev) != PBE_OK) {
-      throw std::runtime_error(std::string("shared KV fence creation failed: ") + pbe_last_error());
+  // One fence, recorded on the stream now, for pages whose last layer was
+  // retired with no stream work in between; then they start retiring.
+  void fence_and_retire(const std::vector<Page*>& done) {
+    if (done.empty()) return;
+    if (arena->device() >= 0) {  // a metadata-only group runs nothing on a GPU
+      pbe_event* ev = nullptr;
+      if (!spare_fences.empty()) {
+        ev = spare_fences.back();
+        spare_fences.pop_back();
+      } else if (pbe_event_create(arena->device(), 0, &ev) != PBE_OK) {
+        throw std::runtime_error(std::string("shared KV fence creation failed: ") + pbe_last_error());
+      }
+      if (pbe_event_record(ev, stream) != PBE_OK) {
+        pbe_event_destroy(ev);
+        throw std::runtime_error(std::string("shared KV fence record failed: ") + pbe_last_error());
+      }
+      fence_users[ev] = done.size();
+      for (Page* p : done) p->fence = ev;
     }
-    if (pbe_event_record(ev, stream) != PBE_OK) {
-      pbe_event_destroy(ev);
-      throw std::runtime_error(std::string("shared KV fence record failed: ") + pbe_last_error());
+    for (Page* p : done) {
+      p->retiring = true;
+      retiring.push_back(p);
     }
-    p.fence = ev;
+  }
+
+  // One layer of one page let go; a page whose last layer this was joins `done`.
+  void retire_locked(int layer, int id, std::vector<Page*>* done) {
+    if (failed) throw std::runtime_error("shared KV page group failed; stop GPU domain");
+    auto found = pages.find(id);
+    if (found == pages.end()) throw std::logic_error("page does not belong to current chunk generation");
+    Page& p = *found->second;
+    if (layer < 0 || layer >= layers) throw std::out_of_range("invalid layer");
+    if (!p.active[layer] || p.retiring || p.reserved[layer]) throw std::logic_error("double/stale page retire");
+    if (layer == 0) {
+      // Roll back reservations the later layers never consumed.
+      for (int l = 1; l < layers; ++l) {
+        if (!p.reserved[l]) continue;
+        auto& q = pending[l];
+        q.erase(std::remove(q.begin(), q.end(), &p), q.end());
+        p.reserved[l] = 0;
+        p.active[l] = 0;
+        --p.active_layers;
+      }
+    }
+    p.active[layer] = 0;
+    // A page is indivisible across layers: one fence after every layer's use.
+    if (--p.active_layers == 0) done->push_back(&p);
   }
 };
 
@@ -236,9 +277,8 @@ SharedKVPageGroup::~SharedKVPageGroup() {
   if (impl_->arena->device() >= 0 &&
       pbe_stream_synchronize(impl_->arena->device(), impl_->stream) != PBE_OK)
     return;
+  for (auto& entry : impl_->fence_users) pbe_event_destroy(entry.first);
   for (auto& entry : impl_->chunks) {
-    for (auto& p : entry.second->pages)
-      if (p.fence) pbe_event_destroy(p.fence);
     try {
       impl_->arena->release(entry.second->lease);
     } catch (...) {  // domain shutdown
@@ -315,34 +355,20 @@ int SharedKVPageGroup::Impl::allocate_locked(int layer) {
   return id;
 }
 
-void SharedKVPageGroup::retire(int layer, int id) {
+void SharedKVPageGroup::retire(int layer, int id) { retire_many(layer, {id}); }
+
+void SharedKVPageGroup::retire_many(int layer, const std::vector<int32_t>& ids) {
   std::lock_guard<std::mutex> lock(impl_->mu);
   Impl& m = *impl_;
-  if (m.failed) throw std::runtime_error("shared KV page group failed; stop GPU domain");
-  auto found = m.pages.find(id);
-  if (found == m.pages.end()) throw std::logic_error("page does not belong to current chunk generation");
-  Impl::Page& p = *found->second;
-  if (layer < 0 || layer >= m.layers) throw std::out_of_range("invalid layer");
-  if (!p.active[layer] || p.retiring || p.reserved[layer]) throw std::logic_error("double/stale page retire");
-  if (layer == 0) {
-    // Roll back reservations the later layers never consumed.
-    for (int l = 1; l < m.layers; ++l) {
-      if (!p.reserved[l]) continue;
-      auto& q = m.pending[l];
-      q.erase(std::remove(q.begin(), q.end(), &p), q.end());
-      p.reserved[l] = 0;
-      p.active[l] = 0;
-      --p.active_layers;
-    }
+  std::vector<Impl::Page*> done;
+  try {
+    for (int32_t id : ids) m.retire_locked(layer, id, &done);
+  } catch (...) {
+    m.fence_and_retire(done);  // what was let go before the bad id retires as usual
+    throw;
   }
-  p.active[layer] = 0;
-  if (--p.active_layers == 0) {
-    // A page is indivisible across layers: one fence after every layer's use.
-    m.record_fence(p);
-    p.retiring = true;
-    m.retiring.push_back(&p);
-    m.collect_locked();
-  }
+  m.fence_and_retire(done);
+  m.collect_locked();
 }
 
 void SharedKVPageGroup::detach_for_takeover(const std::vector<int32_t>& ids, PageTakeover* out) {

@@ -119,6 +119,11 @@ class BlockAllocator {
   void incref(int32_t block_id);
   // Drops one reference; the last one retires the page in the group.
   void free(int32_t block_id);
+  // free() of each id in order; in shared-arena mode the blocks that reach no
+  // references retire together (SharedKVPageGroup::retire_many). An invalid
+  // id throws as free() would, after the ids before it are freed. No
+  // counterpart in the reference.
+  void free_many(const std::vector<int32_t>& block_ids);
   int32_t ref_count(int32_t block_id) const;
   BlockHandle handle(int32_t block_id) const;
   bool is_current(BlockHandle handle) const;

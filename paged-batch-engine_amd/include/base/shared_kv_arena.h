@@ -124,6 +124,12 @@ class SharedKVPageGroup {
   // unconsumed layer reservations. When the last layer retires, a fence is
   // recorded on the stream; the page is reused only after it completes.
   void retire(int layer, int block_id);
+  // retire(layer, id) for each id in order, under one lock; the pages whose
+  // last layer these were share one fence recorded after all of them (the
+  // same stream position as one fence each). An invalid id throws as
+  // retire() would, after the ids before it have retired. No counterpart in
+  // the reference (one event per page).
+  void retire_many(int layer, const std::vector<int32_t>& block_ids);
   int free_blocks(int layer) const;
   int capacity() const;
   uint64_t leased_bytes() const;

@@ -573,6 +573,51 @@ TEST_CASE("page group: a retired page is not handed out again until its fence ha
   CHECK(pbe_arena_destroy(arena) == PBE_OK);
 }
 
+TEST_CASE("page group: a request's pages freed together share one fence; none is reused before it") {
+  const int layers = 3;
+  const uint64_t half = 16 * 2 * 64 * 2, page = 2 * layers * half, arena_bytes = 24 * page;
+  pbe_arena* arena = nullptr;
+  REQUIRE(pbe_arena_create(0, arena_bytes, arena_bytes, 516, &arena) == PBE_OK);
+  pbe_arena_view view{};
+  REQUIRE(pbe_arena_get_view(arena, &view) == PBE_OK);
+  auto owner = std::make_shared<base::LocalChunkOwner>(arena_bytes, 516);
+  owner->register_model("m", arena_bytes);
+  void* stream = nullptr;
+  REQUIRE(pbe_stream_create(0, &stream) == PBE_OK);
+  {
+    auto client = std::make_shared<base::SharedKVArenaClient>(owner, view, "m", arena_bytes, 0);
+    auto group = std::make_shared<base::SharedKVPageGroup>(client, layers, half, 3 * page, stream);
+    auto kv = manager_over(group, 2, 64);
+    const base::RequestId first = kv->register_request();
+    REQUIRE(kv->append_slots(first, 5 * 16));
+    const std::vector<int32_t> held = kv->get_block_ids(first, 0);
+    REQUIRE(held.size() == 5u);
+    g_gate_open.store(false);
+    CHECK(hipLaunchHostFunc(static_cast<hipStream_t>(stream), hold_stream, nullptr) == hipSuccess);
+    kv->free_request(first);  // every layer; the fence lands behind the gate
+    const base::RequestId second = kv->register_request();
+    REQUIRE(kv->append_slots(second, 5 * 16));
+    const std::vector<int32_t> fresh = kv->get_block_ids(second, 0);
+    for (int32_t id : fresh) CHECK(std::find(held.begin(), held.end(), id) == held.end());
+    for (int l = 1; l < layers; ++l) CHECK(kv->get_block_ids(second, l) == fresh);
+    g_gate_open.store(true);  // always, whatever failed above
+    REQUIRE(pbe_stream_synchronize(0, stream) == PBE_OK);
+    group->collect();
+    // every page the second request does not hold, the first request's among them
+    const base::RequestId third = kv->register_request();
+    REQUIRE(kv->append_slots(third, 19 * 16));
+    const std::vector<int32_t>& rest = kv->get_block_ids(third, 0);
+    for (int32_t id : held) CHECK(std::find(rest.begin(), rest.end(), id) != rest.end());
+    kv->free_request(second);
+    kv->free_request(third);
+    REQUIRE(pbe_stream_synchronize(0, stream) == PBE_OK);
+    group->collect();
+    CHECK_EQ(group->leased_bytes(), 0u);
+  }
+  pbe_stream_destroy(0, stream);
+  CHECK(pbe_arena_destroy(arena) == PBE_OK);
+}
+
 TEST_CASE("block allocator: local HIP pools copy one block's payload, FP8 scales included") {
   for (int fp8 = 0; fp8 < 2; ++fp8) {
     base::BlockAllocator a(8, 16, 2, 64, base::DataType::kDataTypeBf16, base::DeviceType::kDeviceHIP,
