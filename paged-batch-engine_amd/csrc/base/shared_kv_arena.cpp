@@ -178,8 +178,9 @@ struct SharedKVPageGroup::Impl {
     }
   }
 
-  // allocate() with the mutex held.
-  int allocate_locked(int layer);
+  // allocate() with the mutex held; `collect` first returns pages whose fences
+  // have passed.
+  int allocate_locked(int layer, bool collect = true);
 
   int reserve(Page& p) {
     const int id = id_of(p);
@@ -299,15 +300,19 @@ int SharedKVPageGroup::allocate(int layer) {
 
 bool SharedKVPageGroup::allocate_many(int layer, int n, std::vector<int32_t>* out) {
   std::lock_guard<std::mutex> lock(impl_->mu);
+  // Fences are looked at once per batch (each look is a runtime query), and
+  // once more before giving up.
+  if (layer == 0 && n > 0) impl_->collect_locked();
   for (int k = 0; k < n; ++k) {
-    const int id = impl_->allocate_locked(layer);
+    int id = impl_->allocate_locked(layer, false);
+    if (id < 0 && layer == 0) id = impl_->allocate_locked(layer, true);
     if (id < 0) return false;
     out->push_back(id);
   }
   return true;
 }
 
-int SharedKVPageGroup::Impl::allocate_locked(int layer) {
+int SharedKVPageGroup::Impl::allocate_locked(int layer, bool collect) {
   Impl& m = *this;
   if (m.failed) throw std::runtime_error("shared KV page group failed; stop GPU domain");
   if (layer < 0 || layer >= m.layers) throw std::invalid_argument("invalid layer");
@@ -319,7 +324,7 @@ int SharedKVPageGroup::Impl::allocate_locked(int layer) {
     p->reserved[layer] = 0;
     return m.id_of(*p);
   }
-  m.collect_locked();
+  if (collect) m.collect_locked();
   if (!m.free_ids.empty()) return m.reserve(*m.pages.at(*m.free_ids.begin()));
   const uint64_t room = m.arena->hard_limit() - m.leased;
   if (room < m.page) return -1;
