@@ -286,3 +286,23 @@ def test_append_argument_errors_are_rejected(torch_cuda):
                               d["q"].data_ptr(), d["out"].data_ptr(), step.batch, 12,
                               d["tab"].data_ptr(), d["sl"].data_ptr(), step.max_blocks, 0,
                               ws.data_ptr(), ws.numel())
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_geometries_equal_scatter_then_decode(torch_cuda, seed):
+    """Seeded random shapes: page dtype, KV heads, head_dim, query heads per KV
+    head, ragged lengths (zeros included) and split counts."""
+    rng = np.random.default_rng(1000 + seed)
+    fp8 = bool(rng.integers(0, 2))
+    H = int(rng.choice([1, 2, 4]))
+    D = int(rng.choice([64, 128]))
+    kvm = int(rng.integers(1, 9))
+    lens = [int(x) for x in rng.integers(0, 700, int(rng.integers(1, 9)))]
+    if not any(lens):
+        lens[0] = 1
+    step = Step(torch_cuda, fp8, H, D, kvm, lens, seed=2000 + seed)
+    splits = int(rng.choice([0, 1, 2, 5, step.max_blocks + 1]))
+    say(f"decode append random seed={seed} fp8={fp8} H={H} D={D} kvm={kvm} lens={lens} splits={splits}")
+    a = step.two_step(splits)
+    b = step.fused(splits)
+    _same(a, b)
