@@ -367,16 +367,28 @@ int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream
   // consecutive pages of a run, in a bound manifest) are merged, so the
   // overlap check, the staging and the kernel see runs instead of planes.
   std::vector<pbe_copy_op> merged;
+  merged.reserve(64);
   {
     std::vector<Range> known;
+    // The allocations last found to hold a source and a destination: most ops
+    // of a bound manifest fall inside them, and the full check (which asks
+    // the runtime once per allocation) runs only for the others.
+    Range last_src{1, 0}, last_dst{1, 0};
+    auto inside = [](const Range& r, uint64_t p, uint64_t n) { return p >= r.begin && p + n <= r.end; };
+    auto check = [&](uint64_t p, uint64_t n, Range* last) {
+      if (inside(*last, p, n)) return true;
+      if (!accessible(reinterpret_cast<const void*>(p), n, device, &known)) return false;
+      for (const Range& r : known)
+        if (inside(r, p, n)) *last = r;
+      return true;
+    };
     for (int64_t i = 0; i < n_ops; ++i) {
       const pbe_copy_op& o = ops[i];
       if (!o.src || !o.dst || !o.bytes)
         return fail(PBE_ERR_INVALID, "op %lld: null pointer or zero bytes", (long long)i);
       if (o.bytes > ~0ull - o.src || o.bytes > ~0ull - o.dst)
         return fail(PBE_ERR_INVALID, "op %lld: span wraps the address space", (long long)i);
-      if (!accessible(reinterpret_cast<const void*>(o.src), o.bytes, device, &known) ||
-          !accessible(reinterpret_cast<const void*>(o.dst), o.bytes, device, &known))
+      if (!check(o.src, o.bytes, &last_src) || !check(o.dst, o.bytes, &last_dst))
         return fail(PBE_ERR_INVALID, "op %lld: endpoint is not device or pinned memory", (long long)i);
       if (!merged.empty()) {
         pbe_copy_op& last = merged.back();

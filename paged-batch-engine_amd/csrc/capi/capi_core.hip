@@ -92,7 +92,13 @@ bool accessible(const void* ptr, uint64_t bytes, int device, std::vector<Range>*
   if (!p || bytes > ~0ull - p) return false;
   for (const Range& r : *known)
     if (p >= r.begin && p + bytes <= r.end) return true;
-  if (arena_registry().contains(p, bytes, device)) return true;
+  {
+    Range seg{};
+    if (arena_registry().segment_of(p, bytes, device, &seg.begin, &seg.end)) {
+      known->push_back(seg);  // later checks of this segment stay in `known`
+      return true;
+    }
+  }
   hipDeviceptr_t base = nullptr;
   size_t size = 0;
   if (hipMemGetAddressRange(&base, &size, const_cast<void*>(ptr)) != hipSuccess || !base) {

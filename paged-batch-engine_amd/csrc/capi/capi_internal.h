@@ -85,6 +85,17 @@ struct ArenaRegistry {
                   entries.end());
   }
   bool contains(uint64_t p, uint64_t bytes, int device) { return device_of(p, bytes) == device; }
+  // The registered segment of `device` holding [p, p+bytes), if any.
+  bool segment_of(uint64_t p, uint64_t bytes, int device, uint64_t* begin, uint64_t* end) {
+    std::lock_guard<std::mutex> lock(mu);
+    for (const Entry& e : entries)
+      if (p >= e.begin && bytes <= e.end - p && p < e.end && e.device == device) {
+        *begin = e.begin;
+        *end = e.end;
+        return true;
+      }
+    return false;
+  }
   // Device of the registered segment holding [p, p+bytes), or -1.
   int device_of(uint64_t p, uint64_t bytes) {
     std::lock_guard<std::mutex> lock(mu);
