@@ -372,6 +372,7 @@ void SharedKVPageGroup::retire_many(int layer, const std::vector<int32_t>& ids) 
     m.fence_and_retire(done);  // what was let go before the bad id retires as usual
     throw;
   }
+  if (done.empty()) return;  // no page finished: nothing new to collect
   m.fence_and_retire(done);
   m.collect_locked();
 }
