@@ -97,9 +97,25 @@ std::vector<ChunkLease> SharedKVArenaClient::take_over(const std::vector<ChunkLe
 
 struct SharedKVPageGroup::Impl {
   struct Chunk;
+  // One flag per layer, stored in the page's Chunk (one allocation per Chunk
+  // rather than two per page).
+  struct LayerFlags {
+    char* data = nullptr;
+    size_t n = 0;
+    char& operator[](size_t i) { return data[i]; }
+    char operator[](size_t i) const { return data[i]; }
+    char* begin() { return data; }
+    char* end() { return data + n; }
+    const char* begin() const { return data; }
+    const char* end() const { return data + n; }
+    void assign(size_t count, char v) {
+      if (count != n) throw std::logic_error("page layer flags have a fixed size");
+      std::fill(data, data + n, v);
+    }
+  };
   struct Page {
     uint64_t offset = 0;
-    std::vector<char> active, reserved;  // per layer
+    LayerFlags active, reserved;  // per layer
     int active_layers = 0;
     bool retiring = false;
     pbe_event* fence = nullptr;
@@ -108,7 +124,17 @@ struct SharedKVPageGroup::Impl {
   struct Chunk {
     ChunkLease lease;
     std::vector<Page> pages;  // fixed size: Page* stay valid
+    std::vector<char> flags;  // pages x {active, reserved} x layers
     size_t free_pages = 0;
+    // Sizes the pages and points their layer flags into `flags`.
+    void lay_out(size_t n_pages, int layers) {
+      pages.resize(n_pages);
+      flags.assign(n_pages * 2 * static_cast<size_t>(layers), 0);
+      for (size_t i = 0; i < n_pages; ++i) {
+        pages[i].active = {flags.data() + 2 * i * layers, static_cast<size_t>(layers)};
+        pages[i].reserved = {flags.data() + (2 * i + 1) * layers, static_cast<size_t>(layers)};
+      }
+    }
   };
 
   std::shared_ptr<SharedKVArenaClient> arena;
@@ -343,12 +369,10 @@ int SharedKVPageGroup::Impl::allocate_locked(int layer, bool collect) {
   }
   auto chunk = std::make_unique<Impl::Chunk>();
   chunk->lease = lease;
-  chunk->pages.resize(lease.bytes / m.page);
+  chunk->lay_out(lease.bytes / m.page, m.layers);
   for (size_t i = 0; i < chunk->pages.size(); ++i) {
     Impl::Page& p = chunk->pages[i];
     p.offset = lease.offset + i * m.page;
-    p.active.assign(m.layers, 0);
-    p.reserved.assign(m.layers, 0);
     p.chunk = chunk.get();
     m.pages.emplace(m.id_of(p), &p);
     m.free_ids.insert(m.id_of(p));
@@ -484,7 +508,7 @@ size_t SharedKVPageGroup::adopt(const PageTakeover& t) {
   for (const ChunkLease& lease : held) {
     auto chunk = std::make_unique<Impl::Chunk>();
     chunk->lease = lease;
-    chunk->pages.resize(lease.bytes / m.page);
+    chunk->lay_out(lease.bytes / m.page, m.layers);
     chunk->free_pages = 0;
     for (size_t i = 0; i < chunk->pages.size(); ++i) {
       Impl::Page& p = chunk->pages[i];
