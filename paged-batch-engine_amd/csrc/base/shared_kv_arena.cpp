@@ -144,8 +144,66 @@ struct SharedKVPageGroup::Impl {
   std::string layout;
   std::unordered_map<uint64_t, std::unique_ptr<Chunk>> chunks;  // by lease id
   std::unordered_map<uint64_t, std::unique_ptr<Chunk>> detached;  // handed to a receiver
-  std::unordered_map<int, Page*> pages;                         // by page id
-  std::set<int> free_ids;
+  // The arena's pages by page index (page id / (2 * layers)): few enough to
+  // index directly, so lookups, inserts and the lowest free id need no tree
+  // or hash nodes.
+  struct PageTable {
+    std::vector<Page*> slots;
+    int stride = 1;
+    void init(size_t n, int page_stride) {
+      slots.assign(n, nullptr);
+      stride = page_stride;
+    }
+    Page* get(int id) const {
+      if (id < 0 || id % stride) return nullptr;
+      const size_t i = static_cast<size_t>(id / stride);
+      return i < slots.size() ? slots[i] : nullptr;
+    }
+    Page* at(int id) const {
+      Page* p = get(id);
+      if (!p) throw std::out_of_range("page id not in the group");
+      return p;
+    }
+    size_t count(int id) const { return get(id) ? 1 : 0; }
+    void emplace(int id, Page* p) { slots.at(static_cast<size_t>(id / stride)) = p; }
+    void erase(int id) {
+      if (get(id)) slots[static_cast<size_t>(id / stride)] = nullptr;
+    }
+  };
+  struct FreeIds {  // a bitmap over page indices, lowest id first
+    std::vector<uint64_t> bits;
+    size_t n = 0;
+    int stride = 1;
+    mutable size_t first = 0;  // no set bit below word `first`
+    void init(size_t pages, int page_stride) {
+      bits.assign((pages + 63) / 64, 0);
+      stride = page_stride;
+    }
+    size_t count(int id) const {
+      const size_t i = static_cast<size_t>(id / stride);
+      return (bits[i / 64] >> (i % 64)) & 1u;
+    }
+    void insert(int id) {
+      const size_t i = static_cast<size_t>(id / stride);
+      const uint64_t b = 1ull << (i % 64);
+      if (!(bits.at(i / 64) & b)) bits[i / 64] |= b, ++n;
+      first = std::min(first, i / 64);
+    }
+    void erase(int id) {
+      const size_t i = static_cast<size_t>(id / stride);
+      const uint64_t b = 1ull << (i % 64);
+      if (bits.at(i / 64) & b) bits[i / 64] &= ~b, --n;
+    }
+    bool empty() const { return n == 0; }
+    size_t size() const { return n; }
+    int lowest() const {
+      for (; first < bits.size(); ++first)
+        if (bits[first]) return static_cast<int>((first * 64 + __builtin_ctzll(bits[first])) * stride);
+      return -1;
+    }
+  };
+  PageTable pages;
+  FreeIds free_ids;
   std::deque<Page*> retiring;
   std::vector<pbe_event*> spare_fences;
   // Pages still holding each recorded fence: pages retired together share one.
@@ -249,9 +307,9 @@ struct SharedKVPageGroup::Impl {
   // One layer of one page let go; a page whose last layer this was joins `done`.
   void retire_locked(int layer, int id, std::vector<Page*>* done) {
     if (failed) throw std::runtime_error("shared KV page group failed; stop GPU domain");
-    auto found = pages.find(id);
-    if (found == pages.end()) throw std::logic_error("page does not belong to current chunk generation");
-    Page& p = *found->second;
+    Page* found = pages.get(id);
+    if (!found) throw std::logic_error("page does not belong to current chunk generation");
+    Page& p = *found;
     if (layer < 0 || layer >= layers) throw std::out_of_range("invalid layer");
     if (!p.active[layer] || p.retiring || p.reserved[layer]) throw std::logic_error("double/stale page retire");
     if (layer == 0) {
@@ -290,6 +348,8 @@ SharedKVPageGroup::SharedKVPageGroup(std::shared_ptr<SharedKVArenaClient> arena,
   impl_->pending.resize(layers);
   impl_->half = half_bytes;
   impl_->page = half_bytes * 2 * layers;
+  impl_->pages.init(impl_->arena->bytes() / impl_->page + 1, 2 * layers);
+  impl_->free_ids.init(impl_->arena->bytes() / impl_->page + 1, 2 * layers);
   impl_->chunk_bytes = round_up(std::max(target, impl_->page), impl_->page);
   impl_->stream = stream;
   impl_->layout = "page-major-gqa-v1:" + std::to_string(layers) + ":" + std::to_string(half_bytes);
@@ -351,7 +411,7 @@ int SharedKVPageGroup::Impl::allocate_locked(int layer, bool collect) {
     return m.id_of(*p);
   }
   if (collect) m.collect_locked();
-  if (!m.free_ids.empty()) return m.reserve(*m.pages.at(*m.free_ids.begin()));
+  if (!m.free_ids.empty()) return m.reserve(*m.pages.at(m.free_ids.lowest()));
   const uint64_t room = m.arena->hard_limit() - m.leased;
   if (room < m.page) return -1;
   const uint64_t want = room >= m.chunk_bytes ? m.chunk_bytes : m.page;
@@ -410,9 +470,9 @@ void SharedKVPageGroup::detach_for_takeover(const std::vector<int32_t>& ids, Pag
   std::unordered_map<int, int> listed;
   std::unordered_map<Impl::Chunk*, size_t> touched;
   for (int32_t id : ids) {
-    auto found = m.pages.find(id);
-    if (found == m.pages.end()) throw std::logic_error("takeover page does not belong to this group");
-    const Impl::Page& p = *found->second;
+    const Impl::Page* found = m.pages.get(id);
+    if (!found) throw std::logic_error("takeover page does not belong to this group");
+    const Impl::Page& p = *found;
     if (p.active_layers != m.layers || p.retiring ||
         std::any_of(p.reserved.begin(), p.reserved.end(), [](char r) { return r != 0; }))
       throw std::logic_error("takeover page is not active in every layer");
