@@ -94,17 +94,19 @@ bool KVCacheManager::append_slots(RequestId id, int32_t num_tokens) {
   if (need > 0) {
     for (int32_t l = 0; l < num_layers_; ++l)
       if (layers_[l]->num_free_blocks() < need) return false;
-    std::vector<std::vector<int32_t>> fresh(num_layers_);
+    // Appended in place; on failure every layer's new blocks are freed and
+    // the tables cut back to where they were (all or nothing).
+    const size_t had = r.blocks[0].size();
     for (int32_t l = 0; l < num_layers_; ++l) {
-      fresh[l].reserve(need);
-      if (!layers_[l]->allocate_many(need, &fresh[l])) {
-        for (int32_t m = l; m >= 0; --m)
-          for (int32_t got : fresh[m]) layers_[m]->free(got);
+      r.blocks[l].reserve(had + need);
+      if (!layers_[l]->allocate_many(need, &r.blocks[l])) {
+        for (int32_t m = l; m >= 0; --m) {
+          for (size_t k = had; k < r.blocks[m].size(); ++k) layers_[m]->free(r.blocks[m][k]);
+          r.blocks[m].resize(had);
+        }
         return false;
       }
     }
-    for (int32_t l = 0; l < num_layers_; ++l)
-      r.blocks[l].insert(r.blocks[l].end(), fresh[l].begin(), fresh[l].end());
   }
   r.tokens += num_tokens;
   return true;
