@@ -593,6 +593,9 @@ def main() -> int:
                     help="with --decode-only: tokens per sequence")
     ap.add_argument("--fp8-only", action="store_true",
                     help="time only the fused FP8 handoff (config 4, both scale modes)")
+    ap.add_argument("--host-paths", action="store_true",
+                    help="run lib/pbe_host_paths: host costs of the C++ connector and of the "
+                         "reference's copy_shared_kv call order at config-2 size (one JSON line)")
     ap.add_argument("--decode-loop-only", action="store_true",
                     help="time only a 28-layer decode step (page write + reader), eager and graph")
     ap.add_argument("--scatter-only", action="store_true",
@@ -605,6 +608,13 @@ def main() -> int:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "the handoff is a same-GPU page migration.", file=sys.stderr)
         return 2
+    if args.host_paths:  # a child process: this one never touches the GPU
+        import subprocess
+        exe = Path(__file__).resolve().parent / "paged-batch-engine_amd" / "lib" / "pbe_host_paths"
+        if not exe.exists():
+            print(f"bench.py: {exe} is missing: run __graft_entry__.build()", file=sys.stderr)
+            return 2
+        return subprocess.run([str(exe)], timeout=300).returncode
 
     import numpy as np
     import torch

@@ -127,6 +127,9 @@ def build(jobs: int = 8) -> Path:
         _run([HIPCC, *HIP_FLAGS, *INCLUDES, f"-I{ROOT / 'tests' / 'cpp'}", str(ROOT / t),
               f"-L{LIB}", "-lpbe_handoff", "-Wl,-rpath,$ORIGIN",
               "-o", str(LIB / "pbe_cpp_gpu_tests")])
+    # bench.py --host-paths: the C++ paths' host costs at config-2 size
+    _run([HIPCC, *HIP_FLAGS, *INCLUDES, str(ROOT / "tests" / "cpp" / "bench_host_paths.cpp"),
+          f"-L{LIB}", "-lpbe_handoff", "-Wl,-rpath,$ORIGIN", "-o", str(LIB / "pbe_host_paths")])
     return so
 
 

@@ -1,0 +1,187 @@
+// Host-side costs of the handoff's C++ paths at config-2 size (Qwen2.5-1.5B,
+// 28 layers, 315 pages), run by `bench.py --host-paths`; prints one JSON object.
+//   - the generic plan form (InProcKVBlockCopyConnector, pd_handoff.cpp:192-213):
+//     per-page BindComponents binding, BindManifestCopyOps, pbe_copy_ops of the
+//     op list, and the connector's submit -> drain;
+//   - the reference's copy_shared_kv call order (split_pd_engine.cpp:49-115)
+//     through serving::CopySharedKVToDecode: append_slots over 28 layers, the
+//     whole call, and free_request afterwards; and the reservation while the
+//     previous request's pages still wait on their fences behind a 1 GiB copy.
+// Every figure is the median over the iterations, in microseconds.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstdio>
+#include <memory>
+#include <numeric>
+#include <random>
+#include <vector>
+
+#include "base/kv_cache_manager.h"
+#include "base/shared_kv_arena.h"
+#include "cache/transfer_plan.h"
+#include "pbe_handoff.h"
+#include "serving/pd_handoff.h"
+#include "serving/split_pd_handoff.h"
+
+namespace {
+
+constexpr int kLayers = 28, kHeads = 2, kDim = 128, kPages = 315, kIters = 25;
+
+double now_us() {
+  return std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+double median(std::vector<double> v) {
+  std::sort(v.begin(), v.end());
+  return v[v.size() / 2];
+}
+
+std::unique_ptr<base::KVCacheManager> manager_over(const std::shared_ptr<base::SharedKVPageGroup>& g) {
+  std::vector<std::unique_ptr<base::BlockAllocator>> layers;
+  for (int l = 0; l < g->layers(); ++l) layers.push_back(std::make_unique<base::BlockAllocator>(16, kHeads, kDim, g, l));
+  return std::make_unique<base::KVCacheManager>(16, g->layers(), std::move(layers));
+}
+
+#define CHECK_OR(cond, code) \
+  do {                       \
+    if (!(cond)) {           \
+      std::fprintf(stderr, "failed: %s\n", #cond); \
+      return code;           \
+    }                        \
+  } while (0)
+
+}  // namespace
+
+int main() {
+  const uint64_t half = 16 * kHeads * kDim * 2, page = 2ull * kLayers * half;
+  const serving::KVPoolDescriptor pool_desc{0, kLayers, 16, kHeads, kDim, base::DataType::kDataTypeBf16,
+                                            base::BlockStorageMode::kPlain};
+  // ---- generic plan form over a 1000-page device arena
+  std::vector<double> bind_us, ops_us, call_us, conn_us;
+  {
+    const uint64_t pages = 1000, bytes = pages * page;
+    uint8_t* arena = nullptr;
+    CHECK_OR(hipMalloc(&arena, bytes) == hipSuccess, 2);
+    serving::ArenaKVPool pool;
+    pool.view.bytes = pool.view.segment_bytes = bytes;
+    pool.view.nseg = 1;
+    pool.view.base[0] = arena;
+    pool.pool = pool_desc;
+    std::vector<int> perm(pages);
+    std::iota(perm.begin(), perm.end(), 0);
+    std::shuffle(perm.begin(), perm.end(), std::mt19937(5));
+    std::vector<int32_t> src, dst;
+    for (int i = 0; i < kPages; ++i) {
+      src.push_back(perm[i] * 2 * kLayers);
+      dst.push_back(perm[kPages + i] * 2 * kLayers);
+    }
+    serving::KVBlockManifest m;
+    m.client_request_id.value = "c2";
+    m.handoff_id.value = 1;
+    m.prompt_tokens = m.computed_tokens = 5040;
+    m.src_pool = m.dst_pool = pool_desc;
+    for (int l = 0; l < kLayers; ++l) m.layer_mappings.push_back({l, src, dst});
+    serving::InProcKVBlockCopyConnector conn(pool, pool, 0);
+    for (int it = 0; it < kIters; ++it) {
+      cache::TransferPlanner planner;
+      std::vector<cache::BoundTransfer> t;
+      double a = now_us();
+      CHECK_OR(serving::BindManifestTransfers(m, pool, pool, &planner, &t), 3);
+      bind_us.push_back(now_us() - a);
+      std::vector<pbe_copy_op> ops;
+      a = now_us();
+      CHECK_OR(serving::BindManifestCopyOps(m, pool, pool, &planner, &ops), 4);
+      ops_us.push_back(now_us() - a);
+      CHECK_OR(hipDeviceSynchronize() == hipSuccess, 5);
+      a = now_us();
+      CHECK_OR(pbe_copy_ops(ops.data(), static_cast<int64_t>(ops.size()), 0, nullptr) == PBE_OK, 6);
+      call_us.push_back(now_us() - a);
+      CHECK_OR(hipDeviceSynchronize() == hipSuccess, 7);
+      a = now_us();
+      serving::HandoffId h;
+      CHECK_OR(conn.submit(m, &h), 8);
+      CHECK_OR(conn.drain(h).ok(), 9);
+      conn_us.push_back(now_us() - a);
+      conn.release(h);
+    }
+    (void)hipFree(arena);
+  }
+  // ---- the reference's call order over KVCacheManager and a shared arena
+  std::vector<double> reserve_us, e2e_us, free_us, busy_us;
+  {
+    const uint64_t arena_bytes = 2000 * page;
+    pbe_arena* arena = nullptr;
+    CHECK_OR(pbe_arena_create(0, arena_bytes, arena_bytes, 77, &arena) == PBE_OK, 10);
+    pbe_arena_view view{};
+    pbe_arena_get_view(arena, &view);
+    auto owner = std::make_shared<base::LocalChunkOwner>(arena_bytes, 77);
+    owner->register_model("prefill", 900 * page);
+    owner->register_model("decode", 1000 * page);
+    void *ps = nullptr, *ds = nullptr;
+    CHECK_OR(pbe_stream_create(0, &ps) == PBE_OK && pbe_stream_create(0, &ds) == PBE_OK, 11);
+    uint8_t *big_a = nullptr, *big_b = nullptr;
+    const uint64_t big = 1ull << 30;
+    CHECK_OR(hipMalloc(&big_a, big) == hipSuccess && hipMalloc(&big_b, big) == hipSuccess, 12);
+    {
+      auto pc = std::make_shared<base::SharedKVArenaClient>(owner, view, "prefill", 900 * page, 0);
+      auto dc = std::make_shared<base::SharedKVArenaClient>(owner, view, "decode", 1000 * page, 0);
+      auto pg = std::make_shared<base::SharedKVPageGroup>(pc, kLayers, half, 2 * 1024 * 1024, ps);
+      auto dg = std::make_shared<base::SharedKVPageGroup>(dc, kLayers, half, 2 * 1024 * 1024, ds);
+      auto p_kv = manager_over(pg);
+      auto d_kv = manager_over(dg);
+      const base::RequestId pr = p_kv->register_request();
+      CHECK_OR(p_kv->append_slots(pr, 5040), 13);
+      serving::SharedKVPrefillResult r;
+      r.shared_arena_epoch = pc->epoch();
+      r.client_request_id.value = "c2";
+      r.handoff_id.value = 1;
+      r.prompt_tokens.assign(5040, 7);
+      r.computed_tokens = 5040;
+      r.first_token = 1;
+      r.src_pool = pool_desc;
+      for (int l = 0; l < kLayers; ++l) r.layers.push_back({l, p_kv->get_block_ids(pr, l)});
+      for (int it = 0; it < kIters; ++it) {
+        double a = now_us();
+        const base::RequestId q = d_kv->register_request();
+        CHECK_OR(d_kv->append_slots(q, 5040), 14);
+        reserve_us.push_back(now_us() - a);
+        d_kv->free_request(q);
+        pbe_stream_synchronize(0, ds);
+        dg->collect();
+        serving::DecodeKVReservation res;
+        a = now_us();
+        CHECK_OR(serving::CopySharedKVToDecode(d_kv.get(), pool_desc, r, ds, &res) == kPages * page, 15);
+        e2e_us.push_back(now_us() - a);
+        // the stream busy: the freed pages' fences stay pending behind a 1 GiB copy
+        pbe_copy_op op{reinterpret_cast<uint64_t>(big_a), reinterpret_cast<uint64_t>(big_b), big};
+        CHECK_OR(pbe_copy_ops(&op, 1, 0, ds) == PBE_OK, 16);
+        a = now_us();
+        d_kv->free_request(res.decode_request_id);
+        free_us.push_back(now_us() - a);
+        a = now_us();
+        const base::RequestId busy = d_kv->register_request();
+        CHECK_OR(d_kv->append_slots(busy, 5040), 17);
+        busy_us.push_back(now_us() - a);
+        d_kv->free_request(busy);
+        pbe_stream_synchronize(0, ds);
+        dg->collect();
+      }
+    }
+    (void)hipFree(big_a);
+    (void)hipFree(big_b);
+    pbe_stream_destroy(0, ps);
+    pbe_stream_destroy(0, ds);
+    pbe_arena_destroy(arena);
+  }
+  std::printf(
+      "{\"workload\": \"c2_host_paths\", \"pages\": %d, \"layers\": %d, \"iterations\": %d, "
+      "\"generic_plan_form_us\": {\"per_page_binding\": %.1f, \"copy_op_binding\": %.1f, "
+      "\"copy_ops_call\": %.1f, \"connector_submit_drain\": %.1f}, "
+      "\"reference_call_order_us\": {\"reserve_28_layers\": %.1f, \"end_to_end\": %.1f, "
+      "\"free_request\": %.1f, \"reserve_under_pending_fences\": %.1f}}\n",
+      kPages, kLayers, kIters, median(bind_us), median(ops_us), median(call_us), median(conn_us),
+      median(reserve_us), median(e2e_us), median(free_us), median(busy_us));
+  return 0;
+}
