@@ -309,6 +309,19 @@ int pbe_paged_decode_pools(const void* key_pool, const void* value_pool, uint64_
                            workspace_bytes, device, stream, false, &pools);
 }
 
+int pbe_paged_decode_append_arena(const pbe_arena_view* kv, int32_t kv_dtype, float* scales,
+                                  uint64_t scale_bytes, const pbe_kv_shape* shape, int32_t layer,
+                                  const void* new_keys, const void* new_values, const void* queries,
+                                  void* outputs, int32_t batch, int32_t q_heads,
+                                  const int32_t* block_tables, const int32_t* seq_lens,
+                                  int32_t max_blocks_per_seq, int32_t splits, void* workspace,
+                                  uint64_t workspace_bytes, int device, void* stream) {
+  if (!new_keys || !new_values) return fail(PBE_ERR_INVALID, "null new keys or values");
+  return paged_decode_call(kv, kv_dtype, scales, scale_bytes, shape, layer, queries, outputs, batch, q_heads,
+                           block_tables, seq_lens, max_blocks_per_seq, splits, workspace, workspace_bytes,
+                           device, stream, false, nullptr, new_keys, new_values);
+}
+
 int pbe_paged_decode_append(void* key_pool, void* value_pool, uint64_t pool_bytes,
                             float* key_scales, float* value_scales, uint64_t scale_pool_bytes,
                             int32_t kv_dtype, int32_t kv_heads, int32_t head_dim, const void* new_keys,

@@ -127,6 +127,10 @@ _SIGNATURES = [
     ("pbe_paged_decode_pools", C.c_int, [_P, _P, C.c_uint64, _P, _P, C.c_uint64, C.c_int32,
                                          C.c_int32, C.c_int32, _P, _P, C.c_int32, C.c_int32, _P,
                                          _P, C.c_int32, C.c_int32, _P, C.c_uint64, C.c_int, _P]),
+    ("pbe_paged_decode_append_arena", C.c_int, [C.POINTER(ArenaView), C.c_int32, _P, C.c_uint64,
+                                                C.POINTER(KvShape), C.c_int32, _P, _P, _P, _P,
+                                                C.c_int32, C.c_int32, _P, _P, C.c_int32, C.c_int32,
+                                                _P, C.c_uint64, C.c_int, _P]),
     ("pbe_paged_decode_append", C.c_int, [_P, _P, C.c_uint64, _P, _P, C.c_uint64, C.c_int32,
                                           C.c_int32, C.c_int32, _P, _P, _P, _P, C.c_int32,
                                           C.c_int32, _P, _P, C.c_int32, C.c_int32, _P, C.c_uint64,
@@ -530,6 +534,19 @@ def paged_decode_append(key_pool: int, value_pool: int, pool_bytes: int, key_sca
                                         new_values or None, queries, outputs, batch, q_heads,
                                         tables, seq_lens, max_blocks, splits, workspace,
                                         workspace_bytes, device, stream or None))
+
+
+def paged_decode_append_arena(view, kv_dtype: int, scales: int, scale_bytes: int, kv, layer: int,
+                              new_keys: int, new_values: int, queries: int, outputs: int,
+                              batch: int, q_heads: int, tables: int, seq_lens: int,
+                              max_blocks: int, splits: int, workspace: int, workspace_bytes: int,
+                              stream: int = 0, device: int = 0) -> None:
+    """pbe_paged_decode_append_arena: the arena form of paged_decode_append."""
+    check(lib().pbe_paged_decode_append_arena(C.byref(view), kv_dtype, scales or None, scale_bytes,
+                                              C.byref(kv), layer, new_keys or None,
+                                              new_values or None, queries, outputs, batch, q_heads,
+                                              tables, seq_lens, max_blocks, splits, workspace,
+                                              workspace_bytes, device, stream or None))
 
 
 PBE_IN_BF16 = 0

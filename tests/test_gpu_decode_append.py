@@ -306,3 +306,49 @@ def test_random_geometries_equal_scatter_then_decode(torch_cuda, seed):
     a = step.two_step(splits)
     b = step.fused(splits)
     _same(a, b)
+
+
+@pytest.mark.parametrize("fp8", [True, False])
+def test_arena_form_on_a_segmented_arena(torch_cuda, fp8):
+    """pbe_paged_decode_append_arena over a 4-segment page-major arena: the arena
+    afterwards equals the oracle's page writer applied to it (scales included),
+    and the outputs equal pbe_paged_decode over that arena, bit for bit."""
+    from tests.test_gpu_decode import DecodeCase
+    torch = torch_cuda
+    say(f"decode append, arena form over a segmented arena, fp8={fp8}")
+    layers, layer, H, D, kvm = 3, 1, 2, 128, 6
+    case = DecodeCase(torch, fp8=fp8, layers=layers, H=H, D=D, kvm=kvm,
+                      seq_lens=[40, 1, 16, 33, 0, 97], seed=61 + fp8, segment_pages=4, layer=layer)
+    assert len(case.bufs) > 1
+    rng = np.random.default_rng(62)
+    kv_rows = O.bf16_from_f32((rng.standard_normal((2, case.batch, H * D)) * 1.5).astype(np.float32))
+    nk = torch.from_numpy(kv_rows[0].view(np.int16)).cuda()
+    nv = torch.from_numpy(kv_rows[1].view(np.int16)).cuda()
+    dt = P.PBE_KV_FP8_E4M3 if fp8 else P.PBE_KV_BF16
+    splits = P.decode_splits(case.batch, H, case.max_blocks, dt)
+    n = P.decode_workspace_bytes(case.batch, H * kvm, D, splits)
+    ws = torch.empty(n, dtype=torch.uint8, device="cuda")
+    P.paged_decode_append_arena(case.view, dt, case.scales.data_ptr() if fp8 else 0,
+                                case.scales.numel() * 4 if fp8 else 0, case.kv, layer,
+                                nk.data_ptr(), nv.data_ptr(), case.q.data_ptr(), case.out.data_ptr(),
+                                case.batch, H * kvm, case.t_dev.data_ptr(), case.s_dev.data_ptr(),
+                                case.max_blocks, splits, ws.data_ptr(), n, stream_ptr(torch))
+    torch.cuda.synchronize()
+    fused = case.out.cpu().numpy().view(np.uint16).copy()
+    # expected pages: the oracle's page writer on the host arena (layer planes)
+    want = case.host.copy()
+    want_sc = case.host_scales.copy() if fp8 else None
+    half, plane = case.half, 16 * H
+    slots = np.array([case.tables[b, (m - 1) // 16] * 16 + (m - 1) % 16 if m > 0 else -1
+                      for b, m in enumerate(case.seq_lens)], np.int32)
+    O.scatter_kv(kv_rows[0], kv_rows[1], slots, 16, H, D, fp8, want[2 * layer * half:],
+                 want[(2 * layer + 1) * half:],
+                 want_sc[2 * layer * plane:] if fp8 else None,
+                 want_sc[(2 * layer + 1) * plane:] if fp8 else None)
+    got = np.concatenate([x.cpu().numpy() for x in case.bufs])
+    assert np.array_equal(got, want)
+    if fp8:
+        assert np.array_equal(case.scales.cpu().numpy().view(np.uint32), want_sc.view(np.uint32))
+    plain = case.run(splits=splits)  # the reader over the written arena
+    assert np.array_equal(fused, case.out.cpu().numpy().view(np.uint16))
+    assert not np.isnan(plain).all()
