@@ -190,15 +190,19 @@ class TimingEvents:
         self.ev = []
 
 
-def _timed(torch, stream, scrub, fn, n):
+def _timed(torch, stream, scrub, fn, n, scrub_fn=None):
     """Mean/min event time (ms) of fn() over n cold launches (scrub before
-    each), between fence-free timing events recorded on the stream."""
+    each: a 1 GiB fill unless scrub_fn is given), between fence-free timing
+    events recorded on the stream."""
     import numpy as np
     ev = TimingEvents(2 * (n + 2))
     sp = stream.cuda_stream
     ts = []
     for i in range(n + 2):
-        scrub.fill_(i & 0xff)
+        if scrub_fn is None:
+            scrub.fill_(i & 0xff)
+        else:
+            scrub_fn(i)
         ev.record(2 * i, sp)
         fn()
         ev.record(2 * i + 1, sp)
@@ -250,6 +254,168 @@ def gpu_reference_pattern(torch, stream, scrub, base, runs, g, alg, n, scrub_eac
             "calls": len(calls), "us_mean": round(us, 2),
             "gbps": round(alg / (us * 1e-6) / 1e9, 1),
             "e2e_us_p50": round(float(np.median(wall)) * 1e6, 1)}
+
+
+def host_paths_timing():
+    """JSON line of lib/pbe_host_paths (tests/cpp/bench_host_paths.cpp) run as
+    a child process, or None when it is not built."""
+    import subprocess
+    exe = Path(__file__).resolve().parent / "paged-batch-engine_amd" / "lib" / "pbe_host_paths"
+    if not exe.exists():
+        print(f"bench.py: {exe} is missing; the reference call order is not timed", file=sys.stderr)
+        return None
+    out = subprocess.run([str(exe)], stdout=subprocess.PIPE, timeout=300, check=True, text=True)
+    return json.loads(out.stdout.strip().splitlines()[-1])
+
+
+def measure_ceilings(torch, P, w, runs, kv, arena, scrub, alg: int, n: int) -> dict:
+    """Ceilings the config-2 kernel time is held against, measured in this run
+    on the same byte count with the same 1 GiB write scrub before each launch:
+      sorted_destination  the same kernel and the plan's own source runs, the
+                          destinations packed into one ascending contiguous
+                          region (what the decode allocator's page placement
+                          costs);
+      vendor_memcpy       one hipMemcpyAsync device-to-device of the same bytes,
+                          contiguous on both sides (also after a read-only scrub,
+                          which the vendor copy is sensitive to);
+      read_only/write_only the copy kernel's two halves alone
+                          (lib/libpbe_ceiling.so): a copy's steady state cannot
+                          beat HBM's rate for either stream at this size;
+      register_staged_copy a contiguous copy whose waves each read 32 KiB before
+                          writing it, the test of whether separating the two
+                          streams in time pays."""
+    import ctypes as C
+    import numpy as np
+    g = w.geometry
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    nbytes = w.pages * g.page_bytes()
+    out = {}
+    # (b) plan sources, contiguous ascending destination in a separate buffer
+    dbuf = torch.empty(nbytes, dtype=torch.uint8, device=arena.device)
+    dview = P.view_of(dbuf.data_ptr(), nbytes)
+    sview = P.view_of(arena.data_ptr(), arena.numel())
+    stride = 2 * g.layers
+    packed, at = [], 0
+    for s_id, _d, k in runs:
+        packed.append((s_id, at * stride, k))
+        at += k
+    with P.RunList.bf16(sview, dview, packed, kv) as srl:
+        ms = _timed(torch, stream, scrub, lambda: srl.copy(sp), n)
+    out["sorted_destination"] = {
+        "what": "same kernel, the plan's source runs, destinations packed into one ascending "
+                "contiguous region", "runs": len(packed),
+        "us_mean": round(ms[0] * 1e3, 2), "gbps": round(alg / (ms[0] * 1e-3) / 1e9, 1)}
+    # (a) vendor copy of the same bytes
+    hip = C.CDLL("libamdhip64.so.7")
+    hip.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+    hip.hipMemcpyAsync.restype = C.c_int
+
+    def vendor():
+        if hip.hipMemcpyAsync(dbuf.data_ptr(), arena.data_ptr(), nbytes, 3, C.c_void_p(sp)) != 0:
+            raise RuntimeError("hipMemcpyAsync failed")
+    ms = _timed(torch, stream, scrub, vendor, n)
+    sums = scrub.view(torch.int64)
+    ms_r = _timed(torch, stream, scrub, vendor, n, scrub_fn=lambda i: sums.sum())
+    out["vendor_memcpy"] = {
+        "what": "one hipMemcpyAsync device-to-device of the same bytes, contiguous",
+        "us_mean": round(ms[0] * 1e3, 2), "gbps": round(alg / (ms[0] * 1e-3) / 1e9, 1),
+        "us_mean_after_read_scrub": round(ms_r[0] * 1e3, 2),
+        "gbps_after_read_scrub": round(alg / (ms_r[0] * 1e-3) / 1e9, 1)}
+    # (c) the two halves of a copy alone
+    so = Path(__file__).resolve().parent / "paged-batch-engine_amd" / "lib" / "libpbe_ceiling.so"
+    if so.exists():
+        cl = C.CDLL(str(so))
+        cl.pbe_ceiling_read.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p,
+                                        C.c_void_p, C.c_void_p]
+        cl.pbe_ceiling_write.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, C.c_void_p,
+                                         C.c_void_p, C.c_void_p]
+        sink = torch.empty(1024, dtype=torch.uint8, device=arena.device)
+        ev = TimingEvents(2)
+
+        def leg(fn):
+            ts = []
+            for i in range(n + 2):
+                scrub.fill_(i & 0xff)
+                if fn(ev.handle(0), ev.handle(1)) != 0:
+                    raise RuntimeError("ceiling kernel launch failed")
+                torch.cuda.synchronize()
+                if i >= 2:
+                    ts.append(ev.elapsed_ms(0, 1))
+            return float(np.mean(ts))
+        r_ms = leg(lambda a, b: cl.pbe_ceiling_read(arena.data_ptr(), nbytes, sink.data_ptr(), sp, a, b))
+        w_ms = leg(lambda a, b: cl.pbe_ceiling_write(dbuf.data_ptr(), nbytes, 7, sp, a, b))
+        cl.pbe_ceiling_phase_copy.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p,
+                                              C.c_void_p, C.c_void_p]
+        p_ms = leg(lambda a, b: cl.pbe_ceiling_phase_copy(arena.data_ptr(), dbuf.data_ptr(), nbytes,
+                                                          sp, a, b))
+        ev.close()
+        out["read_only"] = {"what": "the copy kernel's loads alone over the same bytes",
+                            "bytes": nbytes, "us_mean": round(r_ms * 1e3, 2),
+                            "gbps": round(nbytes / (r_ms * 1e-3) / 1e9, 1)}
+        out["write_only"] = {"what": "the copy kernel's stores alone over the same bytes",
+                             "bytes": nbytes, "us_mean": round(w_ms * 1e3, 2),
+                             "gbps": round(nbytes / (w_ms * 1e-3) / 1e9, 1)}
+        out["read_then_write_us"] = round((r_ms + w_ms) * 1e3, 2)
+        out["register_staged_copy"] = {
+            "what": "contiguous copy of the same bytes, each wave loading 32 KiB into registers "
+                    "before storing it (long read-only then write-only bursts)",
+            "us_mean": round(p_ms * 1e3, 2), "gbps": round(alg / (p_ms * 1e-3) / 1e9, 1)}
+    del dbuf
+    return out
+
+
+LEG_ORDER = ("plan", "sorted_destination", "contiguous", "read_only", "write_only")
+
+
+def ceiling_legs(torch, P, w, runs, kv, arena, scrub, rl, k: int) -> dict:
+    """Launches each leg k times, in LEG_ORDER, each launch after the 1 GiB
+    scrub: the config-2 plan, the same sources into one contiguous ascending
+    destination, the same bytes as one contiguous run, and the copy's
+    read-only and write-only halves. Under rocprofv3 --pmc the copy kernel's
+    dispatches are told apart by this order (profiling.py legs)."""
+    import ctypes as C
+    g = w.geometry
+    sp = torch.cuda.current_stream().cuda_stream
+    nbytes = w.pages * g.page_bytes()
+    stride = 2 * g.layers
+    dbuf = torch.empty(nbytes, dtype=torch.uint8, device=arena.device)
+    dview = P.view_of(dbuf.data_ptr(), nbytes)
+    sview = P.view_of(arena.data_ptr(), arena.numel())
+    packed, at = [], 0
+    for s_id, _d, n_pages in runs:
+        packed.append((s_id, at * stride, n_pages))
+        at += n_pages
+    n_arena = w.arena_bytes // g.page_bytes()
+    srl = P.RunList.bf16(sview, dview, packed, kv)
+    crl = P.RunList.bf16(sview, sview, [(0, stride * (n_arena - w.pages), w.pages)], kv)
+    so = Path(__file__).resolve().parent / "paged-batch-engine_amd" / "lib" / "libpbe_ceiling.so"
+    cl = C.CDLL(str(so))
+    cl.pbe_ceiling_read.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p,
+                                    C.c_void_p, C.c_void_p]
+    cl.pbe_ceiling_write.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, C.c_void_p,
+                                     C.c_void_p, C.c_void_p]
+    sink = torch.empty(1024, dtype=torch.uint8, device=arena.device)
+    legs = {
+        "plan": lambda: rl.copy(sp),
+        "sorted_destination": lambda: srl.copy(sp),
+        "contiguous": lambda: crl.copy(sp),
+        "read_only": lambda: cl.pbe_ceiling_read(arena.data_ptr(), nbytes, sink.data_ptr(), sp,
+                                                 None, None),
+        "write_only": lambda: cl.pbe_ceiling_write(dbuf.data_ptr(), nbytes, 7, sp, None, None),
+    }
+    for name in LEG_ORDER:
+        for i in range(k):
+            scrub.fill_(i & 0xff)
+            rc = legs[name]()
+            if rc:
+                raise RuntimeError(f"{name}: launch failed ({rc})")
+        torch.cuda.synchronize()
+        print(f"leg {name}: {k} launches", file=sys.stderr, flush=True)
+    srl.close()
+    crl.close()
+    return {"legs": list(LEG_ORDER), "launches_each": k, "bytes": nbytes,
+            "algorithmic_bytes": w.algorithmic_bytes()}
 
 
 def measure_extra_configs(torch, P, W, scrub, n: int):
@@ -600,6 +766,9 @@ def main() -> int:
                     help="time only a 28-layer decode step (page write + reader), eager and graph")
     ap.add_argument("--scatter-only", action="store_true",
                     help="time only the page writer (prompt and decode-token scatters)")
+    ap.add_argument("--ceiling-legs", type=int, default=0, metavar="K",
+                    help="only launch the config-2 plan and its ceiling legs K times each, in a "
+                         "fixed order (for rocprofv3 --pmc; summarised by profiling.py legs)")
     ap.add_argument("--calibrate", action="store_true",
                     help="also launch a plain contiguous copy of 256 MiB with the same kernel "
                          "(rocprofv3 --pmc byte-count calibration)")
@@ -663,6 +832,11 @@ def main() -> int:
     info = rl.info()
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
+
+    if args.ceiling_legs:
+        print(json.dumps(ceiling_legs(torch, P, w, runs, kv, arena, scrub, rl, args.ceiling_legs)))
+        rl.close()
+        return 0
 
     # correctness of this exact run: device result vs oracle on the same pool
     from oracle import oracle as O
@@ -744,11 +918,22 @@ def main() -> int:
                   "us_mean": round(c_ms[0] * 1e3, 2),
                   "gbps": round(alg / (c_ms[0] * 1e-3) / 1e9, 1)}
 
+    ceilings = measure_ceilings(torch, P, w, runs, kv, arena, scrub, alg, max(10, args.steps // 4))
+    ceilings["contiguous_same_bytes"] = contiguous
+    best = min(ceilings["sorted_destination"]["us_mean"], ceilings["vendor_memcpy"]["us_mean"])
+    ceilings["headline_over_best_of_sorted_and_vendor"] = round(mean_ms * 1e3 / best, 4)
+
     calib = calibration_copy(torch, P, scrub, args.steps, sp) if args.calibrate else None
 
     if args.extra_configs:
         extra = measure_extra_configs(torch, P, W, scrub, max(10, args.steps // 4))
         Path(args.extra_configs).write_text(json.dumps(extra, indent=1) + "\n")
+
+    # the reference's copy_shared_kv call order through the C++ drop-in API
+    # (serving::CopySharedKVToDecode: reserve over 28 layers, manifest, the
+    # one-launch copy, stream sync, commit_kv) at config-2 size, timed by the
+    # C++ host-path runner in a child process on this GPU
+    ref_order = host_paths_timing()
 
     cpu = None
     if not args.no_cpu:
@@ -780,7 +965,9 @@ def main() -> int:
                        "kernel_min": round(float(times_ms.min()) * 1e3, 2),
                        "launch_between_stream_events_mean": round(outer_ms[0] * 1e3, 2),
                        "handoff_e2e_p50": round(e2e_us, 1),
-                       "handoff_e2e_stream_sync_p50": round(e2e_stream_us, 1)},
+                       "handoff_e2e_stream_sync_p50": round(e2e_stream_us, 1),
+                       "reference_call_order_p50":
+                           ref_order["reference_call_order_us"]["end_to_end"] if ref_order else None},
         "pct_of_peak": round(100 * achieved / PEAK_GBPS, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_GBPS, 4),
@@ -794,6 +981,14 @@ def main() -> int:
     }
     line["gpu_reference_pattern"] = refpat
     line["contiguous_same_bytes"] = contiguous
+    line["ceilings"] = ceilings
+    if ref_order:
+        line["reference_call_order_us"] = dict(
+            ref_order["reference_call_order_us"],
+            what="serving::CopySharedKVToDecode at config-2 size (315 pages, 28 layers), medians of "
+                 f"{ref_order['iterations']} calls: reserve = register_request + append_slots; "
+                 "end_to_end = checks, reserve, manifest, one-launch copy, stream sync, commit_kv; "
+                 "copy_and_sync_alone = pbe_copy_shared_kv + stream sync on the same pages")
     if calib:
         line["calibration_copy"] = calib
     print(json.dumps(line))

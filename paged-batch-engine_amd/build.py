@@ -5,6 +5,7 @@ Compiles, in-tree:
                           drop-in API (include/{base,cache,serving}/*.h)
   lib/pbe_cpp_tests       C++ unit tests of the drop-in API (host-only parts)
   lib/pbe_cpp_gpu_tests   C++ tests that need a GPU (HIP backend, connector)
+  lib/libpbe_ceiling.so   measurement-only read/write stream kernels (bench.py)
 
 Usage: python paged-batch-engine_amd/build.py [--jobs N]
 """
@@ -130,6 +131,10 @@ def build(jobs: int = 8) -> Path:
     # bench.py --host-paths: the C++ paths' host costs at config-2 size
     _run([HIPCC, *HIP_FLAGS, *INCLUDES, str(ROOT / "tests" / "cpp" / "bench_host_paths.cpp"),
           f"-L{LIB}", "-lpbe_handoff", "-Wl,-rpath,$ORIGIN", "-o", str(LIB / "pbe_host_paths")])
+    # bench.py only: read-only and write-only streams at the copy's geometry
+    # (csrc/diag/hbm_ceiling.hip), the HBM ceilings the handoff is held against
+    _run([HIPCC, *HIP_FLAGS, "-shared", str(PKG / "csrc" / "diag" / "hbm_ceiling.hip"),
+          "-o", str(LIB / "libpbe_ceiling.so")])
     return so
 
 

@@ -94,18 +94,40 @@ bool KVCacheManager::append_slots(RequestId id, int32_t num_tokens) {
   if (need > 0) {
     for (int32_t l = 0; l < num_layers_; ++l)
       if (layers_[l]->num_free_blocks() < need) return false;
-    // Appended in place; on failure every layer's new blocks are freed and
-    // the tables cut back to where they were (all or nothing).
+    // Appended in place; on failure (a false return or an exception) every
+    // layer's new blocks are freed and the tables cut back to where they were
+    // (all or nothing).
     const size_t had = r.blocks[0].size();
-    for (int32_t l = 0; l < num_layers_; ++l) {
-      r.blocks[l].reserve(had + need);
-      if (!layers_[l]->allocate_many(need, &r.blocks[l])) {
-        for (int32_t m = l; m >= 0; --m) {
-          for (size_t k = had; k < r.blocks[m].size(); ++k) layers_[m]->free(r.blocks[m][k]);
-          r.blocks[m].resize(had);
+    int32_t l = 0;
+    // best_effort: on the exception path a block the failed call left
+    // half-registered may refuse its free; the cut-back goes on and the
+    // original exception is the one reported.
+    auto cut_back = [&](bool best_effort) {
+      for (int32_t m = std::min(l, num_layers_ - 1); m >= 0; --m) {
+        for (size_t k = had; k < r.blocks[m].size(); ++k) {
+          if (!best_effort) {
+            layers_[m]->free(r.blocks[m][k]);
+            continue;
+          }
+          try {
+            layers_[m]->free(r.blocks[m][k]);
+          } catch (...) {
+          }
         }
-        return false;
+        r.blocks[m].resize(had);
       }
+    };
+    try {
+      for (; l < num_layers_; ++l) {
+        r.blocks[l].reserve(had + need);
+        if (!layers_[l]->allocate_many(need, &r.blocks[l])) {
+          cut_back(false);
+          return false;
+        }
+      }
+    } catch (...) {
+      cut_back(true);
+      throw;
     }
   }
   r.tokens += num_tokens;

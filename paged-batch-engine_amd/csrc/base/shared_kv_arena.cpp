@@ -115,25 +115,29 @@ struct SharedKVPageGroup::Impl {
   };
   struct Page {
     uint64_t offset = 0;
-    LayerFlags active, reserved;  // per layer
+    int32_t id = -1;  // offset / half, fixed when the page is laid out
+    LayerFlags active;  // per layer
     int active_layers = 0;
     bool retiring = false;
+    // Layer 0's reservation of this page is in the reservation log at
+    // sequence `seq`; layer l > 0 still holds it reserved (not yet handed
+    // out) while seq >= that layer's cursor.
+    bool logged = false;
+    uint64_t seq = 0;
     pbe_event* fence = nullptr;
     Chunk* chunk = nullptr;
   };
   struct Chunk {
     ChunkLease lease;
     std::vector<Page> pages;  // fixed size: Page* stay valid
-    std::vector<char> flags;  // pages x {active, reserved} x layers
+    std::vector<char> flags;  // pages x layers (active)
     size_t free_pages = 0;
     // Sizes the pages and points their layer flags into `flags`.
     void lay_out(size_t n_pages, int layers) {
       pages.resize(n_pages);
-      flags.assign(n_pages * 2 * static_cast<size_t>(layers), 0);
-      for (size_t i = 0; i < n_pages; ++i) {
-        pages[i].active = {flags.data() + 2 * i * layers, static_cast<size_t>(layers)};
-        pages[i].reserved = {flags.data() + (2 * i + 1) * layers, static_cast<size_t>(layers)};
-      }
+      flags.assign(n_pages * static_cast<size_t>(layers), 0);
+      for (size_t i = 0; i < n_pages; ++i)
+        pages[i].active = {flags.data() + i * layers, static_cast<size_t>(layers)};
     }
   };
 
@@ -208,12 +212,61 @@ struct SharedKVPageGroup::Impl {
   std::vector<pbe_event*> spare_fences;
   // Pages still holding each recorded fence: pages retired together share one.
   std::unordered_map<pbe_event*, size_t> fence_users;
-  std::vector<std::deque<Page*>> pending;  // per layer: pages reserved by layer 0
+  // Pages reserved by layer 0, in reservation order. Every later layer takes
+  // the same pages in the same order (page-major ids), so one log with a
+  // read cursor per layer replaces a queue per layer: layer 0 appends once
+  // per page, and layer l hands out log[cursor[l]++]. Entry i has sequence
+  // log_base + i; a null entry is a reservation rolled back by layer 0's
+  // retire before every layer took it. cancelled_ahead[l] counts the null
+  // entries at or after cursor[l].
+  std::vector<Page*> log;
+  uint64_t log_base = 0;
+  std::vector<uint64_t> cursor;
+  std::vector<uint64_t> cancelled_ahead;
   uint64_t leased = 0;
   bool failed = false;  // an unacknowledged release can never become reusable
   mutable std::mutex mu;
 
-  int id_of(const Page& p) const { return static_cast<int>(p.offset / half); }
+  int id_of(const Page& p) const { return p.id; }
+
+  uint64_t log_end() const { return log_base + log.size(); }
+  // Layer `layer` has not yet been handed this page of layer 0's reservation.
+  bool reserved(const Page& p, int layer) const {
+    return layer > 0 && p.logged && p.seq >= cursor[layer];
+  }
+  bool any_reserved(const Page& p) const {
+    for (int l = 1; l < layers; ++l)
+      if (reserved(p, l)) return true;
+    return false;
+  }
+  size_t pending_count(int layer) const {
+    return layer > 0 ? static_cast<size_t>(log_end() - cursor[layer] - cancelled_ahead[layer]) : 0;
+  }
+  // Next page of layer 0's reservations for a later layer, or null.
+  Page* take_reserved(int layer) {
+    uint64_t& c = cursor[layer];
+    const uint64_t end = log_end();
+    while (c < end && log[c - log_base] == nullptr) {
+      ++c;
+      --cancelled_ahead[layer];
+    }
+    return c < end ? log[c++ - log_base] : nullptr;
+  }
+  // Drops the log prefix every later layer has read (amortised: only once it
+  // is at least half the log).
+  void trim_log() {
+    uint64_t low = log_end();
+    for (int l = 1; l < layers; ++l) low = std::min(low, cursor[l]);
+    const uint64_t dead = low - log_base;
+    if (dead == log.size()) {
+      log.clear();
+    } else if (dead >= 1024 && 2 * dead >= log.size()) {
+      log.erase(log.begin(), log.begin() + static_cast<std::ptrdiff_t>(dead));
+    } else {
+      return;
+    }
+    log_base = low;
+  }
 
   // True once the fence recorded at the page's last retire has passed.
   bool fence_done(Page& p) {
@@ -272,9 +325,10 @@ struct SharedKVPageGroup::Impl {
     p.active_layers = layers;
     --p.chunk->free_pages;
     free_ids.erase(id);
-    for (int l = 1; l < layers; ++l) {
-      p.reserved[l] = 1;
-      pending[l].push_back(&p);
+    if (layers > 1) {
+      p.logged = true;
+      p.seq = log_end();
+      log.push_back(&p);
     }
     return id;
   }
@@ -311,17 +365,19 @@ struct SharedKVPageGroup::Impl {
     if (!found) throw std::logic_error("page does not belong to current chunk generation");
     Page& p = *found;
     if (layer < 0 || layer >= layers) throw std::out_of_range("invalid layer");
-    if (!p.active[layer] || p.retiring || p.reserved[layer]) throw std::logic_error("double/stale page retire");
-    if (layer == 0) {
+    if (!p.active[layer] || p.retiring || reserved(p, layer)) throw std::logic_error("double/stale page retire");
+    if (layer == 0 && p.logged) {
       // Roll back reservations the later layers never consumed.
+      bool cancelled = false;
       for (int l = 1; l < layers; ++l) {
-        if (!p.reserved[l]) continue;
-        auto& q = pending[l];
-        q.erase(std::remove(q.begin(), q.end(), &p), q.end());
-        p.reserved[l] = 0;
+        if (!reserved(p, l)) continue;
         p.active[l] = 0;
         --p.active_layers;
+        ++cancelled_ahead[l];
+        cancelled = true;
       }
+      if (cancelled) log[p.seq - log_base] = nullptr;
+      p.logged = false;
     }
     p.active[layer] = 0;
     // A page is indivisible across layers: one fence after every layer's use.
@@ -345,7 +401,8 @@ SharedKVPageGroup::SharedKVPageGroup(std::shared_ptr<SharedKVArenaClient> arena,
     throw std::invalid_argument("unsupported shared KV geometry/alignment");
   impl_->arena = std::move(arena);
   impl_->layers = layers;
-  impl_->pending.resize(layers);
+  impl_->cursor.assign(layers, 0);
+  impl_->cancelled_ahead.assign(layers, 0);
   impl_->half = half_bytes;
   impl_->page = half_bytes * 2 * layers;
   impl_->pages.init(impl_->arena->bytes() / impl_->page + 1, 2 * layers);
@@ -386,12 +443,39 @@ int SharedKVPageGroup::allocate(int layer) {
 
 bool SharedKVPageGroup::allocate_many(int layer, int n, std::vector<int32_t>* out) {
   std::lock_guard<std::mutex> lock(impl_->mu);
-  // Fences are looked at once per batch (each look is a runtime query), and
-  // once more before giving up.
-  if (layer == 0 && n > 0) impl_->collect_locked();
+  Impl& m = *impl_;
+  if (m.failed) throw std::runtime_error("shared KV page group failed; stop GPU domain");
+  if (layer < 0 || layer >= m.layers) throw std::invalid_argument("invalid layer");
+  if (n <= 0) return true;
+  if (layer > 0) {
+    // Bulk form of the later layers' allocate: the next n pages of layer 0's
+    // reservations, in order.
+    if (m.pending_count(layer) < static_cast<size_t>(n))
+      throw std::logic_error("Allocate shared pages in layer order");
+    const size_t at = out->size();
+    out->resize(at + static_cast<size_t>(n));
+    int32_t* ids = out->data() + at;
+    for (int k = 0; k < n; ++k) ids[k] = m.take_reserved(layer)->id;
+    m.trim_log();
+    return true;
+  }
+  // Layer 0 collects (returns pages whose fences have passed) before it
+  // leases a Chunk, as allocate() does. Each collect costs a fence query
+  // while pages are retiring, so within one batch a collect that found the
+  // oldest fence still pending is not repeated: that fence passes in stream
+  // order, not within the microseconds a batch takes.
+  m.collect_locked();
+  bool fence_pending = !m.retiring.empty();
   for (int k = 0; k < n; ++k) {
-    int id = impl_->allocate_locked(layer, false);
-    if (id < 0 && layer == 0) id = impl_->allocate_locked(layer, true);
+    if (m.free_ids.empty() && !fence_pending) {
+      m.collect_locked();
+      fence_pending = !m.retiring.empty();
+    }
+    int id = m.allocate_locked(0, false);
+    if (id < 0 && fence_pending) {  // out of room: one last look before giving up
+      id = m.allocate_locked(0, true);
+      fence_pending = !m.retiring.empty();
+    }
     if (id < 0) return false;
     out->push_back(id);
   }
@@ -403,11 +487,9 @@ int SharedKVPageGroup::Impl::allocate_locked(int layer, bool collect) {
   if (m.failed) throw std::runtime_error("shared KV page group failed; stop GPU domain");
   if (layer < 0 || layer >= m.layers) throw std::invalid_argument("invalid layer");
   if (layer > 0) {
-    auto& q = m.pending[layer];
-    if (q.empty()) throw std::logic_error("Allocate shared pages in layer order");
-    Page* p = q.front();
-    q.pop_front();
-    p->reserved[layer] = 0;
+    Page* p = m.take_reserved(layer);
+    if (!p) throw std::logic_error("Allocate shared pages in layer order");
+    if (layer == m.layers - 1) m.trim_log();
     return m.id_of(*p);
   }
   if (collect) m.collect_locked();
@@ -433,6 +515,7 @@ int SharedKVPageGroup::Impl::allocate_locked(int layer, bool collect) {
   for (size_t i = 0; i < chunk->pages.size(); ++i) {
     Impl::Page& p = chunk->pages[i];
     p.offset = lease.offset + i * m.page;
+    p.id = static_cast<int32_t>(p.offset / m.half);
     p.chunk = chunk.get();
     m.pages.emplace(m.id_of(p), &p);
     m.free_ids.insert(m.id_of(p));
@@ -473,8 +556,7 @@ void SharedKVPageGroup::detach_for_takeover(const std::vector<int32_t>& ids, Pag
     const Impl::Page* found = m.pages.get(id);
     if (!found) throw std::logic_error("takeover page does not belong to this group");
     const Impl::Page& p = *found;
-    if (p.active_layers != m.layers || p.retiring ||
-        std::any_of(p.reserved.begin(), p.reserved.end(), [](char r) { return r != 0; }))
+    if (p.active_layers != m.layers || p.retiring || m.any_reserved(p))
       throw std::logic_error("takeover page is not active in every layer");
     if (listed[id]++) throw std::logic_error("takeover page listed twice");
     ++touched[p.chunk];
@@ -573,7 +655,8 @@ size_t SharedKVPageGroup::adopt(const PageTakeover& t) {
     for (size_t i = 0; i < chunk->pages.size(); ++i) {
       Impl::Page& p = chunk->pages[i];
       p.offset = lease.offset + i * m.page;
-      p.reserved.assign(m.layers, 0);
+      p.id = static_cast<int32_t>(p.offset / m.half);
+      p.logged = false;
       p.chunk = chunk.get();
       const int id = m.id_of(p);
       if (moved.count(id)) {
@@ -596,7 +679,8 @@ int SharedKVPageGroup::free_blocks(int layer) const {
   std::lock_guard<std::mutex> lock(impl_->mu);
   uint64_t n = (impl_->arena->hard_limit() - impl_->leased) / impl_->page;
   n += impl_->free_ids.size();
-  n += impl_->pending.at(layer).size();
+  if (layer < 0 || layer >= impl_->layers) throw std::out_of_range("invalid layer");
+  n += impl_->pending_count(layer);
   return static_cast<int>(std::min<uint64_t>(INT32_MAX, n));
 }
 

@@ -27,16 +27,30 @@ uint64_t CopySharedKVToDecode(base::KVCacheManager* manager, const KVPoolDescrip
   request.first_token = source.first_token;
   request.src_pool = source.src_pool;
   request.src_block_ids_per_layer.resize(layers);
+  // Every layer must carry layer 0's page-major ids (split_pd_engine.cpp:78-79,
+  // 91-93), and every layer's allocator views the same arena with the same
+  // plane size, so the bounds and alignment checks run once, on layer 0's
+  // list; the other layers are compared with it as a whole.
+  const std::vector<int32_t>& ids0 = source.layers.front().src_block_ids;
+  const base::BlockAllocator& a0 = manager->allocator(0);
+  const uint64_t half = a0.key_value_bytes_per_block();
+  const uint64_t arena_bytes = a0.shared_arena_bytes();
+  const uint32_t page_stride = static_cast<uint32_t>(stride);
   for (int32_t l = 0; l < layers; ++l) {
     const RemoteKVLayerPayload& layer = source.layers[l];
     const base::BlockAllocator& a = manager->allocator(l);
-    if (layer.layer_idx != l || !a.uses_shared_arena()) throw std::runtime_error("PD shared layout mismatch");
-    const uint64_t half = a.key_value_bytes_per_block();
-    for (int32_t id : layer.src_block_ids)
-      if (id < 0 || (static_cast<uint64_t>(id) + stride) * half > a.shared_arena_bytes() || id % stride != 0)
-        throw std::runtime_error("PD source block outside shared page layout");
-    if (l > 0 && layer.src_block_ids != source.layers.front().src_block_ids)
-      throw std::runtime_error("PD page-major layer IDs disagree");
+    if (layer.layer_idx != l || !a.uses_shared_arena() || a.key_value_bytes_per_block() != half ||
+        a.shared_arena_bytes() != arena_bytes)
+      throw std::runtime_error("PD shared layout mismatch");
+    // a layer that differs from layer 0 is checked in full first, so its
+    // error is the one the per-layer order reports
+    if (l == 0 || layer.src_block_ids != ids0) {
+      for (int32_t id : layer.src_block_ids)
+        if (id < 0 || (static_cast<uint64_t>(id) + stride) * half > arena_bytes ||
+            static_cast<uint32_t>(id) % page_stride != 0)
+          throw std::runtime_error("PD source block outside shared page layout");
+      if (l > 0) throw std::runtime_error("PD page-major layer IDs disagree");
+    }
     request.src_block_ids_per_layer[l] = layer.src_block_ids;
   }
   DecodeKVReservationManager reservations(manager, decode_pool);

@@ -2,6 +2,7 @@
 
     python paged-batch-engine_amd/profiling.py stats <rocprof_dir> --out FILE --command "..."
     python paged-batch-engine_amd/profiling.py pmc <fetch_dir> <write_dir> --out FILE --command "..."
+    python paged-batch-engine_amd/profiling.py legs <pmc_dir>... --launches K --out FILE --command "..."
 
 `stats` reads the kernel trace of a `rocprofv3 --kernel-trace --stats
 --output-format csv` run and writes per-kernel call counts and durations.
@@ -119,6 +120,67 @@ def pmc(fetch_root: str, write_root: str, out: str, command: str, alg_bytes: int
     print(text)
 
 
+# bench.py --ceiling-legs K launches these legs K times each, in this order;
+# the first three are the copy kernel, the last two the measurement streams.
+LEGS = (("plan", COPY_KERNEL), ("sorted_destination", COPY_KERNEL), ("contiguous", COPY_KERNEL),
+        ("read_only", "stream_read_kernel"), ("write_only", "stream_write_kernel"))
+
+
+def _dispatch_counters(root: str):
+    """[(dispatch id, kernel name, {counter: value summed over instances})] in
+    dispatch order."""
+    per, names = defaultdict(lambda: defaultdict(float)), {}
+    for r in _csv_rows(root, "counter_collection.csv"):
+        did = int(r["Dispatch_Id"])
+        per[did][r["Counter_Name"]] += float(r["Counter_Value"])
+        names[did] = r["Kernel_Name"]
+    return [(d, names[d], dict(per[d])) for d in sorted(per)]
+
+
+def legs(roots, launches: int, out: str, command: str) -> None:
+    """Per-leg medians of every counter in the given --pmc runs of
+    bench.py --ceiling-legs (one run per counter pass)."""
+    table = defaultdict(dict)  # leg -> counter -> median
+    for root in roots:
+        rows = _dispatch_counters(root)
+        for leg_i, (leg, kern) in enumerate(LEGS):
+            mine = [c for _, n, c in rows if kern in n]
+            if kern == COPY_KERNEL:  # the last 3k copy dispatches, in leg order
+                mine = mine[-3 * launches:]
+                k0 = leg_i * launches
+                mine = mine[k0:k0 + launches]
+            else:
+                mine = mine[-launches:]
+            if len(mine) != launches:
+                raise RuntimeError(f"{root}: {leg}: {len(mine)} dispatches, expected {launches}")
+            for counter in mine[0]:
+                table[leg][counter] = statistics.median(m[counter] for m in mine)
+    counters = sorted({c for v in table.values() for c in v})
+    w = max(len(c) for c in counters)
+    lines = ["# rocprofv3 --pmc summary: DRAM-side counters of the config-2 handoff and its "
+             "ceiling legs", f"command: {command}",
+             f"medians over {launches} launches per leg, each after a 1 GiB scrub; "
+             "values summed over the counter's instances", "",
+             f"{'counter':<{w}} " + " ".join(f"{leg:>19}" for leg, _ in LEGS)]
+    for c in counters:
+        lines.append(f"{c:<{w}} " + " ".join(f"{table[leg].get(c, float('nan')):>19.0f}"
+                                              for leg, _ in LEGS))
+    # derived ratios where their inputs were collected
+    def ratio(num, den, label):
+        if all(num in table[l] and den in table[l] for l, _ in LEGS):
+            lines.append(f"{label:<{w}} " + " ".join(
+                f"{table[l][num] / max(table[l][den], 1):>19.3f}" for l, _ in LEGS))
+    lines.append("")
+    ratio("TCC_EA0_RDREQ_DRAM_CREDIT_STALL_sum", "TCC_EA0_RDREQ_sum", "rd credit stall / rd req")
+    ratio("TCC_EA0_WRREQ_DRAM_CREDIT_STALL_sum", "TCC_EA0_WRREQ_sum", "wr credit stall / wr req")
+    ratio("TCC_EA0_RDREQ_LEVEL_sum", "GRBM_GUI_ACTIVE", "rd req in flight (avg)")
+    ratio("TCC_EA0_WRREQ_LEVEL_sum", "GRBM_GUI_ACTIVE", "wr req in flight (avg)")
+    text = "\n".join(lines) + "\n"
+    with open(out, "w") as fh:
+        fh.write(text)
+    print(text)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -138,7 +200,15 @@ def main() -> None:
     p.add_argument("--calib-grid", type=int, required=True)
     p.add_argument("--kernel", default=COPY_KERNEL, help="substring of the measured kernel's name")
     p.add_argument("--title", default="HBM traffic of the config-2 handoff copy")
+    q = sub.add_parser("legs")
+    q.add_argument("roots", nargs="+")
+    q.add_argument("--launches", type=int, required=True)
+    q.add_argument("--out", required=True)
+    q.add_argument("--command", required=True)
     a = ap.parse_args()
+    if a.cmd == "legs":
+        legs(a.roots, a.launches, a.out, a.command)
+        return
     if a.cmd == "stats":
         labels = {}
         if a.label:

@@ -109,7 +109,7 @@ int main() {
     (void)hipFree(arena);
   }
   // ---- the reference's call order over KVCacheManager and a shared arena
-  std::vector<double> reserve_us, e2e_us, free_us, busy_us;
+  std::vector<double> reserve_us, e2e_us, free_us, busy_us, copy_us;
   {
     const uint64_t arena_bytes = 2000 * page;
     pbe_arena* arena = nullptr;
@@ -154,7 +154,23 @@ int main() {
         a = now_us();
         CHECK_OR(serving::CopySharedKVToDecode(d_kv.get(), pool_desc, r, ds, &res) == kPages * page, 15);
         e2e_us.push_back(now_us() - a);
+        // the copy and its wait alone, same pages (cold: a 1 GiB copy first)
+        {
+          pbe_copy_op flush{reinterpret_cast<uint64_t>(big_a), reinterpret_cast<uint64_t>(big_b), big};
+          CHECK_OR(pbe_copy_ops(&flush, 1, 0, ds) == PBE_OK, 18);
+          CHECK_OR(pbe_stream_synchronize(0, ds) == PBE_OK, 19);
+          const pbe_kv_shape shape{kLayers, kHeads, kDim, 16};
+          const auto& s_ids = r.layers[0].src_block_ids;
+          const auto& d_ids = res.dst_block_ids_per_layer[0];
+          uint64_t copied = 0;
+          a = now_us();
+          CHECK_OR(pbe_copy_shared_kv(&view, s_ids.data(), d_ids.data(), kPages, &shape, 0, ds,
+                                      &copied) == PBE_OK, 20);
+          CHECK_OR(pbe_stream_synchronize(0, ds) == PBE_OK, 21);
+          copy_us.push_back(now_us() - a);
+        }
         // the stream busy: the freed pages' fences stay pending behind a 1 GiB copy
+        CHECK_OR(pbe_stream_synchronize(0, ds) == PBE_OK, 22);
         pbe_copy_op op{reinterpret_cast<uint64_t>(big_a), reinterpret_cast<uint64_t>(big_b), big};
         CHECK_OR(pbe_copy_ops(&op, 1, 0, ds) == PBE_OK, 16);
         a = now_us();
@@ -180,8 +196,9 @@ int main() {
       "\"generic_plan_form_us\": {\"per_page_binding\": %.1f, \"copy_op_binding\": %.1f, "
       "\"copy_ops_call\": %.1f, \"connector_submit_drain\": %.1f}, "
       "\"reference_call_order_us\": {\"reserve_28_layers\": %.1f, \"end_to_end\": %.1f, "
-      "\"free_request\": %.1f, \"reserve_under_pending_fences\": %.1f}}\n",
+      "\"copy_and_sync_alone\": %.1f, \"free_request\": %.1f, "
+      "\"reserve_under_pending_fences\": %.1f}}\n",
       kPages, kLayers, kIters, median(bind_us), median(ops_us), median(call_us), median(conn_us),
-      median(reserve_us), median(e2e_us), median(free_us), median(busy_us));
+      median(reserve_us), median(e2e_us), median(copy_us), median(free_us), median(busy_us));
   return 0;
 }

@@ -935,6 +935,28 @@ serving::DecodeKVReservationRequest request_for(int32_t computed, int32_t prompt
 }
 }  // namespace
 
+TEST_CASE("kv cache manager: an allocator that throws part-way leaves every layer's table unchanged") {
+  // Layers 0 and 2 over group a, layer 1 over group b: layer 1's allocate
+  // throws (group b holds no layer-0 reservations), after layer 0 has taken
+  // its pages. append_slots must give those pages back and rethrow.
+  Group a(12, 12 * Group::kPage), b(12, 12 * Group::kPage);
+  std::vector<std::unique_ptr<base::BlockAllocator>> layers;
+  layers.push_back(std::make_unique<base::BlockAllocator>(16, 2, 64, a.group, 0));
+  layers.push_back(std::make_unique<base::BlockAllocator>(16, 2, 64, b.group, 1));
+  layers.push_back(std::make_unique<base::BlockAllocator>(16, 2, 64, a.group, 2));
+  base::KVCacheManager kv(16, 3, std::move(layers));
+  const base::RequestId id = kv.register_request();
+  const int32_t free0 = kv.num_free_blocks(0);
+  CHECK_THROWS_AS(kv.append_slots(id, 40), std::logic_error);
+  for (int l = 0; l < 3; ++l) CHECK(kv.get_block_ids(id, l).empty());
+  CHECK_EQ(kv.get_context_len(id), 0);
+  CHECK_EQ(kv.num_free_blocks(0), free0);
+  CHECK_EQ(a.group->leased_bytes(), 0u);  // layer 0's pages went back, Chunk released
+  CHECK_EQ(a.owner->lease_count(), 0u);
+  kv.free_request(id);
+  CHECK_EQ(kv.num_active_requests(), 0);
+}
+
 TEST_CASE("decode reservation: ceil(tokens/16) page-major pages and a valid manifest") {
   Group g(24, 24 * Group::kPage);
   auto kv = manager_over(g.group);

@@ -526,6 +526,106 @@ TEST_CASE("end to end: the reference's copy_shared_kv call order over KVCacheMan
   CHECK(pbe_arena_destroy(arena) == PBE_OK);
 }
 
+TEST_CASE("end to end at config-2 size: 315 pages x 28 layers through CopySharedKVToDecode, bit-exact") {
+  // Qwen2.5-1.5B geometry: 28 layers, 2 KV heads x 128, 16-token pages
+  // (448 KiB). A 5040-token prefill (315 pages) handed to a decode group
+  // whose free pages are fragmented by earlier requests, twice in a row (the
+  // second handoff reuses the first one's pages after their fences pass).
+  const int layers = 28;
+  const uint64_t half = 16 * 2 * 128 * 2, page = 2 * layers * half;
+  const uint64_t n_pages = 760, arena_bytes = n_pages * page;
+  REQUIRE(oracle_copy_handoff() != nullptr);
+  pbe_arena* arena = nullptr;
+  REQUIRE(pbe_arena_create(0, arena_bytes, 0, 5151, &arena) == PBE_OK);
+  pbe_arena_view view{};
+  REQUIRE(pbe_arena_get_view(arena, &view) == PBE_OK);
+  REQUIRE(view.nseg == 1u);
+  auto owner = std::make_shared<base::LocalChunkOwner>(arena_bytes, 5151);
+  owner->register_model("prefill", 330 * page);
+  owner->register_model("decode", 430 * page);
+  void* p_stream = nullptr;
+  void* d_stream = nullptr;
+  REQUIRE(pbe_stream_create(0, &p_stream) == PBE_OK);
+  REQUIRE(pbe_stream_create(0, &d_stream) == PBE_OK);
+  {
+    auto p_client = std::make_shared<base::SharedKVArenaClient>(owner, view, "prefill", 330 * page, 0);
+    auto d_client = std::make_shared<base::SharedKVArenaClient>(owner, view, "decode", 430 * page, 0);
+    auto p_pages = std::make_shared<base::SharedKVPageGroup>(p_client, layers, half, 2 * 1024 * 1024, p_stream);
+    auto d_pages = std::make_shared<base::SharedKVPageGroup>(d_client, layers, half, 2 * 1024 * 1024, d_stream);
+    auto p_kv = manager_over(p_pages, 2, 128);
+    auto d_kv = manager_over(d_pages, 2, 128);
+    // decode side: five requests, then every other one freed -> holes
+    std::vector<base::RequestId> held;
+    for (int k = 0; k < 5; ++k) {
+      held.push_back(d_kv->register_request());
+      REQUIRE(d_kv->append_slots(held.back(), 16 * (7 + 5 * k)));
+    }
+    d_kv->free_request(held[0]);
+    d_kv->free_request(held[2]);
+    d_kv->free_request(held[4]);
+    REQUIRE(pbe_stream_synchronize(0, d_stream) == PBE_OK);
+    const base::RequestId pr = p_kv->register_request();
+    REQUIRE(p_kv->append_slots(pr, 5040));
+    serving::KVPoolDescriptor pool{0, layers, 16, 2, 128, base::DataType::kDataTypeBf16,
+                                   base::BlockStorageMode::kPlain};
+    serving::SharedKVPrefillResult result;
+    result.shared_arena_epoch = p_client->epoch();
+    result.client_request_id.value = "req-5040";
+    result.handoff_id.value = 2;
+    result.prompt_tokens.assign(5040, 7);
+    result.computed_tokens = 5040;
+    result.first_token = 11;
+    result.src_pool = pool;
+    for (int l = 0; l < layers; ++l) result.layers.push_back({l, p_kv->get_block_ids(pr, l)});
+    std::vector<uint8_t> host(arena_bytes), got(arena_bytes);
+    uint64_t x = 0x2545f4914f6cdd1dull;
+    for (uint64_t i = 0; i < arena_bytes / 8; ++i) {
+      x ^= x << 13; x ^= x >> 7; x ^= x << 17;
+      std::memcpy(host.data() + 8 * i, &x, 8);
+    }
+    HIP_OK(hipMemcpy(view.base[0], host.data(), arena_bytes, hipMemcpyHostToDevice));
+    const auto& src = p_kv->get_block_ids(pr, 0);
+    REQUIRE(src.size() == 315u);
+    for (int round = 0; round < 2; ++round) {
+      std::printf("  handoff %d\n", round);
+      std::fflush(stdout);
+      serving::DecodeKVReservation res;
+      const uint64_t copied = serving::CopySharedKVToDecode(d_kv.get(), pool, result, d_stream, &res);
+      CHECK_EQ(copied, 315 * page);
+      REQUIRE(res.valid());
+      CHECK_EQ(d_kv->kv_committed_tokens(res.decode_request_id), 5040);
+      const auto& dst = d_kv->get_block_ids(res.decode_request_id, 0);
+      REQUIRE(dst.size() == 315u);
+      for (int l = 1; l < layers; ++l) CHECK(d_kv->get_block_ids(res.decode_request_id, l) == dst);
+      // the destination is fragmented: it starts in the holes left above
+      int runs = 1;
+      for (size_t i = 1; i < dst.size(); ++i) runs += dst[i] != dst[i - 1] + 2 * layers;
+      CHECK(runs > 1);
+      std::vector<int32_t> s1(315), s2(315), s3(315);
+      CHECK_EQ(oracle_copy_handoff()(host.data(), src.data(), dst.data(), 315, half, layers, s1.data(),
+                                     s2.data(), s3.data()),
+               315 * page);
+      HIP_OK(hipMemcpy(got.data(), view.base[0], arena_bytes, hipMemcpyDeviceToHost));
+      CHECK(std::memcmp(got.data(), host.data(), arena_bytes) == 0);
+      d_kv->free_request(res.decode_request_id);
+      REQUIRE(pbe_stream_synchronize(0, d_stream) == PBE_OK);
+    }
+    p_kv->free_request(pr);
+    d_kv->free_request(held[1]);
+    d_kv->free_request(held[3]);
+    REQUIRE(pbe_stream_synchronize(0, p_stream) == PBE_OK);
+    REQUIRE(pbe_stream_synchronize(0, d_stream) == PBE_OK);
+    p_pages->collect();
+    d_pages->collect();
+    CHECK_EQ(p_pages->leased_bytes(), 0u);
+    CHECK_EQ(d_pages->leased_bytes(), 0u);
+  }
+  CHECK_EQ(owner->lease_count(), 0u);
+  pbe_stream_destroy(0, p_stream);
+  pbe_stream_destroy(0, d_stream);
+  CHECK(pbe_arena_destroy(arena) == PBE_OK);
+}
+
 TEST_CASE("page group: a retired page is not handed out again until its fence has passed") {
   // The deferred unpin of shared_kv_reuse_probe.cpp, with the stream held by
   // a host-function gate: the page's fence is queued behind the gate.
