@@ -48,6 +48,7 @@ HOST_SOURCES = [
     "csrc/cache/transfer_plan.cpp",
     "csrc/cache/page_migration.cpp",
     "csrc/serving/pd_handoff_common.cpp",
+    "csrc/base/trace_range.cpp",
 ]
 # Host C++ that reaches the GPU only through the C ABI (in the library, not in
 # the CPU-only unit-test binary).

@@ -13,6 +13,7 @@
 #include <string>
 #include <vector>
 
+#include "base/trace_range.h"
 #include "capi_internal.h"
 
 using namespace pbe_capi;
@@ -302,6 +303,7 @@ extern "C" {
 int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, const int32_t* dst_ids,
                        int64_t n, const pbe_kv_shape* shape, int device, void* stream,
                        uint64_t* copied) {
+  const base::TraceRange trace("pbe_copy_shared_kv");
   if (copied) *copied = 0;
   if (!view_ok(arena) || !shape_ok(shape) || n <= 0 || !src_ids || !dst_ids || device < 0)
     return fail(PBE_ERR_INVALID, "invalid handoff arguments");

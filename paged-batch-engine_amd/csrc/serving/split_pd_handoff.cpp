@@ -5,11 +5,14 @@
 #include <stdexcept>
 #include <string>
 
+#include "base/trace_range.h"
+
 namespace serving {
 
 uint64_t CopySharedKVToDecode(base::KVCacheManager* manager, const KVPoolDescriptor& decode_pool,
                               const SharedKVPrefillResult& source, void* stream,
                               DecodeKVReservation* reservation) {
+  const base::TraceRange trace("split_pd_shared_kv_copy");  // split_pd_engine.cpp:51
   if (manager == nullptr || reservation == nullptr)
     throw std::invalid_argument("shared KV handoff needs a manager and a reservation output");
   const base::BlockAllocator& first = manager->allocator(0);

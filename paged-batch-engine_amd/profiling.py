@@ -3,6 +3,7 @@
     python paged-batch-engine_amd/profiling.py stats <rocprof_dir> --out FILE --command "..."
     python paged-batch-engine_amd/profiling.py pmc <fetch_dir> <write_dir> --out FILE --command "..."
     python paged-batch-engine_amd/profiling.py legs <pmc_dir>... --launches K --out FILE --command "..."
+    python paged-batch-engine_amd/profiling.py markers <trace_dir> --out FILE --command "..."
 
 `stats` reads the kernel trace of a `rocprofv3 --kernel-trace --stats
 --output-format csv` run and writes per-kernel call counts and durations.
@@ -181,6 +182,44 @@ def legs(roots, launches: int, out: str, command: str) -> None:
     print(text)
 
 
+def markers(root: str, out: str, command: str) -> None:
+    """roctx ranges of a rocprofv3 --marker-trace --kernel-trace run: per range
+    name the count and durations, and per kernel how many of its dispatches
+    ran entirely inside a range of each name (same host thread: the one that
+    pushed the range and enqueued the kernel)."""
+    ranges = defaultdict(list)  # name -> [(pid, start, end)]
+    for r in _csv_rows(root, "marker_api_trace.csv"):
+        name = r.get("Function") or r.get("Message") or ""
+        ranges[name].append((r.get("Thread_Id", ""), int(r["Start_Timestamp"]),
+                             int(r["End_Timestamp"])))
+    kernels = defaultdict(list)
+    for r in _csv_rows(root, "kernel_trace.csv"):
+        kernels[_short(r["Kernel_Name"])].append((r.get("Thread_Id", ""), int(r["Start_Timestamp"]),
+                                                  int(r["End_Timestamp"])))
+    lines = ["# rocprofv3 --marker-trace --kernel-trace summary: roctx ranges around the handoff",
+             f"command: {command}", "",
+             f"{'range':<32} {'count':>6} {'median_us':>10} {'min_us':>9} {'max_us':>9}"]
+    for name, v in sorted(ranges.items()):
+        d = [(e - s) / 1e3 for _, s, e in v]
+        lines.append(f"{name[:32]:<32} {len(v):>6} {statistics.median(d):>10.1f} {min(d):>9.1f} "
+                     f"{max(d):>9.1f}")
+    lines += ["", "kernel dispatches inside each range (start and end within it):",
+              f"{'kernel':<40} {'dispatches':>10}  " + "  ".join(f"{n[:28]:>28}" for n in sorted(ranges))]
+    for k, v in sorted(kernels.items(), key=lambda kv: -len(kv[1])):
+        if "pbe::" not in k and "copy" not in k:
+            continue
+        inside = []
+        for name in sorted(ranges):
+            rs = ranges[name]
+            inside.append(sum(any(p == rp and rs0 <= s and e <= re for rp, rs0, re in rs)
+                              for p, s, e in v))
+        lines.append(f"{k[:40]:<40} {len(v):>10}  " + "  ".join(f"{n:>28}" for n in inside))
+    text = "\n".join(lines) + "\n"
+    with open(out, "w") as fh:
+        fh.write(text)
+    print(text)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -205,7 +244,14 @@ def main() -> None:
     q.add_argument("--launches", type=int, required=True)
     q.add_argument("--out", required=True)
     q.add_argument("--command", required=True)
+    mk = sub.add_parser("markers")
+    mk.add_argument("root")
+    mk.add_argument("--out", required=True)
+    mk.add_argument("--command", required=True)
     a = ap.parse_args()
+    if a.cmd == "markers":
+        markers(a.root, a.out, a.command)
+        return
     if a.cmd == "legs":
         legs(a.roots, a.launches, a.out, a.command)
         return
