@@ -38,6 +38,7 @@ extern "C" {
 #define PBE_ERR_UNKNOWN (-3)     /* completion unknown: retain every resource */
 #define PBE_ERR_NOMEM (-4)
 #define PBE_ERR_UNSUPPORTED (-5)
+#define PBE_ERR_BUSY (-6)        /* a shared resource is in use by queued work on another stream */
 
 #define PBE_MAX_SEGMENTS 16
 #define PBE_IPC_HANDLE_BYTES 64
@@ -330,9 +331,14 @@ int pbe_paged_decode(const pbe_arena_view* kv, int32_t kv_dtype, const float* sc
  * partials fit the array; an explicit split count whose partials need more
  * (pbe_paged_decode_workspace_bytes) is rejected with PBE_ERR_INVALID, as is a
  * batch too large for the array even at one split. All calls on
- * one GPU share the array: calls that overlap in time on one GPU (different
- * streams, or host threads racing) corrupt each other's results; serialize
- * them on one stream. */
+ * one GPU share the array, so calls must not overlap in time: issue them on
+ * one stream. A call on a different stream from the previous call, while that
+ * call's work has not completed, is refused with PBE_ERR_BUSY before anything
+ * is queued (an event recorded after each call is queried on entry; host
+ * threads are serialised by a lock). Under stream capture the guard is off:
+ * the caller orders the graph's replays. The first call on a GPU resolves
+ * the array's address and creates the guard event; later calls allocate
+ * nothing. */
 #define PBE_DECODE_SCRATCH_BYTES (8u << 20)
 int pbe_paged_decode_noalloc(const pbe_arena_view* kv, int32_t kv_dtype, const float* scales,
                              uint64_t scale_bytes, const pbe_kv_shape* shape, int32_t layer,

@@ -86,19 +86,41 @@ static __device__ __align__(256) uint8_t scratch[PBE_DECODE_SCRATCH_BYTES];
 
 namespace {
 
-int scratch_address(int device, void** out) {
-  static std::mutex mu;
-  static void* per_device[64] = {};
+// Per-GPU state of the scratch array: its device address, and the last call
+// that used it: an event recorded on that call's stream after its launches,
+// and the stream. A call on another stream is refused (PBE_ERR_BUSY) while
+// that event has not completed; on the same stream, stream order already
+// serialises the two. `mu` makes check, launch and record one step for
+// racing host threads.
+struct ScratchState {
+  std::mutex mu;
+  void* ptr = nullptr;
+  hipEvent_t last_use = nullptr;
+  void* last_stream = nullptr;
+  bool used = false;
+};
+
+ScratchState& scratch_state(int device) {
+  static ScratchState states[64];
+  return states[device];
+}
+
+// Resolves the array's address and creates the guard event once per GPU
+// (with that GPU current); later calls allocate nothing.
+int scratch_setup(int device, ScratchState** out) {
   if (device < 0 || device >= 64) return fail(PBE_ERR_INVALID, "device %d out of range", device);
-  std::lock_guard<std::mutex> lock(mu);
-  if (!per_device[device]) {
+  ScratchState& st = scratch_state(device);
+  if (!st.ptr) {
     PBE_DEVICE_SCOPE(device);
     void* ptr = nullptr;
     const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !ptr) return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
-    per_device[device] = ptr;
+    hipEvent_t ev = nullptr;
+    PBE_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    st.last_use = ev;
+    st.ptr = ptr;
   }
-  *out = per_device[device];
+  *out = &st;
   return PBE_OK;
 }
 
@@ -287,12 +309,35 @@ int pbe_paged_decode_noalloc(const pbe_arena_view* kv, int32_t kv_dtype, const f
                              const void* queries, void* outputs, int32_t batch, int32_t q_heads,
                              const int32_t* block_tables, const int32_t* seq_lens,
                              int32_t max_blocks_per_seq, int32_t splits, int device, void* stream) {
-  void* ws = nullptr;
-  const int rc = scratch_address(device, &ws);
+  if (device < 0 || device >= 64) return fail(PBE_ERR_INVALID, "device %d out of range", device);
+  ScratchState& st = scratch_state(device);
+  std::lock_guard<std::mutex> lock(st.mu);
+  ScratchState* ready = nullptr;
+  int rc = scratch_setup(device, &ready);
   if (rc != PBE_OK) return rc;
-  return paged_decode_call(kv, kv_dtype, scales, scale_bytes, shape, layer, queries, outputs, batch,
-                           q_heads, block_tables, seq_lens, max_blocks_per_seq, splits, ws,
-                           PBE_DECODE_SCRATCH_BYTES, device, stream, true);
+  PBE_DEVICE_SCOPE(device);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  // Under graph capture nothing runs now: the guard neither checks nor
+  // records (replays of the graph are ordered by whoever launches them).
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  PBE_HIP(hipStreamIsCapturing(s, &capture));
+  const bool live = capture == hipStreamCaptureStatusNone;
+  if (live && st.used && st.last_stream != stream) {
+    const hipError_t q = hipEventQuery(st.last_use);
+    if (q == hipErrorNotReady)
+      return fail(PBE_ERR_BUSY,
+                  "the static decode scratch of device %d is still in use by a call on another "
+                  "stream; wait for that stream or issue both calls on one stream", device);
+    if (q != hipSuccess) return hip_fail(q, "hipEventQuery(decode scratch guard)");
+  }
+  rc = paged_decode_call(kv, kv_dtype, scales, scale_bytes, shape, layer, queries, outputs, batch,
+                         q_heads, block_tables, seq_lens, max_blocks_per_seq, splits, st.ptr,
+                         PBE_DECODE_SCRATCH_BYTES, device, stream, true);
+  if (rc != PBE_OK || !live) return rc;
+  PBE_HIP(hipEventRecord(st.last_use, s));
+  st.last_stream = stream;
+  st.used = true;
+  return PBE_OK;
 }
 
 int pbe_paged_decode_pools(const void* key_pool, const void* value_pool, uint64_t pool_bytes,

@@ -19,6 +19,7 @@ PBE_ERR_HIP = -2
 PBE_ERR_UNKNOWN = -3
 PBE_ERR_NOMEM = -4
 PBE_ERR_UNSUPPORTED = -5
+PBE_ERR_BUSY = -6
 PBE_MAX_SEGMENTS = 16
 PBE_IPC_HANDLE_BYTES = 64
 PBE_FP8_SCALE_PER_TOKEN_HEAD = 0

@@ -89,3 +89,62 @@ def test_noalloc_decode_lowers_an_automatic_split_count_to_fit(torch_cuda):
     got_bits = _noalloc(case, 0).view(np.uint16)
     assert np.array_equal(got_bits, want_bits)
     assert not np.isnan(bf16_to_f64(got_bits)).any()
+
+
+def test_noalloc_decode_refuses_a_second_stream_while_the_first_is_queued(torch_cuda):
+    # Stream a is held by a host function (bounded: it returns after 20 s at
+    # the latest, and the gate is opened in every case), so a call queued on
+    # it keeps the static scratch in use; a call on stream b must then be
+    # refused with PBE_ERR_BUSY before it queues anything, while a second call
+    # on stream a is accepted (stream order serialises it).
+    import ctypes
+    import threading
+    torch = torch_cuda
+    case = DecodeCase(torch, fp8=True, layers=2, H=2, D=128, kvm=6,
+                      seq_lens=[300, 17, 64], seed=31)
+    dtype = P.PBE_KV_FP8_E4M3
+    splits = P.decode_splits(case.batch, case.H, case.max_blocks, dtype)
+    case.out.fill_(0)
+    case.run(splits=splits)
+    want_bits = case.out.cpu().numpy().view(np.uint16).copy()
+
+    def call(out, stream):
+        P.paged_decode_noalloc(case.view, dtype, case.scales.data_ptr(), case.scales.numel() * 4,
+                               case.kv, case.layer, case.q.data_ptr(), out.data_ptr(), case.batch,
+                               case.H * case.kvm, case.t_dev.data_ptr(), case.s_dev.data_ptr(),
+                               case.max_blocks, splits, stream)
+
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    hostfn = ctypes.CFUNCTYPE(None, ctypes.c_void_p)
+    hip.hipLaunchHostFunc.argtypes = [ctypes.c_void_p, hostfn, ctypes.c_void_p]
+    gate = threading.Event()
+
+    def hold(_):
+        gate.wait(20)
+
+    hold_fn = hostfn(hold)  # kept alive until both streams have drained
+    a, b = torch.cuda.Stream(), torch.cuda.Stream()
+    out_a = torch.zeros_like(case.out)
+    out_b = torch.full_like(case.out, 7)
+    torch.cuda.synchronize()
+    say("noalloc decode guard: stream a gated, call on a, then on b")
+    refused = None
+    try:
+        assert hip.hipLaunchHostFunc(a.cuda_stream, hold_fn, None) == 0
+        call(out_a, a.cuda_stream)  # queued behind the gate
+        try:
+            call(out_b, b.cuda_stream)
+        except P.PbeError as e:
+            refused = e
+        call(out_a, a.cuda_stream)  # same stream: accepted
+    finally:
+        gate.set()
+    a.synchronize()
+    torch.cuda.synchronize()
+    assert refused is not None and refused.code == P.PBE_ERR_BUSY, refused
+    assert bool((out_b == 7).all())  # the refused call queued nothing
+    assert np.array_equal(out_a.cpu().numpy().view(np.uint16), want_bits)
+    # once stream a has drained, stream b is accepted and bit-identical
+    call(out_b, b.cuda_stream)
+    b.synchronize()
+    assert np.array_equal(out_b.cpu().numpy().view(np.uint16), want_bits)
