@@ -383,18 +383,6 @@ int pbe_paged_decode_pools(const void* key_pool, const void* value_pool, uint64_
  *   pools are written. A sequence of length 0 writes nothing and reads as
  *   zeros; one whose last block id fails the reader's checks writes nothing
  *   and reads as NaN. */
-/* The same over the page-major arena and a layer, as pbe_paged_decode takes
- * them (segmented arenas included): the new token of sequence b lands at
- * row (seq_lens[b]-1) % 16 of block block_tables[b][(seq_lens[b]-1) / 16] in
- * layer `layer`'s K and V planes, and its FP8 scales in the page-major scale
- * pool. No counterpart in the reference. */
-int pbe_paged_decode_append_arena(const pbe_arena_view* kv, int32_t kv_dtype, float* scales,
-                                  uint64_t scale_bytes, const pbe_kv_shape* shape, int32_t layer,
-                                  const void* new_keys, const void* new_values, const void* queries,
-                                  void* outputs, int32_t batch, int32_t q_heads,
-                                  const int32_t* block_tables, const int32_t* seq_lens,
-                                  int32_t max_blocks_per_seq, int32_t splits, void* workspace,
-                                  uint64_t workspace_bytes, int device, void* stream);
 int pbe_paged_decode_append(void* key_pool, void* value_pool, uint64_t pool_bytes,
                             float* key_scales, float* value_scales, uint64_t scale_pool_bytes,
                             int32_t kv_dtype, int32_t kv_heads, int32_t head_dim, const void* new_keys,
@@ -402,6 +390,20 @@ int pbe_paged_decode_append(void* key_pool, void* value_pool, uint64_t pool_byte
                             int32_t q_heads, const int32_t* block_tables, const int32_t* seq_lens,
                             int32_t max_blocks_per_seq, int32_t splits, void* workspace,
                             uint64_t workspace_bytes, int device, void* stream);
+/* The same over the page-major arena and a layer, as pbe_paged_decode takes
+ * them (segmented arenas included): the new token of sequence b lands at
+ * row (seq_lens[b]-1) % 16 of block block_tables[b][(seq_lens[b]-1) / 16] in
+ * layer `layer`'s K and V planes, and its FP8 scales in the page-major scale
+ * pool. The arena's pages and the scale pool are written (the view is
+ * const because the view struct itself is not changed; the memory it names
+ * is). No counterpart in the reference. */
+int pbe_paged_decode_append_arena(const pbe_arena_view* kv, int32_t kv_dtype, float* scales,
+                                  uint64_t scale_bytes, const pbe_kv_shape* shape, int32_t layer,
+                                  const void* new_keys, const void* new_values, const void* queries,
+                                  void* outputs, int32_t batch, int32_t q_heads,
+                                  const int32_t* block_tables, const int32_t* seq_lens,
+                                  int32_t max_blocks_per_seq, int32_t splits, void* workspace,
+                                  uint64_t workspace_bytes, int device, void* stream);
 
 /* ---- page writer ---------------------------------------------------------
  * Writes n_tokens new tokens' K and V rows into their page slots: the MI355X

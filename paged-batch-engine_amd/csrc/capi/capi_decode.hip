@@ -134,6 +134,10 @@ struct DecodePools {
   const float* key_scales;
   const float* value_scales;
   uint64_t scale_bytes;  // addressable from each scale pointer
+  // the append form's writable views of the same K pool and K scale pool
+  // (null for the read-only entry points)
+  void* key_w = nullptr;
+  float* key_scales_w = nullptr;
 };
 
 // Shared body of the decode entry points. `static_scratch`: the workspace is
@@ -148,7 +152,7 @@ int paged_decode_call(const pbe_arena_view* kv, int32_t kv_dtype, const float* s
                       int32_t max_blocks_per_seq, int32_t splits, void* workspace,
                       uint64_t workspace_bytes, int device, void* stream, bool static_scratch,
                       const DecodePools* pools = nullptr, const void* new_keys = nullptr,
-                      const void* new_values = nullptr) {
+                      const void* new_values = nullptr, float* append_scales = nullptr) {
   if ((!pools && !view_ok(kv)) || !shape_ok(shape))
     return fail(PBE_ERR_INVALID, "invalid decode arena view or shape");
   if (kv_dtype != PBE_KV_BF16 && kv_dtype != PBE_KV_FP8_E4M3)
@@ -259,6 +263,15 @@ int paged_decode_call(const pbe_arena_view* kv, int32_t kv_dtype, const float* s
   p.seq_lens = seq_lens;
   p.new_k = static_cast<const uint16_t*>(new_keys);
   p.new_v = static_cast<const uint16_t*>(new_values);
+  if (append) {  // the memory the append form writes, through non-const pointers
+    if (pools) {
+      p.wbase[0] = static_cast<char*>(pools->key_w);
+      p.wscales = fp8 ? pools->key_scales_w : nullptr;
+    } else {
+      for (uint32_t i = 0; i < kv->nseg; ++i) p.wbase[i] = static_cast<char*>(kv->base[i]);
+      p.wscales = fp8 ? append_scales : nullptr;
+    }
+  }
   const uint64_t rows = (uint64_t)batch * q_heads * splits;
   p.part_acc = static_cast<float*>(workspace);
   p.part_m = p.part_acc + rows * shape->head_dim;
@@ -364,7 +377,7 @@ int pbe_paged_decode_append_arena(const pbe_arena_view* kv, int32_t kv_dtype, fl
   if (!new_keys || !new_values) return fail(PBE_ERR_INVALID, "null new keys or values");
   return paged_decode_call(kv, kv_dtype, scales, scale_bytes, shape, layer, queries, outputs, batch, q_heads,
                            block_tables, seq_lens, max_blocks_per_seq, splits, workspace, workspace_bytes,
-                           device, stream, false, nullptr, new_keys, new_values);
+                           device, stream, false, nullptr, new_keys, new_values, scales);
 }
 
 int pbe_paged_decode_append(void* key_pool, void* value_pool, uint64_t pool_bytes,
@@ -376,7 +389,9 @@ int pbe_paged_decode_append(void* key_pool, void* value_pool, uint64_t pool_byte
                             uint64_t workspace_bytes, int device, void* stream) {
   if (!new_keys || !new_values) return fail(PBE_ERR_INVALID, "null new keys or values");
   const pbe_kv_shape shape{1, kv_heads, head_dim, 16};
-  const DecodePools pools{key_pool, value_pool, pool_bytes, key_scales, value_scales, scale_pool_bytes};
+  DecodePools pools{key_pool, value_pool, pool_bytes, key_scales, value_scales, scale_pool_bytes};
+  pools.key_w = key_pool;
+  pools.key_scales_w = key_scales;
   return paged_decode_call(nullptr, kv_dtype, nullptr, 0, &shape, 0, queries, outputs, batch, q_heads,
                            block_tables, seq_lens, max_blocks_per_seq, splits, workspace,
                            workspace_bytes, device, stream, false, &pools, new_keys, new_values);

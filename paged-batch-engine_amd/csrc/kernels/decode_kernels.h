@@ -47,6 +47,10 @@ struct DecodeParams {
   // read; the payload and scale pools above are then written as well.
   const uint16_t* new_k;
   const uint16_t* new_v;
+  // Append form only: writable views of the payload bases and of the scale
+  // pool (the same memory as kv.base and scales).
+  char* wbase[kDecodeMaxSegments];
+  float* wscales;
 };
 
 // Bytes of the split-K workspace (partial outputs, maxima and sums).

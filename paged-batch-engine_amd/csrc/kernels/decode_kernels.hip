@@ -409,7 +409,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
       if (id >= 0 && id <= p.id_max && page * p.by_stride.d == (uint32_t)id) {
         const int row = seq - 1 - kBlockTokens * last;
         const uint32_t seg = fast_div(page, p.by_seg_pages);
-        char* krow = const_cast<char*>(p.kv.base[seg]) + (uint64_t)(page - seg * p.by_seg_pages.d) * stride * p.half +
+        char* krow = p.wbase[seg] + (uint64_t)(page - seg * p.by_seg_pages.d) * stride * p.half +
                      head_off + (uint64_t)row * token_stride;
         const bool is_v = lane >= 32;
         const int li = lane & 31;
@@ -424,7 +424,7 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
           const u32x2 c = quantise8(x, inv);
           if (act) *reinterpret_cast<u32x2*>(dst + 8 * li) = c;
           if (act && li == 0)
-            const_cast<float*>(p.scales)[(uint64_t)id * kBlockTokens * H +
+            p.wscales[(uint64_t)id * kBlockTokens * H +
                                          (2u * p.layer * kBlockTokens + row) * H + kvh + (is_v ? p.vscale_delta : 0)] = sc;
           nks = __shfl(sc, 0);
           nvs = __shfl(sc, 32);
