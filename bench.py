@@ -716,6 +716,59 @@ def measure_decode(torch, P, scrub, n: int, batch: int = 64, seq: int = 5040, pl
     return res
 
 
+def read_ceiling(torch, scrub, n: int, nbytes: int = 170_704_896) -> dict:
+    """Streaming-read ceilings for the decode reader: about `nbytes` (the FP8
+    reader's bytes per step at 64 x 5,040 tokens) read at shuffled positions
+    by short-lived waves (1 step each) and by long-lived ones (8 and 20 steps
+    each; the reader's waves hold ~20 blocks at 16 splits), each wave keeping
+    4 steps in flight (lib/libpbe_ceiling.so, stream_read_steps_kernel), in two
+    access shapes: contiguous 4 KiB steps, and the FP8 reader's own (8 KiB
+    blocks, each read as two KV heads' 128-byte halves of 256-byte token rows
+    by a pair of waves)."""
+    import ctypes as C
+    import numpy as np
+    so = Path(__file__).resolve().parent / "paged-batch-engine_amd" / "lib" / "libpbe_ceiling.so"
+    cl = C.CDLL(str(so))
+    cl.pbe_ceiling_read_steps.argtypes = [C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_int,
+                                          C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+    dev = torch.device("cuda:0")
+    sp = torch.cuda.current_stream().cuda_stream
+    buf = torch.empty(nbytes // 8192 * 8192, dtype=torch.uint8, device=dev)
+    buf.view(torch.int32).random_()
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    sink = torch.empty(1024, dtype=torch.uint8, device=dev)
+    ev = TimingEvents(2)
+    out = {"what": "reads at shuffled positions, non-temporal loads, 4 steps in flight per wave"}
+    for shape, step in (("contiguous_4k_steps", 4096), ("reader_shape_8k_blocks", 8192)):
+        n_steps = buf.numel() // step
+        order = torch.randperm(n_steps, generator=g, device=dev).to(torch.int32)
+        legs = {"bytes": n_steps * step}
+        for spw in (1, 8, 20):
+            ts = []
+            for i in range(n + 2):
+                scrub.fill_(i & 0xff)
+                rc = cl.pbe_ceiling_read_steps(buf.data_ptr(), order.data_ptr(), n_steps, spw,
+                                               1 if step == 8192 else 0, sink.data_ptr(), sp,
+                                               ev.handle(0), ev.handle(1))
+                if rc:
+                    raise RuntimeError(f"read-steps launch failed ({rc})")
+                torch.cuda.synchronize()
+                if i >= 2:
+                    ts.append(ev.elapsed_ms(0, 1))
+            ms = float(np.mean(ts))
+            waves = (n_steps + spw - 1) // spw * (2 if step == 8192 else 1)
+            legs[f"steps_per_wave_{spw}"] = {
+                "waves": waves, "us_mean": round(ms * 1e3, 2),
+                "gbps": round(n_steps * step / (ms * 1e-3) / 1e9, 1),
+                "grid_threads": (waves + 3) // 4 * 256}
+            print(json.dumps({"read_steps": shape, "spw": spw, **legs[f"steps_per_wave_{spw}"]}),
+                  file=sys.stderr, flush=True)
+        out[shape] = legs
+    ev.close()
+    return out
+
+
 def calibration_copy(torch, P, scrub, steps: int, sp: int) -> dict:
     """One plain 256 MiB run (1024 pages of 256 KiB, offset 0 to offset 256 MiB)
     with the copy kernel: the known byte count that rocprofv3 --pmc counters
@@ -769,6 +822,9 @@ def main() -> int:
     ap.add_argument("--ceiling-legs", type=int, default=0, metavar="K",
                     help="only launch the config-2 plan and its ceiling legs K times each, in a "
                          "fixed order (for rocprofv3 --pmc; summarised by profiling.py legs)")
+    ap.add_argument("--read-ceiling", action="store_true",
+                    help="time the decode reader (FP8 and BF16) beside plain streaming reads of "
+                         "the FP8 reader's bytes by short- and long-lived waves")
     ap.add_argument("--calibrate", action="store_true",
                     help="also launch a plain contiguous copy of 256 MiB with the same kernel "
                          "(rocprofv3 --pmc byte-count calibration)")
@@ -794,6 +850,12 @@ def main() -> int:
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
+    if args.read_ceiling:
+        scrub = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        out = {"decode": measure_decode(torch, P, scrub, max(3, args.steps), 64, 5040, "chunks"),
+               "read_ceiling": read_ceiling(torch, scrub, max(3, args.steps))}
+        print(json.dumps(out))
+        return 0
     if args.decode_only or args.fp8_only or args.scatter_only or args.decode_loop_only:
         scrub = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         sp = torch.cuda.current_stream().cuda_stream

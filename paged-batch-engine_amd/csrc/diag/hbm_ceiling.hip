@@ -86,6 +86,66 @@ void phase_copy_kernel(const uint8_t* src, uint8_t* dst, uint64_t bytes) {
     __builtin_amdgcn_raw_buffer_store_b128(v[u], rd, (u * kWave + lane) * 16u, 0, kStorePolicy);
 }
 
+// Read-only streams in steps at the positions of a list (the decode reader's
+// access: each wave streams its own sequence of scattered blocks), with
+// kReadDepth steps in flight per wave (a ring of registers, as the reader
+// keeps blocks in flight) and non-temporal loads. Wave w reads steps
+// [w*steps_per_wave, (w+1)*steps_per_wave) of `order`.
+//   kReaderShape false: step s is the 4 KiB at base + order[s] * 4 KiB.
+//   kReaderShape true:  the FP8 reader's shape at 2 KV heads x 128 dims: step
+//     s is one 8 KiB block at base + order[s] * 8 KiB (a 4 KiB K plane of
+//     16 token rows x 2 heads x 128 B, then the V plane); waves 2p and 2p+1
+//     read the same steps, each its own head's 128-byte half of every
+//     256-byte token row (16 K rows, then 16 V rows).
+// steps_per_wave = 1 gives short-lived waves; 8 and 20 the reader's
+// long-lived ones.
+constexpr int kReadDepth = 4;
+
+template <bool kReaderShape>
+__global__ __launch_bounds__(kThreads) void stream_read_steps_kernel(
+    const uint8_t* base, const uint32_t* order, uint32_t n_steps, uint32_t steps_per_wave,
+    u32x4* sink) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t w = blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
+  const uint32_t list_w = kReaderShape ? w / 2 : w;
+  const uint32_t s0 = __builtin_amdgcn_readfirstlane(list_w * steps_per_wave);
+  if (s0 >= n_steps) return;
+  const uint32_t s1 = __builtin_amdgcn_readfirstlane(min(s0 + steps_per_wave, n_steps));
+  // reader shape: lane -> (token row, 16-byte piece) of this wave's head
+  const uint32_t lane_off = kReaderShape ? (lane / 8) * 256u + (w & 1) * 128u + (lane % 8) * 16u
+                                         : lane * 16u;
+  u32x4 r[kReadDepth][4];
+  u32x4 acc = {0, 0, 0, 0};
+  auto load = [&](uint32_t s, u32x4* d) {
+    if constexpr (kReaderShape) {
+      const uint8_t* blk = base + (uint64_t)__builtin_amdgcn_readfirstlane(order[s]) * 8192u;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)  // K rows 0-7, 8-15, then V rows 0-7, 8-15
+        d[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+            blk + (u / 2) * 4096u + (u % 2) * 2048u + lane_off));
+    } else {
+      const uint8_t* st = base + (uint64_t)__builtin_amdgcn_readfirstlane(order[s]) * 4096u;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        d[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(st + u * 1024u + lane_off));
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < kReadDepth; ++i)
+    if (s0 + i < s1) load(s0 + i, r[i]);
+  for (uint32_t b = s0; b < s1; b += kReadDepth) {
+#pragma unroll
+    for (int i = 0; i < kReadDepth; ++i) {
+      if (b + i < s1) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc ^= r[i][u];
+      }
+      if (b + i + kReadDepth < s1) load(b + i + kReadDepth, r[i]);
+    }
+  }
+  if (acc.x == 0x9e3779b9u && acc.y == 0x7f4a7c15u && acc.z == 0x85ebca6bu) sink[lane] = acc;
+}
+
 dim3 grid_for(uint64_t bytes) {
   const uint64_t waves = (bytes + kSlice - 1) / kSlice;
   return dim3((unsigned)((waves + kThreads / kWave - 1) / (kThreads / kWave)));
@@ -126,6 +186,30 @@ int pbe_ceiling_phase_copy(const void* src, void* dst, uint64_t bytes, void* str
   hipExtLaunchKernelGGL(phase_copy_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(kThreads), 0,
                         (hipStream_t)stream, (hipEvent_t)start, (hipEvent_t)stop, 0,
                         (const uint8_t*)src, (uint8_t*)dst, bytes);
+  return (int)hipGetLastError();
+}
+
+// Reads n_steps steps at the positions in `order` (device uint32 list),
+// steps_per_wave consecutive list entries per wave: 4 KiB contiguous steps
+// (reader_shape 0, base + order[s] * 4096) or the FP8 reader's 8 KiB blocks
+// read as two heads' half rows by wave pairs (reader_shape 1,
+// base + order[s] * 8192).
+int pbe_ceiling_read_steps(const void* base, const uint32_t* order, uint32_t n_steps,
+                           uint32_t steps_per_wave, int reader_shape, void* sink, void* stream,
+                           void* start, void* stop) {
+  if (!base || !order || !sink || n_steps == 0 || steps_per_wave == 0)
+    return (int)hipErrorInvalidValue;
+  uint32_t waves = (n_steps + steps_per_wave - 1) / steps_per_wave;
+  if (reader_shape) waves *= 2;
+  const dim3 grid((waves + 3) / 4);
+  if (reader_shape)
+    hipExtLaunchKernelGGL(stream_read_steps_kernel<true>, grid, dim3(kThreads), 0,
+                          (hipStream_t)stream, (hipEvent_t)start, (hipEvent_t)stop, 0,
+                          (const uint8_t*)base, order, n_steps, steps_per_wave, (u32x4*)sink);
+  else
+    hipExtLaunchKernelGGL(stream_read_steps_kernel<false>, grid, dim3(kThreads), 0,
+                          (hipStream_t)stream, (hipEvent_t)start, (hipEvent_t)stop, 0,
+                          (const uint8_t*)base, order, n_steps, steps_per_wave, (u32x4*)sink);
   return (int)hipGetLastError();
 }
 
