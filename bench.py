@@ -370,7 +370,7 @@ LEG_ORDER = ("plan", "sorted_destination", "contiguous", "read_only", "write_onl
 
 def ceiling_legs(torch, P, w, runs, kv, arena, scrub, rl, k: int) -> dict:
     """Launches each leg k times, in LEG_ORDER, each launch after the 1 GiB
-    scrub: the config-2 plan, the same sources into one contiguous ascending
+    scrub: the workload's plan (config 2 or 3), the same sources into one contiguous ascending
     destination, the same bytes as one contiguous run, and the copy's
     read-only and write-only halves. Under rocprofv3 --pmc the copy kernel's
     dispatches are told apart by this order (profiling.py legs)."""
@@ -382,6 +382,9 @@ def ceiling_legs(torch, P, w, runs, kv, arena, scrub, rl, k: int) -> dict:
     dbuf = torch.empty(nbytes, dtype=torch.uint8, device=arena.device)
     dview = P.view_of(dbuf.data_ptr(), nbytes)
     sview = P.view_of(arena.data_ptr(), arena.numel())
+    rl_own = rl is None
+    if rl_own:
+        rl = P.RunList.bf16(sview, sview, runs, kv)
     packed, at = [], 0
     for s_id, _d, n_pages in runs:
         packed.append((s_id, at * stride, n_pages))
@@ -414,8 +417,10 @@ def ceiling_legs(torch, P, w, runs, kv, arena, scrub, rl, k: int) -> dict:
         print(f"leg {name}: {k} launches", file=sys.stderr, flush=True)
     srl.close()
     crl.close()
-    return {"legs": list(LEG_ORDER), "launches_each": k, "bytes": nbytes,
-            "algorithmic_bytes": w.algorithmic_bytes()}
+    if rl_own:
+        rl.close()
+    return {"workload": w.name, "legs": list(LEG_ORDER), "launches_each": k, "bytes": nbytes,
+            "algorithmic_bytes": w.algorithmic_bytes(), "runs": len(runs)}
 
 
 def measure_extra_configs(torch, P, W, scrub, n: int):
@@ -822,6 +827,8 @@ def main() -> int:
     ap.add_argument("--ceiling-legs", type=int, default=0, metavar="K",
                     help="only launch the config-2 plan and its ceiling legs K times each, in a "
                          "fixed order (for rocprofv3 --pmc; summarised by profiling.py legs)")
+    ap.add_argument("--legs-config", type=int, default=2, choices=(2, 3),
+                    help="with --ceiling-legs: the workload whose plan the legs follow")
     ap.add_argument("--read-ceiling", action="store_true",
                     help="time the decode reader (FP8 and BF16) beside plain streaming reads of "
                          "the FP8 reader's bytes by short- and long-lived waves")
@@ -875,6 +882,16 @@ def main() -> int:
             out["calibration"] = calibration_copy(torch, P, scrub, args.steps, sp)
         print(json.dumps(out))
         return 0
+    if args.ceiling_legs:
+        w = W.CONFIGS[args.legs_config](0)
+        g = w.geometry
+        kv = P.shape(g.layers, g.kv_heads, g.head_dim, g.page_tokens)
+        arena = torch.empty(w.arena_bytes, dtype=torch.uint8, device=dev)
+        arena.view(torch.int32).random_()
+        scrub = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        runs = P.build_runs(w.src_ids, w.dst_ids, kv)
+        print(json.dumps(ceiling_legs(torch, P, w, runs, kv, arena, scrub, None, args.ceiling_legs)))
+        return 0
     w = W.config2(0)
     g = w.geometry
     kv = P.shape(g.layers, g.kv_heads, g.head_dim, g.page_tokens)
@@ -895,10 +912,6 @@ def main() -> int:
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
 
-    if args.ceiling_legs:
-        print(json.dumps(ceiling_legs(torch, P, w, runs, kv, arena, scrub, rl, args.ceiling_legs)))
-        rl.close()
-        return 0
 
     # correctness of this exact run: device result vs oracle on the same pool
     from oracle import oracle as O

@@ -138,31 +138,54 @@ def _dispatch_counters(root: str):
     return [(d, names[d], dict(per[d])) for d in sorted(per)]
 
 
-def legs(roots, launches: int, out: str, command: str) -> None:
+def _split_legs(items, launches: int, root: str):
+    """{leg: [items]} from [(kernel name, item)] in dispatch order, by LEGS."""
+    out = {}
+    for leg_i, (leg, kern) in enumerate(LEGS):
+        mine = [c for n, c in items if kern in n]
+        if kern == COPY_KERNEL:  # the last 3k copy dispatches, in leg order
+            mine = mine[-3 * launches:]
+            k0 = leg_i * launches
+            mine = mine[k0:k0 + launches]
+        else:
+            mine = mine[-launches:]
+        if len(mine) != launches:
+            raise RuntimeError(f"{root}: {leg}: {len(mine)} dispatches, expected {launches}")
+        out[leg] = mine
+    return out
+
+
+def legs(roots, launches: int, out: str, command: str, trace: str | None = None,
+         title: str = "config-2 handoff", alg_bytes: int = 0, copy_bytes: int = 0) -> None:
     """Per-leg medians of every counter in the given --pmc runs of
-    bench.py --ceiling-legs (one run per counter pass)."""
+    bench.py --ceiling-legs (one run per counter pass), and with `trace` (a
+    --kernel-trace run of the same command) each leg's kernel durations."""
     table = defaultdict(dict)  # leg -> counter -> median
     for root in roots:
         rows = _dispatch_counters(root)
-        for leg_i, (leg, kern) in enumerate(LEGS):
-            mine = [c for _, n, c in rows if kern in n]
-            if kern == COPY_KERNEL:  # the last 3k copy dispatches, in leg order
-                mine = mine[-3 * launches:]
-                k0 = leg_i * launches
-                mine = mine[k0:k0 + launches]
-            else:
-                mine = mine[-launches:]
-            if len(mine) != launches:
-                raise RuntimeError(f"{root}: {leg}: {len(mine)} dispatches, expected {launches}")
+        for leg, mine in _split_legs([(n, c) for _, n, c in rows], launches, root).items():
             for counter in mine[0]:
                 table[leg][counter] = statistics.median(m[counter] for m in mine)
+    durations = {}
+    if trace:
+        rows = sorted(_csv_rows(trace, "kernel_trace.csv"), key=lambda r: int(r["Dispatch_Id"]))
+        items = [(r["Kernel_Name"], int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) for r in rows]
+        durations = {leg: statistics.mean(v) / 1e3 for leg, v in _split_legs(items, launches, trace).items()}
     counters = sorted({c for v in table.values() for c in v})
-    w = max(len(c) for c in counters)
-    lines = ["# rocprofv3 --pmc summary: DRAM-side counters of the config-2 handoff and its "
+    w = max([len(c) for c in counters] + [26])
+    lines = [f"# rocprofv3 --pmc summary: DRAM-side counters of the {title} and its "
              "ceiling legs", f"command: {command}",
              f"medians over {launches} launches per leg, each after a 1 GiB scrub; "
              "values summed over the counter's instances", "",
              f"{'counter':<{w}} " + " ".join(f"{leg:>19}" for leg, _ in LEGS)]
+    if durations:
+        lines.append(f"{'kernel avg_us (trace run)':<{w}} " +
+                     " ".join(f"{durations[leg]:>19.2f}" for leg, _ in LEGS))
+        if alg_bytes and copy_bytes:
+            per = {"plan": alg_bytes, "sorted_destination": alg_bytes, "contiguous": alg_bytes,
+                   "read_only": copy_bytes, "write_only": copy_bytes}
+            lines.append(f"{'GB/s (algorithmic)':<{w}} " + " ".join(
+                f"{per[leg] / (durations[leg] * 1e-6) / 1e9:>19.1f}" for leg, _ in LEGS))
     for c in counters:
         lines.append(f"{c:<{w}} " + " ".join(f"{table[leg].get(c, float('nan')):>19.0f}"
                                               for leg, _ in LEGS))
@@ -244,6 +267,10 @@ def main() -> None:
     q.add_argument("--launches", type=int, required=True)
     q.add_argument("--out", required=True)
     q.add_argument("--command", required=True)
+    q.add_argument("--trace", default=None, help="--kernel-trace run of the same command")
+    q.add_argument("--title", default="config-2 handoff")
+    q.add_argument("--alg-bytes", type=int, default=0)
+    q.add_argument("--copy-bytes", type=int, default=0)
     mk = sub.add_parser("markers")
     mk.add_argument("root")
     mk.add_argument("--out", required=True)
@@ -253,7 +280,7 @@ def main() -> None:
         markers(a.root, a.out, a.command)
         return
     if a.cmd == "legs":
-        legs(a.roots, a.launches, a.out, a.command)
+        legs(a.roots, a.launches, a.out, a.command, a.trace, a.title, a.alg_bytes, a.copy_bytes)
         return
     if a.cmd == "stats":
         labels = {}
