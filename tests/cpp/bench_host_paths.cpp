@@ -110,6 +110,7 @@ int main() {
   }
   // ---- the reference's call order over KVCacheManager and a shared arena
   std::vector<double> reserve_us, e2e_us, free_us, busy_us, copy_us;
+  std::vector<double> step_request_us, step_reserve_us, step_launch_us, step_wait_us, step_commit_us;
   {
     const uint64_t arena_bytes = 2000 * page;
     pbe_arena* arena = nullptr;
@@ -184,6 +185,46 @@ int main() {
         pbe_stream_synchronize(0, ds);
         dg->collect();
       }
+      // The same steps as CopySharedKVToDecode, through the same public calls,
+      // with a timer between them (cold: a 1 GiB copy first).
+      for (int it = 0; it < kIters; ++it) {
+        pbe_copy_op flush{reinterpret_cast<uint64_t>(big_a), reinterpret_cast<uint64_t>(big_b), big};
+        CHECK_OR(pbe_copy_ops(&flush, 1, 0, ds) == PBE_OK, 23);
+        CHECK_OR(pbe_stream_synchronize(0, ds) == PBE_OK, 24);
+        double t0 = now_us();
+        serving::DecodeKVReservationRequest req;
+        req.client_request_id = r.client_request_id;
+        req.handoff_id = r.handoff_id;
+        req.prompt_tokens = static_cast<int32_t>(r.prompt_tokens.size());
+        req.computed_tokens = r.computed_tokens;
+        req.first_token = r.first_token;
+        req.src_pool = r.src_pool;
+        for (const auto& layer : r.layers) req.src_block_ids_per_layer.push_back(layer.src_block_ids);
+        double t1 = now_us();
+        serving::DecodeKVReservationManager reservations(d_kv.get(), pool_desc);
+        serving::DecodeKVReservation res;
+        serving::KVBlockManifest manifest;
+        CHECK_OR(static_cast<bool>(reservations.reserve(req, &res, &manifest)), 25);
+        double t2 = now_us();
+        const pbe_kv_shape shape{kLayers, kHeads, kDim, 16};
+        uint64_t copied = 0;
+        CHECK_OR(pbe_copy_shared_kv(&view, manifest.layer_mappings[0].src_block_ids.data(),
+                                    manifest.layer_mappings[0].dst_block_ids.data(), kPages, &shape, 0,
+                                    ds, &copied) == PBE_OK, 26);
+        double t3 = now_us();
+        CHECK_OR(pbe_stream_synchronize(0, ds) == PBE_OK, 27);
+        double t4 = now_us();
+        CHECK_OR(d_kv->commit_kv(res.decode_request_id, r.computed_tokens), 28);
+        double t5 = now_us();
+        step_request_us.push_back(t1 - t0);
+        step_reserve_us.push_back(t2 - t1);
+        step_launch_us.push_back(t3 - t2);
+        step_wait_us.push_back(t4 - t3);
+        step_commit_us.push_back(t5 - t4);
+        d_kv->free_request(res.decode_request_id);
+        pbe_stream_synchronize(0, ds);
+        dg->collect();
+      }
     }
     (void)hipFree(big_a);
     (void)hipFree(big_b);
@@ -197,8 +238,12 @@ int main() {
       "\"copy_ops_call\": %.1f, \"connector_submit_drain\": %.1f}, "
       "\"reference_call_order_us\": {\"reserve_28_layers\": %.1f, \"end_to_end\": %.1f, "
       "\"copy_and_sync_alone\": %.1f, \"free_request\": %.1f, "
-      "\"reserve_under_pending_fences\": %.1f}}\n",
+      "\"reserve_under_pending_fences\": %.1f, \"steps\": {\"request_copies\": %.1f, "
+      "\"reserve_and_manifest\": %.1f, \"pbe_copy_shared_kv_call\": %.1f, \"stream_wait\": %.1f, "
+      "\"commit_kv\": %.1f}}}\n",
       kPages, kLayers, kIters, median(bind_us), median(ops_us), median(call_us), median(conn_us),
-      median(reserve_us), median(e2e_us), median(copy_us), median(free_us), median(busy_us));
+      median(reserve_us), median(e2e_us), median(copy_us), median(free_us), median(busy_us),
+      median(step_request_us), median(step_reserve_us), median(step_launch_us), median(step_wait_us),
+      median(step_commit_us));
   return 0;
 }
