@@ -3,6 +3,8 @@
 // test/test_cache_transfer_plan.cpp:130-467, test/test_page_migration.cpp:5-25,
 // test/test_serving/test_pd_handoff.cpp:284-296.
 #include <algorithm>
+#include <array>
+#include <map>
 #include <cstring>
 #include <memory>
 #include <numeric>
@@ -864,6 +866,101 @@ TEST_CASE("page group: retiring layer 0 first rolls back unconsumed reservations
   g.group->retire(1, id);
   g.group->retire(0, id);               // drops the layer-2 reservation, page retires
   CHECK_THROWS_AS(g.group->allocate(2), std::logic_error);
+  CHECK_EQ(g.owner->lease_count(), 0u);
+}
+
+TEST_CASE("page group: randomized reservations, rollbacks and retires against a model (long log)") {
+  // 3 layers, 3000 pages: layer 0 may run far ahead of layers 1 and 2, so
+  // the reservation log grows past its trimming threshold; layer-0 retires
+  // roll back pages the later layers never took, in any position of the log.
+  // The model: per layer, the FIFO of page ids layer 0 reserved and that
+  // layer has not taken; per page, which layers hold it.
+  Group g(3000, 3000 * Group::kPage);
+  std::mt19937 rng(2024);
+  std::vector<std::vector<int>> pending(3);  // layers 1, 2
+  std::map<int, std::array<bool, 3>> held;   // page id -> layers holding it
+  auto live_in = [&](int layer) {
+    std::vector<int> ids;
+    for (const auto& e : held)
+      if (e.second[layer]) ids.push_back(e.first);
+    return ids;
+  };
+  auto erase_pending = [&](int layer, int id) {
+    auto& q = pending[layer];
+    auto it = std::find(q.begin(), q.end(), id);
+    if (it == q.end()) return false;
+    q.erase(it);
+    return true;
+  };
+  int max_log = 0;
+  for (int step = 0; step < 12000; ++step) {
+    const int phase = step < 4000 ? 0 : 1;  // first let layer 0 run ahead
+    const int op = static_cast<int>(rng() % 10);
+    if (op < (phase == 0 ? 6 : 3)) {
+      // layer 0 takes 1..8 pages
+      const int n = 1 + static_cast<int>(rng() % 8);
+      std::vector<int32_t> got;
+      // arena full part-way: the pages handed out before stay reserved
+      if (!g.group->allocate_many(0, n, &got)) CHECK(got.size() < static_cast<size_t>(n));
+      else REQUIRE(got.size() == static_cast<size_t>(n));
+      for (int id : got) {
+        CHECK(!held.count(id));  // never a page some layer still holds
+        held[id] = {true, true, true};
+        pending[1].push_back(id);
+        pending[2].push_back(id);
+      }
+      max_log = std::max<int>(max_log, static_cast<int>(pending[2].size()));
+    } else if (op < (phase == 0 ? 8 : 6)) {
+      // a later layer takes the next k of layer 0's reservations, in order
+      const int layer = 1 + static_cast<int>(rng() % 2);
+      const int k = static_cast<int>(rng() % (phase == 0 ? 3 : 12));
+      auto& q = pending[layer];
+      if (static_cast<size_t>(k) > q.size()) {
+        std::vector<int32_t> got;
+        CHECK_THROWS_AS(g.group->allocate_many(layer, k, &got), std::logic_error);
+        continue;
+      }
+      std::vector<int32_t> got;
+      if (k == 1) got.push_back(g.group->allocate(layer));
+      else CHECK(g.group->allocate_many(layer, k, &got));
+      REQUIRE(got.size() == static_cast<size_t>(k));
+      for (int i = 0; i < k; ++i) CHECK_EQ(got[i], q[i]);
+      q.erase(q.begin(), q.begin() + k);
+    } else {
+      // retire one page from one layer that holds it (taken, not pending)
+      const int layer = static_cast<int>(rng() % 3);
+      std::vector<int> ids = live_in(layer);
+      std::vector<int> taken;
+      for (int id : ids)
+        if (layer == 0 || std::find(pending[layer].begin(), pending[layer].end(), id) == pending[layer].end())
+          taken.push_back(id);
+      if (taken.empty()) continue;
+      const int id = taken[rng() % taken.size()];
+      g.group->retire(layer, id);
+      held[id][layer] = false;
+      if (layer == 0)  // reservations the later layers never took go with it
+        for (int l = 1; l < 3; ++l)
+          if (erase_pending(l, id)) held[id][l] = false;
+      if (!held[id][0] && !held[id][1] && !held[id][2]) held.erase(id);
+      CHECK_THROWS_AS(g.group->retire(layer, id), std::logic_error);  // no double retire
+    }
+    // free counts follow the model: later layers can take exactly their pending pages
+    for (int l = 1; l < 3; ++l) {
+      const int room = g.group->free_blocks(l) - g.group->free_blocks(0);
+      CHECK_EQ(room, static_cast<int>(pending[l].size()));
+    }
+  }
+  CHECK(max_log > 1024);  // the log's trimming ran
+  // drain: later layers take what is pending, then every layer retires
+  for (int l = 1; l < 3; ++l) {
+    std::vector<int32_t> got;
+    CHECK(g.group->allocate_many(l, static_cast<int>(pending[l].size()), &got));
+    CHECK(got == std::vector<int32_t>(pending[l].begin(), pending[l].end()));
+  }
+  for (const auto& e : held)
+    for (int l = 2; l >= 0; --l)
+      if (e.second[l]) g.group->retire(l, e.first);
+  CHECK_EQ(g.group->leased_bytes(), 0u);
   CHECK_EQ(g.owner->lease_count(), 0u);
 }
 
