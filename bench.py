@@ -213,6 +213,25 @@ def _timed(torch, stream, scrub, fn, n, scrub_fn=None):
     return float(np.mean(ts)), float(np.min(ts))
 
 
+def _kernel_timed(torch, scrub, launch, n):
+    """Mean/min kernel duration (ms) of n cold launches (1 GiB scrub before
+    each), between fence-free events the runtime stamps at the kernel's own
+    start and end: launch(start_event, stop_event) must launch through
+    hipExtLaunchKernel (RunList.copy_timed, the ceiling kernels). The same
+    method as the headline, so the legs compare like for like."""
+    import numpy as np
+    ev = TimingEvents(2)
+    ts = []
+    for i in range(n + 2):
+        scrub.fill_(i & 0xff)
+        launch(ev.handle(0), ev.handle(1))
+        torch.cuda.synchronize()
+        if i >= 2:
+            ts.append(ev.elapsed_ms(0, 1))
+    ev.close()
+    return float(np.mean(ts)), float(np.min(ts))
+
+
 def gpu_reference_pattern(torch, stream, scrub, base, runs, g, alg, n, scrub_each):
     """Times the reference's copy loop as the reference issues it, on this GPU:
     one hipMemcpyAsync (device to device) per coalesced run, on one stream,
@@ -301,7 +320,7 @@ def measure_ceilings(torch, P, w, runs, kv, arena, scrub, alg: int, n: int) -> d
         packed.append((s_id, at * stride, k))
         at += k
     with P.RunList.bf16(sview, dview, packed, kv) as srl:
-        ms = _timed(torch, stream, scrub, lambda: srl.copy(sp), n)
+        ms = _kernel_timed(torch, scrub, lambda a, b: srl.copy_timed(sp, a, b), n)
     out["sorted_destination"] = {
         "what": "same kernel, the plan's source runs, destinations packed into one ascending "
                 "contiguous region", "runs": len(packed),
@@ -318,7 +337,9 @@ def measure_ceilings(torch, P, w, runs, kv, arena, scrub, alg: int, n: int) -> d
     sums = scrub.view(torch.int64)
     ms_r = _timed(torch, stream, scrub, vendor, n, scrub_fn=lambda i: sums.sum())
     out["vendor_memcpy"] = {
-        "what": "one hipMemcpyAsync device-to-device of the same bytes, contiguous",
+        "what": "one hipMemcpyAsync device-to-device of the same bytes, contiguous; timed "
+                "between events recorded on the stream around the call (the vendor copy "
+                "cannot be bracketed at its kernel, so this includes a launch gap of ~1 us)",
         "us_mean": round(ms[0] * 1e3, 2), "gbps": round(alg / (ms[0] * 1e-3) / 1e9, 1),
         "us_mean_after_read_scrub": round(ms_r[0] * 1e3, 2),
         "gbps_after_read_scrub": round(alg / (ms_r[0] * 1e-3) / 1e9, 1)}
@@ -331,25 +352,18 @@ def measure_ceilings(torch, P, w, runs, kv, arena, scrub, alg: int, n: int) -> d
         cl.pbe_ceiling_write.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, C.c_void_p,
                                          C.c_void_p, C.c_void_p]
         sink = torch.empty(1024, dtype=torch.uint8, device=arena.device)
-        ev = TimingEvents(2)
-
         def leg(fn):
-            ts = []
-            for i in range(n + 2):
-                scrub.fill_(i & 0xff)
-                if fn(ev.handle(0), ev.handle(1)) != 0:
-                    raise RuntimeError("ceiling kernel launch failed")
-                torch.cuda.synchronize()
-                if i >= 2:
-                    ts.append(ev.elapsed_ms(0, 1))
-            return float(np.mean(ts))
+            return _kernel_timed(torch, scrub, fn, n)[0]
         r_ms = leg(lambda a, b: cl.pbe_ceiling_read(arena.data_ptr(), nbytes, sink.data_ptr(), sp, a, b))
         w_ms = leg(lambda a, b: cl.pbe_ceiling_write(dbuf.data_ptr(), nbytes, 7, sp, a, b))
         cl.pbe_ceiling_phase_copy.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p,
                                               C.c_void_p, C.c_void_p]
         p_ms = leg(lambda a, b: cl.pbe_ceiling_phase_copy(arena.data_ptr(), dbuf.data_ptr(), nbytes,
                                                           sp, a, b))
-        ev.close()
+        cl.pbe_ceiling_slice_copy.argtypes = [C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p,
+                                              C.c_void_p, C.c_void_p]
+        t_ms = leg(lambda a, b: cl.pbe_ceiling_slice_copy(arena.data_ptr(), dbuf.data_ptr(), nbytes,
+                                                          sp, a, b))
         out["read_only"] = {"what": "the copy kernel's loads alone over the same bytes",
                             "bytes": nbytes, "us_mean": round(r_ms * 1e3, 2),
                             "gbps": round(nbytes / (r_ms * 1e-3) / 1e9, 1)}
@@ -357,6 +371,10 @@ def measure_ceilings(torch, P, w, runs, kv, arena, scrub, alg: int, n: int) -> d
                              "bytes": nbytes, "us_mean": round(w_ms * 1e3, 2),
                              "gbps": round(nbytes / (w_ms * 1e-3) / 1e9, 1)}
         out["read_then_write_us"] = round((r_ms + w_ms) * 1e3, 2)
+        out["slice_copy_no_run_list"] = {
+            "what": "the copy kernel's slices and cache policies over one contiguous span, "
+                    "no run list to search", "us_mean": round(t_ms * 1e3, 2),
+            "gbps": round(alg / (t_ms * 1e-3) / 1e9, 1)}
         out["register_staged_copy"] = {
             "what": "contiguous copy of the same bytes, each wave loading 32 KiB into registers "
                     "before storing it (long read-only then write-only bursts)",
@@ -988,7 +1006,8 @@ def main() -> int:
     stride = 2 * g.layers
     n_arena = w.arena_bytes // g.page_bytes()
     with P.RunList.bf16(view, view, [(0, stride * (n_arena - w.pages), w.pages)], kv) as crl:
-        c_ms = _timed(torch, stream, scrub, lambda: crl.copy(sp), max(10, args.steps // 4))
+        c_ms = _kernel_timed(torch, scrub, lambda a, b: crl.copy_timed(sp, a, b),
+                             max(10, args.steps // 4))
     contiguous = {"what": "same kernel, same bytes, one contiguous run (pages 0.. -> end of arena)",
                   "us_mean": round(c_ms[0] * 1e3, 2),
                   "gbps": round(alg / (c_ms[0] * 1e-3) / 1e9, 1)}

@@ -57,6 +57,30 @@ __global__ __launch_bounds__(kThreads) void stream_write_kernel(uint8_t* p, uint
     __builtin_amdgcn_raw_buffer_store_b128(v, r, (u * kWave + lane) * 16u, 0, kStorePolicy);
 }
 
+// The copy kernel's geometry and cache policies over one contiguous span with
+// no run list: wave w copies slice w. The difference to the product kernel on
+// one contiguous run is the cost of finding the run.
+__global__ __launch_bounds__(kThreads) void slice_copy_kernel(const uint8_t* src, uint8_t* dst,
+                                                              uint64_t bytes) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint64_t s = (uint64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
+  const uint64_t off = s * kSlice;
+  if (off >= bytes) return;
+  const uint64_t left = bytes - off;
+  const uint32_t n = left >= kSlice ? kSlice : (uint32_t)left;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(src + off), (short)0, n, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rd =
+      __builtin_amdgcn_make_buffer_rsrc(dst + off, (short)0, n, 0x00020000);
+  u32x4 v[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u)
+    v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, (u * kWave + lane) * 16u, 0, kLoadPolicy);
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u)
+    __builtin_amdgcn_raw_buffer_store_b128(v[u], rd, (u * kWave + lane) * 16u, 0, kStorePolicy);
+}
+
 // Register-staged copy: each wave loads a 32 KiB chunk into VGPRs (32
 // vectors per lane, two waves per SIMD), then stores all of it. Tests whether
 // long read-only then write-only bursts per wave beat the copy kernel's
@@ -116,15 +140,17 @@ __global__ __launch_bounds__(kThreads) void stream_read_steps_kernel(
                                          : lane * 16u;
   u32x4 r[kReadDepth][4];
   u32x4 acc = {0, 0, 0, 0};
+  // readfirstlane returns int: list entries are widened through uint32_t so
+  // that none can sign-extend into an address
   auto load = [&](uint32_t s, u32x4* d) {
     if constexpr (kReaderShape) {
-      const uint8_t* blk = base + (uint64_t)__builtin_amdgcn_readfirstlane(order[s]) * 8192u;
+      const uint8_t* blk = base + (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(order[s]) * 8192u;
 #pragma unroll
       for (int u = 0; u < 4; ++u)  // K rows 0-7, 8-15, then V rows 0-7, 8-15
         d[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
             blk + (u / 2) * 4096u + (u % 2) * 2048u + lane_off));
     } else {
-      const uint8_t* st = base + (uint64_t)__builtin_amdgcn_readfirstlane(order[s]) * 4096u;
+      const uint8_t* st = base + (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(order[s]) * 4096u;
 #pragma unroll
       for (int u = 0; u < 4; ++u)
         d[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(st + u * 1024u + lane_off));
@@ -174,6 +200,17 @@ int pbe_ceiling_write(void* p, uint64_t bytes, uint32_t seed, void* stream, void
   hipExtLaunchKernelGGL(stream_write_kernel, grid_for(bytes), dim3(kThreads), 0,
                         (hipStream_t)stream, (hipEvent_t)start, (hipEvent_t)stop, 0,
                         (uint8_t*)p, bytes, seed);
+  return (int)hipGetLastError();
+}
+
+// Copies `bytes` from src to dst (contiguous, non-overlapping) with the copy
+// kernel's slices and no run list.
+int pbe_ceiling_slice_copy(const void* src, void* dst, uint64_t bytes, void* stream, void* start,
+                           void* stop) {
+  if (!src || !dst || bytes == 0 || (bytes >> 44)) return (int)hipErrorInvalidValue;
+  hipExtLaunchKernelGGL(slice_copy_kernel, grid_for(bytes), dim3(kThreads), 0, (hipStream_t)stream,
+                        (hipEvent_t)start, (hipEvent_t)stop, 0, (const uint8_t*)src, (uint8_t*)dst,
+                        bytes);
   return (int)hipGetLastError();
 }
 
