@@ -850,6 +850,10 @@ def main() -> int:
     ap.add_argument("--read-ceiling", action="store_true",
                     help="time the decode reader (FP8 and BF16) beside plain streaming reads of "
                          "the FP8 reader's bytes by short- and long-lived waves")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="time only the config-2 headline kernel (no ceiling legs, no contiguous "
+                         "leg, no reference-pattern or host-path legs): for rocprofv3 runs whose "
+                         "per-kernel averages must be the headline kernel's alone")
     ap.add_argument("--calibrate", action="store_true",
                     help="also launch a plain contiguous copy of 256 MiB with the same kernel "
                          "(rocprofv3 --pmc byte-count calibration)")
@@ -1003,19 +1007,21 @@ def main() -> int:
 
     # the same bytes as one contiguous run, same kernel: the difference to
     # the headline is the cost of the plan's page placement in HBM
-    stride = 2 * g.layers
-    n_arena = w.arena_bytes // g.page_bytes()
-    with P.RunList.bf16(view, view, [(0, stride * (n_arena - w.pages), w.pages)], kv) as crl:
-        c_ms = _kernel_timed(torch, scrub, lambda a, b: crl.copy_timed(sp, a, b),
-                             max(10, args.steps // 4))
-    contiguous = {"what": "same kernel, same bytes, one contiguous run (pages 0.. -> end of arena)",
-                  "us_mean": round(c_ms[0] * 1e3, 2),
-                  "gbps": round(alg / (c_ms[0] * 1e-3) / 1e9, 1)}
-
-    ceilings = measure_ceilings(torch, P, w, runs, kv, arena, scrub, alg, max(10, args.steps // 4))
-    ceilings["contiguous_same_bytes"] = contiguous
-    best = min(ceilings["sorted_destination"]["us_mean"], ceilings["vendor_memcpy"]["us_mean"])
-    ceilings["headline_over_best_of_sorted_and_vendor"] = round(mean_ms * 1e3 / best, 4)
+    contiguous = ceilings = None
+    if not args.headline_only:
+        stride = 2 * g.layers
+        n_arena = w.arena_bytes // g.page_bytes()
+        with P.RunList.bf16(view, view, [(0, stride * (n_arena - w.pages), w.pages)], kv) as crl:
+            c_ms = _kernel_timed(torch, scrub, lambda a, b: crl.copy_timed(sp, a, b),
+                                 max(10, args.steps // 4))
+        contiguous = {"what": "same kernel, same bytes, one contiguous run (pages 0.. -> end of "
+                              "arena)", "us_mean": round(c_ms[0] * 1e3, 2),
+                      "gbps": round(alg / (c_ms[0] * 1e-3) / 1e9, 1)}
+        ceilings = measure_ceilings(torch, P, w, runs, kv, arena, scrub, alg,
+                                    max(10, args.steps // 4))
+        ceilings["contiguous_same_bytes"] = contiguous
+        best = min(ceilings["sorted_destination"]["us_mean"], ceilings["vendor_memcpy"]["us_mean"])
+        ceilings["headline_over_best_of_sorted_and_vendor"] = round(mean_ms * 1e3 / best, 4)
 
     calib = calibration_copy(torch, P, scrub, args.steps, sp) if args.calibrate else None
 
@@ -1027,7 +1033,7 @@ def main() -> int:
     # (serving::CopySharedKVToDecode: reserve over 28 layers, manifest, the
     # one-launch copy, stream sync, commit_kv) at config-2 size, timed by the
     # C++ host-path runner in a child process on this GPU
-    ref_order = host_paths_timing()
+    ref_order = None if args.headline_only else host_paths_timing()
 
     cpu = None
     if not args.no_cpu:
@@ -1074,8 +1080,9 @@ def main() -> int:
         "grid_threads": int(info.slices) * 64,
     }
     line["gpu_reference_pattern"] = refpat
-    line["contiguous_same_bytes"] = contiguous
-    line["ceilings"] = ceilings
+    if contiguous:
+        line["contiguous_same_bytes"] = contiguous
+        line["ceilings"] = ceilings
     if ref_order:
         line["reference_call_order_us"] = dict(
             ref_order["reference_call_order_us"],

@@ -4,6 +4,7 @@
     python paged-batch-engine_amd/profiling.py pmc <fetch_dir> <write_dir> --out FILE --command "..."
     python paged-batch-engine_amd/profiling.py legs <pmc_dir>... --launches K --out FILE --command "..."
     python paged-batch-engine_amd/profiling.py markers <trace_dir> --out FILE --command "..."
+    python paged-batch-engine_amd/profiling.py req <pmc_dir> --grid G [--grid G2] --out FILE --command "..."
 
 `stats` reads the kernel trace of a `rocprofv3 --kernel-trace --stats
 --output-format csv` run and writes per-kernel call counts and durations.
@@ -243,6 +244,32 @@ def markers(root: str, out: str, command: str) -> None:
     print(text)
 
 
+def req(root: str, grids, out: str, command: str, kernel: str = COPY_KERNEL) -> None:
+    """Request counts at the memory interface per dispatch (a --pmc run of
+    TCC_EA0_RDREQ / _32B and TCC_EA0_WRREQ / _64B): medians per grid, and the
+    bytes per read request those give for the grid's known traffic."""
+    rows = [(n, c) for _, n, c in _dispatch_counters(root) if kernel in n]
+    lines = [f"# rocprofv3 --pmc summary: memory-interface request counts of {kernel}",
+             f"command: {command}", ""]
+    by_grid = defaultdict(list)
+    for r in _csv_rows(root, "counter_collection.csv"):
+        if kernel in r["Kernel_Name"]:
+            by_grid[int(r.get("Grid_Size", 0) or 0)].append(int(r["Dispatch_Id"]))
+    per = {d: c for d, _, c in _dispatch_counters(root)}
+    for g in grids:
+        ds = sorted(set(by_grid.get(g, [])))
+        if not ds:
+            raise RuntimeError(f"no {kernel} dispatch with grid {g}")
+        med = {k: statistics.median(per[d][k] for d in ds) for k in per[ds[0]]}
+        lines.append(f"grid {g} ({len(ds)} dispatches): " + ", ".join(
+            f"{k} {v:.0f}" for k, v in sorted(med.items())))
+    del rows
+    text = "\n".join(lines) + "\n"
+    with open(out, "w") as fh:
+        fh.write(text)
+    print(text)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -271,11 +298,19 @@ def main() -> None:
     q.add_argument("--title", default="config-2 handoff")
     q.add_argument("--alg-bytes", type=int, default=0)
     q.add_argument("--copy-bytes", type=int, default=0)
+    rq = sub.add_parser("req")
+    rq.add_argument("root")
+    rq.add_argument("--grid", type=int, action="append", required=True)
+    rq.add_argument("--out", required=True)
+    rq.add_argument("--command", required=True)
     mk = sub.add_parser("markers")
     mk.add_argument("root")
     mk.add_argument("--out", required=True)
     mk.add_argument("--command", required=True)
     a = ap.parse_args()
+    if a.cmd == "req":
+        req(a.root, a.grid, a.out, a.command)
+        return
     if a.cmd == "markers":
         markers(a.root, a.out, a.command)
         return
