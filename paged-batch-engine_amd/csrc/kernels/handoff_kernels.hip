@@ -82,7 +82,11 @@ __device__ __forceinline__ void copy_slice(uint64_t src, uint64_t dst, uint64_t 
 __device__ __forceinline__ void copy_runs_body(const DevRun* __restrict__ runs, uint32_t n_runs,
                                                uint32_t total_slices, uint64_t page_bytes) {
   const uint32_t lane = threadIdx.x % kWave;
-  const uint32_t s = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+  // The slice index is wave-uniform; saying so keeps the run, the addresses
+  // and the buffer resources in SGPRs (a resource the compiler cannot prove
+  // uniform is rebuilt per lane in a readfirstlane loop around every load
+  // and store).
+  const uint32_t s = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + threadIdx.x / kWave);
   if (s >= total_slices) return;
   const uint32_t r = find_run(runs, 0, n_runs, s, lane);
   const DevRun& run = runs[r];
