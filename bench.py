@@ -302,7 +302,10 @@ def measure_ceilings(torch, P, w, runs, kv, arena, scrub, alg: int, n: int) -> d
                           beat HBM's rate for either stream at this size;
       register_staged_copy a contiguous copy whose waves each read 32 KiB before
                           writing it, the test of whether separating the two
-                          streams in time pays."""
+                          streams in time pays;
+      write_side          a cache-resident source written to the plan's scattered
+                          destinations and to a contiguous region: the write path
+                          alone (C2's runs are at most 5 pages, the source's size)."""
     import ctypes as C
     import numpy as np
     g = w.geometry
@@ -325,6 +328,22 @@ def measure_ceilings(torch, P, w, runs, kv, arena, scrub, alg: int, n: int) -> d
         "what": "same kernel, the plan's source runs, destinations packed into one ascending "
                 "contiguous region", "runs": len(packed),
         "us_mean": round(ms[0] * 1e3, 2), "gbps": round(alg / (ms[0] * 1e-3) / 1e9, 1)}
+    # the write side alone: a 5-page source that stays cache-resident after
+    # its first read, copied into the plan's destinations and into one
+    # contiguous region (reads nearly free, so the difference is what the
+    # scattered destinations cost the writes)
+    hot = torch.empty(5 * g.page_bytes(), dtype=torch.uint8, device=arena.device)
+    hview = P.view_of(hot.data_ptr(), hot.numel())
+    hot_runs = [(0, d, k) for _s, d, k in runs]
+    with P.RunList.bf16(hview, sview, hot_runs, kv) as hrl:
+        ms_scat = _kernel_timed(torch, scrub, lambda a, b: hrl.copy_timed(sp, a, b), n)
+    with P.RunList.bf16(hview, dview, [(0, pk[1], pk[2]) for pk in packed], kv) as hrl:
+        ms_cont = _kernel_timed(torch, scrub, lambda a, b: hrl.copy_timed(sp, a, b), n)
+    del hot
+    out["write_side"] = {
+        "what": "a cache-resident 5-page source copied to the plan's destinations / to one "
+                "contiguous region (the plan's run lengths): the write path alone",
+        "scattered_us": round(ms_scat[0] * 1e3, 2), "contiguous_us": round(ms_cont[0] * 1e3, 2)}
     # (a) vendor copy of the same bytes
     hip = C.CDLL("libamdhip64.so.7")
     hip.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
