@@ -24,6 +24,10 @@ namespace {
 struct Resolved {
   std::vector<pbe::DevRun> runs;
   pbe_runlist_info info{};
+  // The first run's source when the sources form one region in run order and
+  // every run holds whole slices (the copy kernel then reads slice s at
+  // linear_src + s * slice without looking the run up first); else 0.
+  uint64_t linear_src = 0;
 };
 
 // Builds device run entries for either kernel. src pages are src_page_bytes
@@ -76,6 +80,10 @@ int resolve_runs(const pbe_arena_view& src, const pbe_arena_view& dst, uint64_t 
     return fail(PBE_ERR_INVALID, "run list writes a byte twice or overwrites its own source");
   out->info.runs = n_runs;
   out->info.slices = slices;
+  bool linear = src_page % slice == 0;
+  for (size_t i = 1; linear && i < src_spans.size(); ++i)
+    linear = src_spans[i].first == src_spans[i - 1].second;
+  out->linear_src = linear ? out->runs.front().src : 0;
   return PBE_OK;
 }
 
@@ -98,6 +106,7 @@ int upload_runlist(Resolved& res, int device, bool fp8, bool has_scales, uint64_
   list->n_runs = (uint32_t)res.runs.size();
   list->total_slices = (uint32_t)res.info.slices;
   list->page_bytes = page_bytes;
+  list->linear_src = res.linear_src;
   list->info = res.info;
   list->kv = kv;
   *out = list;
@@ -183,8 +192,8 @@ int pbe_handoff_copy_timed(const pbe_runlist* list, void* stream, void* start_ev
   if (list->fp8) return fail(PBE_ERR_INVALID, "FP8 run list passed to the BF16 copy");
   PBE_DEVICE_SCOPE(list->device);
   const pbe::LaunchEvents ev{static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event)};
-  PBE_HIP(pbe::launch_copy_runs(list->runs, list->n_runs, list->total_slices, list->page_bytes, ev,
-                                static_cast<hipStream_t>(stream)));
+  PBE_HIP(pbe::launch_copy_runs(list->runs, list->n_runs, list->total_slices, list->page_bytes,
+                                list->linear_src, ev, static_cast<hipStream_t>(stream)));
   return PBE_OK;
 }
 
@@ -337,6 +346,7 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
     list.n_runs = (uint32_t)n_runs;
     list.total_slices = (uint32_t)res.info.slices;
     list.page_bytes = 2ull * shape->layers * half;
+    list.linear_src = res.linear_src;
     std::memcpy(list.runs, res.runs.data(), res.runs.size() * sizeof(pbe::DevRun));
     PBE_HIP(pbe::launch_copy_runs_kernarg(list, s));
     if (copied) *copied = res.info.src_bytes;
@@ -352,7 +362,7 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
   if (rc != PBE_OK) return rc;
   PBE_HIP(pbe::launch_copy_runs(static_cast<const pbe::DevRun*>(dev), (uint32_t)n_runs,
                                 (uint32_t)res.info.slices, 2ull * shape->layers * half,
-                                pbe::LaunchEvents{}, s));
+                                res.linear_src, pbe::LaunchEvents{}, s));
   rc = stage_done(*slot, s);
   if (rc != PBE_OK) return rc;
   if (copied) *copied = res.info.src_bytes;
@@ -447,7 +457,7 @@ int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream
     rc = stage(st, runs.data(), runs.size() * sizeof(pbe::DevRun), s, &slot, &dev);
     if (rc != PBE_OK) return rc;
     PBE_HIP(pbe::launch_copy_runs(static_cast<const pbe::DevRun*>(dev), (uint32_t)runs.size(),
-                                  (uint32_t)slices, 16, pbe::LaunchEvents{}, s));
+                                  (uint32_t)slices, 16, 0, pbe::LaunchEvents{}, s));
     return stage_done(*slot, s);
   }
   // Otherwise: split ops so that every wave moves at most kOpPieceBytes.

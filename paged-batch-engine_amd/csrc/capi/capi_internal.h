@@ -151,6 +151,7 @@ struct pbe_runlist {
   uint32_t n_runs = 0;
   uint32_t total_slices = 0;
   uint64_t page_bytes = 0;      // source bytes per page
+  uint64_t linear_src = 0;      // see pbe::launch_copy_runs
   pbe_runlist_info info{};
   pbe_kv_shape kv{};
 };

@@ -45,6 +45,7 @@ struct KernargRunList {
   uint32_t n_runs;
   uint32_t total_slices;
   uint64_t page_bytes;
+  uint64_t linear_src;  // see launch_copy_runs
   DevRun runs[kKernargRuns];
 };
 static_assert(sizeof(KernargRunList) <= 4096 - 256, "kernel arguments are limited to 4 KiB");
@@ -52,8 +53,13 @@ static_assert(sizeof(KernargRunList) <= 4096 - 256, "kernel arguments are limite
 // One slice of kCopySliceBytes per wave, 256-thread workgroups.
 hipError_t launch_copy_runs_kernarg(const KernargRunList& list, hipStream_t stream);
 
+// linear_src: 0, or the first run's source address when every run's source
+// directly follows the previous run's and every run holds whole slices
+// (then slice s reads linear_src + s * kCopySliceBytes, known without the
+// run list).
 hipError_t launch_copy_runs(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
-                            uint64_t page_bytes, const LaunchEvents& events, hipStream_t stream);
+                            uint64_t page_bytes, uint64_t linear_src, const LaunchEvents& events,
+                            hipStream_t stream);
 
 hipError_t launch_copy_runs_fp8(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
                                 uint64_t page_bytes, uint32_t lanes_per_row,

@@ -76,11 +76,56 @@ __device__ __forceinline__ void copy_slice(uint64_t src, uint64_t dst, uint64_t 
     __builtin_amdgcn_raw_buffer_store_b128(v[u], rd, (u * kWave + lane) * 16u, 0, kStorePolicy);
 }
 
+// Slice s when the sources form one region (linear_src: the first run's
+// source; every run's source follows the previous one and holds whole
+// slices): the source of slice s is linear_src + s * slice whatever the run,
+// so its loads go out before the run is known, and the lookup of the
+// destination runs while they are in flight. Vector loads return in issue
+// order, so only the first search level (one probe per lane, sent before the
+// copy loads) is a vector load; the rest of the search and the run record are
+// scalar loads, which are counted apart and do not wait for the copy's data.
+// n_runs <= 64 * kLinearScan: the second level reads at most kLinearScan
+// entries.
+constexpr uint32_t kLinearScan = 8;
+__device__ __forceinline__ void copy_slice_linear_src(const DevRun* __restrict__ runs,
+                                                      uint32_t n_runs, uint32_t s,
+                                                      uint64_t linear_src, uint32_t lane) {
+  const uint32_t stride = (n_runs + kWave - 1) / kWave;  // <= kLinearScan
+  const uint32_t probe = lane * stride;
+  const uint32_t first = probe < n_runs ? runs[probe].slice_begin : 0xffffffffu;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<void*>(linear_src + (uint64_t)s * kCopySliceBytes), (short)0,
+      kCopySliceBytes, 0x00020000);
+  u32x4 v[kCopyUnroll];
+#pragma unroll
+  for (int u = 0; u < kCopyUnroll; ++u)
+    v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, (u * kWave + lane) * 16u, 0, kLoadPolicy);
+  // level 1: the last probe at or below s (probe 0 is run 0, slice 0)
+  const uint64_t mask = __ballot(first <= s);
+  uint32_t r = ((uint32_t)__popcll(mask) - 1u) * stride;
+  // level 2: up to stride - 1 following entries, scalar
+  const uint32_t end = min(r + stride, n_runs);
+  uint32_t next[kLinearScan];
+#pragma unroll
+  for (uint32_t i = 1; i < kLinearScan; ++i)
+    next[i] = r + i < end ? runs[r + i].slice_begin : 0xffffffffu;
+#pragma unroll
+  for (uint32_t i = 1; i < kLinearScan; ++i) r += next[i] <= s ? 1u : 0u;
+  const uint64_t dst = runs[r].dst + (uint64_t)(s - runs[r].slice_begin) * kCopySliceBytes;
+  const __amdgpu_buffer_rsrc_t rd =
+      __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(dst), (short)0, kCopySliceBytes,
+                                        0x00020000);
+#pragma unroll
+  for (int u = 0; u < kCopyUnroll; ++u)
+    __builtin_amdgcn_raw_buffer_store_b128(v[u], rd, (u * kWave + lane) * 16u, 0, kStorePolicy);
+}
+
 // Identity copy of every run: the device form of the reference's per-run
 // cudaMemcpyAsync loop (split_pd_engine.cpp:96-108). Wave w copies global
 // slice w; it finds its run with the wave-parallel search over the run list.
 __device__ __forceinline__ void copy_runs_body(const DevRun* __restrict__ runs, uint32_t n_runs,
-                                               uint32_t total_slices, uint64_t page_bytes) {
+                                               uint32_t total_slices, uint64_t page_bytes,
+                                               uint64_t linear_src) {
   const uint32_t lane = threadIdx.x % kWave;
   // The slice index is wave-uniform; saying so keeps the run, the addresses
   // and the buffer resources in SGPRs (a resource the compiler cannot prove
@@ -88,6 +133,10 @@ __device__ __forceinline__ void copy_runs_body(const DevRun* __restrict__ runs, 
   // and store).
   const uint32_t s = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + threadIdx.x / kWave);
   if (s >= total_slices) return;
+  if (linear_src && n_runs <= kWave * kLinearScan) {
+    copy_slice_linear_src(runs, n_runs, s, linear_src, lane);
+    return;
+  }
   const uint32_t r = find_run(runs, 0, n_runs, s, lane);
   const DevRun& run = runs[r];
   const uint64_t rel = (uint64_t)(s - run.slice_begin) * kCopySliceBytes;
@@ -95,14 +144,15 @@ __device__ __forceinline__ void copy_runs_body(const DevRun* __restrict__ runs, 
 }
 
 __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_kernel(
-    const DevRun* __restrict__ runs, uint32_t n_runs, uint32_t total_slices, uint64_t page_bytes) {
-  copy_runs_body(runs, n_runs, total_slices, page_bytes);
+    const DevRun* __restrict__ runs, uint32_t n_runs, uint32_t total_slices, uint64_t page_bytes,
+    uint64_t linear_src) {
+  copy_runs_body(runs, n_runs, total_slices, page_bytes, linear_src);
 }
 
 // The same copy with the run list in the kernel arguments (no staging copy).
 // An aggregate kernel argument stays in the kernarg segment and is read there.
 __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_kernarg_kernel(const KernargRunList list) {
-  copy_runs_body(list.runs, list.n_runs, list.total_slices, list.page_bytes);
+  copy_runs_body(list.runs, list.n_runs, list.total_slices, list.page_bytes, list.linear_src);
 }
 
 // Fused BF16 -> FP8 handoff. A row is one (token, kv head) of one K or V
@@ -264,11 +314,12 @@ hipError_t launch_copy_runs_kernarg(const KernargRunList& list, hipStream_t stre
 }
 
 hipError_t launch_copy_runs(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
-                            uint64_t page_bytes, const LaunchEvents& ev, hipStream_t stream) {
+                            uint64_t page_bytes, uint64_t linear_src, const LaunchEvents& ev,
+                            hipStream_t stream) {
   const uint32_t waves = total_slices ? total_slices : 1u;
   hipExtLaunchKernelGGL(copy_runs_kernel, dim3((waves + kWavesPerBlock - 1) / kWavesPerBlock),
                         dim3(kThreadsPerBlock), 0, stream, ev.start, ev.stop, 0, runs, n_runs,
-                        total_slices, page_bytes);
+                        total_slices, page_bytes, linear_src);
   return hipGetLastError();
 }
 

@@ -488,3 +488,62 @@ def test_single_allocation_beyond_4_gib(torch_cuda):
         assert torch.equal(arena[int(d) * page:(int(d) + 1) * page], saved[int(s)]), (s, d)
     for p in canary:
         assert torch.equal(arena[p * page:(p + 1) * page], canary_before[p]), p
+
+
+def _contiguous_source_plan(g: W.Geometry, n_runs: int, n_pages: int, seed: int):
+    """n_pages source pages in one region (pages 0..n_pages-1, in order) cut
+    into n_runs runs whose destinations lie, shuffled and one page apart,
+    above it: the shape of a single prefill's handoff into a fragmented
+    decode group."""
+    rng = np.random.default_rng(seed)
+    cuts = np.sort(rng.choice(np.arange(1, n_pages), n_runs - 1, replace=False))
+    lengths = np.diff(np.concatenate(([0], cuts, [n_pages])))
+    order = rng.permutation(n_runs)
+    dst_start = np.empty(n_runs, np.int64)
+    at = n_pages + 1
+    for r in order:                        # shuffled, with a one-page gap after each
+        dst_start[r] = at
+        at += lengths[r] + 1
+    dst_pages = np.concatenate([np.arange(s, s + n) for s, n in zip(dst_start, lengths)])
+    src = (np.arange(n_pages) * g.stride).astype(np.int32)
+    dst = (dst_pages * g.stride).astype(np.int32)
+    return src, dst, at
+
+
+@pytest.mark.parametrize("n_runs,n_pages,head_dim", [
+    (1, 40, 64), (37, 300, 64), (64, 64, 64), (65, 400, 64), (200, 700, 64),
+    (511, 900, 64), (512, 1024, 64), (513, 1100, 64), (900, 1500, 64),
+    (60, 300, 24),                         # pages of 1.5 slices: no contiguous-source path
+])
+def test_contiguous_sources_across_run_counts(torch_cuda, n_runs, n_pages, head_dim):
+    """Sources in one region take the kernel's contiguous-source path (the
+    source of slice s is known before its run); run counts on both sides of
+    each search-width step and of that path's 512-run limit, through a run
+    list and through the one-call entry point (kernel-argument list up to
+    112 runs, staged list above)."""
+    torch = torch_cuda
+    g = W.Geometry(2, 2 if head_dim == 64 else 1, head_dim)
+    kv = _kv(g)
+    src, dst, total = _contiguous_source_plan(g, n_runs, n_pages, 1000 + n_runs)
+    runs = P.build_runs(src, dst, kv)
+    assert len(runs) == n_runs
+    say(f"contiguous sources runs={n_runs} pages={n_pages} page_bytes={g.page_bytes()}")
+    bufs, view = device_arena(torch, (total + 3) * g.page_bytes())
+    fill_bf16(torch, bufs[0], 1.0, n_runs)
+    torch.cuda.synchronize()
+    expected = snapshot(bufs).copy()
+    O.copy_handoff(expected, src, dst, g.half(), g.layers)
+    with P.RunList.bf16(view, view, runs, kv) as rl:
+        rl.copy(stream_ptr(torch))
+        torch.cuda.synchronize()
+    after = snapshot(bufs)
+    assert np.array_equal(after, expected), first_diff(after, expected)
+    # the same plan again through the one-call entry point, over fresh values
+    fill_bf16(torch, bufs[0], 1.0, n_runs + 7)
+    torch.cuda.synchronize()
+    expected = snapshot(bufs).copy()
+    O.copy_handoff(expected, src, dst, g.half(), g.layers)
+    P.copy_shared_kv(view, src, dst, kv, 0, stream_ptr(torch))
+    torch.cuda.synchronize()
+    after = snapshot(bufs)
+    assert np.array_equal(after, expected), first_diff(after, expected)
