@@ -130,9 +130,6 @@ struct Geo {
   static constexpr int E = kFp8 ? 1 : 2;
   static constexpr int WORDS = D * E / 16;   // key words = value words per lane
   static constexpr int PITCH = D * E + 16;   // LDS row pitch of the value tile
-  // Register sets per wave (SETS-1 blocks in flight), the measured best on
-  // MI355X: FP8 blocks are half the bytes, so more of them stay in flight.
-  static constexpr int SETS = kFp8 ? 4 : 2;
 };
 
 template <int W, bool kFp8>
@@ -146,14 +143,16 @@ struct BlockRegs {
 
 constexpr int kDecodeWaves = 4;
 
-template <int D, bool kFp8, int KVM, bool kAppend>
+// kSets register sets per wave: kSets-1 blocks in flight while one is
+// computed (chosen at launch, see sets_for).
+template <int D, bool kFp8, int KVM, bool kAppend, int kSets>
 __global__ __launch_bounds__(kDecodeWaves * 64) void paged_decode_kernel(
     const DecodeParams p, const int32_t* __restrict__ tables) {
   using G = Geo<D, kFp8>;
   constexpr int E = G::E;
   constexpr int NK = D / 32;  // score MFMAs per block
   constexpr int NT = D / 16;  // value MFMAs (16 head dims each) per block
-  constexpr int W = G::WORDS, SETS = G::SETS, PITCH = G::PITCH;
+  constexpr int W = G::WORDS, SETS = kSets, PITCH = G::PITCH;
   __shared__ __attribute__((aligned(16))) unsigned char lds_v[kDecodeWaves][kBlockTokens * PITCH];
 
   const int lane = threadIdx.x & 63;
@@ -560,15 +559,32 @@ int combine_groups(int64_t rows, int D) {
   return g;
 }
 
+// Register sets of one wave. BF16: two. FP8: two (one block in flight)
+// while a split holds at most 48 blocks, four beyond. Both launches on
+// MI355X, FP8, 2 KV heads x 6 query heads, 1 GiB scrub before each step,
+// two sets against four: 64 x 5,040 tokens (16 splits, 20 blocks each)
+// 39.2-39.5 against 41.2-41.3 us; 64 x 10,080 (40 blocks) 68.9 against
+// 72.0; 128 x 5,040 (8 splits, 40 blocks) 68.8-69.2 against 68.0-71.5;
+// 8 x 5,040 (5 blocks) 17.0 against 18.1; 1 x 32,768 (4 blocks) 18.4
+// against 18.9; 64 x 20,160 (79 blocks) 123.2 against 120.7.
+constexpr int kSetsLongSplit = 48;
+
+template <int D, bool kFp8, int KVM, int kSets>
+void launch_sets(const DecodeParams& p, hipStream_t stream, dim3 grid, dim3 block) {
+  if (p.new_k)
+    hipLaunchKernelGGL((paged_decode_kernel<D, kFp8, KVM, true, kSets>), grid, block, 0, stream, p, p.tables);
+  else
+    hipLaunchKernelGGL((paged_decode_kernel<D, kFp8, KVM, false, kSets>), grid, block, 0, stream, p, p.tables);
+}
+
 template <int D, bool kFp8, int KVM>
 void launch(const DecodeParams& p, hipStream_t stream) {
   const int64_t units = (int64_t)p.batch * p.kv_heads * p.splits;
   const int64_t rows = (int64_t)p.batch * p.q_heads;
   const dim3 grid((unsigned)((units + kDecodeWaves - 1) / kDecodeWaves)), block(kDecodeWaves * 64);
-  if (p.new_k)
-    hipLaunchKernelGGL((paged_decode_kernel<D, kFp8, KVM, true>), grid, block, 0, stream, p, p.tables);
-  else
-    hipLaunchKernelGGL((paged_decode_kernel<D, kFp8, KVM, false>), grid, block, 0, stream, p, p.tables);
+  const int per_split = (p.max_blocks + p.splits - 1) / p.splits;
+  if (kFp8 && per_split > kSetsLongSplit) launch_sets<D, kFp8, KVM, 4>(p, stream, grid, block);
+  else launch_sets<D, kFp8, KVM, 2>(p, stream, grid, block);
   hipLaunchKernelGGL((decode_combine_kernel<D>), dim3((unsigned)rows, (unsigned)combine_groups(rows, D)),
                      dim3(kCombineThreads), 0, stream, p);
 }

@@ -237,7 +237,12 @@ def test_5040_token_prefix_batch(torch_cuda):
     say("decode fp8 5040-token prefixes x3, 28 layers")
     case = DecodeCase(torch_cuda, fp8=True, layers=28, H=2, D=128, kvm=6,
                       seq_lens=[5040, 5040, 5041], seed=4, layer=27)
-    _check(case, case.run())
+    want = _check(case, case.run())
+    # FP8 waves keep one block in flight up to 48 blocks per split and three
+    # beyond: 316 blocks in 1, 4 (79 each), 6 (53) and 7 (46) splits.
+    for splits in (1, 4, 6, 7):
+        say(f"decode fp8 5040-token prefixes splits={splits}")
+        assert close(case.run(splits), want).all(), splits
 
 
 def test_bad_tables_give_nan_only_for_their_sequence(torch_cuda):
