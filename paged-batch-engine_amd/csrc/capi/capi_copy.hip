@@ -24,19 +24,23 @@ namespace {
 struct Resolved {
   std::vector<pbe::DevRun> runs;
   pbe_runlist_info info{};
-  // The first run's source when the sources form one region in run order and
-  // every run holds whole slices (the copy kernel then reads slice s at
-  // linear_src + s * slice without looking the run up first); else 0.
+  // The first run's source when linear slices were asked for, the sources
+  // form one region in run order, every run holds whole linear slices and
+  // the list fits the kernel's one-region search (the copy kernel then reads
+  // slice s at linear_src + s * linear_slice without looking the run up
+  // first; slices are counted in linear_slice); else 0.
   uint64_t linear_src = 0;
 };
 
 // Builds device run entries for either kernel. src pages are src_page_bytes
 // long in the src view, dst pages dst_page_bytes long in the dst view;
-// scale pages (FP8) scale_page_bytes long at scales.
+// scale pages (FP8) scale_page_bytes long at scales. Slices are `slice`
+// source bytes, or `linear_slice` when the one-region path applies (0: the
+// kernel has no such path).
 int resolve_runs(const pbe_arena_view& src, const pbe_arena_view& dst, uint64_t src_half,
                  uint64_t dst_half, int32_t stride, const pbe_run* runs, int64_t n_runs,
                  uint64_t scales, uint64_t scales_bytes, uint64_t scale_page_bytes,
-                 uint32_t slice, Resolved* out) {
+                 uint32_t slice, uint32_t linear_slice, Resolved* out) {
   if (n_runs <= 0 || n_runs > 0x7fffffff) return fail(PBE_ERR_INVALID, "run count out of range");
   const uint64_t src_page = (uint64_t)stride * src_half;
   const uint64_t dst_page = (uint64_t)stride * dst_half;
@@ -79,10 +83,18 @@ int resolve_runs(const pbe_arena_view& src, const pbe_arena_view& dst, uint64_t 
   if (!spans_disjoint(dst_spans, src_spans))
     return fail(PBE_ERR_INVALID, "run list writes a byte twice or overwrites its own source");
   out->info.runs = n_runs;
-  out->info.slices = slices;
-  bool linear = src_page % slice == 0;
+  bool linear = linear_slice && src_page % linear_slice == 0 && (uint64_t)n_runs <= pbe::kLinearMaxRuns;
   for (size_t i = 1; linear && i < src_spans.size(); ++i)
     linear = src_spans[i].first == src_spans[i - 1].second;
+  if (linear) {  // recount in linear slices (whole ones: src_page is a multiple)
+    slices = 0;
+    for (pbe::DevRun& d : out->runs) {
+      d.slice_begin = (uint32_t)slices;
+      slices += (uint64_t)d.pages * (src_page / linear_slice);
+      if (slices > 0xfffffff0ull) return fail(PBE_ERR_INVALID, "run list too large for one launch");
+    }
+  }
+  out->info.slices = slices;
   out->linear_src = linear ? out->runs.front().src : 0;
   return PBE_OK;
 }
@@ -134,7 +146,7 @@ int pbe_runlist_create(const pbe_arena_view* src, const pbe_arena_view* dst, con
   }
   Resolved res;
   int rc = resolve_runs(*src, *dst, half, half, 2 * shape->layers, runs, n_runs, 0, 0, 0,
-                        pbe::kCopySliceBytes, &res);
+                        pbe::kCopySliceBytes, pbe::kLinearSliceBytes, &res);
   if (rc != PBE_OK) return rc;
   return upload_runlist(res, device, false, false, 2ull * shape->layers * half, *shape, out);
 }
@@ -165,7 +177,7 @@ int pbe_runlist_create_fp8(const pbe_arena_view* src, const pbe_arena_view* dst,
   Resolved res;
   int rc = resolve_runs(*src, *dst, half16, half8, 2 * shape->layers, runs, n_runs,
                         reinterpret_cast<uint64_t>(dst_scales), dst_scales_bytes, scale_page,
-                        pbe::kFp8SliceBytes, &res);
+                        pbe::kFp8SliceBytes, 0, &res);
   if (rc != PBE_OK) return rc;
   return upload_runlist(res, device, true, dst_scales != nullptr, 2ull * shape->layers * half16,
                         *shape, out);
@@ -336,7 +348,7 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
   }
   Resolved res;
   rc = resolve_runs(*arena, *arena, half, half, 2 * shape->layers, runs.data(), n_runs, 0, 0, 0,
-                    pbe::kCopySliceBytes, &res);
+                    pbe::kCopySliceBytes, pbe::kLinearSliceBytes, &res);
   if (rc != PBE_OK) return rc;
   PBE_DEVICE_SCOPE(device);
   const hipStream_t s = static_cast<hipStream_t>(stream);
@@ -425,7 +437,7 @@ int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream
   }
   const hipStream_t s = static_cast<hipStream_t>(stream);
   // Spans whose addresses and sizes are all 16-byte multiples are runs of
-  // 16-byte pages for the run kernel: 4 KiB per wave, one launch, and up to
+  // 16-byte pages for the run kernel: 2 KiB per wave, one launch, and up to
   // kKernargRuns spans in the kernel arguments (no staging, so capturable).
   const bool aligned = std::all_of(merged.begin(), merged.end(), [](const pbe_copy_op& o) {
     return ((o.src | o.dst | o.bytes) & 15u) == 0 && o.bytes / 16 <= 0xffffffffull;

@@ -2,8 +2,9 @@
 //
 // A copy kernel moves every byte twice (one read, one write), so its rate is
 // bounded by what HBM gives a pure read stream and a pure write stream of the
-// same size. These two kernels are the copy kernel's halves: one wave per
-// 4 KiB slice, 64 lanes x 16-byte vectors x 4, 256-thread workgroups, the same
+// same size. These two kernels are the copy kernel's halves at its geometry
+// on a one-region plan (config 2): one wave per 1 KiB slice, 64 lanes x one
+// 16-byte vector, 256-thread workgroups, the same
 // buffer cache-policy bits (loads nt; stores sc1 + nt). bench.py times them
 // on the config-2 byte count beside the handoff so the ceiling is measured in
 // every run rather than asserted. They are not part of the handoff library:
@@ -17,8 +18,8 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWave = 64;
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
-constexpr uint32_t kSlice = kWave * 16u * kUnroll;  // 4 KiB per wave
+constexpr int kUnroll = 1;
+constexpr uint32_t kSlice = kWave * 16u * kUnroll;  // 1 KiB per wave, as the product kernel on config 2
 constexpr int kLoadPolicy = 0x02;                   // nt
 constexpr int kStorePolicy = 0x12;                  // sc1 + nt
 
@@ -36,7 +37,9 @@ __global__ __launch_bounds__(kThreads) void stream_read_kernel(const uint8_t* p,
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u)
     v[u] = __builtin_amdgcn_raw_buffer_load_b128(r, (u * kWave + lane) * 16u, 0, kLoadPolicy);
-  u32x4 acc = v[0] ^ v[1] ^ v[2] ^ v[3];
+  u32x4 acc = v[0];
+#pragma unroll
+  for (int u = 1; u < kUnroll; ++u) acc ^= v[u];
   // never true for the bench's data; keeps the loads alive
   if (acc.x == 0x9e3779b9u && acc.y == 0x7f4a7c15u && acc.z == 0x85ebca6bu) sink[lane] = acc;
 }
@@ -84,7 +87,7 @@ __global__ __launch_bounds__(kThreads) void slice_copy_kernel(const uint8_t* src
 // Register-staged copy: each wave loads a 32 KiB chunk into VGPRs (32
 // vectors per lane, two waves per SIMD), then stores all of it. Tests whether
 // long read-only then write-only bursts per wave beat the copy kernel's
-// 4 KiB load-then-store slices (HBM pays a read/write turnaround when the two
+// short load-then-store slices (HBM pays a read/write turnaround when the two
 // streams mix).
 constexpr int kPhaseUnroll = 32;
 constexpr uint32_t kPhaseChunk = kWave * 16u * kPhaseUnroll;  // 32 KiB per wave

@@ -6,8 +6,24 @@
 namespace pbe {
 
 constexpr int kThreadsPerBlock = 256;
-constexpr int kCopyUnroll = 4;  // 16-byte vectors per lane per slice of the identity copy
-constexpr uint32_t kCopySliceBytes = 64u * 16u * kCopyUnroll;  // 4 KiB per wave
+// Slice (the bytes one wave moves) of the identity copy, by path. Plans whose
+// sources form one region take 1 KiB slices (one 16-byte vector per lane):
+// the kernel issues a slice's loads before it looks its run up. Other plans
+// look the run up first and take 2 KiB slices, which spend that lookup on
+// twice the bytes. Measured on MI355X (kernel-bracketing events, 1 GiB scrub
+// before each launch), slices of 4 / 2 / 1 KiB: config 2 (one source
+// region) 48.5-48.9 / 48.1-48.5 / 46.9-47.1 us; config 3 (scattered
+// sources) 124.1-126.0 / 119.5-121.3 / 135.3-136.4 us; config 5 646.6-646.9 /
+// 635.4-636.0 / 729.0-730.2 us. 512-byte slices are bound by workgroup
+// dispatch (64.8 us on config 2), as are 1024-thread workgroups (50.0 us).
+constexpr int kLinearUnroll = 1;
+constexpr uint32_t kLinearSliceBytes = 64u * 16u * kLinearUnroll;  // 1 KiB per wave
+constexpr int kCopyUnroll = 2;  // 16-byte vectors per lane per slice of the identity copy
+constexpr uint32_t kCopySliceBytes = 64u * 16u * kCopyUnroll;      // 2 KiB per wave
+// The one-region path searches at most this many runs (one vector probe per
+// lane, then a scalar scan of at most 8 entries); longer lists take the
+// general path.
+constexpr uint32_t kLinearMaxRuns = 512;
 constexpr int kFp8Unroll = 4;   // 16-byte BF16 vectors per lane per slice of the FP8 copy
 constexpr uint32_t kFp8SliceBytes = 64u * 16u * kFp8Unroll;    // 4 KiB of BF16 source per wave
 
@@ -50,13 +66,15 @@ struct KernargRunList {
 };
 static_assert(sizeof(KernargRunList) <= 4096 - 256, "kernel arguments are limited to 4 KiB");
 
-// One slice of kCopySliceBytes per wave, 256-thread workgroups.
+// One slice per wave (kLinearSliceBytes when linear_src is set, else
+// kCopySliceBytes), 256-thread workgroups.
 hipError_t launch_copy_runs_kernarg(const KernargRunList& list, hipStream_t stream);
 
 // linear_src: 0, or the first run's source address when every run's source
-// directly follows the previous run's and every run holds whole slices
-// (then slice s reads linear_src + s * kCopySliceBytes, known without the
-// run list).
+// directly follows the previous run's, every run holds whole slices of
+// kLinearSliceBytes and there are at most kLinearMaxRuns runs (then slice s,
+// counted in kLinearSliceBytes, reads linear_src + s * kLinearSliceBytes,
+// known without the run list). Otherwise slices are kCopySliceBytes.
 hipError_t launch_copy_runs(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
                             uint64_t page_bytes, uint64_t linear_src, const LaunchEvents& events,
                             hipStream_t stream);

@@ -59,8 +59,8 @@ constexpr int kStorePolicy = 0x12;
 
 // One slice: every lane moves kCopyUnroll 16-byte vectors, all loads issued
 // before the first store. Buffer resources clamp to the slice, so a short
-// last slice of a run needs no per-lane bound test: out-of-range lanes read 0
-// and the hardware drops their stores.
+// last slice of a run (or an op) needs no per-lane bound test: out-of-range
+// lanes read 0 and the hardware drops their stores.
 __device__ __forceinline__ void copy_slice(uint64_t src, uint64_t dst, uint64_t nbytes, uint32_t lane) {
   const uint32_t n = nbytes >= kCopySliceBytes ? kCopySliceBytes : (uint32_t)nbytes;
   const __amdgpu_buffer_rsrc_t rs =
@@ -78,15 +78,17 @@ __device__ __forceinline__ void copy_slice(uint64_t src, uint64_t dst, uint64_t 
 
 // Slice s when the sources form one region (linear_src: the first run's
 // source; every run's source follows the previous one and holds whole
-// slices): the source of slice s is linear_src + s * slice whatever the run,
-// so its loads go out before the run is known, and the lookup of the
-// destination runs while they are in flight. Vector loads return in issue
-// order, so only the first search level (one probe per lane, sent before the
-// copy loads) is a vector load; the rest of the search and the run record are
-// scalar loads, which are counted apart and do not wait for the copy's data.
-// n_runs <= 64 * kLinearScan: the second level reads at most kLinearScan
+// slices of kLinearSliceBytes): the source of slice s is linear_src + s *
+// slice whatever the run, so its loads go out before the run is known, and
+// the lookup of the destination runs while they are in flight. Vector loads
+// return in issue order, so only the first search level (one probe per lane,
+// sent before the copy loads) is a vector load; the rest of the search and
+// the run record are scalar loads, which are counted apart and do not wait
+// for the copy's data. n_runs <= kLinearMaxRuns = 64 * kLinearScan (the host
+// sets linear_src only then): the second level reads at most kLinearScan
 // entries.
 constexpr uint32_t kLinearScan = 8;
+static_assert(kLinearMaxRuns == kWave * kLinearScan, "one probe per lane, then kLinearScan entries");
 __device__ __forceinline__ void copy_slice_linear_src(const DevRun* __restrict__ runs,
                                                       uint32_t n_runs, uint32_t s,
                                                       uint64_t linear_src, uint32_t lane) {
@@ -94,11 +96,11 @@ __device__ __forceinline__ void copy_slice_linear_src(const DevRun* __restrict__
   const uint32_t probe = lane * stride;
   const uint32_t first = probe < n_runs ? runs[probe].slice_begin : 0xffffffffu;
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-      reinterpret_cast<void*>(linear_src + (uint64_t)s * kCopySliceBytes), (short)0,
-      kCopySliceBytes, 0x00020000);
-  u32x4 v[kCopyUnroll];
+      reinterpret_cast<void*>(linear_src + (uint64_t)s * kLinearSliceBytes), (short)0,
+      kLinearSliceBytes, 0x00020000);
+  u32x4 v[kLinearUnroll];
 #pragma unroll
-  for (int u = 0; u < kCopyUnroll; ++u)
+  for (int u = 0; u < kLinearUnroll; ++u)
     v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, (u * kWave + lane) * 16u, 0, kLoadPolicy);
   // level 1: the last probe at or below s (probe 0 is run 0, slice 0)
   const uint64_t mask = __ballot(first <= s);
@@ -111,12 +113,12 @@ __device__ __forceinline__ void copy_slice_linear_src(const DevRun* __restrict__
     next[i] = r + i < end ? runs[r + i].slice_begin : 0xffffffffu;
 #pragma unroll
   for (uint32_t i = 1; i < kLinearScan; ++i) r += next[i] <= s ? 1u : 0u;
-  const uint64_t dst = runs[r].dst + (uint64_t)(s - runs[r].slice_begin) * kCopySliceBytes;
+  const uint64_t dst = runs[r].dst + (uint64_t)(s - runs[r].slice_begin) * kLinearSliceBytes;
   const __amdgpu_buffer_rsrc_t rd =
-      __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(dst), (short)0, kCopySliceBytes,
+      __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(dst), (short)0, kLinearSliceBytes,
                                         0x00020000);
 #pragma unroll
-  for (int u = 0; u < kCopyUnroll; ++u)
+  for (int u = 0; u < kLinearUnroll; ++u)
     __builtin_amdgcn_raw_buffer_store_b128(v[u], rd, (u * kWave + lane) * 16u, 0, kStorePolicy);
 }
 
@@ -133,7 +135,7 @@ __device__ __forceinline__ void copy_runs_body(const DevRun* __restrict__ runs, 
   // and store).
   const uint32_t s = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + threadIdx.x / kWave);
   if (s >= total_slices) return;
-  if (linear_src && n_runs <= kWave * kLinearScan) {
+  if (linear_src) {
     copy_slice_linear_src(runs, n_runs, s, linear_src, lane);
     return;
   }

@@ -298,7 +298,7 @@ def test_copy_ops_merging_keeps_every_op(torch_cuda):
 def test_aligned_op_lists_on_both_sides_of_the_kernel_argument_limit(torch_cuda):
     """16-byte aligned op lists run on the run-list kernel: up to 112 spans in
     the kernel arguments, more through the staging ring. Spans of any 16-byte
-    multiple (a partial last 4 KiB slice is clamped by the buffer resource),
+    multiple (a partial last 2 KiB slice is clamped by the buffer resource),
     scattered destinations, at 1, 112 and 113 spans."""
     torch = torch_cuda
     rng = np.random.default_rng(33)
@@ -513,7 +513,8 @@ def _contiguous_source_plan(g: W.Geometry, n_runs: int, n_pages: int, seed: int)
 @pytest.mark.parametrize("n_runs,n_pages,head_dim", [
     (1, 40, 64), (37, 300, 64), (64, 64, 64), (65, 400, 64), (200, 700, 64),
     (511, 900, 64), (512, 1024, 64), (513, 1100, 64), (900, 1500, 64),
-    (60, 300, 24),                         # pages of 1.5 slices: no contiguous-source path
+    (60, 300, 24),                         # 3 KiB pages: three 1 KiB slices
+    (60, 300, 12),                         # pages of 1.5 KiB slices: no contiguous-source path
 ])
 def test_contiguous_sources_across_run_counts(torch_cuda, n_runs, n_pages, head_dim):
     """Sources in one region take the kernel's contiguous-source path (the
@@ -534,6 +535,13 @@ def test_contiguous_sources_across_run_counts(torch_cuda, n_runs, n_pages, head_
     expected = snapshot(bufs).copy()
     O.copy_handoff(expected, src, dst, g.half(), g.layers)
     with P.RunList.bf16(view, view, runs, kv) as rl:
+        # the path shows in the slice count: 1 KiB slices on the contiguous-
+        # source path (pages of whole KiB, at most 512 runs), else 2 KiB per run
+        page = g.page_bytes()
+        if page % 1024 == 0 and n_runs <= 512:
+            assert rl.info().slices == n_pages * page // 1024
+        else:
+            assert rl.info().slices == sum(-(-int(r[2]) * page // 2048) for r in runs)
         rl.copy(stream_ptr(torch))
         torch.cuda.synchronize()
     after = snapshot(bufs)
