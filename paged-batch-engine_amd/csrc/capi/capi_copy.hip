@@ -177,7 +177,7 @@ int pbe_runlist_create_fp8(const pbe_arena_view* src, const pbe_arena_view* dst,
   Resolved res;
   int rc = resolve_runs(*src, *dst, half16, half8, 2 * shape->layers, runs, n_runs,
                         reinterpret_cast<uint64_t>(dst_scales), dst_scales_bytes, scale_page,
-                        pbe::kFp8SliceBytes, 0, &res);
+                        pbe::kFp8SliceBytes, pbe::kFp8SliceBytes, &res);
   if (rc != PBE_OK) return rc;
   return upload_runlist(res, device, true, dst_scales != nullptr, 2ull * shape->layers * half16,
                         *shape, out);
@@ -235,7 +235,8 @@ int pbe_handoff_copy_fp8_timed(const pbe_runlist* list, int scale_mode, const fl
   PBE_HIP(pbe::launch_copy_runs_fp8(
       list->runs, list->n_runs, list->total_slices, list->page_bytes, (uint32_t)kv.head_dim / 8u,
       rows_per_plane, (uint32_t)kv.kv_heads, rows_per_plane * 2u * (uint32_t)kv.layers,
-      scale_mode == PBE_FP8_SCALE_TABLE, amax_table, ev, static_cast<hipStream_t>(stream)));
+      scale_mode == PBE_FP8_SCALE_TABLE, amax_table, list->linear_src, ev,
+      static_cast<hipStream_t>(stream)));
   return PBE_OK;
 }
 

@@ -79,11 +79,13 @@ hipError_t launch_copy_runs(const DevRun* runs, uint32_t n_runs, uint32_t total_
                             uint64_t page_bytes, uint64_t linear_src, const LaunchEvents& events,
                             hipStream_t stream);
 
+// linear_src: as for launch_copy_runs, with slices of kFp8SliceBytes source
+// bytes.
 hipError_t launch_copy_runs_fp8(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
                                 uint64_t page_bytes, uint32_t lanes_per_row,
                                 uint32_t rows_per_plane, uint32_t kv_heads,
                                 uint32_t rows_per_page, bool table, const float* amax_table,
-                                const LaunchEvents& events, hipStream_t stream);
+                                uint64_t linear_src, const LaunchEvents& events, hipStream_t stream);
 
 hipError_t launch_copy_ops(const DevOp* ops, uint32_t n_ops, hipStream_t stream);
 

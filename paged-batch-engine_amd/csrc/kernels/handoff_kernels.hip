@@ -185,84 +185,124 @@ __device__ __forceinline__ void fp8_step(const u32x4& v, uint32_t row, uint32_t 
   st8(dst, dst_off, quantise8(v, inv));
 }
 
+// A whole slice of the FP8 copy, loaded into v: quantises it into dst and
+// writes its rows' scales (per-token-head) at scales + row. row0 is the row
+// (within its run) of this lane's first 16-byte vector.
 template <int kLanesPerRow, bool kTable>
+__device__ __forceinline__ void fp8_full_slice(const u32x4 (&v)[kFp8Unroll], uint32_t lane,
+                                               gdst_t dst, uint32_t row0, uint64_t scales,
+                                               uint32_t rows_per_plane, uint32_t kv_heads,
+                                               uint32_t rows_per_page,
+                                               const float* __restrict__ amax_table) {
+  constexpr int kUnroll = kFp8Unroll;
+  constexpr uint32_t kRowsPerStep = kWave / kLanesPerRow;
+  constexpr uint32_t kRowsPerSlice = kUnroll * kRowsPerStep;
+  if constexpr (kRowsPerSlice <= kWave) {
+    // Batched per slice: lane j owns row j of the slice. It obtains the
+    // row's amax (per-token-head: the row maximum gathered from the row's
+    // lanes; table: the (layer, K|V, head) entry of the row), computes
+    // 448/amax (and the scale) once, and every lane then fetches its row's
+    // multiplier. Divisions and index arithmetic run once per slice instead
+    // of once per 1 KiB step.
+    const uint32_t slice_row0 = row0 - lane / kLanesPerRow;  // first row of the slice
+    float row_amax;
+    if constexpr (kTable) {
+      const uint32_t in_page = (slice_row0 + lane) % rows_per_page;
+      row_amax = amax_table[(in_page / rows_per_plane) * kv_heads + in_page % kv_heads];
+    } else {
+      float m[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) m[u] = group_max<kLanesPerRow>(amax8(v[u]));
+      const uint32_t j_step = lane / kRowsPerStep, j_row = lane % kRowsPerStep;
+      row_amax = 0.f;
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const float t = __shfl(m[u], (int)(j_row * kLanesPerRow), kWave);
+        if (j_step == (uint32_t)u) row_amax = t;
+      }
+      if (lane < kRowsPerSlice)
+        __builtin_nontemporal_store(row_amax > 0.f ? row_amax / 448.f : 1.f,
+                                    reinterpret_cast<PBE_GLOBAL float*>(scales) + slice_row0 + lane);
+    }
+    const float row_inv = row_amax > 0.f ? 448.f / row_amax : 0.f;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const float inv = __shfl(row_inv, (int)(u * kRowsPerStep + lane / kLanesPerRow), kWave);
+      st8(dst, (u * kWave + lane) * 8u, quantise8(v[u], inv));
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      fp8_step<kLanesPerRow, kTable>(v[u], row0 + u * kRowsPerStep, lane, dst, (u * kWave + lane) * 8u,
+                                     scales, rows_per_plane, kv_heads, rows_per_page, amax_table);
+  }
+}
+
+// Fused BF16 -> FP8 copy of every run, one slice of kFp8SliceBytes source
+// bytes per wave. kLinear: the sources form one region and every run holds
+// whole slices (linear_src, as for the identity copy), so the slice's loads
+// go out before its run is looked up: one vector probe per lane first, the
+// loads, then the ballot, a scalar scan of at most kLinearScan entries and
+// the scalar run record (n_runs <= kLinearMaxRuns).
+template <int kLanesPerRow, bool kTable, bool kLinear>
 __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_fp8_kernel(
     const DevRun* __restrict__ runs, uint32_t n_runs, uint32_t total_slices, uint64_t page_bytes,
     uint32_t rows_per_plane, uint32_t kv_heads, uint32_t rows_per_page,
-    const float* __restrict__ amax_table) {
+    const float* __restrict__ amax_table, uint64_t linear_src) {
   constexpr int kUnroll = kFp8Unroll;
   constexpr uint32_t kSlice = kFp8SliceBytes;           // source bytes per slice
   constexpr uint32_t kRowBytes = kLanesPerRow * 16u;     // source bytes per row
   constexpr uint32_t kRowsPerStep = kWave / kLanesPerRow;
   const uint32_t lane = threadIdx.x % kWave;
-  const uint32_t s = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+  const uint32_t s = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + threadIdx.x / kWave);
   if (s >= total_slices) return;
-  {
-    const uint32_t r = __builtin_amdgcn_readfirstlane(find_run(runs, 0, n_runs, s, lane));
-    const DevRun& run = runs[r];
-    const uint64_t rel = (uint64_t)(s - run.slice_begin) * kSlice;
-    const uint64_t nbytes = (uint64_t)run.pages * page_bytes - rel;
-    gsrc_t src = reinterpret_cast<gsrc_t>(run.src + rel);
-    gdst_t dst = reinterpret_cast<gdst_t>(run.dst + rel / 2);
-    const uint64_t scales = run.aux;
-    const uint32_t row0 = (uint32_t)(rel / kRowBytes) + lane / kLanesPerRow;  // row in the run
-    constexpr uint32_t kRowsPerSlice = kUnroll * kRowsPerStep;
-    if (nbytes >= kSlice) {
-      u32x4 v[kUnroll];
+  if constexpr (kLinear) {
+    const uint32_t stride = (n_runs + kWave - 1) / kWave;  // <= kLinearScan
+    const uint32_t probe = lane * stride;
+    const uint32_t first = probe < n_runs ? runs[probe].slice_begin : 0xffffffffu;
+    gsrc_t src = reinterpret_cast<gsrc_t>(linear_src + (uint64_t)s * kSlice);
+    u32x4 v[kUnroll];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) v[u] = ld16(src, (u * kWave + lane) * 16u);
-      if constexpr (kRowsPerSlice <= kWave) {
-        // Batched per slice: lane j owns row j of the slice. It obtains the
-        // row's amax (per-token-head: the row maximum gathered from the
-        // row's lanes; table: the (layer, K|V, head) entry of the row),
-        // computes 448/amax (and the scale) once, and every lane then
-        // fetches its row's multiplier. Divisions and index arithmetic run
-        // once per slice instead of once per 1 KiB step.
-        const uint32_t slice_row0 = row0 - lane / kLanesPerRow;  // first row of the slice
-        float row_amax;
-        if constexpr (kTable) {
-          const uint32_t in_page = (slice_row0 + lane) % rows_per_page;
-          row_amax = amax_table[(in_page / rows_per_plane) * kv_heads + in_page % kv_heads];
-        } else {
-          float m[kUnroll];
+    for (int u = 0; u < kUnroll; ++u) v[u] = ld16(src, (u * kWave + lane) * 16u);
+    const uint64_t mask = __ballot(first <= s);
+    uint32_t r = ((uint32_t)__popcll(mask) - 1u) * stride;
+    const uint32_t end = min(r + stride, n_runs);
+    uint32_t next[kLinearScan];
 #pragma unroll
-          for (int u = 0; u < kUnroll; ++u) m[u] = group_max<kLanesPerRow>(amax8(v[u]));
-          const uint32_t j_step = lane / kRowsPerStep, j_row = lane % kRowsPerStep;
-          row_amax = 0.f;
+    for (uint32_t i = 1; i < kLinearScan; ++i)
+      next[i] = r + i < end ? runs[r + i].slice_begin : 0xffffffffu;
 #pragma unroll
-          for (int u = 0; u < kUnroll; ++u) {
-            const float t = __shfl(m[u], (int)(j_row * kLanesPerRow), kWave);
-            if (j_step == (uint32_t)u) row_amax = t;
-          }
-          if (lane < kRowsPerSlice)
-            __builtin_nontemporal_store(row_amax > 0.f ? row_amax / 448.f : 1.f,
-                                        reinterpret_cast<PBE_GLOBAL float*>(scales) + slice_row0 +
-                                            lane);
-        }
-        const float row_inv = row_amax > 0.f ? 448.f / row_amax : 0.f;
+    for (uint32_t i = 1; i < kLinearScan; ++i) r += next[i] <= s ? 1u : 0u;
+    const uint64_t rel = (uint64_t)(s - runs[r].slice_begin) * kSlice;
+    fp8_full_slice<kLanesPerRow, kTable>(v, lane, reinterpret_cast<gdst_t>(runs[r].dst + rel / 2),
+                                         (uint32_t)(rel / kRowBytes) + lane / kLanesPerRow,
+                                         runs[r].aux, rows_per_plane, kv_heads, rows_per_page,
+                                         amax_table);
+    return;
+  }
+  const uint32_t r = __builtin_amdgcn_readfirstlane(find_run(runs, 0, n_runs, s, lane));
+  const DevRun& run = runs[r];
+  const uint64_t rel = (uint64_t)(s - run.slice_begin) * kSlice;
+  const uint64_t nbytes = (uint64_t)run.pages * page_bytes - rel;
+  gsrc_t src = reinterpret_cast<gsrc_t>(run.src + rel);
+  gdst_t dst = reinterpret_cast<gdst_t>(run.dst + rel / 2);
+  const uint64_t scales = run.aux;
+  const uint32_t row0 = (uint32_t)(rel / kRowBytes) + lane / kLanesPerRow;  // row in the run
+  if (nbytes >= kSlice) {
+    u32x4 v[kUnroll];
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-          const float inv = __shfl(row_inv, (int)(u * kRowsPerStep + lane / kLanesPerRow), kWave);
-          st8(dst, (u * kWave + lane) * 8u, quantise8(v[u], inv));
-        }
-      } else {
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u)
-          fp8_step<kLanesPerRow, kTable>(v[u], row0 + u * kRowsPerStep, lane, dst,
-                                                  (u * kWave + lane) * 8u, scales, rows_per_plane,
-                                                  kv_heads, rows_per_page, amax_table);
-      }
-    } else {
-      // Last, partial slice of a run: whole rows only (slices are multiples
-      // of the row size), one 1 KiB step at a time.
-      for (uint32_t u = 0; u * kWave * 16u < nbytes; ++u) {
-        const uint32_t off = (u * kWave + lane) * 16u;
-        const u32x4 v = off < nbytes ? ld16(src, off) : u32x4{0u, 0u, 0u, 0u};
-        if (off < nbytes)
-          fp8_step<kLanesPerRow, kTable>(v, row0 + u * kRowsPerStep, lane, dst, off / 2,
-                                                  scales, rows_per_plane, kv_heads,
-                                                  rows_per_page, amax_table);
-      }
+    for (int u = 0; u < kUnroll; ++u) v[u] = ld16(src, (u * kWave + lane) * 16u);
+    fp8_full_slice<kLanesPerRow, kTable>(v, lane, dst, row0, scales, rows_per_plane, kv_heads,
+                                         rows_per_page, amax_table);
+  } else {
+    // Last, partial slice of a run: whole rows only (slices are multiples
+    // of the row size), one 1 KiB step at a time.
+    for (uint32_t u = 0; u * kWave * 16u < nbytes; ++u) {
+      const uint32_t off = (u * kWave + lane) * 16u;
+      const u32x4 v = off < nbytes ? ld16(src, off) : u32x4{0u, 0u, 0u, 0u};
+      if (off < nbytes)
+        fp8_step<kLanesPerRow, kTable>(v, row0 + u * kRowsPerStep, lane, dst, off / 2, scales,
+                                       rows_per_plane, kv_heads, rows_per_page, amax_table);
     }
   }
 }
@@ -326,19 +366,32 @@ hipError_t launch_copy_runs(const DevRun* runs, uint32_t n_runs, uint32_t total_
 }
 
 namespace {
+template <int L, bool kLinear>
+void launch_fp8_path(bool table, uint32_t blocks, hipStream_t stream, const LaunchEvents& ev,
+                     const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
+                     uint64_t page_bytes, uint32_t rows_per_plane, uint32_t kv_heads,
+                     uint32_t rows_per_page, const float* amax_table, uint64_t linear_src) {
+  if (table)
+    hipExtLaunchKernelGGL((copy_runs_fp8_kernel<L, true, kLinear>), dim3(blocks), dim3(kThreadsPerBlock),
+                          0, stream, ev.start, ev.stop, 0, runs, n_runs, total_slices, page_bytes,
+                          rows_per_plane, kv_heads, rows_per_page, amax_table, linear_src);
+  else
+    hipExtLaunchKernelGGL((copy_runs_fp8_kernel<L, false, kLinear>), dim3(blocks), dim3(kThreadsPerBlock),
+                          0, stream, ev.start, ev.stop, 0, runs, n_runs, total_slices, page_bytes,
+                          rows_per_plane, kv_heads, rows_per_page, amax_table, linear_src);
+}
+
 template <int L>
 void launch_fp8(bool table, uint32_t blocks, hipStream_t stream, const LaunchEvents& ev,
                 const DevRun* runs, uint32_t n_runs, uint32_t total_slices, uint64_t page_bytes,
                 uint32_t rows_per_plane, uint32_t kv_heads, uint32_t rows_per_page,
-                const float* amax_table) {
-  if (table)
-    hipExtLaunchKernelGGL((copy_runs_fp8_kernel<L, true>), dim3(blocks), dim3(kThreadsPerBlock), 0,
-                          stream, ev.start, ev.stop, 0, runs, n_runs, total_slices, page_bytes,
-                          rows_per_plane, kv_heads, rows_per_page, amax_table);
+                const float* amax_table, uint64_t linear_src) {
+  if (linear_src)
+    launch_fp8_path<L, true>(table, blocks, stream, ev, runs, n_runs, total_slices, page_bytes,
+                             rows_per_plane, kv_heads, rows_per_page, amax_table, linear_src);
   else
-    hipExtLaunchKernelGGL((copy_runs_fp8_kernel<L, false>), dim3(blocks), dim3(kThreadsPerBlock), 0,
-                          stream, ev.start, ev.stop, 0, runs, n_runs, total_slices, page_bytes,
-                          rows_per_plane, kv_heads, rows_per_page, amax_table);
+    launch_fp8_path<L, false>(table, blocks, stream, ev, runs, n_runs, total_slices, page_bytes,
+                              rows_per_plane, kv_heads, rows_per_page, amax_table, 0);
 }
 }  // namespace
 
@@ -346,14 +399,14 @@ hipError_t launch_copy_runs_fp8(const DevRun* runs, uint32_t n_runs, uint32_t to
                                 uint64_t page_bytes, uint32_t lanes_per_row,
                                 uint32_t rows_per_plane, uint32_t kv_heads,
                                 uint32_t rows_per_page, bool table, const float* amax_table,
-                                const LaunchEvents& ev, hipStream_t stream) {
+                                uint64_t linear_src, const LaunchEvents& ev, hipStream_t stream) {
   const uint32_t waves = total_slices ? total_slices : 1u;
   const uint32_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
   // One instantiation per row width (head_dim / 8 lanes), a shape, not a tuning choice.
 #define PBE_FP8_CASE(L)                                                                      \
   case L:                                                                                    \
     launch_fp8<L>(table, blocks, stream, ev, runs, n_runs, total_slices, page_bytes,         \
-                  rows_per_plane, kv_heads, rows_per_page, amax_table);                      \
+                  rows_per_plane, kv_heads, rows_per_page, amax_table, linear_src);          \
     return hipGetLastError();
   switch (lanes_per_row) {
     PBE_FP8_CASE(1)

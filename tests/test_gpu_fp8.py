@@ -186,3 +186,39 @@ def test_fp8_destination_beyond_4_gib(torch_cuda):
     got_sc = scales.view(n_dst, scale_page)[idx].cpu().numpy().reshape(-1)
     assert np.array_equal(got, dst_exp), first_diff(got, dst_exp)
     assert np.array_equal(got_sc, sc_exp), first_diff(got_sc, sc_exp)
+
+
+@pytest.mark.parametrize("mode", [P.PBE_FP8_SCALE_PER_TOKEN_HEAD, P.PBE_FP8_SCALE_TABLE])
+@pytest.mark.parametrize("layers,kv_heads,head_dim,n_runs,n_pages", [
+    (4, 2, 8, 40, 200),        # one lane per row: rows per slice exceed the wave
+    (2, 2, 64, 3, 30),
+    (3, 2, 128, 100, 400),
+    (1, 1, 512, 20, 60),       # 64 lanes per row
+    (2, 2, 64, 512, 1100),     # the contiguous-source path's run limit
+    (2, 2, 64, 513, 1100),     # one run past it: the general path
+    (1, 1, 8, 30, 120),        # 512-byte source pages: not whole slices, general path
+])
+def test_fp8_contiguous_sources(torch_cuda, mode, layers, kv_heads, head_dim, n_runs, n_pages):
+    """One prefill's pages in one source region, cut into runs whose
+    destinations are shuffled one page apart: the FP8 kernel's contiguous-
+    source path (a slice's loads before its run) where the pages hold whole
+    slices and the list has at most 512 runs, the general path otherwise."""
+    torch = torch_cuda
+    g = W.Geometry(layers, kv_heads, head_dim)
+    rng = np.random.default_rng(n_runs * 7 + head_dim)
+    cuts = np.sort(rng.choice(np.arange(1, n_pages), n_runs - 1, replace=False))
+    lengths = np.diff(np.concatenate(([0], cuts, [n_pages])))
+    starts = np.empty(n_runs, np.int64)
+    at = 0
+    for r in rng.permutation(n_runs):
+        starts[r] = at
+        at += lengths[r] + 1
+    dst_pages = np.concatenate([np.arange(s, s + n) for s, n in zip(starts, lengths)])
+    pools = Fp8Pools(torch, g, max(n_pages, at))
+    fill_bf16(torch, pools.src, 1.0, n_runs, 0.01, 40.0)
+    src = (np.arange(n_pages) * g.stride).astype(np.int32)
+    dst = (dst_pages * g.stride).astype(np.int32)
+    assert len(P.build_runs(src, dst, pools.kv)) == n_runs
+    amax = rng.uniform(2.5, 5.0, (2 * g.layers, g.kv_heads))
+    say(f"fp8 contiguous sources mode={mode} L={layers} H={kv_heads} D={head_dim} runs={n_runs}")
+    _check(torch, pools, src, dst, mode, amax)
