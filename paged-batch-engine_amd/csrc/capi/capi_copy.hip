@@ -30,6 +30,23 @@ struct Resolved {
   // slice s at linear_src + s * linear_slice without looking the run up
   // first; slices are counted in linear_slice); else 0.
   uint64_t linear_src = 0;
+  // With linear_src: the runs' first slices as a compact array, which the
+  // kernel's one-region search probes (4 bytes per run instead of one
+  // 32-byte record per probe). Device images place it after the records.
+  std::vector<uint32_t> starts;
+
+  size_t image_bytes() const { return runs.size() * sizeof(pbe::DevRun) + starts.size() * 4; }
+  void image(void* dst) const {
+    std::memcpy(dst, runs.data(), runs.size() * sizeof(pbe::DevRun));
+    if (!starts.empty())
+      std::memcpy(static_cast<char*>(dst) + runs.size() * sizeof(pbe::DevRun), starts.data(),
+                  starts.size() * 4);
+  }
+  const uint32_t* starts_in(const void* dev_image) const {
+    return starts.empty() ? nullptr
+                          : reinterpret_cast<const uint32_t*>(static_cast<const char*>(dev_image) +
+                                                              runs.size() * sizeof(pbe::DevRun));
+  }
 };
 
 // Builds device run entries for either kernel. src pages are src_page_bytes
@@ -96,6 +113,9 @@ int resolve_runs(const pbe_arena_view& src, const pbe_arena_view& dst, uint64_t 
   }
   out->info.slices = slices;
   out->linear_src = linear ? out->runs.front().src : 0;
+  out->starts.clear();
+  if (linear)
+    for (const pbe::DevRun& d : out->runs) out->starts.push_back(d.slice_begin);
   return PBE_OK;
 }
 
@@ -104,9 +124,11 @@ int upload_runlist(Resolved& res, int device, bool fp8, bool has_scales, uint64_
   PBE_DEVICE_SCOPE(device);
   pbe_runlist* list = new (std::nothrow) pbe_runlist;
   if (!list) return fail(PBE_ERR_NOMEM, "run list object");
-  const size_t bytes = res.runs.size() * sizeof(pbe::DevRun);
+  const size_t bytes = res.image_bytes();
+  std::vector<char> image(bytes);
+  res.image(image.data());
   hipError_t e = hipMalloc(&list->runs, bytes);
-  if (e == hipSuccess) e = hipMemcpy(list->runs, res.runs.data(), bytes, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(list->runs, image.data(), bytes, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
     if (list->runs) (void)hipFree(list->runs);
     delete list;
@@ -119,6 +141,7 @@ int upload_runlist(Resolved& res, int device, bool fp8, bool has_scales, uint64_
   list->total_slices = (uint32_t)res.info.slices;
   list->page_bytes = page_bytes;
   list->linear_src = res.linear_src;
+  list->starts = res.starts_in(list->runs);
   list->info = res.info;
   list->kv = kv;
   *out = list;
@@ -204,8 +227,9 @@ int pbe_handoff_copy_timed(const pbe_runlist* list, void* stream, void* start_ev
   if (list->fp8) return fail(PBE_ERR_INVALID, "FP8 run list passed to the BF16 copy");
   PBE_DEVICE_SCOPE(list->device);
   const pbe::LaunchEvents ev{static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event)};
-  PBE_HIP(pbe::launch_copy_runs(list->runs, list->n_runs, list->total_slices, list->page_bytes,
-                                list->linear_src, ev, static_cast<hipStream_t>(stream)));
+  PBE_HIP(pbe::launch_copy_runs(list->runs, list->starts, list->n_runs, list->total_slices,
+                                list->page_bytes, list->linear_src, ev,
+                                static_cast<hipStream_t>(stream)));
   return PBE_OK;
 }
 
@@ -233,7 +257,8 @@ int pbe_handoff_copy_fp8_timed(const pbe_runlist* list, int scale_mode, const fl
   const uint32_t rows_per_plane = (uint32_t)(kv.page_tokens * kv.kv_heads);
   const pbe::LaunchEvents ev{static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event)};
   PBE_HIP(pbe::launch_copy_runs_fp8(
-      list->runs, list->n_runs, list->total_slices, list->page_bytes, (uint32_t)kv.head_dim / 8u,
+      list->runs, list->starts, list->n_runs, list->total_slices, list->page_bytes,
+      (uint32_t)kv.head_dim / 8u,
       rows_per_plane, (uint32_t)kv.kv_heads, rows_per_plane * 2u * (uint32_t)kv.layers,
       scale_mode == PBE_FP8_SCALE_TABLE, amax_table, list->linear_src, ev,
       static_cast<hipStream_t>(stream)));
@@ -371,11 +396,13 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
   std::lock_guard<std::mutex> lock(st.mu);
   void* dev = nullptr;
   StagingSlot* slot = nullptr;
-  rc = stage(st, res.runs.data(), res.runs.size() * sizeof(pbe::DevRun), s, &slot, &dev);
+  std::vector<char> image(res.image_bytes());
+  res.image(image.data());
+  rc = stage(st, image.data(), image.size(), s, &slot, &dev);
   if (rc != PBE_OK) return rc;
-  PBE_HIP(pbe::launch_copy_runs(static_cast<const pbe::DevRun*>(dev), (uint32_t)n_runs,
-                                (uint32_t)res.info.slices, 2ull * shape->layers * half,
-                                res.linear_src, pbe::LaunchEvents{}, s));
+  PBE_HIP(pbe::launch_copy_runs(static_cast<const pbe::DevRun*>(dev), res.starts_in(dev),
+                                (uint32_t)n_runs, (uint32_t)res.info.slices,
+                                2ull * shape->layers * half, res.linear_src, pbe::LaunchEvents{}, s));
   rc = stage_done(*slot, s);
   if (rc != PBE_OK) return rc;
   if (copied) *copied = res.info.src_bytes;
@@ -469,8 +496,9 @@ int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream
     StagingSlot* slot = nullptr;
     rc = stage(st, runs.data(), runs.size() * sizeof(pbe::DevRun), s, &slot, &dev);
     if (rc != PBE_OK) return rc;
-    PBE_HIP(pbe::launch_copy_runs(static_cast<const pbe::DevRun*>(dev), (uint32_t)runs.size(),
-                                  (uint32_t)slices, 16, 0, pbe::LaunchEvents{}, s));
+    PBE_HIP(pbe::launch_copy_runs(static_cast<const pbe::DevRun*>(dev), nullptr,
+                                  (uint32_t)runs.size(), (uint32_t)slices, 16, 0,
+                                  pbe::LaunchEvents{}, s));
     return stage_done(*slot, s);
   }
   // Otherwise: split ops so that every wave moves at most kOpPieceBytes.

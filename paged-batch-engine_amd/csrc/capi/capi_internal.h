@@ -152,6 +152,7 @@ struct pbe_runlist {
   uint32_t total_slices = 0;
   uint64_t page_bytes = 0;      // source bytes per page
   uint64_t linear_src = 0;      // see pbe::launch_copy_runs
+  const uint32_t* starts = nullptr;  // with linear_src: the runs' first slices, inside `runs`
   pbe_runlist_info info{};
   pbe_kv_shape kv{};
 };

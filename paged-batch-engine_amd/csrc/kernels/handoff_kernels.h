@@ -75,13 +75,16 @@ hipError_t launch_copy_runs_kernarg(const KernargRunList& list, hipStream_t stre
 // kLinearSliceBytes and there are at most kLinearMaxRuns runs (then slice s,
 // counted in kLinearSliceBytes, reads linear_src + s * kLinearSliceBytes,
 // known without the run list). Otherwise slices are kCopySliceBytes.
-hipError_t launch_copy_runs(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
-                            uint64_t page_bytes, uint64_t linear_src, const LaunchEvents& events,
-                            hipStream_t stream);
+// starts: null, or (with linear_src) the runs' slice_begin values as a
+// compact device array, which the one-region search probes.
+hipError_t launch_copy_runs(const DevRun* runs, const uint32_t* starts, uint32_t n_runs,
+                            uint32_t total_slices, uint64_t page_bytes, uint64_t linear_src,
+                            const LaunchEvents& events, hipStream_t stream);
 
 // linear_src: as for launch_copy_runs, with slices of kFp8SliceBytes source
 // bytes.
-hipError_t launch_copy_runs_fp8(const DevRun* runs, uint32_t n_runs, uint32_t total_slices,
+hipError_t launch_copy_runs_fp8(const DevRun* runs, const uint32_t* starts, uint32_t n_runs,
+                                uint32_t total_slices,
                                 uint64_t page_bytes, uint32_t lanes_per_row,
                                 uint32_t rows_per_plane, uint32_t kv_heads,
                                 uint32_t rows_per_page, bool table, const float* amax_table,
