@@ -378,6 +378,22 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
   if (rc != PBE_OK) return rc;
   PBE_DEVICE_SCOPE(device);
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (res.linear_src && (uint64_t)n_runs <= pbe::kKernargLinearRuns) {
+    // A one-region plan rides in the kernel arguments as run starts and
+    // destinations (up to 256 runs): no staging copy, no fence.
+    pbe::KernargLinearList list{};
+    list.n_runs = (uint32_t)n_runs;
+    list.total_slices = (uint32_t)res.info.slices;
+    list.linear_src = res.linear_src;
+    std::fill(std::begin(list.starts), std::end(list.starts), 0xffffffffu);
+    for (size_t i = 0; i < res.runs.size(); ++i) {
+      list.starts[i] = res.runs[i].slice_begin;
+      list.dst[i] = res.runs[i].dst;
+    }
+    PBE_HIP(pbe::launch_copy_runs_kernarg_linear(list, s));
+    if (copied) *copied = res.info.src_bytes;
+    return PBE_OK;
+  }
   if ((uint64_t)n_runs <= pbe::kKernargRuns) {
     // Short lists ride in the kernel arguments: no staging copy, no fence.
     pbe::KernargRunList list{};

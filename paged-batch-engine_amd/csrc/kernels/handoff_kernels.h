@@ -70,6 +70,21 @@ static_assert(sizeof(KernargRunList) <= 4096 - 256, "kernel arguments are limite
 // kCopySliceBytes), 256-thread workgroups.
 hipError_t launch_copy_runs_kernarg(const KernargRunList& list, hipStream_t stream);
 
+// Kernel-argument form of a one-region plan (linear_src set): only what that
+// path reads, so up to 256 runs fit: each run's first slice and its first
+// destination byte. Slices are kLinearSliceBytes. Slots past n_runs hold
+// starts 0xffffffff (the kernel's search reads all 256).
+constexpr uint32_t kKernargLinearRuns = 256;
+struct KernargLinearList {
+  uint32_t n_runs;
+  uint32_t total_slices;
+  uint64_t linear_src;
+  uint32_t starts[kKernargLinearRuns];
+  uint64_t dst[kKernargLinearRuns];
+};
+static_assert(sizeof(KernargLinearList) <= 4096 - 256, "kernel arguments are limited to 4 KiB");
+hipError_t launch_copy_runs_kernarg_linear(const KernargLinearList& list, hipStream_t stream);
+
 // linear_src: 0, or the first run's source address when every run's source
 // directly follows the previous run's, every run holds whole slices of
 // kLinearSliceBytes and there are at most kLinearMaxRuns runs (then slice s,

@@ -169,6 +169,39 @@ __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_kernarg_kernel(con
                  list.linear_src);
 }
 
+// The one-region path with its runs in the kernel arguments: the slice's
+// loads go out first, then a binary search over the runs' first slices with
+// scalar loads from the argument segment (counted apart from the copy's
+// loads, so the search runs while the data is in flight), then the stores.
+__global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_kernarg_linear_kernel(
+    const KernargLinearList list) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t s = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + threadIdx.x / kWave);
+  if (s >= list.total_slices) return;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<void*>(list.linear_src + (uint64_t)s * kLinearSliceBytes), (short)0,
+      kLinearSliceBytes, 0x00020000);
+  u32x4 v[kLinearUnroll];
+#pragma unroll
+  for (int u = 0; u < kLinearUnroll; ++u)
+    v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, (u * kWave + lane) * 16u, 0, kLoadPolicy);
+  // largest r with starts[r] <= s (starts[0] = 0; slots past n_runs hold
+  // 0xffffffff): eight halving steps over the 256 slots, straight-line so
+  // the loads above stay first
+  uint32_t lo = 0;
+#pragma unroll
+  for (uint32_t step = kKernargLinearRuns / 2; step >= 1; step /= 2) {
+    const uint32_t mid = lo + step;  // <= 255
+    lo = list.starts[mid] <= s ? mid : lo;
+  }
+  const uint64_t dst = list.dst[lo] + (uint64_t)(s - list.starts[lo]) * kLinearSliceBytes;
+  const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+      reinterpret_cast<void*>(dst), (short)0, kLinearSliceBytes, 0x00020000);
+#pragma unroll
+  for (int u = 0; u < kLinearUnroll; ++u)
+    __builtin_amdgcn_raw_buffer_store_b128(v[u], rd, (u * kWave + lane) * 16u, 0, kStorePolicy);
+}
+
 // Fused BF16 -> FP8 handoff. A row is one (token, kv head) of one K or V
 // plane: head_dim BF16 values = kLanesPerRow lanes x 8 values. Rows are laid
 // out [layer][K|V][token][head] within a page on both sides, so a row's index
@@ -364,6 +397,16 @@ hipError_t launch_copy_runs_kernarg(const KernargRunList& list, hipStream_t stre
   const uint32_t waves = list.total_slices ? list.total_slices : 1u;
   hipLaunchKernelGGL(copy_runs_kernarg_kernel, dim3((waves + kWavesPerBlock - 1) / kWavesPerBlock),
                      dim3(kThreadsPerBlock), 0, stream, list);
+  return hipGetLastError();
+}
+
+hipError_t launch_copy_runs_kernarg_linear(const KernargLinearList& list, hipStream_t stream) {
+  if (list.n_runs == 0 || list.n_runs > kKernargLinearRuns || !list.linear_src)
+    return hipErrorInvalidValue;
+  const uint32_t waves = list.total_slices ? list.total_slices : 1u;
+  hipLaunchKernelGGL(copy_runs_kernarg_linear_kernel,
+                     dim3((waves + kWavesPerBlock - 1) / kWavesPerBlock), dim3(kThreadsPerBlock), 0,
+                     stream, list);
   return hipGetLastError();
 }
 
