@@ -4,7 +4,7 @@
 // bounded by what HBM gives a pure read stream and a pure write stream of the
 // same size. These two kernels are the copy kernel's halves at its geometry
 // on a one-region plan (config 2): one wave per 1 KiB slice, 64 lanes x one
-// 16-byte vector, 256-thread workgroups, the same
+// 16-byte vector, 512-thread workgroups, the same
 // buffer cache-policy bits (loads nt; stores sc1 + nt). bench.py times them
 // on the config-2 byte count beside the handoff so the ceiling is measured in
 // every run rather than asserted. They are not part of the handoff library:
@@ -18,15 +18,16 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWave = 64;
 constexpr int kThreads = 256;
+constexpr int kCopyThreads = 512;  // the product kernel's workgroup on a one-region plan
 constexpr int kUnroll = 1;
 constexpr uint32_t kSlice = kWave * 16u * kUnroll;  // 1 KiB per wave, as the product kernel on config 2
 constexpr int kLoadPolicy = 0x02;                   // nt
 constexpr int kStorePolicy = 0x12;                  // sc1 + nt
 
-__global__ __launch_bounds__(kThreads) void stream_read_kernel(const uint8_t* p, uint64_t bytes,
+__global__ __launch_bounds__(kCopyThreads) void stream_read_kernel(const uint8_t* p, uint64_t bytes,
                                                                u32x4* sink) {
   const uint32_t lane = threadIdx.x % kWave;
-  const uint64_t s = (uint64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
+  const uint64_t s = (uint64_t)blockIdx.x * (kCopyThreads / kWave) + threadIdx.x / kWave;
   const uint64_t off = s * kSlice;
   if (off >= bytes) return;
   const uint64_t left = bytes - off;
@@ -44,10 +45,10 @@ __global__ __launch_bounds__(kThreads) void stream_read_kernel(const uint8_t* p,
   if (acc.x == 0x9e3779b9u && acc.y == 0x7f4a7c15u && acc.z == 0x85ebca6bu) sink[lane] = acc;
 }
 
-__global__ __launch_bounds__(kThreads) void stream_write_kernel(uint8_t* p, uint64_t bytes,
+__global__ __launch_bounds__(kCopyThreads) void stream_write_kernel(uint8_t* p, uint64_t bytes,
                                                                 uint32_t seed) {
   const uint32_t lane = threadIdx.x % kWave;
-  const uint64_t s = (uint64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
+  const uint64_t s = (uint64_t)blockIdx.x * (kCopyThreads / kWave) + threadIdx.x / kWave;
   const uint64_t off = s * kSlice;
   if (off >= bytes) return;
   const uint64_t left = bytes - off;
@@ -63,10 +64,10 @@ __global__ __launch_bounds__(kThreads) void stream_write_kernel(uint8_t* p, uint
 // The copy kernel's geometry and cache policies over one contiguous span with
 // no run list: wave w copies slice w. The difference to the product kernel on
 // one contiguous run is the cost of finding the run.
-__global__ __launch_bounds__(kThreads) void slice_copy_kernel(const uint8_t* src, uint8_t* dst,
+__global__ __launch_bounds__(kCopyThreads) void slice_copy_kernel(const uint8_t* src, uint8_t* dst,
                                                               uint64_t bytes) {
   const uint32_t lane = threadIdx.x % kWave;
-  const uint64_t s = (uint64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
+  const uint64_t s = (uint64_t)blockIdx.x * (kCopyThreads / kWave) + threadIdx.x / kWave;
   const uint64_t off = s * kSlice;
   if (off >= bytes) return;
   const uint64_t left = bytes - off;
@@ -177,7 +178,7 @@ __global__ __launch_bounds__(kThreads) void stream_read_steps_kernel(
 
 dim3 grid_for(uint64_t bytes) {
   const uint64_t waves = (bytes + kSlice - 1) / kSlice;
-  return dim3((unsigned)((waves + kThreads / kWave - 1) / (kThreads / kWave)));
+  return dim3((unsigned)((waves + kCopyThreads / kWave - 1) / (kCopyThreads / kWave)));
 }
 
 }  // namespace
@@ -190,7 +191,7 @@ extern "C" {
 int pbe_ceiling_read(const void* p, uint64_t bytes, void* sink, void* stream, void* start,
                      void* stop) {
   if (!p || !sink || bytes == 0 || (bytes >> 44)) return (int)hipErrorInvalidValue;
-  hipExtLaunchKernelGGL(stream_read_kernel, grid_for(bytes), dim3(kThreads), 0,
+  hipExtLaunchKernelGGL(stream_read_kernel, grid_for(bytes), dim3(kCopyThreads), 0,
                         (hipStream_t)stream, (hipEvent_t)start, (hipEvent_t)stop, 0,
                         (const uint8_t*)p, bytes, (u32x4*)sink);
   return (int)hipGetLastError();
@@ -200,7 +201,7 @@ int pbe_ceiling_read(const void* p, uint64_t bytes, void* sink, void* stream, vo
 int pbe_ceiling_write(void* p, uint64_t bytes, uint32_t seed, void* stream, void* start,
                       void* stop) {
   if (!p || bytes == 0 || (bytes >> 44)) return (int)hipErrorInvalidValue;
-  hipExtLaunchKernelGGL(stream_write_kernel, grid_for(bytes), dim3(kThreads), 0,
+  hipExtLaunchKernelGGL(stream_write_kernel, grid_for(bytes), dim3(kCopyThreads), 0,
                         (hipStream_t)stream, (hipEvent_t)start, (hipEvent_t)stop, 0,
                         (uint8_t*)p, bytes, seed);
   return (int)hipGetLastError();
@@ -211,7 +212,7 @@ int pbe_ceiling_write(void* p, uint64_t bytes, uint32_t seed, void* stream, void
 int pbe_ceiling_slice_copy(const void* src, void* dst, uint64_t bytes, void* stream, void* start,
                            void* stop) {
   if (!src || !dst || bytes == 0 || (bytes >> 44)) return (int)hipErrorInvalidValue;
-  hipExtLaunchKernelGGL(slice_copy_kernel, grid_for(bytes), dim3(kThreads), 0, (hipStream_t)stream,
+  hipExtLaunchKernelGGL(slice_copy_kernel, grid_for(bytes), dim3(kCopyThreads), 0, (hipStream_t)stream,
                         (hipEvent_t)start, (hipEvent_t)stop, 0, (const uint8_t*)src, (uint8_t*)dst,
                         bytes);
   return (int)hipGetLastError();

@@ -6,6 +6,11 @@
 namespace pbe {
 
 constexpr int kThreadsPerBlock = 256;
+// Workgroup of the one-region path (1 KiB slices): 8 waves, half as many
+// workgroups to dispatch. MI355X, config 2: 46.0 us against 46.4 us with 256
+// threads and 46.9 us with 128; config 3 (general path) keeps 256 threads
+// (119.2 us against 121.6 us with 512).
+constexpr int kLinearThreadsPerBlock = 512;
 // Slice (the bytes one wave moves) of the identity copy, by path. Plans whose
 // sources form one region take 1 KiB slices (one 16-byte vector per lane):
 // the kernel issues a slice's loads before it looks its run up. Other plans

@@ -135,6 +135,7 @@ __device__ __forceinline__ void copy_slice_linear_src(const DevRun* __restrict__
 // Identity copy of every run: the device form of the reference's per-run
 // cudaMemcpyAsync loop (split_pd_engine.cpp:96-108). Wave w copies global
 // slice w; it finds its run with the wave-parallel search over the run list.
+template <int kThreads>
 __device__ __forceinline__ void copy_runs_body(const DevRun* __restrict__ runs,
                                                const uint32_t* __restrict__ starts, uint32_t n_runs,
                                                uint32_t total_slices, uint64_t page_bytes,
@@ -144,7 +145,7 @@ __device__ __forceinline__ void copy_runs_body(const DevRun* __restrict__ runs,
   // and the buffer resources in SGPRs (a resource the compiler cannot prove
   // uniform is rebuilt per lane in a readfirstlane loop around every load
   // and store).
-  const uint32_t s = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + threadIdx.x / kWave);
+  const uint32_t s = __builtin_amdgcn_readfirstlane(blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave);
   if (s >= total_slices) return;
   if (linear_src) {
     copy_slice_linear_src(runs, starts, n_runs, s, linear_src, lane);
@@ -156,27 +157,30 @@ __device__ __forceinline__ void copy_runs_body(const DevRun* __restrict__ runs,
   copy_slice(run.src + rel, run.dst + rel, (uint64_t)run.pages * page_bytes - rel, lane);
 }
 
-__global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_kernel(
+// kThreads: kLinearThreadsPerBlock for one-region plans, else kThreadsPerBlock.
+template <int kThreads>
+__global__ __launch_bounds__(kThreads) void copy_runs_kernel(
     const DevRun* __restrict__ runs, const uint32_t* __restrict__ starts, uint32_t n_runs,
     uint32_t total_slices, uint64_t page_bytes, uint64_t linear_src) {
-  copy_runs_body(runs, starts, n_runs, total_slices, page_bytes, linear_src);
+  copy_runs_body<kThreads>(runs, starts, n_runs, total_slices, page_bytes, linear_src);
 }
 
 // The same copy with the run list in the kernel arguments (no staging copy).
 // An aggregate kernel argument stays in the kernarg segment and is read there.
 __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_kernarg_kernel(const KernargRunList list) {
-  copy_runs_body(list.runs, nullptr, list.n_runs, list.total_slices, list.page_bytes,
-                 list.linear_src);
+  copy_runs_body<kThreadsPerBlock>(list.runs, nullptr, list.n_runs, list.total_slices,
+                                   list.page_bytes, list.linear_src);
 }
 
 // The one-region path with its runs in the kernel arguments: the slice's
 // loads go out first, then a binary search over the runs' first slices with
 // scalar loads from the argument segment (counted apart from the copy's
 // loads, so the search runs while the data is in flight), then the stores.
-__global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_kernarg_linear_kernel(
+__global__ __launch_bounds__(kLinearThreadsPerBlock) void copy_runs_kernarg_linear_kernel(
     const KernargLinearList list) {
   const uint32_t lane = threadIdx.x % kWave;
-  const uint32_t s = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + threadIdx.x / kWave);
+  const uint32_t s = __builtin_amdgcn_readfirstlane(blockIdx.x * (kLinearThreadsPerBlock / kWave) +
+                                                    threadIdx.x / kWave);
   if (s >= list.total_slices) return;
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       reinterpret_cast<void*>(list.linear_src + (uint64_t)s * kLinearSliceBytes), (short)0,
@@ -404,8 +408,9 @@ hipError_t launch_copy_runs_kernarg_linear(const KernargLinearList& list, hipStr
   if (list.n_runs == 0 || list.n_runs > kKernargLinearRuns || !list.linear_src)
     return hipErrorInvalidValue;
   const uint32_t waves = list.total_slices ? list.total_slices : 1u;
+  constexpr uint32_t kWavesLinear = kLinearThreadsPerBlock / kWave;
   hipLaunchKernelGGL(copy_runs_kernarg_linear_kernel,
-                     dim3((waves + kWavesPerBlock - 1) / kWavesPerBlock), dim3(kThreadsPerBlock), 0,
+                     dim3((waves + kWavesLinear - 1) / kWavesLinear), dim3(kLinearThreadsPerBlock), 0,
                      stream, list);
   return hipGetLastError();
 }
@@ -414,9 +419,18 @@ hipError_t launch_copy_runs(const DevRun* runs, const uint32_t* starts, uint32_t
                             uint32_t total_slices, uint64_t page_bytes, uint64_t linear_src,
                             const LaunchEvents& ev, hipStream_t stream) {
   const uint32_t waves = total_slices ? total_slices : 1u;
-  hipExtLaunchKernelGGL(copy_runs_kernel, dim3((waves + kWavesPerBlock - 1) / kWavesPerBlock),
-                        dim3(kThreadsPerBlock), 0, stream, ev.start, ev.stop, 0, runs, starts,
-                        n_runs, total_slices, page_bytes, linear_src);
+  if (linear_src) {
+    constexpr uint32_t kWavesLinear = kLinearThreadsPerBlock / kWave;
+    hipExtLaunchKernelGGL(copy_runs_kernel<kLinearThreadsPerBlock>,
+                          dim3((waves + kWavesLinear - 1) / kWavesLinear),
+                          dim3(kLinearThreadsPerBlock), 0, stream, ev.start, ev.stop, 0, runs,
+                          starts, n_runs, total_slices, page_bytes, linear_src);
+  } else {
+    hipExtLaunchKernelGGL(copy_runs_kernel<kThreadsPerBlock>,
+                          dim3((waves + kWavesPerBlock - 1) / kWavesPerBlock),
+                          dim3(kThreadsPerBlock), 0, stream, ev.start, ev.stop, 0, runs, starts,
+                          n_runs, total_slices, page_bytes, linear_src);
+  }
   return hipGetLastError();
 }
 
