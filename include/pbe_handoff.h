@@ -256,10 +256,14 @@ int pbe_handoff_copy_fp8_timed(const pbe_runlist* list, int scale_mode, const fl
 
 /* ---- one-call form of copy_shared_kv's data path -----------------------
  * Validates ids against the arena (as split_pd_engine.cpp:70-77), coalesces,
- * builds and uploads a run list, launches one copy and returns the copied
- * bytes in *copied (the reference's return value, split_pd_engine.cpp:107,114).
- * The run list is released after the launch completes on `stream`; the call
- * does not wait for the copy. */
+ * builds a run list, launches one copy and returns the copied bytes in
+ * *copied (the reference's return value, split_pd_engine.cpp:107,114). The
+ * run list travels in the kernel arguments when the sources form one region
+ * and it has at most 256 runs, or when it has at most 112 runs: no staging
+ * copy, so such calls can be captured into a HIP graph. Longer lists go
+ * through the library's staging ring (released after the launch completes on
+ * `stream`); those calls refuse a capturing stream with
+ * PBE_ERR_UNSUPPORTED. The call does not wait for the copy. */
 int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids,
                        const int32_t* dst_ids, int64_t n, const pbe_kv_shape* shape,
                        int device, void* stream, uint64_t* copied);

@@ -406,7 +406,7 @@ int pbe_copy_shared_kv(const pbe_arena_view* arena, const int32_t* src_ids, cons
     if (copied) *copied = res.info.src_bytes;
     return PBE_OK;
   }
-  rc = refuse_capture(s, "pbe_copy_shared_kv with more than 112 runs");
+  rc = refuse_capture(s, "pbe_copy_shared_kv with a run list longer than the kernel arguments hold");
   if (rc != PBE_OK) return rc;
   Staging& st = staging_for(device);
   std::lock_guard<std::mutex> lock(st.mu);

@@ -74,8 +74,8 @@ def test_decode_step_replays_from_a_graph(torch_cuda):
 
 
 def test_staged_calls_refuse_capture(torch_cuda):
-    """pbe_copy_ops and pbe_copy_shared_kv with more than 112 spans / runs
-    stage their lists in a reused ring, so under capture they return
+    """pbe_copy_ops with more than 112 spans and pbe_copy_shared_kv with more
+    than 112 runs whose sources are scattered stage their lists in a reused ring, so under capture they return
     PBE_ERR_UNSUPPORTED before queueing anything; the prebuilt run list
     captured in the same graph still replays correctly. A short op list rides
     in the kernel arguments and is captured like a prebuilt run list."""
@@ -205,3 +205,36 @@ def test_decode_loop_step_replays_from_a_graph(torch_cuda, fused):
         want = O.paged_decode_pools(kp, vp, True, ks, vs, H, D, qh, tables, lens)
         got = bf16_to_f64(out.cpu().numpy().view(np.uint16))
         assert close(got, want).all(), step
+
+
+def test_one_region_plan_of_150_runs_is_captured(torch_cuda):
+    """A one-region plan (one prefill's pages) of 150 runs travels in the
+    kernel arguments as run starts and destinations, so pbe_copy_shared_kv is
+    captured (more than the 112 runs the record form holds) and every replay
+    matches the oracle."""
+    from tests.test_gpu_handoff import _contiguous_source_plan, _kv
+    torch = torch_cuda
+    g = W.Geometry(2, 2, 64)
+    kv = _kv(g)
+    src, dst, total = _contiguous_source_plan(g, 150, 400, 77)
+    assert len(P.build_runs(src, dst, kv)) == 150
+    say("graph capture of a one-region 150-run pbe_copy_shared_kv")
+    arena = torch.empty((total + 3) * g.page_bytes(), dtype=torch.uint8, device="cuda")
+    view = P.view_of(arena.data_ptr(), arena.numel())
+    fill_bf16(torch, arena, 1.0, 5)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            P.copy_shared_kv(view, src, dst, kv, 0, side.cuda_stream)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        fill_bf16(torch, arena, 1.0, 60 + rep)
+        torch.cuda.synchronize()
+        expected = arena.cpu().numpy().copy()
+        O.copy_handoff(expected, src, dst, g.half(), g.layers)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = arena.cpu().numpy()
+        assert np.array_equal(got, expected), (rep, first_diff(got, expected))
