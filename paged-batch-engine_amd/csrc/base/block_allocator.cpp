@@ -84,12 +84,31 @@ BlockAllocator::BlockAllocator(int32_t block_size, int32_t num_kv_heads, int32_t
   if (num_blocks_ <= 0 || static_cast<int64_t>(num_blocks_) * block_size_ > INT32_MAX)
     throw std::invalid_argument("Shared arena exceeds int32 slot mapping range");
   pool_id_ = next_pool_id();
-  ref_counts_.assign(num_blocks_, 0);
-  generations_.assign(num_blocks_, 0);
+  // Only page ids (multiples of 2L) are ever handed out here, so the counts
+  // are kept per page: dense for the pages of one request, where an array
+  // per addressable id put every page's entry on its own cache line.
+  id_stride_ = 2 * group_->layers();
+  // id / stride as (id * mul) >> shift with mul = floor(2^shift / stride) + 1
+  // and shift = 32 + ceil(log2 stride): exact for every 32-bit id (the
+  // round-up method for unsigned division by a constant).
+  int lg = 0;
+  while ((1ll << lg) < id_stride_) ++lg;
+  div_shift_ = 32 + lg;
+  div_mul_ = (1ull << div_shift_) / static_cast<uint64_t>(id_stride_) + 1;
+  const int32_t pages = (num_blocks_ + id_stride_ - 1) / id_stride_;
+  ref_counts_.assign(pages, 0);
+  generations_.assign(pages, 0);
 }
 
 void BlockAllocator::check_id(int32_t block_id) const {
   if (block_id < 0 || block_id >= num_blocks_) throw std::out_of_range("block_id out of range");
+}
+
+int32_t BlockAllocator::slot(int32_t block_id) const {
+  check_id(block_id);
+  if (id_stride_ == 1) return block_id;
+  const int32_t k = static_cast<int32_t>((static_cast<uint64_t>(block_id) * div_mul_) >> div_shift_);
+  return k * id_stride_ == block_id ? k : -1;
 }
 
 int32_t BlockAllocator::allocate() {
@@ -102,12 +121,13 @@ int32_t BlockAllocator::allocate() {
     id = free_queue_.front();
     free_queue_.pop_front();
   }
-  check_id(id);
-  if (ref_counts_[id] != 0) throw std::logic_error("allocated block still has outstanding references");
-  if (generations_[id] == std::numeric_limits<uint64_t>::max())
+  const int32_t k = slot(id);
+  if (k < 0) throw std::logic_error("page group handed out a non-page id");
+  if (ref_counts_[k] != 0) throw std::logic_error("allocated block still has outstanding references");
+  if (generations_[k] == std::numeric_limits<uint64_t>::max())
     throw std::logic_error("block generation exhausted");
-  ++generations_[id];
-  ref_counts_[id] = 1;
+  ++generations_[k];
+  ref_counts_[k] = 1;
   return id;
 }
 
@@ -123,27 +143,27 @@ bool BlockAllocator::allocate_many(int32_t n, std::vector<int32_t>* out) {
   const size_t first = out->size();
   const bool all = group_->allocate_many(layer_, n, out);
   for (size_t i = first; i < out->size(); ++i) {
-    const int32_t id = (*out)[i];
-    check_id(id);
-    if (ref_counts_[id] != 0) throw std::logic_error("allocated block still has outstanding references");
-    if (generations_[id] == std::numeric_limits<uint64_t>::max())
+    const int32_t k = slot((*out)[i]);
+    if (k < 0) throw std::logic_error("page group handed out a non-page id");
+    if (ref_counts_[k] != 0) throw std::logic_error("allocated block still has outstanding references");
+    if (generations_[k] == std::numeric_limits<uint64_t>::max())
       throw std::logic_error("block generation exhausted");
-    ++generations_[id];
-    ref_counts_[id] = 1;
+    ++generations_[k];
+    ref_counts_[k] = 1;
   }
   return all;
 }
 
 void BlockAllocator::incref(int32_t block_id) {
-  check_id(block_id);
-  if (ref_counts_[block_id] <= 0) throw std::logic_error("Cannot incref a free block");
-  ++ref_counts_[block_id];
+  const int32_t k = slot(block_id);
+  if (k < 0 || ref_counts_[k] <= 0) throw std::logic_error("Cannot incref a free block");
+  ++ref_counts_[k];
 }
 
 void BlockAllocator::free(int32_t block_id) {
-  check_id(block_id);
-  if (ref_counts_[block_id] <= 0) throw std::logic_error("Double free of block");
-  if (--ref_counts_[block_id] == 0) {
+  const int32_t k = slot(block_id);
+  if (k < 0 || ref_counts_[k] <= 0) throw std::logic_error("Double free of block");
+  if (--ref_counts_[k] == 0) {
     if (group_) group_->retire(layer_, block_id);
     else free_queue_.push_back(block_id);
   }
@@ -158,9 +178,9 @@ void BlockAllocator::free_many(const std::vector<int32_t>& block_ids) {
   released.reserve(block_ids.size());
   try {
     for (int32_t id : block_ids) {
-      check_id(id);
-      if (ref_counts_[id] <= 0) throw std::logic_error("Double free of block");
-      if (--ref_counts_[id] == 0) released.push_back(id);
+      const int32_t k = slot(id);
+      if (k < 0 || ref_counts_[k] <= 0) throw std::logic_error("Double free of block");
+      if (--ref_counts_[k] == 0) released.push_back(id);
     }
   } catch (...) {
     group_->retire_many(layer_, released);
@@ -170,19 +190,20 @@ void BlockAllocator::free_many(const std::vector<int32_t>& block_ids) {
 }
 
 int32_t BlockAllocator::ref_count(int32_t block_id) const {
-  check_id(block_id);
-  return ref_counts_[block_id];
+  const int32_t k = slot(block_id);
+  return k < 0 ? 0 : ref_counts_[k];
 }
 
 BlockHandle BlockAllocator::handle(int32_t block_id) const {
-  check_id(block_id);
-  if (ref_counts_[block_id] <= 0) throw std::logic_error("handle of a free block");
-  return {block_id, generations_[block_id], pool_id_};
+  const int32_t k = slot(block_id);
+  if (k < 0 || ref_counts_[k] <= 0) throw std::logic_error("handle of a free block");
+  return {block_id, generations_[k], pool_id_};
 }
 
 bool BlockAllocator::is_current(BlockHandle h) const {
-  return h.pool_id == pool_id_ && h.block_id >= 0 && h.block_id < num_blocks_ &&
-         ref_counts_[h.block_id] > 0 && generations_[h.block_id] == h.generation;
+  if (h.pool_id != pool_id_ || h.block_id < 0 || h.block_id >= num_blocks_) return false;
+  const int32_t k = slot(h.block_id);
+  return k >= 0 && ref_counts_[k] > 0 && generations_[k] == h.generation;
 }
 
 size_t BlockAllocator::key_value_bytes_per_block() const {

@@ -4,6 +4,7 @@
 #include "base/shared_kv_arena.h"
 
 #include <algorithm>
+#include <cstring>
 #include <deque>
 #include <limits>
 #include <set>
@@ -220,6 +221,9 @@ struct SharedKVPageGroup::Impl {
   // retire before every layer took it. cancelled_ahead[l] counts the null
   // entries at or after cursor[l].
   std::vector<Page*> log;
+  // The same entries' page ids (a bulk copy for a layer with no rolled-back
+  // entry ahead of its cursor).
+  std::vector<int32_t> log_ids;
   uint64_t log_base = 0;
   std::vector<uint64_t> cursor;
   std::vector<uint64_t> cancelled_ahead;
@@ -260,8 +264,10 @@ struct SharedKVPageGroup::Impl {
     const uint64_t dead = low - log_base;
     if (dead == log.size()) {
       log.clear();
+      log_ids.clear();
     } else if (dead >= 1024 && 2 * dead >= log.size()) {
       log.erase(log.begin(), log.begin() + static_cast<std::ptrdiff_t>(dead));
+      log_ids.erase(log_ids.begin(), log_ids.begin() + static_cast<std::ptrdiff_t>(dead));
     } else {
       return;
     }
@@ -329,6 +335,7 @@ struct SharedKVPageGroup::Impl {
       p.logged = true;
       p.seq = log_end();
       log.push_back(&p);
+      log_ids.push_back(id);
     }
     return id;
   }
@@ -376,7 +383,10 @@ struct SharedKVPageGroup::Impl {
         ++cancelled_ahead[l];
         cancelled = true;
       }
-      if (cancelled) log[p.seq - log_base] = nullptr;
+      if (cancelled) {
+        log[p.seq - log_base] = nullptr;
+        log_ids[p.seq - log_base] = -1;
+      }
       p.logged = false;
     }
     p.active[layer] = 0;
@@ -455,7 +465,13 @@ bool SharedKVPageGroup::allocate_many(int layer, int n, std::vector<int32_t>* ou
     const size_t at = out->size();
     out->resize(at + static_cast<size_t>(n));
     int32_t* ids = out->data() + at;
-    for (int k = 0; k < n; ++k) ids[k] = m.take_reserved(layer)->id;
+    if (m.cancelled_ahead[layer] == 0) {  // no rolled-back entry ahead: one copy
+      uint64_t& c = m.cursor[layer];
+      std::memcpy(ids, m.log_ids.data() + (c - m.log_base), static_cast<size_t>(n) * sizeof(int32_t));
+      c += static_cast<uint64_t>(n);
+    } else {
+      for (int k = 0; k < n; ++k) ids[k] = m.take_reserved(layer)->id;
+    }
     m.trim_log();
     return true;
   }

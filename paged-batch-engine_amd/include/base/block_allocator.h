@@ -164,6 +164,10 @@ class BlockAllocator {
 
  private:
   void check_id(int32_t block_id) const;
+  // Index of block_id in ref_counts_ / generations_: the id itself in
+  // local-pool mode; id / 2L in shared-arena mode, -1 for an id that is not a
+  // page id (never allocated there). Throws out_of_range like check_id.
+  int32_t slot(int32_t block_id) const;
   std::shared_ptr<SharedKVPageGroup> group_;  // shared-arena mode only
   int32_t block_size_, num_kv_heads_, head_size_, layer_ = 0;
   int32_t num_blocks_ = 0;
@@ -171,6 +175,9 @@ class BlockAllocator {
   DeviceType device_ = DeviceType::kDeviceHIP;
   int device_index_ = -1;
   KVCacheStorageSpec storage_spec_;
+  int32_t id_stride_ = 1;  // shared-arena mode: 2L (page ids only)
+  uint64_t div_mul_ = 0;   // id / id_stride_ by multiply and shift (slot())
+  int div_shift_ = 0;
   std::vector<int32_t> ref_counts_;
   std::vector<uint64_t> generations_;
   // Local-pool mode: [K pool][V pool][K scales][V scales] in one allocation.
