@@ -1545,6 +1545,21 @@ TEST_CASE("block allocator (shared arena): per-layer ids, refcounts, payload poi
   CHECK(!layers[0]->is_current(h));
   CHECK_EQ(layers[0]->shared_arena_epoch(), 9u);
   CHECK_EQ(layers[0]->shared_arena_bytes(), (size_t)(12 * Group::kPage));
+  // ids that are not page ids (not multiples of 2L = 6) are never allocated:
+  // no references, no handle, and incref/free refuse them like a free block;
+  // ids past the arena are out of range
+  for (int l = 0; l < 3; ++l) {
+    for (int id : {a + 1, a + 5, b + 3}) {
+      CHECK_EQ(layers[l]->ref_count(id), 0);
+      CHECK_THROWS_AS(layers[l]->incref(id), std::logic_error);
+      CHECK_THROWS_AS(layers[l]->free(id), std::logic_error);
+      CHECK_THROWS_AS(layers[l]->handle(id), std::logic_error);
+      CHECK(!layers[l]->is_current(base::BlockHandle{id, 1, h.pool_id}));
+    }
+    CHECK_THROWS_AS(layers[l]->ref_count(1 << 30), std::out_of_range);
+  }
+  // the page counts stay per page: b still holds one reference per layer
+  for (int l = 0; l < 3; ++l) CHECK_EQ(layers[l]->ref_count(b), 1);
 }
 
 TEST_CASE("block allocator: the pool view binds the planes without owning the allocation queue") {
