@@ -398,8 +398,81 @@ def measure_ceilings(torch, P, w, runs, kv, arena, scrub, alg: int, n: int) -> d
             "what": "contiguous copy of the same bytes, each wave loading 32 KiB into registers "
                     "before storing it (long read-only then write-only bursts)",
             "us_mean": round(p_ms * 1e3, 2), "gbps": round(alg / (p_ms * 1e-3) / 1e9, 1)}
+        out.update(wave_timeline(torch, cl, w, runs, arena, dbuf, scrub, sp, n))
     del dbuf
     return out
+
+
+def wave_timeline(torch, cl, w, runs, arena, dbuf, scrub, sp, n: int) -> dict:
+    """The copy at the product's one-region geometry (1 KiB slices, 512-thread
+    workgroups) from the plan's contiguous sources into the plan's destinations
+    and into one contiguous region, every wave stamping the 100 MHz real-time
+    counter at its start, when its load returned and when its store completed
+    (lib/libpbe_ceiling.so, timeline_copy_kernel); and an empty kernel with the
+    same grid (the dispatch alone). Medians over n launches, each after the
+    1 GiB scrub."""
+    import ctypes as C
+    import numpy as np
+    g = w.geometry
+    half, slice_bytes = g.half(), 1024
+    per_page = g.page_bytes() // slice_bytes
+    stride = 2 * g.layers
+    cl.pbe_ceiling_timeline_copy.argtypes = [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p,
+                                             C.c_void_p, C.c_void_p, C.c_void_p]
+    cl.pbe_ceiling_empty.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+    src_ids = [r[0] for r in runs]
+    assert all(src_ids[i + 1] == src_ids[i] + runs[i][2] * stride for i in range(len(runs) - 1)), \
+        "the timeline legs need the plan's sources in one region"
+    src = arena.data_ptr() + runs[0][0] * half
+    n_slices = w.pages * per_page
+    within = np.arange(per_page * max(r[2] for r in runs), dtype=np.uint64) * slice_bytes
+    plan = np.concatenate([np.uint64(arena.data_ptr() + d * half) + within[:k * per_page]
+                           for _s, d, k in runs])
+    region = np.uint64(dbuf.data_ptr()) + np.arange(n_slices, dtype=np.uint64) * slice_bytes
+    stamps = torch.empty(3 * n_slices, dtype=torch.int64, device=arena.device)
+    ev = TimingEvents(2)
+    res = {}
+    for name, table in (("plan", plan), ("contiguous", region)):
+        dst_of = torch.from_numpy(table.view(np.int64)).to(arena.device)
+        rows = []
+        for i in range(n + 2):
+            scrub.fill_(i & 0xff)
+            rc = cl.pbe_ceiling_timeline_copy(src, dst_of.data_ptr(), n_slices, stamps.data_ptr(),
+                                              sp, ev.handle(0), ev.handle(1))
+            if rc:
+                raise RuntimeError(f"timeline copy failed ({rc})")
+            torch.cuda.synchronize()
+            if i < 2:
+                continue
+            t = stamps.cpu().numpy().reshape(-1, 3).astype(np.int64)
+            t0 = t[:, 0].min()
+            done = np.sort(t[:, 2] - t0) * 0.01  # us
+            lo, hi = done[int(0.1 * n_slices)], done[int(0.9 * n_slices)]
+            rows.append([ev.elapsed_ms(0, 1) * 1e3, done[0], lo, hi, done[-1],
+                         0.8 * n_slices * 2 * slice_bytes / ((hi - lo) * 1e-6) / 1e12,
+                         np.median(t[:, 1] - t[:, 0]) * 0.01, np.median(t[:, 2] - t[:, 1]) * 0.01])
+        m = np.median(np.array(rows), axis=0)
+        res[name] = {"kernel_us": round(m[0], 2), "first_slice_done_us": round(m[1], 2),
+                     "p10_done_us": round(m[2], 2), "p90_done_us": round(m[3], 2),
+                     "last_slice_done_us": round(m[4], 2), "steady_tbps_p10_p90": round(m[5], 3),
+                     "load_wait_us_median": round(m[6], 2), "store_wait_us_median": round(m[7], 2)}
+        del dst_of
+    sink = torch.empty(4096, dtype=torch.uint8, device=arena.device)
+    ts = []
+    for i in range(n + 2):
+        rc = cl.pbe_ceiling_empty(n_slices, sink.data_ptr(), sp, ev.handle(0), ev.handle(1))
+        if rc:
+            raise RuntimeError(f"empty kernel failed ({rc})")
+        torch.cuda.synchronize()
+        if i >= 2:
+            ts.append(ev.elapsed_ms(0, 1) * 1e3)
+    ev.close()
+    return {"wave_timeline": {
+                "what": "one-region copy geometry into the plan's destinations / one contiguous "
+                        "region, every wave stamping the 100 MHz real-time counter at start, "
+                        "load return and store completion; times from the first wave's start",
+                **res},
+            "dispatch_only_us": round(float(np.median(ts)), 2)}
 
 
 LEG_ORDER = ("plan", "sorted_destination", "contiguous", "read_only", "write_only")

@@ -176,6 +176,45 @@ __global__ __launch_bounds__(kThreads) void stream_read_steps_kernel(
   if (acc.x == 0x9e3779b9u && acc.y == 0x7f4a7c15u && acc.z == 0x85ebca6bu) sink[lane] = acc;
 }
 
+// The copy kernel's one-region geometry (1 KiB slices, 512-thread
+// workgroups, loads nt, stores sc1 + nt) over a contiguous source, each
+// slice's destination taken from a per-slice table (a plan's destinations
+// without its run lookup), with lane 0 of every wave recording the 100 MHz
+// real-time counter when the wave starts, when its load has returned and when
+// its store has completed: stamps[3 * s + 0..2]. A timeline of the copy: when
+// the first slices complete (fill), the steady completion rate, and how the
+// last ones drain.
+__global__ __launch_bounds__(kCopyThreads) void timeline_copy_kernel(const uint8_t* src,
+                                                                     const uint64_t* dst_of,
+                                                                     uint32_t n_slices,
+                                                                     uint64_t* stamps) {
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t s = __builtin_amdgcn_readfirstlane(blockIdx.x * (kCopyThreads / kWave) + threadIdx.x / kWave);
+  if (s >= n_slices) return;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(src + (uint64_t)s * kSlice), (short)0, kSlice, 0x00020000);
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16u, 0, kLoadPolicy);
+  const uint64_t dst = dst_of[s];
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+  const __amdgpu_buffer_rsrc_t rd =
+      __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(dst), (short)0, kSlice, 0x00020000);
+  __builtin_amdgcn_raw_buffer_store_b128(v, rd, lane * 16u, 0, kStorePolicy);
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  const uint64_t t2 = __builtin_amdgcn_s_memrealtime();
+  if (lane == 0) {
+    stamps[3ull * s] = t0;
+    stamps[3ull * s + 1] = t1;
+    stamps[3ull * s + 2] = t2;
+  }
+}
+
+// Nothing but the dispatch: the copy's grid and workgroup on the C2 plan.
+__global__ __launch_bounds__(kCopyThreads) void empty_kernel(uint32_t n, uint32_t* sink) {
+  if (n == 0xffffffffu) sink[threadIdx.x] = blockIdx.x;
+}
+
 dim3 grid_for(uint64_t bytes) {
   const uint64_t waves = (bytes + kSlice - 1) / kSlice;
   return dim3((unsigned)((waves + kCopyThreads / kWave - 1) / (kCopyThreads / kWave)));
@@ -251,6 +290,30 @@ int pbe_ceiling_read_steps(const void* base, const uint32_t* order, uint32_t n_s
     hipExtLaunchKernelGGL(stream_read_steps_kernel<false>, grid, dim3(kThreads), 0,
                           (hipStream_t)stream, (hipEvent_t)start, (hipEvent_t)stop, 0,
                           (const uint8_t*)base, order, n_steps, steps_per_wave, (u32x4*)sink);
+  return (int)hipGetLastError();
+}
+
+// Timeline copy of n_slices 1 KiB slices from the contiguous src to
+// dst_of[s] (device table of n_slices destination addresses); stamps: device
+// buffer of 3 * n_slices uint64 (100 MHz real-time counter values).
+int pbe_ceiling_timeline_copy(const void* src, const uint64_t* dst_of, uint32_t n_slices,
+                              uint64_t* stamps, void* stream, void* start, void* stop) {
+  if (!src || !dst_of || !stamps || n_slices == 0) return (int)hipErrorInvalidValue;
+  constexpr uint32_t w = kCopyThreads / kWave;
+  hipExtLaunchKernelGGL(timeline_copy_kernel, dim3((n_slices + w - 1) / w), dim3(kCopyThreads), 0,
+                        (hipStream_t)stream, (hipEvent_t)start, (hipEvent_t)stop, 0,
+                        (const uint8_t*)src, dst_of, n_slices, stamps);
+  return (int)hipGetLastError();
+}
+
+// An empty kernel with the grid of n_slices one-slice waves in 512-thread
+// workgroups: the dispatch alone.
+int pbe_ceiling_empty(uint32_t n_slices, void* sink, void* stream, void* start, void* stop) {
+  if (!sink || n_slices == 0) return (int)hipErrorInvalidValue;
+  constexpr uint32_t w = kCopyThreads / kWave;
+  hipExtLaunchKernelGGL(empty_kernel, dim3((n_slices + w - 1) / w), dim3(kCopyThreads), 0,
+                        (hipStream_t)stream, (hipEvent_t)start, (hipEvent_t)stop, 0, n_slices,
+                        (uint32_t*)sink);
   return (int)hipGetLastError();
 }
 
