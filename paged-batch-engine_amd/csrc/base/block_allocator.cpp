@@ -88,13 +88,7 @@ BlockAllocator::BlockAllocator(int32_t block_size, int32_t num_kv_heads, int32_t
   // are kept per page: dense for the pages of one request, where an array
   // per addressable id put every page's entry on its own cache line.
   id_stride_ = 2 * group_->layers();
-  // id / stride as (id * mul) >> shift with mul = floor(2^shift / stride) + 1
-  // and shift = 32 + ceil(log2 stride): exact for every 32-bit id (the
-  // round-up method for unsigned division by a constant).
-  int lg = 0;
-  while ((1ll << lg) < id_stride_) ++lg;
-  div_shift_ = 32 + lg;
-  div_mul_ = (1ull << div_shift_) / static_cast<uint64_t>(id_stride_) + 1;
+  page_index_ = PageIndex(id_stride_);
   const int32_t pages = (num_blocks_ + id_stride_ - 1) / id_stride_;
   ref_counts_.assign(pages, 0);
   generations_.assign(pages, 0);
@@ -106,9 +100,7 @@ void BlockAllocator::check_id(int32_t block_id) const {
 
 int32_t BlockAllocator::slot(int32_t block_id) const {
   check_id(block_id);
-  if (id_stride_ == 1) return block_id;
-  const int32_t k = static_cast<int32_t>((static_cast<uint64_t>(block_id) * div_mul_) >> div_shift_);
-  return k * id_stride_ == block_id ? k : -1;
+  return id_stride_ == 1 ? block_id : page_index_.of(block_id);
 }
 
 int32_t BlockAllocator::allocate() {

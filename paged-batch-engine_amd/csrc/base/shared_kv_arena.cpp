@@ -3,6 +3,8 @@
 // fences are C-ABI events recorded on the group's stream.
 #include "base/shared_kv_arena.h"
 
+#include "base/page_index.h"
+
 #include <algorithm>
 #include <cstring>
 #include <deque>
@@ -155,14 +157,15 @@ struct SharedKVPageGroup::Impl {
   struct PageTable {
     std::vector<Page*> slots;
     int stride = 1;
+    PageIndex index;
     void init(size_t n, int page_stride) {
       slots.assign(n, nullptr);
       stride = page_stride;
+      index = PageIndex(page_stride);
     }
     Page* get(int id) const {
-      if (id < 0 || id % stride) return nullptr;
-      const size_t i = static_cast<size_t>(id / stride);
-      return i < slots.size() ? slots[i] : nullptr;
+      const int32_t i = index.of(id);
+      return i >= 0 && static_cast<size_t>(i) < slots.size() ? slots[static_cast<size_t>(i)] : nullptr;
     }
     Page* at(int id) const {
       Page* p = get(id);

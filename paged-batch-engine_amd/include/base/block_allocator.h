@@ -21,6 +21,7 @@
 
 #include "base/base.h"
 #include "base/kv_cache_format.h"
+#include "base/page_index.h"
 #include "base/shared_kv_arena.h"
 
 namespace base {
@@ -176,8 +177,7 @@ class BlockAllocator {
   int device_index_ = -1;
   KVCacheStorageSpec storage_spec_;
   int32_t id_stride_ = 1;  // shared-arena mode: 2L (page ids only)
-  uint64_t div_mul_ = 0;   // id / id_stride_ by multiply and shift (slot())
-  int div_shift_ = 0;
+  PageIndex page_index_;   // id / id_stride_ without a division (slot())
   std::vector<int32_t> ref_counts_;
   std::vector<uint64_t> generations_;
   // Local-pool mode: [K pool][V pool][K scales][V scales] in one allocation.
