@@ -27,6 +27,7 @@
 #include "serving/split_pd_admission.h"
 #include "base/block_allocator.h"
 #include "base/kv_cache_manager.h"
+#include "base/page_index.h"
 
 using namespace cache;
 
@@ -1497,6 +1498,26 @@ TEST_CASE("TakeOverSharedKV: whole-Chunk requests move without a copy; refusals 
   CHECK_EQ(v.d->leased_bytes(), 0u);
   v.p->reattach(tk3);
   TwoGroups::retire_all(*v.p, c);
+}
+
+TEST_CASE("page index: multiply-shift quotient equals id / stride, -1 off the page grid") {
+  // every id below 2^20 for every even stride 2..256 (2L for 1..128 layers),
+  // and a spread of ids up to INT32_MAX
+  std::mt19937 rng(11);
+  for (int32_t stride = 2; stride <= 256; stride += 2) {
+    const base::PageIndex pi(stride);
+    for (int32_t id = 0; id < (1 << 20); ++id)
+      REQUIRE(pi.of(id) == (id % stride == 0 ? id / stride : -1));
+    for (int k = 0; k < 20000; ++k) {
+      const int32_t id = static_cast<int32_t>(rng() & 0x7fffffffu);
+      REQUIRE(pi.of(id) == (id % stride == 0 ? id / stride : -1));
+      const int32_t page = id / stride;
+      REQUIRE(pi.of(page * stride) == page);
+    }
+    CHECK_EQ(pi.of(-stride), -1);
+    CHECK_EQ(pi.of(INT32_MAX - INT32_MAX % stride), INT32_MAX / stride);
+  }
+  CHECK_EQ(base::PageIndex(1).of(12345), 12345);
 }
 
 TEST_CASE("block allocator (shared arena): per-layer ids, refcounts, payload pointers") {
