@@ -19,9 +19,11 @@ from __future__ import annotations
 import argparse
 import csv
 import glob
+import json
 import os
 import statistics
 from collections import defaultdict
+from pathlib import Path
 
 CALIB_BYTES = 256 << 20     # the --calibrate plain copy reads and writes this much
 COPY_KERNEL = "copy_runs_kernel"
@@ -270,6 +272,43 @@ def req(root: str, grids, out: str, command: str, kernel: str = COPY_KERNEL) -> 
     print(text)
 
 
+def ceilings(bench_json: str, out: str, command: str) -> None:
+    """The headline and its ceiling legs from one bench.py line (the last JSON
+    line of its output), as a text summary."""
+    line = [l for l in Path(bench_json).read_text().splitlines() if l.startswith("{")][-1]
+    d = json.loads(line)
+    c = d["ceilings"]
+    rows = [("headline (the C2 plan)", d["latency_us"]["kernel_mean"], d["value"])]
+    for k in ("sorted_destination", "contiguous_same_bytes", "slice_copy_no_run_list",
+              "register_staged_copy"):
+        leg = c.get(k) or d.get(k)
+        if leg:
+            rows.append((k, leg["us_mean"], leg["gbps"]))
+    lines = ["# bench.py ceiling legs of the config-2 handoff (one run, mean kernel us)",
+             f"command: {command}", "",
+             f"{'leg':<32} {'us':>8} {'GB/s':>9}"]
+    lines += [f"{n:<32} {u:>8.2f} {g:>9.1f}" for n, u, g in rows]
+    v = c["vendor_memcpy"]
+    lines.append(f"{'vendor_memcpy':<32} {v['us_mean']:>8.2f} {v['gbps']:>9.1f}   "
+                 f"(after a read-only scrub: {v['us_mean_after_read_scrub']:.2f} us)")
+    lines.append(f"{'read_only / write_only':<32} {c['read_only']['us_mean']:>8.2f} / "
+                 f"{c['write_only']['us_mean']:.2f}   read then write: {c['read_then_write_us']:.2f}")
+    ws = c["write_side"]
+    lines.append(f"{'write_side (plan / contiguous)':<32} {ws['scattered_us']:>8.2f} / {ws['contiguous_us']:.2f}")
+    lines.append(f"headline_over_best_of_sorted_and_vendor: {c['headline_over_best_of_sorted_and_vendor']}")
+    lines.append(f"dispatch_only_us (empty kernel, the copy's grid): {c['dispatch_only_us']}")
+    lines += ["", "wave timeline (times from the first wave's start, us; medians over launches):",
+              f"{'':<28} {'plan':>10} {'contiguous':>11}"]
+    t = c["wave_timeline"]
+    for k in ("kernel_us", "first_slice_done_us", "p10_done_us", "p90_done_us",
+              "last_slice_done_us", "steady_tbps_p10_p90", "load_wait_us_median",
+              "store_wait_us_median"):
+        lines.append(f"{k:<28} {t['plan'][k]:>10} {t['contiguous'][k]:>11}")
+    text = "\n".join(lines) + "\n"
+    Path(out).write_text(text)
+    print(text)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -303,6 +342,10 @@ def main() -> None:
     rq.add_argument("--grid", type=int, action="append", required=True)
     rq.add_argument("--out", required=True)
     rq.add_argument("--command", required=True)
+    ce = sub.add_parser("ceilings")
+    ce.add_argument("bench_json")
+    ce.add_argument("--out", required=True)
+    ce.add_argument("--command", required=True)
     mk = sub.add_parser("markers")
     mk.add_argument("root")
     mk.add_argument("--out", required=True)
@@ -310,6 +353,9 @@ def main() -> None:
     a = ap.parse_args()
     if a.cmd == "req":
         req(a.root, a.grid, a.out, a.command)
+        return
+    if a.cmd == "ceilings":
+        ceilings(a.bench_json, a.out, a.command)
         return
     if a.cmd == "markers":
         markers(a.root, a.out, a.command)
