@@ -512,6 +512,7 @@ def _contiguous_source_plan(g: W.Geometry, n_runs: int, n_pages: int, seed: int)
 
 @pytest.mark.parametrize("n_runs,n_pages,head_dim", [
     (1, 40, 64), (37, 300, 64), (64, 64, 64), (65, 400, 64), (200, 700, 64),
+    (256, 600, 64), (257, 600, 64),        # the one-call kernel-argument list's limit
     (511, 900, 64), (512, 1024, 64), (513, 1100, 64), (900, 1500, 64),
     (60, 300, 24),                         # 3 KiB pages: three 1 KiB slices
     (60, 300, 12),                         # pages of 1.5 KiB slices: no contiguous-source path
