@@ -200,7 +200,7 @@ int pbe_runlist_create_fp8(const pbe_arena_view* src, const pbe_arena_view* dst,
   Resolved res;
   int rc = resolve_runs(*src, *dst, half16, half8, 2 * shape->layers, runs, n_runs,
                         reinterpret_cast<uint64_t>(dst_scales), dst_scales_bytes, scale_page,
-                        pbe::kFp8SliceBytes, pbe::kFp8SliceBytes, &res);
+                        pbe::kFp8SliceBytes, pbe::kFp8LinearSliceBytes, &res);
   if (rc != PBE_OK) return rc;
   return upload_runlist(res, device, true, dst_scales != nullptr, 2ull * shape->layers * half16,
                         *shape, out);

@@ -31,6 +31,13 @@ constexpr uint32_t kCopySliceBytes = 64u * 16u * kCopyUnroll;      // 2 KiB per 
 constexpr uint32_t kLinearMaxRuns = 512;
 constexpr int kFp8Unroll = 4;   // 16-byte BF16 vectors per lane per slice of the FP8 copy
 constexpr uint32_t kFp8SliceBytes = 64u * 16u * kFp8Unroll;    // 4 KiB of BF16 source per wave
+// The FP8 copy's slice on the one-region path (loads before the run lookup):
+// 2 KiB of BF16 source. MI355X, config 4 (bench events), slices of 4 / 2 /
+// 1 KiB on that path: per-token-head scales 40.4 / 39.1 / 50.6 us, table
+// mode 39.4 / 39.1 / 48.7 us. The general path keeps 4 KiB (2 KiB there, with
+// the lookup first: 42.9 against 40.9 us).
+constexpr int kFp8LinearUnroll = 2;
+constexpr uint32_t kFp8LinearSliceBytes = 64u * 16u * kFp8LinearUnroll;
 
 // Device form of one run: resolved addresses in this process's mapping.
 // slice_begin is the exclusive prefix of slices over the preceding runs.
@@ -101,8 +108,8 @@ hipError_t launch_copy_runs(const DevRun* runs, const uint32_t* starts, uint32_t
                             uint32_t total_slices, uint64_t page_bytes, uint64_t linear_src,
                             const LaunchEvents& events, hipStream_t stream);
 
-// linear_src: as for launch_copy_runs, with slices of kFp8SliceBytes source
-// bytes.
+// linear_src: as for launch_copy_runs, with slices of kFp8LinearSliceBytes
+// source bytes (kFp8SliceBytes without it).
 hipError_t launch_copy_runs_fp8(const DevRun* runs, const uint32_t* starts, uint32_t n_runs,
                                 uint32_t total_slices,
                                 uint64_t page_bytes, uint32_t lanes_per_row,

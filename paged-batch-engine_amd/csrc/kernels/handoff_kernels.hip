@@ -237,13 +237,12 @@ __device__ __forceinline__ void fp8_step(const u32x4& v, uint32_t row, uint32_t 
 // A whole slice of the FP8 copy, loaded into v: quantises it into dst and
 // writes its rows' scales (per-token-head) at scales + row. row0 is the row
 // (within its run) of this lane's first 16-byte vector.
-template <int kLanesPerRow, bool kTable>
-__device__ __forceinline__ void fp8_full_slice(const u32x4 (&v)[kFp8Unroll], uint32_t lane,
+template <int kLanesPerRow, bool kTable, int kUnroll>
+__device__ __forceinline__ void fp8_full_slice(const u32x4 (&v)[kUnroll], uint32_t lane,
                                                gdst_t dst, uint32_t row0, uint64_t scales,
                                                uint32_t rows_per_plane, uint32_t kv_heads,
                                                uint32_t rows_per_page,
                                                const float* __restrict__ amax_table) {
-  constexpr int kUnroll = kFp8Unroll;
   constexpr uint32_t kRowsPerStep = kWave / kLanesPerRow;
   constexpr uint32_t kRowsPerSlice = kUnroll * kRowsPerStep;
   if constexpr (kRowsPerSlice <= kWave) {
@@ -287,9 +286,10 @@ __device__ __forceinline__ void fp8_full_slice(const u32x4 (&v)[kFp8Unroll], uin
   }
 }
 
-// Fused BF16 -> FP8 copy of every run, one slice of kFp8SliceBytes source
-// bytes per wave. kLinear: the sources form one region and every run holds
-// whole slices (linear_src, as for the identity copy), so the slice's loads
+// Fused BF16 -> FP8 copy of every run, one slice per wave: kFp8SliceBytes of
+// source, kFp8LinearSliceBytes with kLinear. kLinear: the sources form one
+// region and every run holds whole slices (linear_src, as for the identity
+// copy), so the slice's loads
 // go out before its run is looked up: one vector probe per lane first, the
 // loads, then the ballot, a scalar scan of at most kLinearScan entries and
 // the scalar run record (n_runs <= kLinearMaxRuns).
@@ -298,8 +298,8 @@ __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_fp8_kernel(
     const DevRun* __restrict__ runs, const uint32_t* __restrict__ starts, uint32_t n_runs,
     uint32_t total_slices, uint64_t page_bytes, uint32_t rows_per_plane, uint32_t kv_heads,
     uint32_t rows_per_page, const float* __restrict__ amax_table, uint64_t linear_src) {
-  constexpr int kUnroll = kFp8Unroll;
-  constexpr uint32_t kSlice = kFp8SliceBytes;           // source bytes per slice
+  constexpr int kUnroll = kLinear ? kFp8LinearUnroll : kFp8Unroll;
+  constexpr uint32_t kSlice = 64u * 16u * kUnroll;       // source bytes per slice
   constexpr uint32_t kRowBytes = kLanesPerRow * 16u;     // source bytes per row
   constexpr uint32_t kRowsPerStep = kWave / kLanesPerRow;
   const uint32_t lane = threadIdx.x % kWave;
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_fp8_kernel(
 #pragma unroll
     for (uint32_t i = 1; i < kLinearScan; ++i) r += next[i] <= s ? 1u : 0u;
     const uint64_t rel = (uint64_t)(s - runs[r].slice_begin) * kSlice;
-    fp8_full_slice<kLanesPerRow, kTable>(v, lane, reinterpret_cast<gdst_t>(runs[r].dst + rel / 2),
+    fp8_full_slice<kLanesPerRow, kTable, kUnroll>(v, lane, reinterpret_cast<gdst_t>(runs[r].dst + rel / 2),
                                          (uint32_t)(rel / kRowBytes) + lane / kLanesPerRow,
                                          runs[r].aux, rows_per_plane, kv_heads, rows_per_page,
                                          amax_table);
@@ -341,7 +341,7 @@ __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_fp8_kernel(
     u32x4 v[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) v[u] = ld16(src, (u * kWave + lane) * 16u);
-    fp8_full_slice<kLanesPerRow, kTable>(v, lane, dst, row0, scales, rows_per_plane, kv_heads,
+    fp8_full_slice<kLanesPerRow, kTable, kUnroll>(v, lane, dst, row0, scales, rows_per_plane, kv_heads,
                                          rows_per_page, amax_table);
   } else {
     // Last, partial slice of a run: whole rows only (slices are multiples
