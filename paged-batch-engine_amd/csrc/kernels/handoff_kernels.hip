@@ -293,8 +293,14 @@ __device__ __forceinline__ void fp8_full_slice(const u32x4 (&v)[kUnroll], uint32
 // go out before its run is looked up: one vector probe per lane first, the
 // loads, then the ballot, a scalar scan of at most kLinearScan entries and
 // the scalar run record (n_runs <= kLinearMaxRuns).
+// Workgroup of the FP8 copy: kLinearThreadsPerBlock on the one-region path
+// (table mode 39.0-39.1 against 39.5-39.6 us with 256 threads on config 4,
+// per-token-head unchanged), else kThreadsPerBlock.
+template <bool kLinear>
+constexpr int fp8_threads() { return kLinear ? kLinearThreadsPerBlock : kThreadsPerBlock; }
+
 template <int kLanesPerRow, bool kTable, bool kLinear>
-__global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_fp8_kernel(
+__global__ __launch_bounds__(fp8_threads<kLinear>()) void copy_runs_fp8_kernel(
     const DevRun* __restrict__ runs, const uint32_t* __restrict__ starts, uint32_t n_runs,
     uint32_t total_slices, uint64_t page_bytes, uint32_t rows_per_plane, uint32_t kv_heads,
     uint32_t rows_per_page, const float* __restrict__ amax_table, uint64_t linear_src) {
@@ -303,7 +309,8 @@ __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_fp8_kernel(
   constexpr uint32_t kRowBytes = kLanesPerRow * 16u;     // source bytes per row
   constexpr uint32_t kRowsPerStep = kWave / kLanesPerRow;
   const uint32_t lane = threadIdx.x % kWave;
-  const uint32_t s = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + threadIdx.x / kWave);
+  const uint32_t s = __builtin_amdgcn_readfirstlane(blockIdx.x * (fp8_threads<kLinear>() / kWave) +
+                                                    threadIdx.x / kWave);
   if (s >= total_slices) return;
   if constexpr (kLinear) {
     const uint32_t stride = (n_runs + kWave - 1) / kWave;  // <= kLinearScan
@@ -436,32 +443,34 @@ hipError_t launch_copy_runs(const DevRun* runs, const uint32_t* starts, uint32_t
 
 namespace {
 template <int L, bool kLinear>
-void launch_fp8_path(bool table, uint32_t blocks, hipStream_t stream, const LaunchEvents& ev,
+void launch_fp8_path(bool table, uint32_t waves, hipStream_t stream, const LaunchEvents& ev,
                      const DevRun* runs, const uint32_t* starts, uint32_t n_runs,
                      uint32_t total_slices, uint64_t page_bytes, uint32_t rows_per_plane,
                      uint32_t kv_heads, uint32_t rows_per_page, const float* amax_table,
                      uint64_t linear_src) {
+  constexpr uint32_t per_block = fp8_threads<kLinear>() / kWave;
+  const dim3 blocks((waves + per_block - 1) / per_block), threads(fp8_threads<kLinear>());
   if (table)
-    hipExtLaunchKernelGGL((copy_runs_fp8_kernel<L, true, kLinear>), dim3(blocks), dim3(kThreadsPerBlock),
+    hipExtLaunchKernelGGL((copy_runs_fp8_kernel<L, true, kLinear>), blocks, threads,
                           0, stream, ev.start, ev.stop, 0, runs, starts, n_runs, total_slices,
                           page_bytes, rows_per_plane, kv_heads, rows_per_page, amax_table, linear_src);
   else
-    hipExtLaunchKernelGGL((copy_runs_fp8_kernel<L, false, kLinear>), dim3(blocks), dim3(kThreadsPerBlock),
+    hipExtLaunchKernelGGL((copy_runs_fp8_kernel<L, false, kLinear>), blocks, threads,
                           0, stream, ev.start, ev.stop, 0, runs, starts, n_runs, total_slices,
                           page_bytes, rows_per_plane, kv_heads, rows_per_page, amax_table, linear_src);
 }
 
 template <int L>
-void launch_fp8(bool table, uint32_t blocks, hipStream_t stream, const LaunchEvents& ev,
+void launch_fp8(bool table, uint32_t waves, hipStream_t stream, const LaunchEvents& ev,
                 const DevRun* runs, const uint32_t* starts, uint32_t n_runs, uint32_t total_slices,
                 uint64_t page_bytes, uint32_t rows_per_plane, uint32_t kv_heads,
                 uint32_t rows_per_page, const float* amax_table, uint64_t linear_src) {
   if (linear_src)
-    launch_fp8_path<L, true>(table, blocks, stream, ev, runs, starts, n_runs, total_slices,
+    launch_fp8_path<L, true>(table, waves, stream, ev, runs, starts, n_runs, total_slices,
                              page_bytes, rows_per_plane, kv_heads, rows_per_page, amax_table,
                              linear_src);
   else
-    launch_fp8_path<L, false>(table, blocks, stream, ev, runs, nullptr, n_runs, total_slices,
+    launch_fp8_path<L, false>(table, waves, stream, ev, runs, nullptr, n_runs, total_slices,
                               page_bytes, rows_per_plane, kv_heads, rows_per_page, amax_table, 0);
 }
 }  // namespace
@@ -473,11 +482,10 @@ hipError_t launch_copy_runs_fp8(const DevRun* runs, const uint32_t* starts, uint
                                 uint32_t rows_per_page, bool table, const float* amax_table,
                                 uint64_t linear_src, const LaunchEvents& ev, hipStream_t stream) {
   const uint32_t waves = total_slices ? total_slices : 1u;
-  const uint32_t blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
   // One instantiation per row width (head_dim / 8 lanes), a shape, not a tuning choice.
 #define PBE_FP8_CASE(L)                                                                      \
   case L:                                                                                    \
-    launch_fp8<L>(table, blocks, stream, ev, runs, starts, n_runs, total_slices, page_bytes, \
+    launch_fp8<L>(table, waves, stream, ev, runs, starts, n_runs, total_slices, page_bytes,  \
                   rows_per_plane, kv_heads, rows_per_page, amax_table, linear_src);          \
     return hipGetLastError();
   switch (lanes_per_row) {
