@@ -50,20 +50,22 @@ int32_t pbe_paged_decode_splits(int32_t batch, int32_t kv_heads, int32_t max_blo
   if (batch <= 0 || kv_heads <= 0 || max_blocks_per_seq <= 0) return 1;
   // One wave per SIMD (4 per CU) of the current GPU, rounded down so no
   // partial extra round of waves trails the launch; FP8 pages take two per
-  // SIMD when every split still holds at least 16 blocks; at least 4 blocks
-  // (64 tokens) per split. Measured on MI355X (256 CUs), 5040-token
-  // sequences, both launches: FP8 batch 64 at 16 splits 35.7 us stage 1
-  // against 40.9 us at 8; batch 128: 8 splits 66.7 us against 74.5 us at 4;
-  // batch 32: 16 splits 28.9 us against 30.8 us at 32; batch 16: 32 splits
-  // 22.9 us against 27.9 us at 64. BF16 batch 64: 54.6 us stage 1 at 8
-  // splits against 56.5 us at 16. One 32768-token sequence: 512 splits (4
-  // blocks each) 12.0 + 5.9 us against 13.5 + 4.7 at 256 and 15.9 + 7.9 at 1024.
+  // SIMD when every split still holds at least 8 blocks; at least 4 blocks
+  // (64 tokens) per split. Measured on MI355X (256 CUs), FP8, both launches:
+  // 5040-token sequences, batch 64: 16 splits 39.1 us against 40.9 us at 8;
+  // batch 32: 32 splits 26.7 us against 30.2 us at 16; batch 128: 8 splits
+  // 65.9 us against 84.1 us at 4 and 72.9 us at 16; batch 16: 32 splits
+  // 20.9 us, 20.7 us at 64. 2048-token sequences, batch 64: 16 splits 24.6 us
+  // against 27.0 us at 8 and 28.1 us at 32. One 160,000-token sequence (10,000
+  // blocks): 1024 splits 29.5 us against 31.6 us at 512. BF16 batch 64: 54.6
+  // us stage 1 at 8 splits against 56.5 us at 16. One 32768-token sequence:
+  // 512 splits (4 blocks each) 12.0 + 5.9 us against 13.5 + 4.7 at 256.
   const int64_t simds = 4ll * decode_cus();
   const int64_t units = (int64_t)batch * kv_heads;
   int64_t splits = std::max<int64_t>(1, simds / units);
   if (kv_dtype == PBE_KV_FP8_E4M3) {
     const int64_t two = std::max<int64_t>(1, 2 * simds / units);
-    if ((max_blocks_per_seq + two - 1) / two >= 16) splits = two;
+    if ((max_blocks_per_seq + two - 1) / two >= 8) splits = two;
   }
   splits = std::min<int64_t>(splits, (max_blocks_per_seq + 3) / 4);
   splits = std::min<int64_t>(splits, pbe::kDecodeMaxSplits);

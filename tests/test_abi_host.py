@@ -85,17 +85,19 @@ def test_invalid_arguments_are_rejected_on_the_host():
 
 def test_decode_split_count_by_page_dtype():
     """pbe_paged_decode_splits: at most 1024 waves (batch x kv_heads x splits),
-    FP8 pages 2048 while every split keeps >= 16 blocks, >= 4 blocks per
-    split, at most 1024 splits. The choices at 5040 tokens (315 blocks) are the
-    ones measured fastest on MI355X."""
+    FP8 pages 2048 while every split keeps >= 8 blocks, >= 4 blocks per
+    split, at most 1024 splits. The choices at 5040 tokens (315 blocks) and
+    2048 tokens (128 blocks) are the ones measured fastest on MI355X."""
     fp8, bf16 = P.PBE_KV_FP8_E4M3, P.PBE_KV_BF16
     assert P.decode_splits(64, 2, 315, fp8) == 16
     assert P.decode_splits(64, 2, 315, bf16) == 8
     assert P.decode_splits(128, 2, 315, fp8) == 8
     assert P.decode_splits(128, 2, 315, bf16) == 4
-    assert P.decode_splits(32, 2, 315, fp8) == 16   # 32 splits would leave < 16 blocks each
+    assert P.decode_splits(32, 2, 315, fp8) == 32   # 10 blocks each
+    assert P.decode_splits(64, 2, 128, fp8) == 16   # 8 blocks each
+    assert P.decode_splits(32, 2, 128, fp8) == 16   # 32 splits would leave 4 blocks each
     assert P.decode_splits(16, 2, 315, fp8) == 32
-    assert P.decode_splits(1, 2, 10000, fp8) == 512  # one wave per SIMD, ~20 blocks each
+    assert P.decode_splits(1, 2, 10000, fp8) == 1024  # two waves per SIMD, ~10 blocks each
     assert P.decode_splits(1, 2, 2048, fp8) == 512   # a 32K-token sequence: 4 blocks per split
     assert P.decode_splits(1, 2, 315, fp8) == 79     # at least 4 blocks per split
     assert P.decode_splits(1, 1, 7, bf16) == 2      # at least 4 blocks per split
