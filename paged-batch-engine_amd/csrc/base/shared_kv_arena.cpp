@@ -486,10 +486,6 @@ bool SharedKVPageGroup::allocate_many(int layer, int n, std::vector<int32_t>* ou
   m.collect_locked();
   bool fence_pending = !m.retiring.empty();
   for (int k = 0; k < n; ++k) {
-    if (m.free_ids.empty() && !fence_pending) {
-      m.collect_locked();
-      fence_pending = !m.retiring.empty();
-    }
     int id = m.allocate_locked(0, false);
     if (id < 0 && fence_pending) {  // out of room: one last look before giving up
       id = m.allocate_locked(0, true);
