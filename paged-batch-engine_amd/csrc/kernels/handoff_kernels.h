@@ -29,6 +29,16 @@ constexpr uint32_t kCopySliceBytes = 64u * 16u * kCopyUnroll;      // 2 KiB per 
 // lane, then a scalar scan of at most 8 entries); longer lists take the
 // general path.
 constexpr uint32_t kLinearMaxRuns = 512;
+// Workgroups per XCD group (xcd_grouped in xcd_order.h), by path. MI355X,
+// kernel-bracketing events, two runs of 60 launches: the one-region path at
+// 16 workgroups (128 KiB) per group, config 2 45.4-45.5 us against 45.7-46.1
+// in dispatch order (4: 47.2, 8: 46.4, 64: 45.4, 256: 46.1, one contiguous
+// eighth per XCD: 45.4-45.5 but the contiguous copy 45.1 against 44.5); the
+// general path at 64 (512 KiB, about one page), config 3 115.2-115.3 us
+// against 119.3-121.0 and config 5 598-599 us against 635-638 (16: 116.5 /
+// 601, 32: 115.7 / 594, 128: 115.6 / 598, 256: 116.0 / 602).
+constexpr uint32_t kLinearXcdGroup = 16;
+constexpr uint32_t kCopyXcdGroup = 64;
 constexpr int kFp8Unroll = 4;   // 16-byte BF16 vectors per lane per slice of the FP8 copy
 constexpr uint32_t kFp8SliceBytes = 64u * 16u * kFp8Unroll;    // 4 KiB of BF16 source per wave
 // The FP8 copy's slice on the one-region path (loads before the run lookup):

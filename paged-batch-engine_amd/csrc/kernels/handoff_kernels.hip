@@ -19,6 +19,7 @@
 
 #include "fp8_device.h"
 #include "handoff_kernels.h"
+#include "xcd_order.h"
 
 namespace pbe {
 namespace {
@@ -145,7 +146,10 @@ __device__ __forceinline__ void copy_runs_body(const DevRun* __restrict__ runs,
   // and the buffer resources in SGPRs (a resource the compiler cannot prove
   // uniform is rebuilt per lane in a readfirstlane loop around every load
   // and store).
-  const uint32_t s = __builtin_amdgcn_readfirstlane(blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave);
+  const uint32_t s = __builtin_amdgcn_readfirstlane(
+      xcd_grouped(blockIdx.x, gridDim.x, kThreads == kLinearThreadsPerBlock ? kLinearXcdGroup : kCopyXcdGroup) *
+          (kThreads / kWave) +
+      threadIdx.x / kWave);
   if (s >= total_slices) return;
   if (linear_src) {
     copy_slice_linear_src(runs, starts, n_runs, s, linear_src, lane);
@@ -179,7 +183,7 @@ __global__ __launch_bounds__(kThreadsPerBlock) void copy_runs_kernarg_kernel(con
 __global__ __launch_bounds__(kLinearThreadsPerBlock) void copy_runs_kernarg_linear_kernel(
     const KernargLinearList list) {
   const uint32_t lane = threadIdx.x % kWave;
-  const uint32_t s = __builtin_amdgcn_readfirstlane(blockIdx.x * (kLinearThreadsPerBlock / kWave) +
+  const uint32_t s = __builtin_amdgcn_readfirstlane(xcd_grouped(blockIdx.x, gridDim.x, kLinearXcdGroup) * (kLinearThreadsPerBlock / kWave) +
                                                     threadIdx.x / kWave);
   if (s >= list.total_slices) return;
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(

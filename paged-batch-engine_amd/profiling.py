@@ -159,7 +159,8 @@ def _split_legs(items, launches: int, root: str):
 
 
 def legs(roots, launches: int, out: str, command: str, trace: str | None = None,
-         title: str = "config-2 handoff", alg_bytes: int = 0, copy_bytes: int = 0) -> None:
+         title: str = "config-2 handoff", alg_bytes: int = 0, copy_bytes: int = 0,
+         kind: str = "DRAM-side counters") -> None:
     """Per-leg medians of every counter in the given --pmc runs of
     bench.py --ceiling-legs (one run per counter pass), and with `trace` (a
     --kernel-trace run of the same command) each leg's kernel durations."""
@@ -176,7 +177,7 @@ def legs(roots, launches: int, out: str, command: str, trace: str | None = None,
         durations = {leg: statistics.mean(v) / 1e3 for leg, v in _split_legs(items, launches, trace).items()}
     counters = sorted({c for v in table.values() for c in v})
     w = max([len(c) for c in counters] + [26])
-    lines = [f"# rocprofv3 --pmc summary: DRAM-side counters of the {title} and its "
+    lines = [f"# rocprofv3 --pmc summary: {kind} of the {title} and its "
              "ceiling legs", f"command: {command}",
              f"medians over {launches} launches per leg, each after a 1 GiB scrub; "
              "values summed over the counter's instances", "",
@@ -335,6 +336,7 @@ def main() -> None:
     q.add_argument("--command", required=True)
     q.add_argument("--trace", default=None, help="--kernel-trace run of the same command")
     q.add_argument("--title", default="config-2 handoff")
+    q.add_argument("--kind", default="DRAM-side counters")
     q.add_argument("--alg-bytes", type=int, default=0)
     q.add_argument("--copy-bytes", type=int, default=0)
     rq = sub.add_parser("req")
@@ -361,7 +363,8 @@ def main() -> None:
         markers(a.root, a.out, a.command)
         return
     if a.cmd == "legs":
-        legs(a.roots, a.launches, a.out, a.command, a.trace, a.title, a.alg_bytes, a.copy_bytes)
+        legs(a.roots, a.launches, a.out, a.command, a.trace, a.title, a.alg_bytes, a.copy_bytes,
+             a.kind)
         return
     if a.cmd == "stats":
         labels = {}

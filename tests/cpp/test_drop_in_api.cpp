@@ -28,6 +28,7 @@
 #include "base/block_allocator.h"
 #include "base/kv_cache_manager.h"
 #include "base/page_index.h"
+#include "kernels/xcd_order.h"
 
 using namespace cache;
 
@@ -1518,6 +1519,36 @@ TEST_CASE("page index: multiply-shift quotient equals id / stride, -1 off the pa
     CHECK_EQ(pi.of(INT32_MAX - INT32_MAX % stride), INT32_MAX / stride);
   }
   CHECK_EQ(base::PageIndex(1).of(12345), 12345);
+}
+
+TEST_CASE("xcd grouping: the copy kernels' workgroup renumbering is a bijection") {
+  // every grid size up to 5,000 workgroups and a few large ones, for group
+  // sizes 1..128 (the copy kernels use 16 and 64)
+  std::vector<uint32_t> sizes;
+  for (uint32_t nb = 1; nb <= 5000; ++nb) sizes.push_back(nb);
+  for (uint32_t nb : {17640u, 35281u, 65536u, 1048575u}) sizes.push_back(nb);
+  std::vector<uint32_t> seen;
+  for (uint32_t g : {1u, 2u, 3u, 16u, 64u, 128u}) {
+    for (uint32_t nb : sizes) {
+      if (nb > 5000 && g != 16 && g != 64) continue;
+      seen.assign(nb, 0);
+      for (uint32_t b = 0; b < nb; ++b) {
+        const uint32_t at = pbe::xcd_grouped(b, nb, g);
+        REQUIRE(at < nb);
+        ++seen[at];
+      }
+      REQUIRE(std::all_of(seen.begin(), seen.end(), [](uint32_t c) { return c == 1; }));
+    }
+  }
+  // a full round: XCD x (workgroups x, x + 8, ...) holds positions [16x, 16x + 16)
+  for (uint32_t b = 0; b < 128; ++b) {
+    const uint32_t at = pbe::xcd_grouped(b, 128, 16);
+    REQUIRE(at / 16 == b % pbe::kXcds);
+    REQUIRE(at % 16 == b / pbe::kXcds);
+  }
+  // the trailing partial round keeps dispatch order
+  CHECK_EQ(pbe::xcd_grouped(130, 131, 16), 130u);
+  CHECK_EQ(pbe::xcd_grouped(5, 7, 1), 5u);
 }
 
 TEST_CASE("block allocator (shared arena): per-layer ids, refcounts, payload pointers") {
