@@ -29,16 +29,18 @@ constexpr uint32_t kCopySliceBytes = 64u * 16u * kCopyUnroll;      // 2 KiB per 
 // lane, then a scalar scan of at most 8 entries); longer lists take the
 // general path.
 constexpr uint32_t kLinearMaxRuns = 512;
-// Workgroups per XCD group (xcd_grouped in xcd_order.h), by path. MI355X,
-// kernel-bracketing events, two runs of 60 launches: the one-region path at
-// 16 workgroups (128 KiB) per group, config 2 45.4-45.5 us against 45.7-46.1
-// in dispatch order (4: 47.2, 8: 46.4, 64: 45.4, 256: 46.1, one contiguous
-// eighth per XCD: 45.4-45.5 but the contiguous copy 45.1 against 44.5); the
-// general path at 64 (512 KiB, about one page), config 3 115.2-115.3 us
-// against 119.3-121.0 and config 5 598-599 us against 635-638 (16: 116.5 /
-// 601, 32: 115.7 / 594, 128: 115.6 / 598, 256: 116.0 / 602).
-constexpr uint32_t kLinearXcdGroup = 16;
-constexpr uint32_t kCopyXcdGroup = 64;
+// Workgroups per XCD group (xcd_grouped in xcd_order.h), by path: 24 on the
+// one-region path (192 KiB per group), 48 on the general path (384 KiB).
+// MI355X, kernel-bracketing events, three alternating runs of 60 launches,
+// mean us, (one-region, general) groups: (24, 48) config 2 45.64, one
+// contiguous run 44.11, config 3 115.31, config 5 598.8; (16, 64) 45.96 /
+// 44.70 / 115.96 / 601.0; (20, 40) 45.78 / 44.23 / 116.06 / 605.6; (32, 48)
+// 46.43 / 44.72 / 115.33 / 599.1. Dispatch order: config 2 45.7-46.3,
+// config 3 119.3-121.0, config 5 635-638. Further from these: one-region 4 /
+// 8 / 12 / 256 (config 2 47.2 / 46.4 / 46.1 / 46.1); general 16 / 96 / 256
+// (config 3 116.5 / 115.2 / 116.0) and 4 KiB general slices at 32 (123.9).
+constexpr uint32_t kLinearXcdGroup = 24;
+constexpr uint32_t kCopyXcdGroup = 48;
 constexpr int kFp8Unroll = 4;   // 16-byte BF16 vectors per lane per slice of the FP8 copy
 constexpr uint32_t kFp8SliceBytes = 64u * 16u * kFp8Unroll;    // 4 KiB of BF16 source per wave
 // The FP8 copy's slice on the one-region path (loads before the run lookup):

@@ -1523,14 +1523,14 @@ TEST_CASE("page index: multiply-shift quotient equals id / stride, -1 off the pa
 
 TEST_CASE("xcd grouping: the copy kernels' workgroup renumbering is a bijection") {
   // every grid size up to 5,000 workgroups and a few large ones, for group
-  // sizes 1..128 (the copy kernels use 16 and 64)
+  // sizes 1..128 (the copy kernels use 24 and 48)
   std::vector<uint32_t> sizes;
   for (uint32_t nb = 1; nb <= 5000; ++nb) sizes.push_back(nb);
   for (uint32_t nb : {17640u, 35281u, 65536u, 1048575u}) sizes.push_back(nb);
   std::vector<uint32_t> seen;
-  for (uint32_t g : {1u, 2u, 3u, 16u, 64u, 128u}) {
+  for (uint32_t g : {1u, 2u, 3u, 16u, 24u, 48u, 64u, 128u}) {
     for (uint32_t nb : sizes) {
-      if (nb > 5000 && g != 16 && g != 64) continue;
+      if (nb > 5000 && g != 24 && g != 48) continue;
       seen.assign(nb, 0);
       for (uint32_t b = 0; b < nb; ++b) {
         const uint32_t at = pbe::xcd_grouped(b, nb, g);
