@@ -556,3 +556,50 @@ def test_contiguous_sources_across_run_counts(torch_cuda, n_runs, n_pages, head_
     torch.cuda.synchronize()
     after = snapshot(bufs)
     assert np.array_equal(after, expected), first_diff(after, expected)
+
+
+# Workgroup rounds of the copy kernels' XCD grouping: 8 XCDs x 24 workgroups
+# of 512 threads (1 KiB slices) on the contiguous-source path, 8 x 48 of 256
+# threads (2 KiB slices) on the general path. A 16 KiB page is two workgroups
+# on either path, so a round is 96 pages there and 192 pages here.
+@pytest.mark.parametrize("path,n_pages", [
+    ("contiguous", 95), ("contiguous", 96), ("contiguous", 97), ("contiguous", 200),
+    ("general", 191), ("general", 192), ("general", 193), ("general", 400),
+])
+def test_grids_at_xcd_group_round_boundaries(torch_cuda, path, n_pages):
+    """Grids below one round of XCD groups (dispatch order kept), of exactly
+    whole rounds, and of whole rounds plus a partial one: every slice is
+    copied exactly once, through a run list and through the one-call entry
+    point, the whole arena compared with the oracle."""
+    torch = torch_cuda
+    g = W.Geometry(2, 2, 64)
+    assert g.page_bytes() == 16384
+    kv = _kv(g)
+    if path == "contiguous":
+        src, dst, total = _contiguous_source_plan(g, max(1, n_pages // 3), n_pages, 2000 + n_pages)
+        arena_pages = total + 3
+        slices = n_pages * 16
+    else:
+        w = W.small(seed=n_pages, layers=2, kv_heads=2, head_dim=64, n_pages=4 * n_pages + 16,
+                    handoff_pages=n_pages)
+        src, dst = w.src_ids, w.dst_ids
+        arena_pages = 4 * n_pages + 16
+        slices = n_pages * 8
+    runs = P.build_runs(src, dst, kv)
+    say(f"xcd rounds path={path} pages={n_pages} runs={len(runs)}")
+    bufs, view = device_arena(torch, arena_pages * g.page_bytes())
+    for rep, seed in enumerate((n_pages, n_pages + 1)):
+        fill_bf16(torch, bufs[0], 1.0, seed)
+        torch.cuda.synchronize()
+        expected = snapshot(bufs).copy()
+        O.copy_handoff(expected, src, dst, g.half(), g.layers)
+        if rep == 0:
+            with P.RunList.bf16(view, view, runs, kv) as rl:
+                assert rl.info().slices == slices
+                rl.copy(stream_ptr(torch))
+                torch.cuda.synchronize()
+        else:
+            P.copy_shared_kv(view, src, dst, kv, 0, stream_ptr(torch))
+            torch.cuda.synchronize()
+        after = snapshot(bufs)
+        assert np.array_equal(after, expected), first_diff(after, expected)
