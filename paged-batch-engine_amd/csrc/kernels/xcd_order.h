@@ -18,8 +18,8 @@ constexpr uint32_t kXcds = 8;
 // reads and writes in every run in flight; in groups, each XCD streams
 // through its own stretch of the plan. Measured, not derived: on MI355X the
 // scattered plans (configs 3 and 5) run 3-6% faster, while rocprofv3 shows
-// the same UTCL1 translation misses (config 2: 2,152 per launch against
-// 2,256 in dispatch order) and 2-4% more DRAM requests in flight.
+// the same UTCL1 translation misses (config 2: 2,090-2,189 per launch
+// against 2,256 in dispatch order) and 2-4% more DRAM requests in flight.
 constexpr uint32_t xcd_grouped(uint32_t b, uint32_t nb, uint32_t g) {
   const uint32_t round = kXcds * g;
   const uint32_t tail = nb / round * round;
