@@ -44,14 +44,42 @@ PoolGeometry geometry_of(const ArenaKVPool& p) {
   return g;
 }
 
+// The block id a pool's lookups last saw and, when that id is a page id whose
+// whole page span [id, id + stride) lies in one segment of the view, the
+// span's base: the page's planes are then base + plane * half, with no
+// segment division per component (every layer of a page-major manifest
+// shares the id, so a page costs one lookup per pool).
+struct PageMemo {
+  int32_t id = -1;
+  bool page_id = false;
+  uint8_t* base = nullptr;
+};
+
 // Component address of (layer, kind) of block `id` in a page-major pool.
 bool component_address(const ArenaKVPool& p, const PoolGeometry& g, const cache::ComponentDescriptor& c,
-                       int32_t id, uint8_t** out) {
+                       int32_t id, PageMemo* memo, uint8_t** out) {
   const uint64_t plane = 2ull * c.layer + (c.kind == cache::ComponentKind::kValue ||
                                             c.kind == cache::ComponentKind::kValueScale);
-  if (id < 0 || id % g.stride) return false;
-  if (c.kind == cache::ComponentKind::kKey || c.kind == cache::ComponentKind::kValue)
+  if (id != memo->id) {
+    memo->id = id;
+    memo->page_id = id >= 0 && id % g.stride == 0;
+    memo->base = nullptr;
+    uint8_t* a = nullptr;
+    if (memo->page_id &&
+        address_of(p.view, static_cast<uint64_t>(id) * g.half, static_cast<uint64_t>(g.stride) * g.half, &a))
+      memo->base = a;
+  }
+  if (!memo->page_id) return false;
+  if (c.kind == cache::ComponentKind::kKey || c.kind == cache::ComponentKind::kValue) {
+    // a plane of a page inside one segment is inside it too; otherwise the
+    // plane is checked on its own (a page may cross a segment boundary
+    // while each plane stays inside one)
+    if (memo->base && plane < static_cast<uint64_t>(g.stride)) {
+      *out = memo->base + plane * g.half;
+      return true;
+    }
     return address_of(p.view, (static_cast<uint64_t>(id) + plane) * g.half, g.half, out);
+  }
   // scales: [page][layer][K|V][token][head] fp32
   if (!p.scales) return false;
   const uint64_t page = static_cast<uint64_t>(id) / static_cast<uint64_t>(g.stride);
@@ -73,6 +101,7 @@ struct ManifestBinding {
   cache::PageSchema src_schema, dst_schema;
   std::shared_ptr<const cache::TransferPlan> plan;
   cache::LayoutDescriptor src_layout, dst_layout;
+  std::vector<size_t> src_bytes, dst_bytes;  // byte_size() of each schema component
 };
 
 base::Status prepare(const KVBlockManifest& manifest, const ArenaKVPool& source,
@@ -104,6 +133,8 @@ base::Status prepare(const KVBlockManifest& manifest, const ArenaKVPool& source,
   if (!status) return status;
   status = planner->compile(b->src_schema, b->dst_schema, cache::TransferPlacement::kExactDirect, &b->plan);
   if (!status) return status;
+  for (const auto& c : b->src_schema.components) b->src_bytes.push_back(c.byte_size());
+  for (const auto& c : b->dst_schema.components) b->dst_bytes.push_back(c.byte_size());
   std::vector<size_t> src_order(b->src_schema.components.size()), dst_order(b->dst_schema.components.size());
   std::iota(src_order.begin(), src_order.end(), 0);
   std::iota(dst_order.begin(), dst_order.end(), 0);
@@ -121,17 +152,20 @@ base::Status endpoints(const ManifestBinding& b, const ArenaKVPool& source, cons
   dst->components.clear();
   src->components.reserve(b.src_schema.components.size());
   dst->components.reserve(b.dst_schema.components.size());
-  for (const auto& c : b.src_schema.components) {
+  PageMemo src_memo, dst_memo;
+  for (size_t i = 0; i < b.src_schema.components.size(); ++i) {
+    const auto& c = b.src_schema.components[i];
     uint8_t* a = nullptr;
-    if (!component_address(source, b.src_geo, c, b.by_layer[c.layer]->src_block_ids[page], &a))
+    if (!component_address(source, b.src_geo, c, b.by_layer[c.layer]->src_block_ids[page], &src_memo, &a))
       return InvalidArgument("source block outside its page-major arena");
-    src->components.push_back({c, a, c.byte_size()});
+    src->components.push_back({c, a, b.src_bytes[i]});
   }
-  for (const auto& c : b.dst_schema.components) {
+  for (size_t i = 0; i < b.dst_schema.components.size(); ++i) {
+    const auto& c = b.dst_schema.components[i];
     uint8_t* a = nullptr;
-    if (!component_address(destination, b.dst_geo, c, b.by_layer[c.layer]->dst_block_ids[page], &a))
+    if (!component_address(destination, b.dst_geo, c, b.by_layer[c.layer]->dst_block_ids[page], &dst_memo, &a))
       return InvalidArgument("destination block outside its page-major arena");
-    dst->components.push_back({c, a, c.byte_size()});
+    dst->components.push_back({c, a, b.dst_bytes[i]});
   }
   return base::error::Success();
 }
@@ -203,16 +237,32 @@ base::Status BindManifestCopyOps(const KVBlockManifest& manifest, const ArenaKVP
     pieces.push_back({si, di, static_cast<uint64_t>(op.source - src.components[si].data),
                       static_cast<uint64_t>(op.destination - dst.components[di].data), op.bytes});
   }
-  std::vector<pbe_copy_op> out;
-  out.reserve(b.pages * pieces.size());
+  // Every later page: its component addresses only (each checked as
+  // endpoints() checks it), then the template's operations.
+  std::vector<uint64_t> src_at(src.components.size()), dst_at(dst.components.size());
+  for (size_t i = 0; i < src_at.size(); ++i) src_at[i] = reinterpret_cast<uint64_t>(src.components[i].data);
+  for (size_t i = 0; i < dst_at.size(); ++i) dst_at[i] = reinterpret_cast<uint64_t>(dst.components[i].data);
+  std::vector<pbe_copy_op> out(b.pages * pieces.size());
+  pbe_copy_op* o = out.data();
   for (size_t page = 0; page < b.pages; ++page) {
     if (page) {
-      status = endpoints(b, source, destination, page, &src, &dst);
-      if (!status) return status;
+      PageMemo src_memo, dst_memo;
+      for (size_t i = 0; i < src_at.size(); ++i) {
+        const auto& c = b.src_schema.components[i];
+        uint8_t* a = nullptr;
+        if (!component_address(source, b.src_geo, c, b.by_layer[c.layer]->src_block_ids[page], &src_memo, &a))
+          return InvalidArgument("source block outside its page-major arena");
+        src_at[i] = reinterpret_cast<uint64_t>(a);
+      }
+      for (size_t i = 0; i < dst_at.size(); ++i) {
+        const auto& c = b.dst_schema.components[i];
+        uint8_t* a = nullptr;
+        if (!component_address(destination, b.dst_geo, c, b.by_layer[c.layer]->dst_block_ids[page], &dst_memo, &a))
+          return InvalidArgument("destination block outside its page-major arena");
+        dst_at[i] = reinterpret_cast<uint64_t>(a);
+      }
     }
-    for (const Piece& p : pieces)
-      out.push_back({reinterpret_cast<uint64_t>(src.components[p.src_span].data) + p.src_off,
-                     reinterpret_cast<uint64_t>(dst.components[p.dst_span].data) + p.dst_off, p.bytes});
+    for (const Piece& p : pieces) *o++ = {src_at[p.src_span] + p.src_off, dst_at[p.dst_span] + p.dst_off, p.bytes};
   }
   *ops = std::move(out);
   return base::error::Success();

@@ -310,6 +310,44 @@ def ceilings(bench_json: str, out: str, command: str) -> None:
     print(text)
 
 
+def hostpaths(log: str, out: str, command: str) -> None:
+    """The JSON line of bench.py --host-paths as a labelled table."""
+    line = [l for l in Path(log).read_text().splitlines() if l.startswith("{")][-1]
+    d = json.loads(line)
+    g, r = d["generic_plan_form_us"], d["reference_call_order_us"]
+    st = r["steps"]
+    rows = [
+        ("generic plan form (InProcKVBlockCopyConnector)", None),
+        ("per-page BindComponents binding (BindManifestTransfers)", g["per_page_binding"]),
+        ("template binding (BindManifestCopyOps)", g["copy_op_binding"]),
+        ("pbe_copy_ops host call for the 17,640 component ops", g["copy_ops_call"]),
+        ("connector submit -> drain", g["connector_submit_drain"]),
+        ("", None),
+        ("reference copy_shared_kv call order (serving::CopySharedKVToDecode)", None),
+        ("append_slots, 28 layers (register_request + append_slots)", r["reserve_28_layers"]),
+        ("end to end (reserve, manifest, copy, sync, commit_kv)", r["end_to_end"]),
+        ("the copy and its wait alone (pbe_copy_shared_kv + sync)", r["copy_and_sync_alone"]),
+        ("free_request afterwards", r["free_request"]),
+        ("append_slots while 315 freed pages wait on fences", r["reserve_under_pending_fences"]),
+        ("", None),
+        ("the same steps through the same public calls, one timer between each (cold cache)", None),
+        ("request copies (28 source lists)", st["request_copies"]),
+        ("DecodeKVReservationManager::reserve (pages + manifest)", st["reserve_and_manifest"]),
+        ("pbe_copy_shared_kv call (checks, runs, launch)", st["pbe_copy_shared_kv_call"]),
+        ("stream wait (the kernel and its completion)", st["stream_wait"]),
+        ("commit_kv", st["commit_kv"]),
+    ]
+    lines = [f"# Host costs of the handoff's C++ paths at config-2 size ({d['pages']} pages, "
+             f"{d['layers']} layers), MI355X box", f"command: {command}",
+             f"medians over {d['iterations']} iterations, microseconds", ""]
+    for name, v in rows:
+        lines.append(name if v is None else f"  {name:<57}{v:>7.1f}")
+    lines += ["", "raw line:", line]
+    text = "\n".join(lines) + "\n"
+    Path(out).write_text(text)
+    print(text)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -348,6 +386,10 @@ def main() -> None:
     ce.add_argument("bench_json")
     ce.add_argument("--out", required=True)
     ce.add_argument("--command", required=True)
+    hp = sub.add_parser("hostpaths")
+    hp.add_argument("log")
+    hp.add_argument("--out", required=True)
+    hp.add_argument("--command", required=True)
     mk = sub.add_parser("markers")
     mk.add_argument("root")
     mk.add_argument("--out", required=True)
@@ -358,6 +400,9 @@ def main() -> None:
         return
     if a.cmd == "ceilings":
         ceilings(a.bench_json, a.out, a.command)
+        return
+    if a.cmd == "hostpaths":
+        hostpaths(a.log, a.out, a.command)
         return
     if a.cmd == "markers":
         markers(a.root, a.out, a.command)
