@@ -104,22 +104,33 @@ struct ManifestBinding {
   std::vector<size_t> src_bytes, dst_bytes;  // byte_size() of each schema component
 };
 
-base::Status prepare(const KVBlockManifest& manifest, const ArenaKVPool& source,
-                     const ArenaKVPool& destination, cache::TransferPlanner* planner, ManifestBinding* b) {
+// The manifest's mapping of each layer and its page count, checked against
+// the pools' layer count.
+base::Status map_layers(const KVBlockManifest& manifest, const ArenaKVPool& source,
+                        const ArenaKVPool& destination, std::vector<const KVBlockMapping*>* by_layer,
+                        size_t* pages) {
   const int32_t layers = source.pool.layer_num;
   if (layers != destination.pool.layer_num || static_cast<int32_t>(manifest.layer_mappings.size()) != layers)
     return InvalidArgument("semantic transfer layer coverage mismatch");
-  b->by_layer.assign(layers, nullptr);
+  by_layer->assign(layers, nullptr);
+  *pages = 0;
   for (const auto& m : manifest.layer_mappings) {
-    if (m.layer_idx < 0 || m.layer_idx >= layers || b->by_layer[m.layer_idx] ||
+    if (m.layer_idx < 0 || m.layer_idx >= layers || (*by_layer)[m.layer_idx] ||
         m.src_block_ids.size() != m.dst_block_ids.size())
       return InvalidArgument("semantic transfer mapping is incomplete or duplicate");
-    if (b->pages && b->pages != m.src_block_ids.size())
+    if (*pages && *pages != m.src_block_ids.size())
       return InvalidArgument("semantic transfer page coverage mismatch");
-    b->pages = m.src_block_ids.size();
-    b->by_layer[m.layer_idx] = &m;
+    *pages = m.src_block_ids.size();
+    (*by_layer)[m.layer_idx] = &m;
   }
-  if (!b->pages) return InvalidArgument("semantic transfer has no pages");
+  if (!*pages) return InvalidArgument("semantic transfer has no pages");
+  return base::error::Success();
+}
+
+base::Status prepare(const KVBlockManifest& manifest, const ArenaKVPool& source,
+                     const ArenaKVPool& destination, cache::TransferPlanner* planner, ManifestBinding* b) {
+  base::Status status = map_layers(manifest, source, destination, &b->by_layer, &b->pages);
+  if (!status) return status;
   b->src_geo = geometry_of(source);
   b->dst_geo = geometry_of(destination);
 
@@ -127,7 +138,7 @@ base::Status prepare(const KVBlockManifest& manifest, const ArenaKVPool& source,
     return cache::MakeKVPageSchema(1, d.layer_num, d.block_size, d.kv_head_num, d.head_size,
                                    base::MakeKVCacheStorageSpec(d.dtype, d.storage_mode), out);
   };
-  base::Status status = schema_of(source.pool, &b->src_schema);
+  status = schema_of(source.pool, &b->src_schema);
   if (!status) return status;
   status = schema_of(destination.pool, &b->dst_schema);
   if (!status) return status;
@@ -207,6 +218,80 @@ base::Status BindManifestTransfers(const KVBlockManifest& manifest, const ArenaK
   return base::error::Success();
 }
 
+// What the copy ops of any manifest between two pools share: the pools'
+// binding (schemas, plan, layouts; no layer mapping) and the first bound
+// page's operations as (component span, offset) pieces. Every page follows
+// the pieces at its own component addresses.
+struct CopyOpTemplate {
+  struct Piece {
+    size_t src_span, dst_span;
+    uint64_t src_off, dst_off, bytes;
+  };
+  ManifestBinding pools;  // by_layer cleared: the template outlives its manifest
+  std::vector<Piece> pieces;
+};
+
+namespace {
+
+// Binds page 0 of `b`'s manifest in full and keeps its operations as pieces.
+base::Status make_template(ManifestBinding&& b, const ArenaKVPool& source, const ArenaKVPool& destination,
+                           CopyOpTemplate* t) {
+  cache::ConstComponentEndpoint src;
+  cache::MutableComponentEndpoint dst;
+  base::Status status = endpoints(b, source, destination, 0, &src, &dst);
+  if (!status) return status;
+  cache::BoundTransfer first;
+  status = cache::BoundTransfer::BindComponents(*b.plan, b.src_schema, b.dst_schema, src, dst, &first);
+  if (!status) return status;
+  t->pieces.clear();
+  t->pieces.reserve(first.operations().size());
+  for (const auto& op : first.operations()) {
+    const size_t si = span_holding(src.components, op.source, op.bytes);
+    const size_t di = span_holding(dst.components, op.destination, op.bytes);
+    if (si == src.components.size() || di == dst.components.size())
+      return base::error::InternalError("bound operation outside its component span");
+    t->pieces.push_back({si, di, static_cast<uint64_t>(op.source - src.components[si].data),
+                         static_cast<uint64_t>(op.destination - dst.components[di].data), op.bytes});
+  }
+  b.by_layer.clear();
+  b.pages = 0;
+  t->pools = std::move(b);
+  return base::error::Success();
+}
+
+// The ops of every page: its component addresses, each checked as
+// endpoints() checks it, then the template's pieces at those addresses.
+base::Status emit_ops(const CopyOpTemplate& t, const std::vector<const KVBlockMapping*>& by_layer,
+                      size_t pages, const ArenaKVPool& source, const ArenaKVPool& destination,
+                      std::vector<pbe_copy_op>* ops) {
+  const ManifestBinding& b = t.pools;
+  std::vector<uint64_t> src_at(b.src_schema.components.size()), dst_at(b.dst_schema.components.size());
+  std::vector<pbe_copy_op> out(pages * t.pieces.size());
+  pbe_copy_op* o = out.data();
+  for (size_t page = 0; page < pages; ++page) {
+    PageMemo src_memo, dst_memo;
+    for (size_t i = 0; i < src_at.size(); ++i) {
+      const auto& c = b.src_schema.components[i];
+      uint8_t* a = nullptr;
+      if (!component_address(source, b.src_geo, c, by_layer[c.layer]->src_block_ids[page], &src_memo, &a))
+        return InvalidArgument("source block outside its page-major arena");
+      src_at[i] = reinterpret_cast<uint64_t>(a);
+    }
+    for (size_t i = 0; i < dst_at.size(); ++i) {
+      const auto& c = b.dst_schema.components[i];
+      uint8_t* a = nullptr;
+      if (!component_address(destination, b.dst_geo, c, by_layer[c.layer]->dst_block_ids[page], &dst_memo, &a))
+        return InvalidArgument("destination block outside its page-major arena");
+      dst_at[i] = reinterpret_cast<uint64_t>(a);
+    }
+    for (const auto& p : t.pieces) *o++ = {src_at[p.src_span] + p.src_off, dst_at[p.dst_span] + p.dst_off, p.bytes};
+  }
+  *ops = std::move(out);
+  return base::error::Success();
+}
+
+}  // namespace
+
 base::Status BindManifestCopyOps(const KVBlockManifest& manifest, const ArenaKVPool& source,
                                  const ArenaKVPool& destination, cache::TransferPlanner* planner,
                                  std::vector<pbe_copy_op>* ops) {
@@ -214,58 +299,12 @@ base::Status BindManifestCopyOps(const KVBlockManifest& manifest, const ArenaKVP
   ManifestBinding b;
   base::Status status = prepare(manifest, source, destination, planner, &b);
   if (!status) return status;
-  // The first page is bound in full; its operations, as (span, offset)
-  // pairs, are the template every page follows.
-  cache::ConstComponentEndpoint src;
-  cache::MutableComponentEndpoint dst;
-  status = endpoints(b, source, destination, 0, &src, &dst);
+  const std::vector<const KVBlockMapping*> by_layer = b.by_layer;
+  const size_t pages = b.pages;
+  CopyOpTemplate t;
+  status = make_template(std::move(b), source, destination, &t);
   if (!status) return status;
-  cache::BoundTransfer first;
-  status = cache::BoundTransfer::BindComponents(*b.plan, b.src_schema, b.dst_schema, src, dst, &first);
-  if (!status) return status;
-  struct Piece {
-    size_t src_span, dst_span;
-    uint64_t src_off, dst_off, bytes;
-  };
-  std::vector<Piece> pieces;
-  pieces.reserve(first.operations().size());
-  for (const auto& op : first.operations()) {
-    const size_t si = span_holding(src.components, op.source, op.bytes);
-    const size_t di = span_holding(dst.components, op.destination, op.bytes);
-    if (si == src.components.size() || di == dst.components.size())
-      return base::error::InternalError("bound operation outside its component span");
-    pieces.push_back({si, di, static_cast<uint64_t>(op.source - src.components[si].data),
-                      static_cast<uint64_t>(op.destination - dst.components[di].data), op.bytes});
-  }
-  // Every later page: its component addresses only (each checked as
-  // endpoints() checks it), then the template's operations.
-  std::vector<uint64_t> src_at(src.components.size()), dst_at(dst.components.size());
-  for (size_t i = 0; i < src_at.size(); ++i) src_at[i] = reinterpret_cast<uint64_t>(src.components[i].data);
-  for (size_t i = 0; i < dst_at.size(); ++i) dst_at[i] = reinterpret_cast<uint64_t>(dst.components[i].data);
-  std::vector<pbe_copy_op> out(b.pages * pieces.size());
-  pbe_copy_op* o = out.data();
-  for (size_t page = 0; page < b.pages; ++page) {
-    if (page) {
-      PageMemo src_memo, dst_memo;
-      for (size_t i = 0; i < src_at.size(); ++i) {
-        const auto& c = b.src_schema.components[i];
-        uint8_t* a = nullptr;
-        if (!component_address(source, b.src_geo, c, b.by_layer[c.layer]->src_block_ids[page], &src_memo, &a))
-          return InvalidArgument("source block outside its page-major arena");
-        src_at[i] = reinterpret_cast<uint64_t>(a);
-      }
-      for (size_t i = 0; i < dst_at.size(); ++i) {
-        const auto& c = b.dst_schema.components[i];
-        uint8_t* a = nullptr;
-        if (!component_address(destination, b.dst_geo, c, b.by_layer[c.layer]->dst_block_ids[page], &dst_memo, &a))
-          return InvalidArgument("destination block outside its page-major arena");
-        dst_at[i] = reinterpret_cast<uint64_t>(a);
-      }
-    }
-    for (const Piece& p : pieces) *o++ = {src_at[p.src_span] + p.src_off, dst_at[p.dst_span] + p.dst_off, p.bytes};
-  }
-  *ops = std::move(out);
-  return base::error::Success();
+  return emit_ops(t, by_layer, pages, source, destination, ops);
 }
 
 InProcKVBlockCopyConnector::InProcKVBlockCopyConnector(ArenaKVPool source, ArenaKVPool destination,
@@ -291,7 +330,26 @@ base::Status InProcKVBlockCopyConnector::submit(const KVBlockManifest& manifest,
   if (!status) return status;
   *handle = {next_handoff_id_++};
   std::vector<pbe_copy_op> ops;
-  status = BindManifestCopyOps(manifest, source_, destination_, &planner_, &ops);
+  // The pools are the connector's own, so their binding and the op template
+  // are made once, from the first manifest that binds; each handoff then
+  // only maps its layers and emits its pages' ops.
+  if (template_) {
+    std::vector<const KVBlockMapping*> by_layer;
+    size_t pages = 0;
+    status = map_layers(manifest, source_, destination_, &by_layer, &pages);
+    if (status) status = emit_ops(*template_, by_layer, pages, source_, destination_, &ops);
+  } else {
+    ManifestBinding b;
+    status = prepare(manifest, source_, destination_, &planner_, &b);
+    if (status) {
+      const std::vector<const KVBlockMapping*> by_layer = b.by_layer;
+      const size_t pages = b.pages;
+      auto t = std::make_shared<CopyOpTemplate>();
+      status = make_template(std::move(b), source_, destination_, t.get());
+      if (status) status = emit_ops(*t, by_layer, pages, source_, destination_, &ops);
+      if (status) template_ = std::move(t);
+    }
+  }
   uint64_t bytes = 0;
   if (status) {
     for (const auto& op : ops) bytes += op.bytes;

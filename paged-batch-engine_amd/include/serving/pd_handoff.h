@@ -6,6 +6,7 @@
 #define PBE_INCLUDE_SERVING_PD_HANDOFF_H_
 
 #include <cstdint>
+#include <memory>
 #include <string>
 #include <utility>
 #include <vector>
@@ -147,6 +148,10 @@ base::Status BindManifestCopyOps(const KVBlockManifest& manifest, const ArenaKVP
                                  const ArenaKVPool& destination, cache::TransferPlanner* planner,
                                  std::vector<pbe_copy_op>* ops);
 
+// The binding of a pool pair and its per-page op template (defined with the
+// connector).
+struct CopyOpTemplate;
+
 // InProcKVBlockCopyConnector (pd_handoff.cpp:80-213) over arena pools: each
 // handoff is bound through the TransferPlan and all of its component copies
 // (2*layers per page, plus scales for FP8 pools) run as one op-list kernel on
@@ -183,6 +188,7 @@ class InProcKVBlockCopyConnector final : public KVTransferConnector {
   void* stream_ = nullptr;
   bool owns_stream_ = false;
   cache::TransferPlanner planner_;
+  std::shared_ptr<const CopyOpTemplate> template_;
   uint64_t next_handoff_id_ = 1;
   uint64_t copied_bytes_ = 0;
   size_t last_ops_ = 0;

@@ -353,6 +353,8 @@ TEST_CASE("generic plan form: InProcKVBlockCopyConnector equals the run copy, BF
     const int st = 2 * layers;
     const std::vector<int32_t> src = {1 * st, 2 * st, 3 * st, 7 * st, 9 * st};
     const std::vector<int32_t> dst = {10 * st, 11 * st, 20 * st, 21 * st, 22 * st};
+    const std::vector<int32_t> src2 = {4 * st, 5 * st, 6 * st};
+    const std::vector<int32_t> dst2 = {13 * st, 14 * st, 15 * st};
     serving::KVBlockManifest m;
     m.client_request_id.value = "g";
     m.handoff_id.value = 3;
@@ -366,17 +368,38 @@ TEST_CASE("generic plan form: InProcKVBlockCopyConnector equals the run copy, BF
       CHECK(conn.drain(h).ok());
       CHECK_EQ(conn.last_op_count(), src.size() * 2 * layers * (fp8 ? 2 : 1));
       conn.release(h);
+      // Later handoffs reuse the binding the first one made: another plan
+      // with another page count, then manifests the binding must still refuse
+      // (a bad id on the first page or a later one, a missing layer).
+      serving::KVBlockManifest m2 = m;
+      for (auto& lm : m2.layer_mappings) lm = {lm.layer_idx, src2, dst2};
+      REQUIRE(conn.submit(m2, &h));
+      CHECK(conn.drain(h).ok());
+      CHECK_EQ(conn.last_op_count(), src2.size() * 2 * layers * (fp8 ? 2 : 1));
+      conn.release(h);
+      serving::HandoffId bad;
+      for (const auto& ids : {std::vector<int32_t>{99 * st, 14 * st, 15 * st},
+                              std::vector<int32_t>{13 * st, 14 * st, 5 * st + 1}}) {
+        serving::KVBlockManifest mb = m;
+        for (auto& lm : mb.layer_mappings) lm = {lm.layer_idx, src2, ids};
+        CHECK(!conn.submit(mb, &bad));
+        CHECK(conn.poll(bad).state == serving::KVTransferState::kFailed);
+      }
+      serving::KVBlockManifest short_layers = m2;
+      short_layers.layer_mappings.pop_back();
+      CHECK(!conn.submit(short_layers, &bad));
     }
     std::vector<uint8_t> got(bytes), got_sc(host_sc.size());
     HIP_OK(hipMemcpy(got.data(), arena, bytes, hipMemcpyDeviceToHost));
     HIP_OK(hipMemcpy(got_sc.data(), scales, got_sc.size(), hipMemcpyDeviceToHost));
     std::vector<uint8_t> want = host, want_sc = host_sc;
-    for (size_t i = 0; i < src.size(); ++i) {
-      std::memcpy(want.data() + dst[i] / st * page, host.data() + src[i] / st * page, page);
-      if (fp8)
-        std::memcpy(want_sc.data() + dst[i] / st * scale_page, host_sc.data() + src[i] / st * scale_page,
-                    scale_page);
-    }
+    for (const auto& [from, to] : {std::make_pair(src, dst), std::make_pair(src2, dst2)})
+      for (size_t i = 0; i < from.size(); ++i) {
+        std::memcpy(want.data() + to[i] / st * page, host.data() + from[i] / st * page, page);
+        if (fp8)
+          std::memcpy(want_sc.data() + to[i] / st * scale_page, host_sc.data() + from[i] / st * scale_page,
+                      scale_page);
+      }
     CHECK(got == want);
     CHECK(got_sc == want_sc);
     (void)hipFree(arena);
