@@ -310,7 +310,8 @@ int pbe_copy_ops(const pbe_copy_op* ops, int64_t n_ops, int device, void* stream
 #define PBE_KV_FP8_E4M3 1
 /* Split count for a decode launch on the current GPU (its CU count sets the
  * wave budget): kv_dtype as for pbe_paged_decode (FP8 pages run two waves per
- * SIMD, BF16 pages one). max_blocks_per_seq here should be the block count of
+ * SIMD while every split keeps at least 8 blocks, BF16 pages one; at least 4
+ * blocks per split). max_blocks_per_seq here should be the block count of
  * the longest live sequence, not the block-table capacity: a table sized for
  * the maximum context would pick splits too short to keep the reader busy.
  * Size the workspace with the result. */
