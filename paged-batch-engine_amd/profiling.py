@@ -322,6 +322,9 @@ def hostpaths(log: str, out: str, command: str) -> None:
         ("template binding (BindManifestCopyOps)", g["copy_op_binding"]),
         ("pbe_copy_ops host call for the 17,640 component ops", g["copy_ops_call"]),
         ("connector submit -> drain", g["connector_submit_drain"]),
+        *([("HIP TransferBackend, 315 page transfers (submit, drain)", g["hip_backend_315_transfers"]),
+           ("the 17,640 ops, a hipMemcpyAsync each (reference pattern)", g["per_op_memcpy_17640"])]
+          if "hip_backend_315_transfers" in g else []),
         ("", None),
         ("reference copy_shared_kv call order (serving::CopySharedKVToDecode)", None),
         ("append_slots, 28 layers (register_request + append_slots)", r["reserve_28_layers"]),

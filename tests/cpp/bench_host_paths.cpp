@@ -2,7 +2,10 @@
 // 28 layers, 315 pages), run by `bench.py --host-paths`; prints one JSON object.
 //   - the generic plan form (InProcKVBlockCopyConnector, pd_handoff.cpp:192-213):
 //     per-page BindComponents binding, BindManifestCopyOps, pbe_copy_ops of the
-//     op list, and the connector's submit -> drain;
+//     op list, and the connector's submit -> drain; the 315 per-page
+//     BoundTransfers through the HIP TransferBackend (submit all, drain), and
+//     their 17,640 component ops as one hipMemcpyAsync each, the reference
+//     CudaTransferBackend's pattern (cuda_transfer_backend.cpp:19-128);
 //   - the reference's copy_shared_kv call order (split_pd_engine.cpp:49-115)
 //     through serving::CopySharedKVToDecode: append_slots over 28 layers, the
 //     whole call, and free_request afterwards; and the reservation while the
@@ -20,6 +23,7 @@
 
 #include "base/kv_cache_manager.h"
 #include "base/shared_kv_arena.h"
+#include "cache/page_migration.h"
 #include "cache/transfer_plan.h"
 #include "pbe_handoff.h"
 #include "serving/pd_handoff.h"
@@ -59,7 +63,7 @@ int main() {
   const serving::KVPoolDescriptor pool_desc{0, kLayers, 16, kHeads, kDim, base::DataType::kDataTypeBf16,
                                             base::BlockStorageMode::kPlain};
   // ---- generic plan form over a 1000-page device arena
-  std::vector<double> bind_us, ops_us, call_us, conn_us;
+  std::vector<double> bind_us, ops_us, call_us, conn_us, backend_us, per_op_us;
   {
     const uint64_t pages = 1000, bytes = pages * page;
     uint8_t* arena = nullptr;
@@ -84,6 +88,10 @@ int main() {
     m.src_pool = m.dst_pool = pool_desc;
     for (int l = 0; l < kLayers; ++l) m.layer_mappings.push_back({l, src, dst});
     serving::InProcKVBlockCopyConnector conn(pool, pool, 0);
+    auto backend = cache::MakeHipTransferBackend(512, 0);
+    CHECK_OR(backend != nullptr, 10);
+    hipStream_t ref_stream = nullptr;
+    CHECK_OR(hipStreamCreateWithFlags(&ref_stream, hipStreamNonBlocking) == hipSuccess, 11);
     for (int it = 0; it < kIters; ++it) {
       cache::TransferPlanner planner;
       std::vector<cache::BoundTransfer> t;
@@ -106,6 +114,37 @@ int main() {
       conn_us.push_back(now_us() - a);
       conn.release(h);
     }
+    // Then, apart (their thousands of runtime calls would otherwise sit
+    // between the legs above): the page transfers through the HIP backend,
+    // and the same ops as one async memcpy each.
+    {
+      cache::TransferPlanner planner;
+      std::vector<cache::BoundTransfer> t;
+      CHECK_OR(serving::BindManifestTransfers(m, pool, pool, &planner, &t), 16);
+      for (int it = 0; it < kIters; ++it) {
+        // the page transfers through the HIP backend: one launch per transfer
+        // on its in-order stream, the last drain waits for all
+        const cache::MigrationId base_id = 1000ull * (it + 1);
+        double a = now_us();
+        for (size_t i = 0; i < t.size(); ++i) {
+          const auto r = backend->submit(base_id + i, cache::TransferDirection::kGpuToGpu, t[i]);
+          CHECK_OR(r == cache::BackendResult::kPending || r == cache::BackendResult::kSucceeded, 12);
+        }
+        for (size_t i = 0; i < t.size(); ++i)
+          CHECK_OR(backend->drain(base_id + i) == cache::BackendResult::kSucceeded, 13);
+        backend_us.push_back(now_us() - a);
+        for (size_t i = 0; i < t.size(); ++i) backend->release(base_id + i);
+        // the reference backend's pattern: one async memcpy per component op
+        a = now_us();
+        for (const auto& bt : t)
+          for (const auto& op : bt.operations())
+            CHECK_OR(hipMemcpyAsync(op.destination, op.source, op.bytes, hipMemcpyDeviceToDevice, ref_stream) ==
+                         hipSuccess, 14);
+        CHECK_OR(hipStreamSynchronize(ref_stream) == hipSuccess, 15);
+        per_op_us.push_back(now_us() - a);
+      }
+    }
+    (void)hipStreamDestroy(ref_stream);
     (void)hipFree(arena);
   }
   // ---- the reference's call order over KVCacheManager and a shared arena
@@ -235,13 +274,15 @@ int main() {
   std::printf(
       "{\"workload\": \"c2_host_paths\", \"pages\": %d, \"layers\": %d, \"iterations\": %d, "
       "\"generic_plan_form_us\": {\"per_page_binding\": %.1f, \"copy_op_binding\": %.1f, "
-      "\"copy_ops_call\": %.1f, \"connector_submit_drain\": %.1f}, "
+      "\"copy_ops_call\": %.1f, \"connector_submit_drain\": %.1f, "
+      "\"hip_backend_315_transfers\": %.1f, \"per_op_memcpy_17640\": %.1f}, "
       "\"reference_call_order_us\": {\"reserve_28_layers\": %.1f, \"end_to_end\": %.1f, "
       "\"copy_and_sync_alone\": %.1f, \"free_request\": %.1f, "
       "\"reserve_under_pending_fences\": %.1f, \"steps\": {\"request_copies\": %.1f, "
       "\"reserve_and_manifest\": %.1f, \"pbe_copy_shared_kv_call\": %.1f, \"stream_wait\": %.1f, "
       "\"commit_kv\": %.1f}}}\n",
       kPages, kLayers, kIters, median(bind_us), median(ops_us), median(call_us), median(conn_us),
+      median(backend_us), median(per_op_us),
       median(reserve_us), median(e2e_us), median(copy_us), median(free_us), median(busy_us),
       median(step_request_us), median(step_reserve_us), median(step_launch_us), median(step_wait_us),
       median(step_commit_us));
