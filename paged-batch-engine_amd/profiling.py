@@ -344,7 +344,7 @@ def hostpaths(log: str, out: str, command: str) -> None:
              f"{d['layers']} layers), MI355X box", f"command: {command}",
              f"medians over {d['iterations']} iterations, microseconds", ""]
     for name, v in rows:
-        lines.append(name if v is None else f"  {name:<57}{v:>7.1f}")
+        lines.append(name if v is None else f"  {name:<58}{v:>8.1f}")
     lines += ["", "raw line:", line]
     text = "\n".join(lines) + "\n"
     Path(out).write_text(text)
