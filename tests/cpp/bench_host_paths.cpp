@@ -62,16 +62,15 @@ int main() {
   const uint64_t half = 16 * kHeads * kDim * 2, page = 2ull * kLayers * half;
   const serving::KVPoolDescriptor pool_desc{0, kLayers, 16, kHeads, kDim, base::DataType::kDataTypeBf16,
                                             base::BlockStorageMode::kPlain};
-  // ---- generic plan form over a 1000-page device arena
+  // ---- generic plan form over a 1000-page device arena, made as the library
+  // makes pools (pbe_arena_create: its allocation is in the library's registry)
   std::vector<double> bind_us, ops_us, call_us, conn_us, backend_us, per_op_us;
   {
     const uint64_t pages = 1000, bytes = pages * page;
-    uint8_t* arena = nullptr;
-    CHECK_OR(hipMalloc(&arena, bytes) == hipSuccess, 2);
+    pbe_arena* arena = nullptr;
+    CHECK_OR(pbe_arena_create(0, bytes, bytes, 1, &arena) == PBE_OK, 2);
     serving::ArenaKVPool pool;
-    pool.view.bytes = pool.view.segment_bytes = bytes;
-    pool.view.nseg = 1;
-    pool.view.base[0] = arena;
+    pbe_arena_get_view(arena, &pool.view);
     pool.pool = pool_desc;
     std::vector<int> perm(pages);
     std::iota(perm.begin(), perm.end(), 0);
@@ -145,7 +144,7 @@ int main() {
       }
     }
     (void)hipStreamDestroy(ref_stream);
-    (void)hipFree(arena);
+    pbe_arena_destroy(arena);
   }
   // ---- the reference's call order over KVCacheManager and a shared arena
   std::vector<double> reserve_us, e2e_us, free_us, busy_us, copy_us;
