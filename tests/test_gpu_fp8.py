@@ -222,3 +222,24 @@ def test_fp8_contiguous_sources(torch_cuda, mode, layers, kv_heads, head_dim, n_
     amax = rng.uniform(2.5, 5.0, (2 * g.layers, g.kv_heads))
     say(f"fp8 contiguous sources mode={mode} L={layers} H={kv_heads} D={head_dim} runs={n_runs}")
     _check(torch, pools, src, dst, mode, amax)
+
+
+@pytest.mark.parametrize("mode", [P.PBE_FP8_SCALE_PER_TOKEN_HEAD, P.PBE_FP8_SCALE_TABLE])
+def test_fp8_scattered_sources_many_runs(torch_cuda, mode):
+    """The general path at the 1.5B geometry: 200 pages in runs of 1-4 on
+    scattered sources, which the run list reorders by destination address;
+    destinations, scales and every other byte against the oracle."""
+    torch = torch_cuda
+    n_pages = 4 * 200 + 16
+    w = W.small(seed=77, layers=28, kv_heads=2, head_dim=128, n_pages=n_pages, handoff_pages=200,
+                max_run=4)
+    g = w.geometry
+    kv = P.shape(g.layers, g.kv_heads, g.head_dim, g.page_tokens)
+    runs = P.build_runs(w.src_ids, w.dst_ids, kv)
+    assert len(runs) > 50
+    assert any(runs[i][1] > runs[i + 1][1] for i in range(len(runs) - 1))  # not already in dst order
+    pools = Fp8Pools(torch, g, n_pages)
+    fill_bf16(torch, pools.src, 1.0, 77, 0.001, 40.0)
+    amax = np.random.default_rng(77).uniform(2.5, 5.0, (2 * g.layers, g.kv_heads))
+    say(f"fp8 scattered many runs mode={mode} runs={len(runs)}")
+    _check(torch, pools, w.src_ids, w.dst_ids, mode, amax)
